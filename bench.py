@@ -1,0 +1,261 @@
+"""Benchmark of the tensor-relational sparse einsum on one MI355X.
+
+Workload (the headline configuration): 'ij,jk->ik' with A a 16384 x 16384
+bf16 block-sparse matrix (128 x 128 tiles, 5% of tiles nonzero, uniform,
+N(0,1)) and B a dense 16384 x 4096 bf16 matrix (N(0, 1/sqrt(16384))) held as
+a 128 x 128 tile relation; fp32 accumulation and output.  Synthetic, seeded
+(numpy default_rng(0)), resident in HBM before timing.
+
+A step is one execute_sparse call on the resident relations: tile join
+(count + fill), segment plan (count + fill) and the fused gather + MFMA tile
+GEMM + segment sum, including the two host synchronisations the data-
+dependent sizes need.  value = effective TFLOP/s = nonzero-tile FLOPs
+(2*M*N*K per matched pair) / step time.
+
+Also reported: every stage timed alone with HIP events on the stream the
+kernels run on (the reference's unfused phase split: join, gather, per-pair
+GEMM, segment sum; plus tiling), achieved GB/s against HBM for
+join+gather+segment-sum, the roofline of the dominant kernel, and the CPU
+oracle timed on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2516.6, "fp32": 157.3}
+METRIC = "effective TFLOP/s (nnz tiles) + HBM GB/s per einsum, 1 MI355X vs host CPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def event_time_ms(fn, reps: int) -> float:
+    """Average duration of fn() over reps, with HIP events on the current stream."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def wall_time_ms(fn, reps: int) -> float:
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / reps
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json), or None when absent."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text()).get(kernel)
+        return None if d is None else float(d["hbm_bytes_per_dispatch"])
+    except Exception:
+        return None
+
+
+def cpu_baseline(w, band_tiles: int):
+    """The oracle (NumPy restatement of the reference path, fp32 math) on the
+    A rows in the first `band_tiles` row tiles."""
+    from oracle import reference_path as R
+    from oracle import workload as W
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        cores = os.cpu_count() or 1
+    L, Rr = w["lhs"], w["rhs"]
+    band = L.coords[:, 0] < band_tiles
+    sub = R.Rel(L.coords[band], L.values[band], L.shape, L.tile_shape)
+    t0 = time.perf_counter()
+    li, _ = R.coordinate_join(sub.coords, Rr.coords, w["join_keys"])
+    out = R.execute_sparse(sub, Rr, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                           precision="fp32")
+    t = time.perf_counter() - t0
+    flops = W.flops_gemm(w["kernel_string"], L.tile_shape, Rr.tile_shape, len(li))
+    rows = band_tiles * L.tile_shape[0]
+    return {
+        "value": flops / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": (f"A rows 0-{rows - 1} ({band_tiles} of {L.shape[0] // L.tile_shape[0]} row "
+                   f"tiles, {len(li)} of the pairs, {out.coords.shape[0]} output tiles) x full B; "
+                   f"join + gather + fp32 einsum + segment sum in {t:.1f} s (the join runs "
+                   f"twice: once to count the sample's FLOPs)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path runs "
+              "one process per GPU and this build has no multi-GPU mode)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from einjax_amd import SparseTensorRelation, _device, execute_sparse
+    from einjax_amd.execution import sparse_dispatch as sd
+    from oracle import generators as G
+    from oracle import workload as W
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    t0 = time.perf_counter()
+    w = G.workload_blocksparse_16k()
+    L, Rr = w["lhs"], w["rhs"]
+    log(f"generated {w['name']} in {time.perf_counter() - t0:.1f} s")
+
+    def dev(r):
+        return SparseTensorRelation(torch.from_numpy(r.coords).cuda(),
+                                    torch.from_numpy(r.values).cuda().to(torch.bfloat16), r.shape,
+                                    r.tile_shape)
+
+    lhs, rhs = dev(L), dev(Rr)
+    torch.cuda.synchronize()
+    jk, ak, ks = w["join_keys"], w["agg_keys"], w["kernel_string"]
+
+    def step():
+        return execute_sparse(lhs, rhs, jk, ks, ak)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    P_pairs = None
+
+    # ---- stages ----------------------------------------------------------
+    lc, rc = lhs.coords, rhs.coords
+    li, ri = sd._join_dev(lhs, rhs, jk, lc, rc)
+    P = li.numel()
+    radices = [sd._grid(lhs if s == 0 else rhs, d) for s, d in ak]
+    coords, offs, perm, _ = _device.segment_plan(lc, rc, li, ri, ak, radices)
+    U = coords.shape[0]
+    desc = _device.describe(ks, L.tile_shape, Rr.tile_shape)
+    reps = 10
+    t_join = wall_time_ms(lambda: sd._join_dev(lhs, rhs, jk, lc, rc), reps)
+    t_plan = wall_time_ms(lambda: _device.segment_plan(lc, rc, li, ri, ak, radices), reps)
+    t_fused = event_time_ms(
+        lambda: _device.segment_einsum(desc, lhs.values, rhs.values, li, ri, perm, offs), reps)
+    ga = _device.gather_tiles(lhs.values, li)
+    gb = _device.gather_tiles(rhs.values, ri)
+    t_gather = event_time_ms(lambda: (_device.gather_tiles(lhs.values, li),
+                                      _device.gather_tiles(rhs.values, ri)), reps)
+    t_pair = event_time_ms(lambda: _device.pair_einsum(desc, ga, gb, n_pairs=P), reps)
+    pv = _device.pair_einsum(desc, ga, gb, n_pairs=P)
+    t_segsum = event_time_ms(lambda: _device.segment_sum(pv, perm, offs), reps)
+    del ga, gb, pv
+    dense_a = lhs.to_dense()
+    t_bucket = wall_time_ms(lambda: _device.bucket_dense(dense_a, L.tile_shape), 5)
+    del dense_a
+    torch.cuda.synchronize()
+
+    e = 2
+    F = W.flops_gemm(ks, L.tile_shape, Rr.tile_shape, P)
+    B_join = W.bytes_join(L.coords.shape[0], Rr.coords.shape[0], P)
+    B_gather = W.bytes_gather(P, L.tile_shape, Rr.tile_shape, e)
+    B_segsum = W.bytes_segsum(P, U, (L.tile_shape[0], Rr.tile_shape[1]), 2)
+    B_bucket = W.bytes_bucket(int(np.prod(L.shape)), L.coords.shape[0], L.tile_shape, e, 2)
+    n_lhs_used = len(np.unique(li.cpu().numpy()))
+    n_rhs_used = len(np.unique(ri.cpu().numpy()))
+    B_fused = W.bytes_fused(n_lhs_used, n_rhs_used, L.tile_shape, Rr.tile_shape, e, U,
+                            (L.tile_shape[0], Rr.tile_shape[1]), 2)
+    jgs_gbs = (B_join + B_gather + B_segsum) / ((t_join + t_gather + t_segsum) * 1e-3) / 1e9
+    fused_tflops = F / (t_fused * 1e-3) / 1e12
+    kernel_name = "tile_gemm_kernel<bf16,128,128,64>"
+    traffic = load_traffic(kernel_name)
+
+    res = {
+        "metric": METRIC,
+        "value": F / (ms_step * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded numpy default_rng(0); relations resident in HBM)",
+        "config": {
+            "workload": "block-sparse x dense 'ij,jk->ik': A 16384x16384 bf16, 128x128 tiles, "
+                        "5% tile density uniform; B dense 16384x4096 bf16 N(0,1/128); fp32 "
+                        "accumulate",
+            "pairs": P, "output_tiles": U, "lhs_tiles": int(L.coords.shape[0]),
+            "rhs_tiles": int(Rr.coords.shape[0]), "gflop": F / 1e9,
+        },
+        "roofline": {
+            "bound": "mfma", "kernel": kernel_name,
+            "achieved": fused_tflops, "peak": MFMA_PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
+            "frac": fused_tflops / MFMA_PEAK_TFLOPS["bf16"],
+            "traffic": traffic,
+            "algorithmic_bytes": B_fused,
+        },
+        "stages_ms": {
+            "join": t_join, "segment_plan": t_plan, "fused_gemm_segsum": t_fused,
+            "gather": t_gather, "pair_gemm": t_pair, "segment_sum": t_segsum,
+            "bucket_dense_A": t_bucket,
+        },
+        "stages_gbs": {
+            "join": B_join / (t_join * 1e-3) / 1e9,
+            "gather": B_gather / (t_gather * 1e-3) / 1e9,
+            "segment_sum": B_segsum / (t_segsum * 1e-3) / 1e9,
+            "bucket_dense_A": B_bucket / (t_bucket * 1e-3) / 1e9,
+            "join_gather_segsum": jgs_gbs,
+            "join_gather_segsum_hbm_frac": jgs_gbs / HBM_PEAK_GBS,
+        },
+        "unfused_tflops": F / ((t_join + t_plan + t_gather + t_pair + t_segsum) * 1e-3) / 1e12,
+        "pair_gemm_tflops": F / (t_pair * 1e-3) / 1e12,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on a sample ...")
+        res["cpu_baseline"] = cpu_baseline(w, band_tiles=16)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,237 @@
+"""Device-side phases of the sparse-einsum path, on HIP through libejhip.so.
+
+Every function takes and returns torch tensors resident on the current
+GPU; torch supplies the memory and the current stream, all arithmetic runs
+in the library's kernels.  Sizes that depend on the data (pairs, segments,
+tiles) come back through the library's *_count calls, one host
+synchronisation each.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from math import prod
+
+import torch
+
+from . import _lib
+from ._lib import check, i32_array, i64_array
+
+_VALUE_DTYPES = {torch.float32: _lib.EJ_F32, torch.bfloat16: _lib.EJ_BF16}
+
+
+def require_gpu() -> torch.device:
+    """The current GPU; raises when none is visible (there is no CPU path)."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("the sparse-einsum path runs on a ROCm GPU and none is visible")
+    _lib.load()
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def stream_ptr() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None and t.numel() > 0 else 0)
+
+
+def workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def value_code(t: torch.Tensor) -> int:
+    try:
+        return _VALUE_DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"tile values must be float32 or bfloat16 on the device, got {t.dtype}")
+
+
+def as_coords(t: torch.Tensor, device) -> torch.Tensor:
+    t = t.to(device=device, dtype=torch.int32)
+    if t.dim() == 1:
+        t = t.reshape(-1, 1) if t.numel() else t.reshape(0, 0)
+    return t.contiguous()
+
+
+def as_index(t: torch.Tensor, device) -> torch.Tensor:
+    return t.to(device=device, dtype=torch.int64).contiguous().reshape(-1)
+
+
+# ---------------------------------------------------------------------------
+
+def coords_range(coords: torch.Tensor) -> tuple[list[int], list[int]]:
+    """Per-column (min, max) of int32 coordinates [n, ncols]."""
+    n, nc = coords.shape
+    lo_hi = (ctypes.c_int32 * max(1, 2 * nc))()
+    ws = workspace(8 * max(nc, 1), coords.device)
+    check(_lib.load().ej_coords_range(ptr(coords), n, nc, lo_hi, ptr(ws), ws.numel(),
+                                      stream_ptr()), "ej_coords_range")
+    return [lo_hi[2 * c] for c in range(nc)], [lo_hi[2 * c + 1] for c in range(nc)]
+
+
+def join(lhs_coords: torch.Tensor, rhs_coords: torch.Tensor, join_keys, radices,
+         order: int = _lib.EJ_ORDER_PROBE) -> tuple[torch.Tensor, torch.Tensor]:
+    """Matched (lhs_idx, rhs_idx) int64 pairs in the reference's order."""
+    lib = _lib.load()
+    dev = lhs_coords.device
+    n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
+    nk = len(join_keys)
+    ld = i32_array([k[0] for k in join_keys])
+    rd = i32_array([k[1] for k in join_keys])
+    rad = i64_array(radices)
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_join_workspace_size(n_l, n_r, order, ctypes.byref(nbytes)),
+          "ej_join_workspace_size")
+    ws = workspace(nbytes.value, dev)
+    n_pairs = ctypes.c_int64()
+    check(lib.ej_join_count(ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r,
+                            rhs_coords.shape[1], nk, ld, rd, rad, order, ptr(ws), ws.numel(),
+                            ctypes.byref(n_pairs), stream_ptr()), "ej_join_count")
+    P = n_pairs.value
+    li = torch.empty(P, dtype=torch.int64, device=dev)
+    ri = torch.empty(P, dtype=torch.int64, device=dev)
+    check(lib.ej_join_fill(n_l, n_r, nk, order, ptr(ws), ws.numel(), P, ptr(li), ptr(ri), P,
+                           stream_ptr()), "ej_join_fill")
+    return li, ri
+
+
+def output_coords(lhs_coords, rhs_coords, lhs_idx, rhs_idx, agg_keys) -> torch.Tensor:
+    n_out = len(agg_keys)
+    P = lhs_idx.numel()
+    out = torch.empty((P, n_out), dtype=torch.int32, device=lhs_coords.device)
+    check(_lib.load().ej_output_coords(
+        ptr(lhs_coords), lhs_coords.shape[1], ptr(rhs_coords), rhs_coords.shape[1], ptr(lhs_idx),
+        ptr(rhs_idx), P, n_out, i32_array([s for s, _ in agg_keys]),
+        i32_array([d for _, d in agg_keys]), ptr(out), stream_ptr()), "ej_output_coords")
+    return out
+
+
+def segment_plan(lhs_coords, rhs_coords, lhs_idx, rhs_idx, agg_keys, radices):
+    """Groups pairs by output coordinate.
+
+    Returns (out_coords int32 [U, n_out], seg_offsets int32 [U+1],
+    perm int32 [P], seg_ids int32 [P])."""
+    lib = _lib.load()
+    dev = lhs_coords.device
+    P = lhs_idx.numel()
+    n_out = len(agg_keys)
+    src = i32_array([s for s, _ in agg_keys])
+    dim = i32_array([d for _, d in agg_keys])
+    rad = i64_array(radices)
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_segment_workspace_size(P, ctypes.byref(nbytes)), "ej_segment_workspace_size")
+    ws = workspace(nbytes.value, dev)
+    n_seg = ctypes.c_int64()
+    check(lib.ej_segment_count(ptr(lhs_coords), lhs_coords.shape[1], ptr(rhs_coords),
+                               rhs_coords.shape[1], ptr(lhs_idx), ptr(rhs_idx), P, n_out, src, dim,
+                               rad, ptr(ws), ws.numel(), ctypes.byref(n_seg), stream_ptr()),
+          "ej_segment_count")
+    U = n_seg.value
+    out_coords = torch.empty((U, n_out), dtype=torch.int32, device=dev)
+    offsets = torch.empty(U + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(P, dtype=torch.int32, device=dev)
+    seg_ids = torch.empty(P, dtype=torch.int32, device=dev)
+    check(lib.ej_segment_fill(P, U, n_out, rad, ptr(ws), ws.numel(), ptr(out_coords),
+                              ptr(offsets), ptr(perm), ptr(seg_ids), U, stream_ptr()),
+          "ej_segment_fill")
+    return out_coords, offsets, perm, seg_ids
+
+
+def gather_tiles(values: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """values[idx] for whole tiles (the reference's fancy-index gather)."""
+    n = idx.numel()
+    out = torch.empty((n, *values.shape[1:]), dtype=values.dtype, device=values.device)
+    tile_bytes = values.element_size() * prod(values.shape[1:])
+    if n == 0 or tile_bytes == 0:
+        return out
+    check(_lib.load().ej_gather_tiles(ptr(values), values.shape[0], tile_bytes, ptr(idx), n,
+                                      ptr(out), stream_ptr()), "ej_gather_tiles")
+    return out
+
+
+def describe(kernel_string: str, lhs_tile, rhs_tile) -> _lib.EinsumDesc:
+    d = _lib.EinsumDesc()
+    check(_lib.load().ej_einsum_describe(kernel_string.encode(), i64_array(lhs_tile),
+                                         len(lhs_tile), i64_array(rhs_tile), len(rhs_tile),
+                                         ctypes.byref(d)), "ej_einsum_describe")
+    return d
+
+
+def _out_tile(desc: _lib.EinsumDesc) -> tuple:
+    return tuple(int(desc.out_ext[i]) for i in range(desc.n_out))
+
+
+def pair_einsum(desc, lhs_values, rhs_values, lhs_idx=None, rhs_idx=None, n_pairs=None):
+    """fp32 [P, *out_tile]: the tile einsum of every matched pair."""
+    code = value_code(lhs_values)
+    if rhs_values.dtype != lhs_values.dtype:
+        raise TypeError("both operands must have the same value dtype")
+    P = lhs_idx.numel() if lhs_idx is not None else int(n_pairs)
+    out = torch.empty((P, *_out_tile(desc)), dtype=torch.float32, device=lhs_values.device)
+    check(_lib.load().ej_pair_einsum(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
+                                     lhs_values.shape[0], rhs_values.shape[0], ptr(lhs_idx),
+                                     ptr(rhs_idx), P, ptr(out), stream_ptr()), "ej_pair_einsum")
+    return out
+
+
+def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_offsets):
+    """fp32 [U, *out_tile]: fused gather + tile einsum + segment sum."""
+    code = value_code(lhs_values)
+    if rhs_values.dtype != lhs_values.dtype:
+        raise TypeError("both operands must have the same value dtype")
+    U = seg_offsets.numel() - 1
+    out = torch.empty((U, *_out_tile(desc)), dtype=torch.float32, device=lhs_values.device)
+    check(_lib.load().ej_segment_einsum(ctypes.byref(desc), code, ptr(lhs_values),
+                                        ptr(rhs_values), lhs_values.shape[0], rhs_values.shape[0],
+                                        ptr(lhs_idx), ptr(rhs_idx), ptr(perm), ptr(seg_offsets),
+                                        U, ptr(out), stream_ptr()), "ej_segment_einsum")
+    return out
+
+
+def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:
+    """fp32 [U, *tile]: per-segment sums in plan order."""
+    U = seg_offsets.numel() - 1
+    tile = tuple(pair_values.shape[1:])
+    out = torch.empty((U, *tile), dtype=torch.float32, device=pair_values.device)
+    check(_lib.load().ej_segment_sum(ptr(pair_values), max(prod(tile), 1), ptr(perm),
+                                     ptr(seg_offsets), U, ptr(out), stream_ptr()),
+          "ej_segment_sum")
+    return out
+
+
+def bucket_dense(dense: torch.Tensor, tile_shape) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense tensor -> (coords int32 [T, nd], values [T, *tile_shape]).
+
+    float32 / bfloat16 tiles keep the input dtype; float64 input decides
+    occupancy in float64 and yields float32 tiles."""
+    lib = _lib.load()
+    code = _lib.EJ_F64 if dense.dtype == torch.float64 else value_code(dense)
+    out_dtype = torch.float32 if dense.dtype == torch.float64 else dense.dtype
+    dense = dense.contiguous()
+    nd = dense.dim()
+    shape = i64_array(dense.shape)
+    tile = i64_array(tile_shape)
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_bucket_workspace_size(nd, shape, tile, ctypes.byref(nbytes)),
+          "ej_bucket_workspace_size")
+    ws = workspace(nbytes.value, dense.device)
+    n_tiles = ctypes.c_int64()
+    check(lib.ej_bucket_dense_count(ptr(dense), code, nd, shape, tile, ptr(ws), ws.numel(),
+                                    ctypes.byref(n_tiles), stream_ptr()), "ej_bucket_dense_count")
+    T = n_tiles.value
+    coords = torch.empty((T, nd), dtype=torch.int32, device=dense.device)
+    values = torch.empty((T, *tile_shape), dtype=out_dtype, device=dense.device)
+    check(lib.ej_bucket_dense_fill(ptr(dense), code, nd, shape, tile, ptr(ws), ws.numel(), T,
+                                   ptr(coords), ptr(values), T, stream_ptr()),
+          "ej_bucket_dense_fill")
+    return coords, values
+
+
+def relation_to_dense(coords, values, shape, tile_shape) -> torch.Tensor:
+    code = value_code(values)
+    dense = torch.empty(tuple(shape), dtype=values.dtype, device=values.device)
+    check(_lib.load().ej_relation_to_dense(ptr(coords), ptr(values), coords.shape[0], code,
+                                           len(shape), i64_array(shape), i64_array(tile_shape),
+                                           ptr(dense), stream_ptr()), "ej_relation_to_dense")
+    return dense

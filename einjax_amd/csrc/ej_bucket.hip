@@ -1,0 +1,302 @@
+// Coordinate-to-tile bucketing of a dense tensor, and its inverse.
+//
+// Reference: SparseTensor.to_relation (tensor/sparse.py:160-219) takes the
+// nonzero elements (values != 0, :184-187), computes idx // tile and
+// idx % tile (:200-201), orders the distinct tile coordinates
+// lexicographically with np.unique(axis=0) (:204-206) and scatters the
+// nonzero values into zero tiles (:210-212).  For a dense row-major input
+// the lexicographic order of tile coordinates is the row-major order of the
+// tile grid, so no sort is needed:
+//   count: one pass over the dense tensor flags every tile holding an
+//          element != 0; an exclusive scan of the flags gives each kept
+//          tile its slot and the tile count T;
+//   fill:  one workgroup per kept tile copies it into the packed
+//          [T, *tile] array (zeros normalised to +0.0, as the reference's
+//          scatter into np.zeros leaves them) and writes its coordinates.
+#include "ej_internal.h"
+
+namespace ej {
+namespace {
+
+struct BucketGeom {
+  int32_t nd;
+  int64_t shape[EJ_MAX_DIMS], tile[EJ_MAX_DIMS], grid[EJ_MAX_DIMS];
+  int64_t dstride[EJ_MAX_DIMS];  // dense row-major strides
+  int64_t tile_elems, n_tiles;   // elements per tile, tiles in the grid
+  int64_t inner;                 // tile[nd-1]: contiguous run length in HBM
+  int64_t rows;                  // tile_elems / inner
+};
+
+int make_geom(int32_t ndim, const int64_t *shape, const int64_t *tile, BucketGeom *g) {
+  EJ_CHECK_ARG(ndim >= 1 && ndim <= EJ_MAX_DIMS, "ndim=%d outside [1, %d]", ndim, EJ_MAX_DIMS);
+  EJ_CHECK_ARG(shape && tile, "null shape");
+  g->nd = ndim;
+  g->tile_elems = 1;
+  g->n_tiles = 1;
+  for (int d = 0; d < ndim; ++d) {
+    EJ_CHECK_ARG(tile[d] >= 1 && shape[d] >= 0, "bad extent in dim %d", d);
+    EJ_CHECK_ARG(shape[d] % tile[d] == 0, "tile_shape[%d]=%lld does not evenly divide shape[%d]=%lld",
+                 d, (long long)tile[d], d, (long long)shape[d]);
+    g->shape[d] = shape[d];
+    g->tile[d] = tile[d];
+    g->grid[d] = shape[d] / tile[d];
+    g->tile_elems *= tile[d];
+    g->n_tiles *= g->grid[d];
+  }
+  int64_t s = 1;
+  for (int d = ndim - 1; d >= 0; --d) {
+    g->dstride[d] = s;
+    s *= shape[d];
+  }
+  g->inner = tile[ndim - 1];
+  g->rows = g->tile_elems / g->inner;
+  return EJ_OK;
+}
+
+// Dense offset of the first element of tile t (row-major tile id).
+__device__ inline int64_t tile_origin(const BucketGeom &g, int64_t t) {
+  int64_t off = 0;
+  for (int d = g.nd - 1; d >= 0; --d) {
+    int64_t c = t % g.grid[d];
+    t /= g.grid[d];
+    off += c * g.tile[d] * g.dstride[d];
+  }
+  return off;
+}
+
+// Dense offset (relative to the tile origin) of row r of a tile, where a row
+// is a run of `inner` contiguous elements.
+__device__ inline int64_t row_offset(const BucketGeom &g, int64_t r) {
+  int64_t off = 0;
+  for (int d = g.nd - 2; d >= 0; --d) {
+    int64_t c = r % g.tile[d];
+    r /= g.tile[d];
+    off += c * g.dstride[d];
+  }
+  return off;
+}
+
+__device__ inline bool nonzero(double x) { return x != 0.0; }  // NaN != 0 holds
+__device__ inline bool nonzero(float x) { return x != 0.0f; }
+__device__ inline bool nonzero(uint16_t x) { return (x & 0x7fffu) != 0; }  // bf16: +-0 are zero
+// Tile element as stored: zeros become +0.0 (the reference scatters the
+// nonzero values into np.zeros tiles); float64 input is rounded to fp32.
+__device__ inline float stored(double x) {
+  float f = static_cast<float>(x);
+  return f == 0.0f ? 0.0f : f;
+}
+__device__ inline float stored(float x) { return x == 0.0f ? 0.0f : x; }
+__device__ inline uint16_t stored(uint16_t x) { return (x & 0x7fffu) ? x : 0; }
+
+// One workgroup per tile: rows are spread over the threads, the innermost
+// run is read contiguously.
+template <typename T>
+__global__ __launch_bounds__(256) void tile_flags_kernel(const T *__restrict__ dense,
+                                                         BucketGeom g, int64_t *flags) {
+  const int64_t t = blockIdx.x;
+  const T *base = dense + tile_origin(g, t);
+  int any = 0;
+  const int64_t total = g.tile_elems;
+  for (int64_t e = threadIdx.x; e < total && !any; e += 256) {
+    const int64_t r = e / g.inner, c = e % g.inner;
+    if (nonzero(base[row_offset(g, r) + c])) any = 1;
+  }
+  any = __syncthreads_or(any);
+  if (threadIdx.x == 0) flags[t] = any ? 1 : 0;
+}
+
+__global__ void slot_map_kernel(const int64_t *flags, const int64_t *excl, int64_t n,
+                                int64_t *tile_of_slot) {
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < n && flags[t]) tile_of_slot[excl[t]] = t;
+}
+
+template <typename T, typename U>
+__global__ __launch_bounds__(256) void tile_copy_kernel(const T *__restrict__ dense, BucketGeom g,
+                                                        const int64_t *tile_of_slot,
+                                                        int32_t *coords, U *__restrict__ values) {
+  const int64_t slot = blockIdx.x;
+  int64_t t = tile_of_slot[slot];
+  if (threadIdx.x == 0) {
+    int64_t tt = t;
+    for (int d = g.nd - 1; d >= 0; --d) {
+      coords[slot * g.nd + d] = static_cast<int32_t>(tt % g.grid[d]);
+      tt /= g.grid[d];
+    }
+  }
+  const T *base = dense + tile_origin(g, t);
+  U *dst = values + slot * g.tile_elems;
+  for (int64_t e = threadIdx.x; e < g.tile_elems; e += 256) {
+    const int64_t r = e / g.inner, c = e % g.inner;
+    dst[e] = stored(base[row_offset(g, r) + c]);
+  }
+}
+
+template <typename T>
+__global__ void fill_zero_kernel(T *p, int64_t n) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (; i < n; i += stride) p[i] = T(0);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void scatter_tiles_kernel(const int32_t *coords,
+                                                            const T *__restrict__ values,
+                                                            BucketGeom g, T *__restrict__ dense) {
+  const int64_t slot = blockIdx.x;
+  int64_t origin = 0;
+  for (int d = 0; d < g.nd; ++d) {
+    const int64_t c = coords[slot * g.nd + d];
+    if (c < 0 || c >= g.grid[d]) return;  // outside the grid: skipped
+    origin += c * g.tile[d] * g.dstride[d];
+  }
+  const T *src = values + slot * g.tile_elems;
+  for (int64_t e = threadIdx.x; e < g.tile_elems; e += 256) {
+    const int64_t r = e / g.inner, c = e % g.inner;
+    dense[origin + row_offset(g, r) + c] = src[e];
+  }
+}
+
+struct BucketWs {
+  int64_t *scalars, *flags, *excl, *tile_of_slot;
+  void *scan_ws;
+  size_t bytes;
+};
+
+BucketWs carve_bucket(void *base, int64_t n_tiles) {
+  Carver c(base);
+  BucketWs w;
+  w.scalars = c.take<int64_t>(4);
+  w.flags = c.take<int64_t>(n_tiles);
+  w.excl = c.take<int64_t>(n_tiles);
+  w.tile_of_slot = c.take<int64_t>(n_tiles);
+  w.scan_ws = c.take<char>(static_cast<int64_t>(scan_workspace_bytes(n_tiles)));
+  w.bytes = c.off;
+  return w;
+}
+
+}  // namespace
+}  // namespace ej
+
+using namespace ej;
+
+extern "C" int ej_bucket_workspace_size(int32_t ndim, const int64_t *shape,
+                                        const int64_t *tile_shape, size_t *bytes) {
+  clear_error();
+  EJ_CHECK_ARG(bytes, "bytes is null");
+  BucketGeom g;
+  EJ_TRY(make_geom(ndim, shape, tile_shape, &g));
+  *bytes = carve_bucket(nullptr, g.n_tiles).bytes;
+  return EJ_OK;
+}
+
+extern "C" int ej_bucket_dense_count(const void *dense, int32_t dtype, int32_t ndim,
+                                     const int64_t *shape, const int64_t *tile_shape,
+                                     void *workspace, size_t workspace_bytes, int64_t *n_tiles,
+                                     ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(n_tiles, "n_tiles is null");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  BucketGeom g;
+  EJ_TRY(make_geom(ndim, shape, tile_shape, &g));
+  if (g.n_tiles == 0 || g.tile_elems == 0) {
+    *n_tiles = 0;
+    return EJ_OK;
+  }
+  EJ_CHECK_ARG(g.n_tiles < (int64_t(1) << 32), "tile grid too large for one launch");
+  EJ_CHECK_ARG(dense, "dense is null");
+  BucketWs w = carve_bucket(workspace, g.n_tiles);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL(tile_flags_kernel<double>, dim3(static_cast<unsigned>(g.n_tiles)),
+                       dim3(256), 0, stream, static_cast<const double *>(dense), g, w.flags);
+  else if (dtype == EJ_F32)
+    hipLaunchKernelGGL(tile_flags_kernel<float>, dim3(static_cast<unsigned>(g.n_tiles)), dim3(256),
+                       0, stream, static_cast<const float *>(dense), g, w.flags);
+  else
+    hipLaunchKernelGGL(tile_flags_kernel<uint16_t>, dim3(static_cast<unsigned>(g.n_tiles)),
+                       dim3(256), 0, stream, static_cast<const uint16_t *>(dense), g, w.flags);
+  EJ_LAUNCH_CHECK();
+  EJ_TRY(scan_exclusive_i64(w.flags, w.excl, g.n_tiles, w.scalars, w.scan_ws, stream));
+  hipLaunchKernelGGL(slot_map_kernel, dim3(grid_for(g.n_tiles)), dim3(kBlock), 0, stream, w.flags,
+                     w.excl, g.n_tiles, w.tile_of_slot);
+  EJ_LAUNCH_CHECK();
+  int64_t host = 0;
+  EJ_HIP(hipMemcpyAsync(&host, w.scalars, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  EJ_HIP(hipStreamSynchronize(stream));
+  *n_tiles = host;
+  return EJ_OK;
+}
+
+extern "C" int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t ndim,
+                                    const int64_t *shape, const int64_t *tile_shape,
+                                    const void *workspace, size_t workspace_bytes,
+                                    int64_t n_tiles, int32_t *coords, void *values,
+                                    int64_t capacity, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  BucketGeom g;
+  EJ_TRY(make_geom(ndim, shape, tile_shape, &g));
+  EJ_CHECK_ARG(n_tiles >= 0 && n_tiles <= g.n_tiles, "n_tiles out of range");
+  if (capacity < n_tiles) {
+    set_error("tile capacity %lld < %lld tiles", (long long)capacity, (long long)n_tiles);
+    return EJ_E_CAPACITY;
+  }
+  if (n_tiles == 0) return EJ_OK;
+  EJ_CHECK_ARG(dense && coords && values, "null pointer argument");
+  BucketWs w = carve_bucket(const_cast<void *>(workspace), g.n_tiles);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL((tile_copy_kernel<double, float>), dim3(static_cast<unsigned>(n_tiles)),
+                       dim3(256), 0, stream, static_cast<const double *>(dense), g,
+                       w.tile_of_slot, coords, static_cast<float *>(values));
+  else if (dtype == EJ_F32)
+    hipLaunchKernelGGL((tile_copy_kernel<float, float>), dim3(static_cast<unsigned>(n_tiles)),
+                       dim3(256), 0, stream, static_cast<const float *>(dense), g,
+                       w.tile_of_slot, coords, static_cast<float *>(values));
+  else
+    hipLaunchKernelGGL((tile_copy_kernel<uint16_t, uint16_t>), dim3(static_cast<unsigned>(n_tiles)),
+                       dim3(256), 0, stream, static_cast<const uint16_t *>(dense), g,
+                       w.tile_of_slot, coords, static_cast<uint16_t *>(values));
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+extern "C" int ej_relation_to_dense(const int32_t *coords, const void *values, int64_t n_tiles,
+                                    int32_t dtype, int32_t ndim, const int64_t *shape,
+                                    const int64_t *tile_shape, void *dense,
+                                    ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  BucketGeom g;
+  EJ_TRY(make_geom(ndim, shape, tile_shape, &g));
+  EJ_CHECK_ARG(n_tiles >= 0 && n_tiles < (int64_t(1) << 32), "n_tiles out of range");
+  int64_t total = 1;
+  for (int d = 0; d < ndim; ++d) total *= shape[d];
+  if (total == 0) return EJ_OK;
+  EJ_CHECK_ARG(dense, "dense is null");
+  const unsigned zb = static_cast<unsigned>(ceil_div(total, 256) < 65536 ? ceil_div(total, 256) : 65536);
+  if (dtype == EJ_F32)
+    hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(zb), dim3(256), 0, stream,
+                       static_cast<float *>(dense), total);
+  else
+    hipLaunchKernelGGL(fill_zero_kernel<uint16_t>, dim3(zb), dim3(256), 0, stream,
+                       static_cast<uint16_t *>(dense), total);
+  EJ_LAUNCH_CHECK();
+  if (n_tiles == 0) return EJ_OK;
+  EJ_CHECK_ARG(coords && values, "null pointer argument");
+  if (dtype == EJ_F32)
+    hipLaunchKernelGGL(scatter_tiles_kernel<float>, dim3(static_cast<unsigned>(n_tiles)), dim3(256),
+                       0, stream, coords, static_cast<const float *>(values), g,
+                       static_cast<float *>(dense));
+  else
+    hipLaunchKernelGGL(scatter_tiles_kernel<uint16_t>, dim3(static_cast<unsigned>(n_tiles)),
+                       dim3(256), 0, stream, coords, static_cast<const uint16_t *>(values), g,
+                       static_cast<uint16_t *>(dense));
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}

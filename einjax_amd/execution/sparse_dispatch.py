@@ -1,0 +1,381 @@
+"""The tensor-relational sparse einsum on the GPU (reference:
+execution/sparse_dispatch.py).
+
+Phases, each a HIP kernel family in libejhip.so:
+  1. coordinate join     -> matched (lhs_idx, rhs_idx), reference pair order
+  2. segment plan        -> pairs grouped by output coordinate (sorted)
+  3. tile einsum         -> fused with the gather and the segment sum
+                            (default), or per pair + a separate segment sum
+                            (``fused=False``, the reference's phase split)
+
+Function names, arguments, results and errors follow the reference.
+Arguments may be host NumPy arrays (results come back as NumPy, as in the
+reference) or GPU torch tensors (results stay on the GPU).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .. import _device, _lib
+from ..tensor.sparse import SparseTensorRelation, _is_torch
+
+__all__ = [
+    "coordinate_join", "kernel_einsum", "segment_sum", "execute_sparse",
+    "execute_sharded_sparse", "_add_batch_dim", "_infer_output_tile_shape",
+    "_compute_output_coords", "_partition_matched_pairs",
+]
+
+
+# ---------------------------------------------------------------------------
+# Residency helpers.
+
+def _on_host(*xs) -> bool:
+    """True when any array argument is host-resident (NumPy / CPU tensor)."""
+    for x in xs:
+        if isinstance(x, SparseTensorRelation):
+            if not x.is_device:
+                return True
+        elif x is not None and not (_is_torch(x) and x.is_cuda):
+            return True
+    return False
+
+
+def _dev(x, dtype=None):
+    import torch
+
+    dev = _device.require_gpu()
+    if _is_torch(x):
+        t = x
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(x))
+    return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
+
+
+def _dev_values(v):
+    """Tile values on the GPU as float32, or bfloat16 when already bfloat16."""
+    import torch
+
+    t = _dev(v)
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        t = t.to(torch.float32)
+    return t
+
+
+def _dev_coords(c, ndim):
+    import torch
+
+    t = _dev(c, torch.int32)
+    if t.numel() == 0:
+        return t.reshape(0, ndim)
+    return t.reshape(t.shape[0], -1)
+
+
+def _host(t):
+    import torch
+
+    if not _is_torch(t):
+        return t
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    return t.cpu().numpy()
+
+
+def _same_dtype(a, b):
+    import torch
+
+    if a.dtype != b.dtype:
+        return a.to(torch.float32), b.to(torch.float32)
+    return a, b
+
+
+def _grid(rel: SparseTensorRelation, d: int) -> int:
+    t = rel.tile_shape[d] if d < len(rel.tile_shape) else 1
+    s = rel.shape[d] if d < len(rel.shape) else 1
+    return max(1, -(-s // max(t, 1)))
+
+
+def _host_col_max(coords, d) -> int:
+    if _is_torch(coords) or coords.shape[0] == 0:
+        return 0
+    return int(np.max(coords[:, d])) + 1
+
+
+def _retry_radices(fn, make_radices, cols):
+    """Runs fn(radices) with radices from grid metadata; if a coordinate
+    falls outside them, sizes the radices from the data and runs again."""
+    try:
+        return fn(make_radices(None))
+    except ValueError as e:
+        if "outside [0, radix)" not in str(e):
+            raise
+    maxima = []
+    for coords, d in cols:
+        lo, hi = _device.coords_range(coords)
+        if coords.shape[0] and lo[d] < 0:
+            raise ValueError("tile coordinates must be non-negative")
+        maxima.append(hi[d] + 1 if coords.shape[0] else 1)
+    return fn(make_radices(maxima))
+
+
+# ---------------------------------------------------------------------------
+# Phase 1: join.
+
+def _join_dev(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys, lc, rc,
+              order=_lib.EJ_ORDER_PROBE):
+    keys = [tuple(k) for k in join_keys]
+
+    def radices(maxima):
+        out = []
+        for i, (a, b) in enumerate(keys):
+            r = max(_grid(lhs, a), _grid(rhs, b), _host_col_max(lhs.coords, a),
+                    _host_col_max(rhs.coords, b))
+            if maxima is not None:
+                r = max(r, maxima[2 * i], maxima[2 * i + 1])
+            out.append(r)
+        return out
+
+    cols = [c for a, b in keys for c in ((lc, a), (rc, b))]
+    return _retry_radices(lambda r: _device.join(lc, rc, keys, r, order), radices, cols)
+
+
+def coordinate_join(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys):
+    """Matched tile pairs on join_keys = [(lhs_dim, rhs_dim), ...]
+    (reference: sparse_dispatch.py:29-82).
+
+    Pair order is the reference hash join's: rhs index ascending, then lhs
+    index ascending; no keys gives the lhs-major cross product.  Returns int64
+    (lhs_idx, rhs_idx)."""
+    host = _on_host(lhs, rhs)
+    lc = _dev_coords(lhs.coords, lhs.ndim)
+    rc = _dev_coords(rhs.coords, rhs.ndim)
+    li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
+    return (_host(li), _host(ri)) if host else (li, ri)
+
+
+# ---------------------------------------------------------------------------
+# Phase 2: tile einsum.
+
+def _add_batch_dim(kernel_string: str, batch_label: str = "z") -> str:
+    """"ij,jk->ik" -> "zij,zjk->zik" (reference: sparse_dispatch.py:481-503)."""
+    if "->" not in kernel_string:
+        raise ValueError(f"kernel_string must contain '->': {kernel_string}")
+    inputs_str, output_str = kernel_string.split("->")
+    return ",".join(batch_label + t for t in inputs_str.split(",")) + "->" + batch_label + output_str
+
+
+def _infer_output_tile_shape(kernel_string: str, lhs_tile_shape, rhs_tile_shape) -> tuple:
+    """Output tile shape from label sizes, rhs sizes overriding lhs
+    (reference: sparse_dispatch.py:506-545); KeyError for a label absent
+    from both inputs."""
+    if "->" not in kernel_string:
+        raise ValueError(f"kernel_string must contain '->': {kernel_string}")
+    inputs_str, output_str = kernel_string.split("->")
+    terms = inputs_str.split(",")
+    sizes = {}
+    if len(terms) >= 1:
+        for d, lab in enumerate(terms[0]):
+            if d < len(lhs_tile_shape):
+                sizes[lab] = lhs_tile_shape[d]
+    if len(terms) >= 2:
+        for d, lab in enumerate(terms[1]):
+            if d < len(rhs_tile_shape):
+                sizes[lab] = rhs_tile_shape[d]
+    return tuple(sizes[lab] for lab in output_str)
+
+
+def kernel_einsum(lhs_values, rhs_values, lhs_indices, rhs_indices, kernel_string: str):
+    """einsum(kernel_string) of every matched tile pair, float32
+    [P, *out_tile] (reference: sparse_dispatch.py:85-126).  No pairs gives
+    zeros of the lhs values' dtype."""
+    host = _on_host(lhs_values, rhs_values, lhs_indices, rhs_indices)
+    n = int(lhs_indices.shape[0]) if hasattr(lhs_indices, "shape") else len(lhs_indices)
+    lt, rt = tuple(lhs_values.shape[1:]), tuple(rhs_values.shape[1:])
+    if n == 0:
+        out_tile = _infer_output_tile_shape(kernel_string, lt, rt)
+        if host:
+            return np.zeros((0, *out_tile), dtype=_host(lhs_values[:0]).dtype)
+        import torch
+
+        return torch.zeros((0, *out_tile), dtype=lhs_values.dtype, device=lhs_values.device)
+    _add_batch_dim(kernel_string)  # same ValueError as the reference for a missing "->"
+    desc = _device.describe(kernel_string, lt, rt)
+    a, b = _same_dtype(_dev_values(lhs_values), _dev_values(rhs_values))
+    li = _dev(np.asarray(lhs_indices) if not _is_torch(lhs_indices) else lhs_indices)
+    ri = _dev(np.asarray(rhs_indices) if not _is_torch(rhs_indices) else rhs_indices)
+    import torch
+
+    out = _device.pair_einsum(desc, a, b, li.to(torch.int64), ri.to(torch.int64))
+    return _host(out) if host else out
+
+
+# ---------------------------------------------------------------------------
+# Phase 3: aggregation.
+
+def _compute_output_coords(lhs, rhs, lhs_indices, rhs_indices, join_keys, agg_keys,
+                           output_shape, output_tile_shape):
+    """Per-pair output tile coordinate, int32 [P, len(output_tile_shape)]
+    (reference: sparse_dispatch.py:174-223)."""
+    import torch
+
+    host = _on_host(lhs, rhs, lhs_indices, rhs_indices)
+    n_out = len(output_tile_shape)
+    P = int(lhs_indices.shape[0]) if hasattr(lhs_indices, "shape") else len(lhs_indices)
+    if P == 0:
+        z = np.zeros((0, n_out), np.int32)
+        return z if host else torch.zeros((0, n_out), dtype=torch.int32,
+                                          device=_device.require_gpu())
+    lc = _dev_coords(lhs.coords, lhs.ndim)
+    rc = _dev_coords(rhs.coords, rhs.ndim)
+    li = _dev(lhs_indices, torch.int64)
+    ri = _dev(rhs_indices, torch.int64)
+    oc = _device.output_coords(lc, rc, li, ri, [tuple(k) for k in agg_keys][:n_out])
+    if oc.shape[1] < n_out:
+        oc = torch.cat([oc, oc.new_zeros((P, n_out - oc.shape[1]))], dim=1)
+    return _host(oc) if host else oc
+
+
+def _plan_from_coords(oc):
+    """Segment plan of bare output coordinates (int32 [P, nd] on the GPU)."""
+    import torch
+
+    P, nd = oc.shape
+    idx = torch.arange(P, dtype=torch.int64, device=oc.device)
+    agg = [(0, d) for d in range(nd)]
+    if nd == 0:
+        return _device.segment_plan(oc, oc, idx, idx, agg, [])
+    # No grid metadata: size the radices from the data directly.
+    lo, hi = _device.coords_range(oc)
+    if min(lo) < 0:
+        raise ValueError("output coordinates must be non-negative")
+    return _device.segment_plan(oc, oc, idx, idx, agg, [h + 1 for h in hi])
+
+
+def segment_sum(values, output_coords):
+    """Sums the pair tiles of equal output coordinate (reference:
+    sparse_dispatch.py:129-171).  Returns (unique_coords int32 [U, nd] in
+    ascending lexicographic order, aggregated float32 [U, *tile]); tiles are
+    added in pair order, as the reference does."""
+    import torch
+
+    host = _on_host(values, output_coords)
+    if (values.shape[0] if hasattr(values, "shape") else len(values)) == 0:
+        nd = output_coords.shape[1] if output_coords.ndim > 1 else 0
+        tile = tuple(values.shape[1:]) if values.ndim > 1 else ()
+        if host:
+            return np.zeros((0, nd), np.int32), np.zeros((0, *tile), dtype=_host(values[:0]).dtype)
+        return (torch.zeros((0, nd), dtype=torch.int32, device=values.device),
+                torch.zeros((0, *tile), dtype=values.dtype, device=values.device))
+    oc = _dev_coords(output_coords, output_coords.shape[1] if output_coords.ndim > 1 else 0)
+    vals = _dev(values, torch.float32)
+    coords, offsets, perm, _ = _plan_from_coords(oc)
+    agg = _device.segment_sum(vals, perm, offsets)
+    return (_host(coords), _host(agg)) if host else (coords, agg)
+
+
+# ---------------------------------------------------------------------------
+# End to end.
+
+def _empty_result(lhs, n_out, out_tile, output_shape, host):
+    import torch
+
+    if host:
+        dt = _host(lhs.values[:0]).dtype
+        return SparseTensorRelation(np.zeros((0, n_out), np.int32),
+                                    np.zeros((0, *out_tile), dtype=dt), output_shape, out_tile)
+    dev = _device.require_gpu()
+    return SparseTensorRelation(torch.zeros((0, n_out), dtype=torch.int32, device=dev),
+                                torch.zeros((0, *out_tile), dtype=lhs.values.dtype, device=dev),
+                                output_shape, out_tile)
+
+
+def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys,
+                   kernel_string: str, agg_keys, output_shape=None, output_tile_shape=None, *,
+                   fused: bool = True) -> SparseTensorRelation:
+    """Sparse tensor-relational einsum (reference: sparse_dispatch.py:226-297).
+
+    join_keys: [(lhs_dim, rhs_dim)] contracted tile dims; kernel_string: the
+    per-tile einsum; agg_keys: [(0 | 1, dim)] sources of the output tile
+    coordinates.  Output tile shape and shape are inferred as the reference
+    does when omitted.  ``fused=True`` (default) runs the gather, the tile
+    einsum and the segment sum as one kernel writing every output tile once;
+    ``fused=False`` runs the reference's phase split (per-pair results, then
+    the segment sum in pair order).  Returns coords int32 [U, nd] sorted and
+    float32 values [U, *output_tile_shape]."""
+    if output_tile_shape is None:
+        output_tile_shape = _infer_output_tile_shape(kernel_string, lhs.tile_shape,
+                                                     rhs.tile_shape)
+    if output_shape is None:
+        output_shape = tuple(lhs.shape[d] if s == 0 else rhs.shape[d] for s, d in agg_keys)
+    output_tile_shape = tuple(output_tile_shape)
+    output_shape = tuple(output_shape)
+    _add_batch_dim(kernel_string)
+    host = _on_host(lhs, rhs)
+    agg = [tuple(k) for k in agg_keys]
+
+    lc = _dev_coords(lhs.coords, lhs.ndim)
+    rc = _dev_coords(rhs.coords, rhs.ndim)
+    li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
+    if li.numel() == 0:
+        return _empty_result(lhs, len(output_tile_shape), output_tile_shape, output_shape, host)
+
+    def radices(maxima):
+        out = []
+        for d, (s, dim) in enumerate(agg):
+            rel = lhs if s == 0 else rhs
+            r = max(_grid(rel, dim), _host_col_max(rel.coords, dim))
+            if maxima is not None:
+                r = max(r, maxima[d])
+            out.append(r)
+        return out
+
+    cols = [((lc if s == 0 else rc), dim) for s, dim in agg]
+    coords, offsets, perm, _ = _retry_radices(
+        lambda r: _device.segment_plan(lc, rc, li, ri, agg, r), radices, cols)
+    desc = _device.describe(kernel_string, lhs.tile_shape, rhs.tile_shape)
+    a, b = _same_dtype(_dev_values(lhs.values), _dev_values(rhs.values))
+    if fused:
+        vals = _device.segment_einsum(desc, a, b, li, ri, perm, offsets)
+    else:
+        pair_vals = _device.pair_einsum(desc, a, b, li, ri)
+        vals = _device.segment_sum(pair_vals, perm, offsets)
+    n_out = len(output_tile_shape)
+    if coords.shape[1] != n_out:
+        import torch
+
+        coords = coords[:, :n_out] if coords.shape[1] > n_out else torch.cat(
+            [coords, coords.new_zeros((coords.shape[0], n_out - coords.shape[1]))], dim=1)
+    if tuple(vals.shape[1:]) != output_tile_shape and vals[0].numel() == int(
+            np.prod(output_tile_shape)):
+        vals = vals.reshape((vals.shape[0], *output_tile_shape))
+    out = SparseTensorRelation(coords, vals, output_shape, output_tile_shape)
+    return out.to_host() if host else out
+
+
+def _partition_matched_pairs(num_matches: int, num_devices: int) -> list:
+    """Contiguous, near-equal pair ranges per device, remainder to the first
+    devices (reference: sparse_dispatch.py:300-327)."""
+    if num_matches == 0:
+        return [(0, 0)] * num_devices
+    base, rem = divmod(num_matches, num_devices)
+    parts, off = [], 0
+    for d in range(num_devices):
+        size = base + (1 if d < rem else 0)
+        parts.append((off, off + size))
+        off += size
+    return parts
+
+
+def execute_sharded_sparse(lhs, rhs, join_keys, kernel_string, agg_keys, output_shape=None,
+                           output_tile_shape=None, mesh=None, num_devices=None):
+    """Single-GPU form of the reference's multi-device entry
+    (sparse_dispatch.py:330-478): without a mesh, or with one device, it is
+    execute_sparse, exactly as in the reference (:377-393).  More devices are
+    outside this library (one process drives one GPU)."""
+    if num_devices is None:
+        num_devices = 1 if mesh is None else len(getattr(mesh, "devices", [None]).flat)
+    if mesh is None or num_devices <= 1:
+        return execute_sparse(lhs, rhs, join_keys, kernel_string, agg_keys, output_shape,
+                              output_tile_shape)
+    raise NotImplementedError("multi-device sparse execution is not part of this library: "
+                              "run one process per GPU, each on its share of the segments")

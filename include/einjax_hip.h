@@ -1,0 +1,240 @@
+/*
+ * einjax_hip.h -- C ABI of the MI355X (gfx950) tensor-relational sparse-einsum path.
+ *
+ * The reference runs this path as host NumPy plus one jnp.einsum call
+ * (execution/sparse_dispatch.py:226-297).  This library replaces its phases
+ * with HIP kernels behind plain C entry points:
+ *
+ *   tiling        ej_bucket_dense_count / ej_bucket_dense_fill
+ *                 (replaces SparseTensor.to_relation, tensor/sparse.py:160-219)
+ *   join          ej_join_count / ej_join_fill
+ *                 (replaces coordinate_join, execution/sparse_dispatch.py:29-82;
+ *                  coordinate_join_hash / coordinate_join_sorted,
+ *                  kernels/pallas_gather.py:19-76 / :79-174)
+ *   output coords ej_output_coords
+ *                 (replaces _compute_output_coords, execution/sparse_dispatch.py:174-223)
+ *   segment plan  ej_segment_count / ej_segment_fill
+ *                 (the grouping half of segment_sum, execution/sparse_dispatch.py:155-162)
+ *   gather        ej_gather_tiles
+ *                 (replaces lhs_values[lhs_indices], execution/sparse_dispatch.py:118-119)
+ *   tile einsum   ej_einsum_describe / ej_pair_einsum / ej_segment_einsum
+ *                 (replaces jnp.einsum(_add_batch_dim(kernel_string)),
+ *                  execution/sparse_dispatch.py:121-126)
+ *   segment sum   ej_segment_sum
+ *                 (the accumulation half of segment_sum, execution/sparse_dispatch.py:164-171)
+ *
+ * Conventions
+ *   - Every pointer argument named *_coords, *_values, *_idx, *keys, perm,
+ *     seg_*, out*, dense and workspace is a DEVICE pointer.  Small descriptor
+ *     arrays (dims, radices, shapes, agg_*) and the scalar outputs n_pairs,
+ *     n_segments, n_tiles are HOST pointers.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
+ *     Functions whose name ends in _count synchronize `stream` because they
+ *     return a data-dependent size to the host; every other function is
+ *     asynchronous.
+ *   - A *_count call leaves its state in the caller's workspace; the matching
+ *     *_fill call must receive the same workspace, unmodified.
+ *   - Return value: EJ_OK (0) or a negative EJ_E_* status.  ej_last_error()
+ *     returns a thread-local message for the last failing call.
+ *   - No global mutable state: calls on different streams with different
+ *     workspaces may run concurrently.
+ *   - Coordinates are int32, row-major [n, ncols].  Pair indices are int64,
+ *     as the reference returns them.  Values are EJ_F32 or EJ_BF16; tile
+ *     einsum results are always fp32 (the reference computes the per-pair
+ *     einsum in float32, sparse_dispatch.py:125).
+ */
+#ifndef EINJAX_HIP_H
+#define EINJAX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EJ_ABI_VERSION 1
+
+#define EJ_OK 0
+#define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
+#define EJ_E_CAPACITY (-2)    /* output buffer smaller than the counted size */
+#define EJ_E_HIP (-3)         /* HIP runtime error */
+#define EJ_E_UNSUPPORTED (-4) /* valid request this build does not implement */
+#define EJ_E_RANGE (-5)       /* a coordinate lies outside its declared grid */
+
+#define EJ_F32 0
+#define EJ_BF16 1
+#define EJ_F64 2 /* dense input of the bucketing calls only; tiles come out fp32 */
+
+/* Pair orders of the join.  With n_keys == 0 both give the cross product in
+ * lhs-major order (sparse_dispatch.py:53-59, pallas_gather.py:50-54). */
+#define EJ_ORDER_PROBE 0  /* hash join order: rhs index ascending, then lhs
+                             index ascending (sparse_dispatch.py:65-80) */
+#define EJ_ORDER_SORTED 1 /* sort-merge order: key ascending, then lhs-major
+                             nested product of the stably sorted key groups
+                             (pallas_gather.py:130-172) */
+
+#define EJ_MAX_DIMS 8   /* tile / coordinate rank limit */
+#define EJ_MAX_KEYS 8   /* join keys and output dims */
+#define EJ_MAX_LABELS 8 /* distinct labels per group in a tile einsum */
+
+typedef void *ej_stream_t; /* hipStream_t */
+
+/* Canonical form of a binary tile einsum "lhs,rhs->out" (both operands, one
+ * output; the reference passes exactly two operands, sparse_dispatch.py:125).
+ * Produced by ej_einsum_describe; treat it as opaque input to the einsum
+ * entry points.  Strides are in elements of a row-major tile. */
+typedef struct ej_einsum_desc {
+  int32_t n_out;                    /* output labels (output tile rank) */
+  int32_t n_red;                    /* contracted labels */
+  int64_t out_ext[EJ_MAX_LABELS];   /* extent of each output label */
+  int64_t out_a[EJ_MAX_LABELS];     /* lhs stride of each output label (0 if absent) */
+  int64_t out_b[EJ_MAX_LABELS];     /* rhs stride of each output label (0 if absent) */
+  int64_t red_ext[EJ_MAX_LABELS];   /* extent of each contracted label */
+  int64_t red_a[EJ_MAX_LABELS];     /* lhs stride of each contracted label (0 if absent) */
+  int64_t red_b[EJ_MAX_LABELS];     /* rhs stride of each contracted label (0 if absent) */
+  int64_t a_elems, b_elems, c_elems; /* elements per lhs / rhs / output tile */
+  /* GEMM form (valid when is_gemm == 1): C[b][m][n] = sum_k A[b][m][k] B[b][k][n] */
+  int32_t is_gemm;
+  int32_t pad_;
+  int64_t batch, m, n, k;
+  int64_t a_sb, a_sm, a_sk;
+  int64_t b_sb, b_sk, b_sn;
+  int64_t c_sb, c_sm, c_sn;
+} ej_einsum_desc;
+
+/* ---- diagnostics ------------------------------------------------------- */
+int ej_version(void);
+const char *ej_last_error(void);
+
+/* ---- tile einsum description ------------------------------------------- */
+/* Parses `kernel_string` (e.g. "ij,jk->ik") against the two tile shapes.
+ * Label extents come from the tile shapes; a label whose extent differs
+ * between the operands, an output label absent from both inputs, a repeated
+ * output label, a missing "->" or a third operand give EJ_E_INVAL
+ * (reference: _add_batch_dim raises without "->", sparse_dispatch.py:494-495;
+ * _infer_output_tile_shape raises KeyError for an unknown output label, :544). */
+int ej_einsum_describe(const char *kernel_string, const int64_t *lhs_tile, int32_t lhs_ndim,
+                       const int64_t *rhs_tile, int32_t rhs_ndim, ej_einsum_desc *desc);
+
+/* ---- join (reference: coordinate_join, sparse_dispatch.py:29-82) -------- */
+/* radices[i] bounds key column i on both sides: 0 <= coord < radices[i].
+ * A coordinate outside that range gives EJ_E_RANGE. */
+int ej_join_workspace_size(int64_t n_lhs, int64_t n_rhs, int32_t order, size_t *bytes);
+int ej_join_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                  const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols, int32_t n_keys,
+                  const int32_t *lhs_dims, const int32_t *rhs_dims, const int64_t *radices,
+                  int32_t order, void *workspace, size_t workspace_bytes, int64_t *n_pairs,
+                  ej_stream_t stream);
+/* Writes the n_pairs matched pairs counted by ej_join_count.  capacity is
+ * the length of lhs_idx / rhs_idx; capacity < n_pairs gives EJ_E_CAPACITY. */
+int ej_join_fill(int64_t n_lhs, int64_t n_rhs, int32_t n_keys, int32_t order,
+                 const void *workspace, size_t workspace_bytes, int64_t n_pairs,
+                 int64_t *lhs_idx, int64_t *rhs_idx, int64_t capacity, ej_stream_t stream);
+
+/* ---- output coordinates (reference: _compute_output_coords, :174-223) --- */
+/* out[p][d] = (agg_src[d] == 0 ? lhs : rhs).coords[idx[p]][agg_dim[d]] */
+int ej_output_coords(const int32_t *lhs_coords, int32_t lhs_ncols, const int32_t *rhs_coords,
+                     int32_t rhs_ncols, const int64_t *lhs_idx, const int64_t *rhs_idx,
+                     int64_t n_pairs, int32_t n_out, const int32_t *agg_src,
+                     const int32_t *agg_dim, int32_t *out, ej_stream_t stream);
+
+/* ---- coordinate ranges -------------------------------------------------- */
+/* Per-column minimum and maximum of int32 coordinates [n, ncols]:
+ * lo_hi[2c] = min, lo_hi[2c+1] = max (HOST output; synchronizes `stream`).
+ * n == 0 gives min 0, max -1.  workspace: device, >= 8 * ncols bytes.
+ * Used to size key radices for bare coordinate arrays, which the reference
+ * accepts without grid metadata (segment_sum, sparse_dispatch.py:129-132;
+ * coordinate_join_hash / _sorted, pallas_gather.py:19-23, :79-83). */
+int ej_coords_range(const int32_t *coords, int64_t n, int32_t ncols, int32_t *lo_hi,
+                    void *workspace, size_t workspace_bytes, ej_stream_t stream);
+
+/* ---- segment plan (reference: segment_sum grouping, :155-162) ----------- */
+/* Groups the pairs by output coordinate.  Segment u is the u-th distinct
+ * output coordinate in ascending lexicographic order (the reference's
+ * sorted(coord_keys)); its pairs are perm[seg_offsets[u] .. seg_offsets[u+1])
+ * in ascending pair index (the reference's accumulation order).
+ * radices[d] bounds output dimension d.  Requires n_pairs < 2^31. */
+int ej_segment_workspace_size(int64_t n_pairs, size_t *bytes);
+int ej_segment_count(const int32_t *lhs_coords, int32_t lhs_ncols, const int32_t *rhs_coords,
+                     int32_t rhs_ncols, const int64_t *lhs_idx, const int64_t *rhs_idx,
+                     int64_t n_pairs, int32_t n_out, const int32_t *agg_src,
+                     const int32_t *agg_dim, const int64_t *radices, void *workspace,
+                     size_t workspace_bytes, int64_t *n_segments, ej_stream_t stream);
+/* out_coords int32 [n_segments, n_out]; seg_offsets int32 [n_segments + 1];
+ * perm int32 [n_pairs]; seg_ids int32 [n_pairs] (may be NULL): the segment of
+ * each pair in pair order.  capacity bounds n_segments. */
+int ej_segment_fill(int64_t n_pairs, int64_t n_segments, int32_t n_out, const int64_t *radices,
+                    const void *workspace, size_t workspace_bytes, int32_t *out_coords,
+                    int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids, int64_t capacity,
+                    ej_stream_t stream);
+
+/* ---- gather (reference: values[indices], sparse_dispatch.py:118-119) ---- */
+/* out[i] = values[idx[i]] for whole tiles of tile_bytes each.  Indices
+ * outside [0, n_tiles) produce a zero tile. */
+int ej_gather_tiles(const void *values, int64_t n_tiles, int64_t tile_bytes, const int64_t *idx,
+                    int64_t n, void *out, ej_stream_t stream);
+
+/* ---- tile einsum (reference: kernel_einsum, sparse_dispatch.py:85-126) -- */
+/* GEMM-shaped descriptors (is_gemm == 1) with 32-multiple M and N, a K that
+ * is a multiple of 32 (bf16) or 16 (fp32) and 16-byte aligned operand rows
+ * run on the MFMA kernel; every other descriptor, or one whose is_gemm the
+ * caller cleared, runs on the generic strided kernel.  A pair whose tile
+ * index lies outside [0, n_*_tiles) contributes nothing.
+ * Per-pair mode: out[p] = einsum(lhs_values[lhs_idx[p]], rhs_values[rhs_idx[p]])
+ * for p < n_pairs, fp32 [n_pairs, c_elems].  lhs_idx / rhs_idx may be NULL,
+ * meaning pair p reads tile p (a gathered panel). */
+int ej_pair_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
+                   const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
+                   const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs, float *out,
+                   ej_stream_t stream);
+/* Fused mode (gather + einsum + segment sum): out[u] = sum over the pairs
+ * of segment u, in plan order, of the per-pair einsum; fp32
+ * [n_segments, c_elems], each output tile written once, no atomics. */
+int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
+                      const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
+                      const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
+                      const int32_t *seg_offsets, int64_t n_segments, float *out,
+                      ej_stream_t stream);
+
+/* ---- segment sum (reference: segment_sum accumulation, :164-171) -------- */
+/* out[u] = sum_{q in [seg_offsets[u], seg_offsets[u+1])} pair_values[perm[q]],
+ * added sequentially in q order in fp32 (the reference's order and dtype). */
+int ej_segment_sum(const float *pair_values, int64_t tile_elems, const int32_t *perm,
+                   const int32_t *seg_offsets, int64_t n_segments, float *out,
+                   ej_stream_t stream);
+
+/* ---- tiling (reference: SparseTensor.to_relation, tensor/sparse.py:160-219) */
+/* Dense row-major input of rank ndim.  A tile is kept iff it holds an element
+ * that compares != 0 (NaN counts as nonzero, -0.0 does not, as the
+ * reference's `values != 0` filter); kept tiles appear in ascending
+ * lexicographic coordinate order; inside a kept tile every element that
+ * compares == 0 is written as +0.0.  tile_shape must divide shape
+ * (EJ_E_INVAL otherwise, as the reference raises ValueError).
+ * dtype EJ_F32 or EJ_BF16 keeps the dtype in the tiles.  dtype EJ_F64 decides
+ * occupancy on the float64 values (the reference's dtype, sparse.py:260) and
+ * writes fp32 tiles (the precision its einsum computes in). */
+int ej_bucket_workspace_size(int32_t ndim, const int64_t *shape, const int64_t *tile_shape,
+                             size_t *bytes);
+int ej_bucket_dense_count(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
+                          const int64_t *tile_shape, void *workspace, size_t workspace_bytes,
+                          int64_t *n_tiles, ej_stream_t stream);
+/* coords int32 [n_tiles, ndim]; values [n_tiles, *tile_shape] of `dtype`
+ * (fp32 for EJ_F64 input). */
+int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
+                         const int64_t *tile_shape, const void *workspace,
+                         size_t workspace_bytes, int64_t n_tiles, int32_t *coords, void *values,
+                         int64_t capacity, ej_stream_t stream);
+
+/* ---- relation to dense (reference: SparseTensorRelation.to_dense, :75-90) */
+/* Writes every tile of the relation into `dense` (row-major `shape`, fp32 or
+ * bf16 like `values`).  Elements not covered by a tile are set to zero. */
+int ej_relation_to_dense(const int32_t *coords, const void *values, int64_t n_tiles,
+                         int32_t dtype, int32_t ndim, const int64_t *shape,
+                         const int64_t *tile_shape, void *dense, ej_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EINJAX_HIP_H */

@@ -1,0 +1,158 @@
+"""The C-ABI library: loads, exports every declared symbol, and its
+host-only logic (kernel-string description, workspace sizing, argument
+validation) behaves as documented.  No GPU work is launched here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from einjax_amd import _lib
+from einjax_amd._lib import EinsumDesc, i32_array, i64_array
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "einjax_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(ej_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 18
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version():
+    assert _lib.load().ej_version() == 1
+
+
+def describe(spec, lt, rt):
+    d = EinsumDesc()
+    st = _lib.load().ej_einsum_describe(spec.encode(), i64_array(lt), len(lt), i64_array(rt),
+                                        len(rt), ctypes.byref(d))
+    return st, d
+
+
+@pytest.mark.parametrize("spec,lt,rt,gemm", [
+    ("ij,jk->ik", (128, 128), (128, 128), (1, 128, 128, 128, 0, 128, 1, 0, 128, 1, 0, 128, 1)),
+    ("bij,bjk->bik", (1, 64, 64), (1, 64, 64), (1, 64, 64, 64, 0, 64, 1, 0, 64, 1, 0, 64, 1)),
+    ("ijk,kl->ijl", (32, 32, 32), (32, 32), (1, 1024, 32, 32, 0, 32, 1, 0, 32, 1, 0, 32, 1)),
+    ("ij,kj->ik", (32, 16), (64, 16), (1, 32, 64, 16, 0, 16, 1, 0, 1, 16, 0, 64, 1)),
+    ("ji,jk->ik", (16, 32), (16, 64), (1, 32, 64, 16, 0, 1, 32, 0, 64, 1, 0, 64, 1)),
+    ("bij,bjk->bik", (4, 32, 16), (4, 16, 8), (4, 32, 8, 16, 512, 16, 1, 128, 8, 1, 256, 8, 1)),
+])
+def test_describe_gemm_forms(spec, lt, rt, gemm):
+    st, d = describe(spec, lt, rt)
+    assert st == 0
+    assert d.is_gemm == 1
+    got = (d.batch, d.m, d.n, d.k, d.a_sb, d.a_sm, d.a_sk, d.b_sb, d.b_sk, d.b_sn, d.c_sb,
+           d.c_sm, d.c_sn)
+    assert got == gemm
+
+
+@pytest.mark.parametrize("spec,lt,rt,n_out,n_red,c_elems,gemm", [
+    ("i,j->ij", (3,), (4,), 2, 0, 12, 1),
+    ("i,i->", (5,), (5,), 0, 1, 1, 1),
+    ("ij,ij->ij", (3, 4), (3, 4), 2, 0, 12, 1),
+    ("ii,ij->j", (3, 3), (3, 4), 1, 1, 4, 0),
+    ("ij,kl->ij", (1, 1), (1, 1), 2, 2, 1, 0),
+    ("ik,kj->ji", (4, 5), (5, 6), 2, 1, 24, 1),   # GEMM with a transposed output
+    ("ijk,jl->il", (2, 3, 4), (3, 5), 2, 2, 10, 0),  # k contracted on one side only
+])
+def test_describe_general_forms(spec, lt, rt, n_out, n_red, c_elems, gemm):
+    st, d = describe(spec, lt, rt)
+    assert st == 0
+    assert (d.n_out, d.n_red, d.c_elems, d.is_gemm) == (n_out, n_red, c_elems, gemm)
+    if spec == "ik,kj->ji":
+        assert (d.m, d.n, d.k, d.c_sm, d.c_sn) == (4, 6, 5, 1, 4)
+
+
+@pytest.mark.parametrize("spec,lt,rt,status", [
+    ("ij,jk", (2, 2), (2, 2), _lib.EJ_E_INVAL),          # no "->"
+    ("ij,jk,kl->il", (2, 2), (2, 2), _lib.EJ_E_INVAL),   # three operands
+    ("ij,jk->iq", (2, 2), (2, 2), _lib.EJ_E_INVAL),      # unknown output label
+    ("ij,jk->ik", (2, 3), (4, 2), _lib.EJ_E_INVAL),      # extent mismatch
+    ("ij,jk->ii", (2, 2), (2, 2), _lib.EJ_E_INVAL),      # repeated output label
+    ("ij,jk->ik", (2, 2, 2), (2, 2), _lib.EJ_E_INVAL),   # rank mismatch
+    ("...j,jk->...k", (2, 2), (2, 2), _lib.EJ_E_UNSUPPORTED),
+])
+def test_describe_errors(spec, lt, rt, status):
+    st, _ = describe(spec, lt, rt)
+    assert st == status
+    assert _lib.load().ej_last_error()
+
+
+def test_workspace_sizes_grow_with_input():
+    lib = _lib.load()
+    a, b = ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.ej_join_workspace_size(10, 10, 0, ctypes.byref(a)) == 0
+    assert lib.ej_join_workspace_size(100000, 100000, 0, ctypes.byref(b)) == 0
+    assert b.value > a.value > 0
+    assert lib.ej_join_workspace_size(1, 1, 7, ctypes.byref(a)) == _lib.EJ_E_INVAL
+    assert lib.ej_segment_workspace_size(1000, ctypes.byref(a)) == 0 and a.value > 8000
+    assert lib.ej_bucket_workspace_size(2, i64_array([8, 8]), i64_array([2, 4]),
+                                        ctypes.byref(a)) == 0
+    assert lib.ej_bucket_workspace_size(2, i64_array([8, 8]), i64_array([3, 4]),
+                                        ctypes.byref(a)) == _lib.EJ_E_INVAL
+
+
+def test_join_count_host_paths():
+    """Cross products and empty sides are sized on the host (no device work)."""
+    lib = _lib.load()
+    n = ctypes.c_int64(-1)
+    st = lib.ej_join_count(None, 7, 2, None, 5, 2, 0, None, None, None, 0, None, 0,
+                           ctypes.byref(n), None)
+    assert st == 0 and n.value == 35
+    st = lib.ej_join_count(None, 0, 2, None, 5, 2, 1, i32_array([1]), i32_array([0]),
+                           i64_array([4]), 0, None, 0, ctypes.byref(n), None)
+    assert st == 0 and n.value == 0
+    # a key dim outside the coordinate rank is rejected before any device work
+    st = lib.ej_join_count(None, 3, 2, None, 5, 2, 1, i32_array([2]), i32_array([0]),
+                           i64_array([4]), 0, None, 0, ctypes.byref(n), None)
+    assert st == _lib.EJ_E_INVAL
+
+
+def test_fill_capacity_error():
+    lib = _lib.load()
+    st = lib.ej_join_fill(3, 4, 0, 0, None, 0, 12, None, None, 11, None)
+    assert st == _lib.EJ_E_CAPACITY
+    assert b"capacity" in lib.ej_last_error()
+    st = lib.ej_segment_fill(10, 5, 2, i64_array([4, 4]), None, 0, None, None, None, None, 4,
+                             None)
+    assert st == _lib.EJ_E_CAPACITY
+
+
+def test_key_space_overflow_is_unsupported():
+    lib = _lib.load()
+    n = ctypes.c_int64()
+    big = i64_array([1 << 40, 1 << 40])
+    # pointers are never dereferenced: the key-space check fails first
+    fake = ctypes.c_void_p(16)
+    st = lib.ej_join_count(fake, 1, 2, fake, 1, 2, 2, i32_array([0, 1]), i32_array([0, 1]), big,
+                           0, None, 0, ctypes.byref(n), None)
+    assert st == _lib.EJ_E_UNSUPPORTED
+
+
+def test_coords_range_empty_is_host_only():
+    lib = _lib.load()
+    lo_hi = (ctypes.c_int32 * 4)()
+    assert lib.ej_coords_range(None, 0, 2, lo_hi, None, 0, None) == 0
+    assert list(lo_hi) == [0, -1, 0, -1]
+
+
+def test_error_status_mapping():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EJ_E_INVAL, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.EJ_E_UNSUPPORTED, "x")
+    with pytest.raises(_lib.CapacityError):
+        _lib.check(_lib.EJ_E_CAPACITY, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.EJ_E_HIP, "x")

@@ -1,0 +1,438 @@
+"""GPU parity: every phase of the HIP path against the oracle.
+
+Index work (joins, output coordinates, segment plans, tiling coordinates)
+must be bit-exact; values must agree within rel-L2 <= 1e-5 (fp32) or
+<= 1e-2 (bf16, against fp32-or-better math on the bf16-rounded inputs).
+"""
+
+import zlib
+
+import numpy as np
+import numpy.testing as npt
+import pytest
+import torch
+
+from oracle import generators as G
+from oracle import reference_path as R
+
+import einjax_amd as ej
+from einjax_amd import SparseTensor, SparseTensorRelation
+from einjax_amd.execution import sparse_dispatch as sd
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp32": 1e-5, "bf16": 1e-2}
+
+
+def note(*a):
+    print("[case]", *a, flush=True)
+
+
+def dev_rel(r: R.Rel, dtype="fp32", device="cuda"):
+    """Oracle relation -> device SparseTensorRelation (fp32 or bf16 values)."""
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    vals = torch.from_numpy(np.ascontiguousarray(r.values, dtype=np.float32)).to(device)
+    return SparseTensorRelation(torch.from_numpy(r.coords).to(device), vals.to(tdt), r.shape,
+                                r.tile_shape)
+
+
+def host_rel(r: R.Rel):
+    return SparseTensorRelation(r.coords, r.values, r.shape, r.tile_shape)
+
+
+# ---------------------------------------------------------------------------
+# joins
+
+def test_join_golden_vectors(gpu):
+    g = np.load("tests/golden/join_order.npz")
+    for name in g["names"]:
+        note("join golden", name)
+        lc, rc = g[f"{name}__lhs"], g[f"{name}__rhs"]
+        keys = [tuple(k) for k in g[f"{name}__keys"].tolist()]
+        hl, hr = ej.coordinate_join_hash(lc, rc, keys)
+        npt.assert_array_equal(hl, g[f"{name}__hash_lhs"], err_msg=name)
+        npt.assert_array_equal(hr, g[f"{name}__hash_rhs"], err_msg=name)
+        sl, sr = ej.coordinate_join_sorted(lc, rc, keys)
+        npt.assert_array_equal(sl, g[f"{name}__sorted_lhs"], err_msg=name)
+        npt.assert_array_equal(sr, g[f"{name}__sorted_rhs"], err_msg=name)
+        assert hl.dtype == np.int64 and sl.dtype == np.int64
+
+
+@pytest.mark.parametrize("name", list(G.WORKLOADS))
+def test_join_and_plan_full_size(gpu, name):
+    """Join pairs, output coordinates and the segment plan at the workloads'
+    full sizes, bit-exact against the oracle."""
+    note("join+plan full size", name)
+    w = G.WORKLOADS[name](values=False)
+    L, Rr = w["lhs"], w["rhs"]
+    li_o, ri_o = R.coordinate_join(L.coords, Rr.coords, w["join_keys"])
+    lhs = SparseTensorRelation(torch.from_numpy(L.coords).cuda(), None, L.shape, L.tile_shape)
+    rhs = SparseTensorRelation(torch.from_numpy(Rr.coords).cuda(), None, Rr.shape, Rr.tile_shape)
+    lc, rc = lhs.coords, rhs.coords
+    li, ri = sd._join_dev(lhs, rhs, w["join_keys"], lc, rc)
+    npt.assert_array_equal(li.cpu().numpy(), li_o)
+    npt.assert_array_equal(ri.cpu().numpy(), ri_o)
+    oc_o = R.compute_output_coords(L.coords, Rr.coords, li_o, ri_o, w["agg_keys"])
+    from einjax_amd import _device
+
+    oc = _device.output_coords(lc, rc, li, ri, w["agg_keys"])
+    npt.assert_array_equal(oc.cpu().numpy(), oc_o)
+    radices = [max(sd._grid(lhs if s == 0 else rhs, d), 1) for s, d in w["agg_keys"]]
+    coords, off, perm, seg = _device.segment_plan(lc, rc, li, ri, w["agg_keys"], radices)
+    uc_o, perm_o, off_o, seg_o = R.segment_plan(oc_o)
+    npt.assert_array_equal(coords.cpu().numpy(), uc_o)
+    npt.assert_array_equal(off.cpu().numpy(), off_o)
+    npt.assert_array_equal(perm.cpu().numpy(), perm_o)
+    npt.assert_array_equal(seg.cpu().numpy(), seg_o)
+
+
+def test_join_edge_cases(gpu):
+    note("join edge cases")
+    e = np.zeros((0, 2), np.int32)
+    one = np.array([[0, 0]], np.int32)
+    for fn in (ej.coordinate_join_hash, ej.coordinate_join_sorted):
+        li, ri = fn(e, e, [(1, 0)])
+        assert len(li) == 0 and li.dtype == np.int64
+        li, ri = fn(one, e, [])
+        assert len(li) == 0
+        li, ri = fn(np.array([[0], [1]]), np.array([[0], [1], [2]]), [])
+        npt.assert_array_equal(li, [0, 0, 0, 1, 1, 1])
+        npt.assert_array_equal(ri, [0, 1, 2, 0, 1, 2])
+        li, ri = fn(np.array([[0, 0]]), np.array([[1, 0]]), [(0, 0)])
+        assert len(li) == 0
+    # all rows share one key: the output is the full product, in order
+    lc = np.zeros((300, 1), np.int32)
+    rc = np.zeros((200, 1), np.int32)
+    li, ri = ej.coordinate_join_hash(lc, rc, [0])
+    hl, hr = R.coordinate_join_hash(lc, rc, [0])
+    npt.assert_array_equal(li, hl)
+    npt.assert_array_equal(ri, hr)
+    # coordinates beyond the declared grid still join (radices sized from data)
+    lhs = SparseTensorRelation(np.array([[0, 9], [1, 3]], np.int32), np.ones((2, 1, 1)), (2, 4),
+                               (1, 1))
+    rhs = SparseTensorRelation(np.array([[9, 0], [3, 1]], np.int32), np.ones((2, 1, 1)), (4, 2),
+                               (1, 1))
+    li, ri = ej.coordinate_join(lhs, rhs, [(1, 0)])
+    npt.assert_array_equal(li, [0, 1])
+    npt.assert_array_equal(ri, [0, 1])
+
+
+# ---------------------------------------------------------------------------
+# tile einsum
+
+EINSUM_CASES = [
+    # spec, lhs tile, rhs tile (MFMA layouts first, then generic strings)
+    ("ij,jk->ik", (64, 64), (64, 64)),
+    ("ij,jk->ik", (128, 128), (128, 128)),
+    ("ij,jk->ik", (32, 32), (32, 32)),
+    ("ij,jk->ik", (128, 64), (64, 32)),
+    ("ij,kj->ik", (64, 32), (64, 32)),
+    ("ji,jk->ik", (64, 64), (64, 128)),
+    ("ji,kj->ik", (32, 64), (32, 32)),
+    ("bij,bjk->bik", (1, 64, 64), (1, 64, 64)),
+    ("bij,bjk->bik", (4, 32, 32), (4, 32, 64)),
+    ("ijk,kl->ijl", (8, 16, 32), (32, 32)),
+    ("ik,kj->ji", (32, 32), (32, 64)),
+    ("i,j->ij", (3,), (4,)),
+    ("i,i->", (5,), (5,)),
+    ("ij,ij->ij", (3, 4), (3, 4)),
+    ("ii,ij->j", (4, 4), (4, 3)),
+    ("ij,kl->ij", (1, 1), (1, 1)),
+    ("ijk,jl->il", (2, 3, 4), (3, 5)),
+    ("ij,jk->ik", (5, 7), (7, 3)),
+    ("ij,jk->ik", (48, 16), (16, 40)),
+]
+
+
+def _rand_tiles(rng, n, tile, dtype):
+    v = rng.standard_normal((n, *tile)).astype(np.float32)
+    return R.bf16_round(v) if dtype == "bf16" else v
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("spec,lt,rt", EINSUM_CASES)
+def test_pair_einsum(gpu, spec, lt, rt, dtype):
+    note("pair einsum", spec, lt, rt, dtype)
+    rng = np.random.default_rng(zlib.crc32(repr((spec, lt, rt)).encode()))
+    nl, nr, P = 7, 5, 23
+    lv, rv = _rand_tiles(rng, nl, lt, dtype), _rand_tiles(rng, nr, rt, dtype)
+    li = rng.integers(0, nl, P)
+    ri = rng.integers(0, nr, P)
+    want = R.kernel_einsum(lv, rv, li, ri, spec, precision="fp64")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    got = ej.kernel_einsum(torch.from_numpy(lv).cuda().to(tdt), torch.from_numpy(rv).cuda().to(tdt),
+                           torch.from_numpy(li).cuda(), torch.from_numpy(ri).cuda(), spec)
+    assert got.dtype == torch.float32
+    assert tuple(got.shape) == want.shape
+    err = R.rel_l2(got.cpu().numpy(), want)
+    assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("spec,lt,rt", EINSUM_CASES[:11])
+def test_segment_einsum_matches_pairs_plus_segsum(gpu, spec, lt, rt, dtype):
+    """Fused mode == per-pair results summed in plan order (within fp32
+    rounding), on random segment structure with skewed segment lengths."""
+    note("segment einsum", spec, lt, rt, dtype)
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(5)
+    nl, nr, P = 9, 6, 60
+    lv, rv = _rand_tiles(rng, nl, lt, dtype), _rand_tiles(rng, nr, rt, dtype)
+    li = rng.integers(0, nl, P)
+    ri = rng.integers(0, nr, P)
+    oc = np.minimum(rng.zipf(1.6, size=(P, 1)) - 1, 11).astype(np.int32)
+    uc, perm, off, _ = R.segment_plan(oc)
+    pairs = R.kernel_einsum(lv, rv, li, ri, spec, precision="fp64")
+    want = np.stack([pairs[perm[off[u]:off[u + 1]]].sum(0) for u in range(len(uc))])
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    desc = _device.describe(spec, lt, rt)
+    got = _device.segment_einsum(desc, torch.from_numpy(lv).cuda().to(tdt),
+                                 torch.from_numpy(rv).cuda().to(tdt),
+                                 torch.from_numpy(li).cuda(), torch.from_numpy(ri).cuda(),
+                                 torch.from_numpy(perm).cuda(), torch.from_numpy(off).cuda())
+    err = R.rel_l2(got.cpu().numpy(), want)
+    assert err <= TOL[dtype], err
+
+
+def test_gemm_index_out_of_range_contributes_nothing(gpu):
+    note("einsum out-of-range index")
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(0)
+    lv = rng.standard_normal((3, 32, 32)).astype(np.float32)
+    rv = rng.standard_normal((2, 32, 32)).astype(np.float32)
+    desc = _device.describe("ij,jk->ik", (32, 32), (32, 32))
+    li = torch.tensor([0, 5, -1], dtype=torch.int64, device="cuda")
+    ri = torch.tensor([1, 0, 0], dtype=torch.int64, device="cuda")
+    out = _device.pair_einsum(desc, torch.from_numpy(lv).cuda(), torch.from_numpy(rv).cuda(), li,
+                              ri).cpu().numpy()
+    npt.assert_allclose(out[0], lv[0] @ rv[1], rtol=1e-5, atol=1e-4)
+    assert np.all(out[1] == 0) and np.all(out[2] == 0)
+
+
+# ---------------------------------------------------------------------------
+# segment sum
+
+def test_segment_sum_known_answers_and_order(gpu):
+    note("segment_sum known answers")
+    c, a = ej.segment_sum(np.array([[[1.0, 0], [0, 1]], [[2.0, 0], [0, 2]]]),
+                          np.array([[0, 0], [0, 0]], np.int32))
+    assert c.shape == (1, 2)
+    npt.assert_allclose(a[0], 3 * np.eye(2))
+    c, a = ej.segment_sum(np.array([[[1.0]], [[2.0]], [[3.0]]]),
+                          np.array([[2, 0], [0, 0], [1, 0]], np.int32))
+    npt.assert_array_equal(c, [[0, 0], [1, 0], [2, 0]])
+    npt.assert_array_equal(a[:, 0, 0], [2, 3, 1])
+    c, a = ej.segment_sum(np.zeros((0, 2, 2)), np.zeros((0, 2), np.int32))
+    assert c.shape == (0, 2) and a.shape == (0, 2, 2)
+    # pair-order fp32 accumulation is bit-identical to the oracle's
+    rng = np.random.default_rng(1)
+    oc = rng.integers(0, 6, size=(500, 2)).astype(np.int32)
+    v = rng.standard_normal((500, 4, 8)).astype(np.float32) * 1e3
+    c, a = ej.segment_sum(v, oc)
+    c_o, a_o = R.segment_sum(v, oc)
+    npt.assert_array_equal(c, c_o)
+    npt.assert_array_equal(a, a_o)
+
+
+# ---------------------------------------------------------------------------
+# end to end: the reference's own cases through the drop-in API
+
+def _rel(dense, tile):
+    return SparseTensor("t", dense).to_relation(tile)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_reference_end_to_end_cases(gpu, fused):
+    note("reference end-to-end cases, fused =", fused)
+    A, B = np.array([[1.0, 2.0], [3.0, 4.0]]), np.eye(2)
+    out = ej.execute_sparse(_rel(A, (1, 1)), _rel(B, (1, 1)), [(1, 0)], "ij,jk->ik",
+                            [(0, 0), (1, 1)], (2, 2), (1, 1), fused=fused)
+    npt.assert_allclose(out.to_dense(), A @ B, atol=1e-6)
+    A, B = np.diag([1.0, 2, 3, 4]), np.diag([5.0, 6, 7, 8])
+    out = ej.execute_sparse(_rel(A, (1, 1)), _rel(B, (1, 1)), [(1, 0)], "ij,jk->ik",
+                            [(0, 0), (1, 1)], (4, 4), (1, 1), fused=fused)
+    npt.assert_allclose(out.to_dense(), A @ B, atol=1e-6)
+    A = np.array([[1.0, 2, 0, 0], [3, 4, 0, 0], [0, 0, 5, 6], [0, 0, 7, 8]])
+    out = ej.execute_sparse(_rel(A, (2, 2)), _rel(np.eye(4), (2, 2)), [(1, 0)], "ij,jk->ik",
+                            [(0, 0), (1, 1)], (4, 4), (2, 2), fused=fused)
+    npt.assert_allclose(out.to_dense(), A, atol=1e-6)
+    a, b = np.array([1.0, 0, 3]), np.array([0.0, 2, 4])
+    out = ej.execute_sparse(_rel(a.reshape(3, 1), (1, 1)), _rel(b.reshape(1, 3), (1, 1)), [],
+                            "ij,kl->ij", [(0, 0), (1, 1)], (3, 3), (1, 1), fused=fused)
+    npt.assert_allclose(out.to_dense(), np.outer(a, b), atol=1e-6)
+    A, B = np.diag([1.0, 2, 3]), np.diag([4.0, 5, 6])
+    out = ej.execute_sparse(_rel(A, (1, 1)), _rel(B, (1, 1)), [(0, 0), (1, 1)], "ij,ij->ij",
+                            [(0, 0), (0, 1)], (3, 3), (1, 1), fused=fused)
+    npt.assert_allclose(out.to_dense(), A * B, atol=1e-6)
+    A = np.zeros((4, 4)); A[0, 0] = 1
+    B = np.zeros((4, 4)); B[2, 2] = 1
+    out = ej.execute_sparse(_rel(A, (2, 2)), _rel(B, (2, 2)), [(1, 0)], "ij,jk->ik",
+                            [(0, 0), (1, 1)], (4, 4), (2, 2), fused=fused)
+    assert out.num_tuples == 0
+    npt.assert_allclose(out.to_dense(), np.zeros((4, 4)))
+    A, B = np.diag([1.0, 2]), np.diag([3.0, 4])
+    out = ej.execute_sparse(_rel(A, (1, 1)), _rel(B, (1, 1)), [(1, 0)], "ij,jk->ik",
+                            [(0, 0), (1, 1)], fused=fused)
+    npt.assert_allclose(out.to_dense(), A @ B, atol=1e-6)
+
+
+def test_block_sparse_matmul_api(gpu):
+    note("block_sparse_matmul api")
+    A = np.array([[1.0, 0, 2, 0], [0, 3, 0, 4], [5, 0, 6, 0]])
+    B = np.array([[1.0, 0], [0, 2], [3, 0], [0, 4]])
+    out = ej.block_sparse_matmul_generic(_rel(A, (1, 1)), _rel(B, (1, 1)))
+    npt.assert_allclose(out.to_dense(), A @ B, atol=1e-6)
+    la, rb = _rel(np.array([[1.0, 2], [3, 4]]), (1, 1)), _rel(np.eye(2), (1, 1))
+    out = ej.block_sparse_matmul(la.coords, la.values, rb.coords, rb.values, (1, 1, 1), (2, 2),
+                                 (2, 2))
+    npt.assert_allclose(out.to_dense(), [[1, 2], [3, 4]], atol=1e-6)
+    assert out.shape == (2, 2) and out.tile_shape == (1, 1)
+    A = np.zeros((4, 4)); A[0, 0] = 1
+    B = np.zeros((4, 4)); B[2, 2] = 1
+    out = ej.block_sparse_matmul_generic(_rel(A, (2, 2)), _rel(B, (2, 2)))
+    assert out.num_tuples == 0 and out.values.dtype == np.float64
+    reg = ej.KernelRegistry()
+    fn = reg.lookup("ij,jk->ik", backend="gpu", sparsity="sparse")
+    assert fn is ej.block_sparse_matmul_generic
+    assert reg.lookup("ij,kj->ik", backend="gpu", sparsity="sparse") is ej.execute_sparse
+
+
+@pytest.mark.parametrize("name", ["blocksparse_1k", "order3_small", "banded_small",
+                                  "zipf_small"])
+@pytest.mark.parametrize("fused", [True, False])
+def test_workload_end_to_end(gpu, name, fused):
+    """Whole execute_sparse against the oracle's (fp64-accumulated) result:
+    coordinates bit-exact, values within the dtype's tolerance."""
+    note("workload end-to-end", name, "fused =", fused)
+    if name == "blocksparse_1k":
+        w = G.workload_blocksparse_1k()
+    elif name == "order3_small":
+        w = G.workload_order3(n=512, l=128, density=0.02)
+    elif name == "banded_small":
+        w = G.workload_batched_banded(b=2, n=1024)
+    else:
+        w = G.workload_sparse_sparse_zipf(n=4096)
+    want = R.execute_sparse(w["lhs"], w["rhs"], w["join_keys"], w["kernel_string"],
+                            w["agg_keys"], precision="fp64")
+    lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
+    got = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                            fused=fused)
+    assert got.is_device
+    npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+    err = R.rel_l2(got.values.cpu().numpy(), want.values)
+    assert err <= TOL[w["dtype"]], err
+    # host inputs give host outputs with the same content
+    if name == "blocksparse_1k" and fused:
+        h = ej.execute_sparse(host_rel(w["lhs"]), host_rel(w["rhs"]), w["join_keys"],
+                              w["kernel_string"], w["agg_keys"])
+        assert isinstance(h.values, np.ndarray) and h.values.dtype == np.float32
+        npt.assert_array_equal(h.coords, want.coords)
+        npt.assert_array_equal(h.values, got.values.cpu().numpy())
+
+
+def test_headline_workload_full_size(gpu):
+    """16384^2 block-sparse (5%, 128^2 bf16 tiles) x dense 16384x4096 at full
+    size: coordinates bit-exact, a checksum of checksums (C @ x against
+    A @ (B @ x) in float64), fused == unfused, and a row-band subset
+    against the oracle's full result."""
+    note("headline workload full size")
+    w = G.workload_blocksparse_16k()
+    L, Rr = w["lhs"], w["rhs"]
+    lhs, rhs = dev_rel(L, "bf16"), dev_rel(Rr, "bf16")
+    fused = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    unfused = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                                fused=False)
+    torch.cuda.synchronize()
+    assert fused.num_tuples == 4096
+    npt.assert_array_equal(fused.coords.cpu().numpy(), unfused.coords.cpu().numpy())
+    fv, uv = fused.values.cpu().numpy(), unfused.values.cpu().numpy()
+    assert R.rel_l2(fv, uv) <= 1e-5
+    # checksum: C x == A (B x), float64 on the host
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(4096)
+    Bx = np.zeros(16384)
+    for (bi, bk), t in zip(Rr.coords, Rr.values):
+        Bx[bi * 128:(bi + 1) * 128] += t.astype(np.float64) @ x[bk * 128:(bk + 1) * 128]
+    ABx = np.zeros(16384)
+    for (ai, aj), t in zip(L.coords, L.values):
+        ABx[ai * 128:(ai + 1) * 128] += t.astype(np.float64) @ Bx[aj * 128:(aj + 1) * 128]
+    Cx = np.zeros(16384)
+    for (ci, ck), t in zip(fused.coords.cpu().numpy(), fv):
+        Cx[ci * 128:(ci + 1) * 128] += t.astype(np.float64) @ x[ck * 128:(ck + 1) * 128]
+    assert R.rel_l2(Cx, ABx) <= 1e-5
+    # a band of 8 row-tiles against the oracle
+    band = L.coords[:, 0] < 8
+    sub = R.Rel(L.coords[band], L.values[band], L.shape, L.tile_shape)
+    want = R.execute_sparse(sub, Rr, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                            precision="fp64")
+    rows = fused.coords.cpu().numpy()[:, 0] < 8
+    npt.assert_array_equal(fused.coords.cpu().numpy()[rows], want.coords)
+    assert R.rel_l2(fv[rows], want.values) <= TOL["bf16"]
+    assert R.rel_l2(fv[rows], want.values) <= 1e-5  # bf16 products are exact in fp32
+
+
+def test_fused_is_deterministic(gpu):
+    note("determinism")
+    w = G.workload_sparse_sparse_zipf(n=4096)
+    lhs, rhs = dev_rel(w["lhs"]), dev_rel(w["rhs"])
+    a = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    b = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    assert torch.equal(a.coords, b.coords)
+    assert torch.equal(a.values.view(torch.int32), b.values.view(torch.int32))
+
+
+# ---------------------------------------------------------------------------
+# tiling
+
+@pytest.mark.parametrize("dtype", ["f64host", "f32", "bf16"])
+def test_to_relation_parity(gpu, dtype):
+    note("to_relation", dtype)
+    rng = np.random.default_rng(4)
+    d = rng.standard_normal((64, 96)) * np.kron(rng.random((8, 6)) < 0.3, np.ones((8, 16)))
+    d[3, 5] = np.nan  # NaN is nonzero
+    d[60, 0] = -0.0  # -0.0 is zero
+    d[9, 17] = 1e-300  # nonzero in float64 only
+    tile = (8, 16)
+    if dtype == "f64host":
+        src = d
+        want = R.dense_to_relation(d, tile)
+    else:
+        f = d.astype(np.float32)
+        if dtype == "bf16":
+            f = R.bf16_round(f)
+        want = R.dense_to_relation(f.astype(np.float64), tile)
+        t = torch.from_numpy(f).cuda()
+        src = t.to(torch.bfloat16) if dtype == "bf16" else t
+    got = SparseTensor("x", src).to_relation(tile)
+    gc = got.coords.cpu().numpy() if dtype != "f64host" else got.coords
+    gv = (got.values.float().cpu().numpy() if dtype != "f64host" else got.values)
+    npt.assert_array_equal(gc, want.coords)
+    npt.assert_array_equal(gv, want.values.astype(np.float32))  # NaN == NaN, +0.0 for zeros
+    assert not np.any(np.signbit(gv[gv == 0]))
+
+
+def test_to_relation_edge_cases(gpu):
+    note("to_relation edges")
+    with pytest.raises(ValueError):
+        SparseTensor("x", np.eye(3)).to_relation((2, 2))
+    r = SparseTensor("z", np.zeros((4, 4))).to_relation((2, 2))
+    assert r.coords.shape == (0, 2) and r.values.shape == (0, 2, 2)
+    d = np.zeros((4, 4, 4)); d[0, 0, 0] = 1.0; d[3, 3, 3] = 2.0
+    r = SparseTensor("t3", d).to_relation((2, 2, 2))
+    npt.assert_array_equal(r.coords, [[0, 0, 0], [1, 1, 1]])
+    npt.assert_array_equal(r.to_dense(), d)
+    r = SparseTensor("v", np.array([0.0, 1, 0, 3, 0, 0])).to_relation((2,))
+    npt.assert_array_equal(r.coords, [[0], [1]])
+
+
+def test_device_to_dense_roundtrip(gpu):
+    note("device to_dense")
+    w = G.workload_blocksparse_1k()
+    rel = dev_rel(w["lhs"])
+    dense = rel.to_dense()
+    assert dense.is_cuda
+    npt.assert_array_equal(dense.cpu().numpy(), R.relation_to_dense(w["lhs"]).astype(np.float32))
+    back = SparseTensor("a", dense).to_relation((32, 32))
+    assert torch.equal(back.coords, rel.coords) and torch.equal(back.values, rel.values)
