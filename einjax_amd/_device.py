@@ -101,8 +101,8 @@ def output_coords(lhs_coords, rhs_coords, lhs_idx, rhs_idx, agg_keys) -> torch.T
     P = lhs_idx.numel()
     out = torch.empty((P, n_out), dtype=torch.int32, device=lhs_coords.device)
     check(_lib.load().ej_output_coords(
-        ptr(lhs_coords), lhs_coords.shape[1], ptr(rhs_coords), rhs_coords.shape[1], ptr(lhs_idx),
-        ptr(rhs_idx), P, n_out, i32_array([s for s, _ in agg_keys]),
+        ptr(lhs_coords), lhs_coords.shape[0], lhs_coords.shape[1], ptr(rhs_coords),
+        rhs_coords.shape[0], rhs_coords.shape[1], ptr(lhs_idx), ptr(rhs_idx), P, n_out, i32_array([s for s, _ in agg_keys]),
         i32_array([d for _, d in agg_keys]), ptr(out), stream_ptr()), "ej_output_coords")
     return out
 
@@ -123,9 +123,10 @@ def segment_plan(lhs_coords, rhs_coords, lhs_idx, rhs_idx, agg_keys, radices):
     check(lib.ej_segment_workspace_size(P, ctypes.byref(nbytes)), "ej_segment_workspace_size")
     ws = workspace(nbytes.value, dev)
     n_seg = ctypes.c_int64()
-    check(lib.ej_segment_count(ptr(lhs_coords), lhs_coords.shape[1], ptr(rhs_coords),
-                               rhs_coords.shape[1], ptr(lhs_idx), ptr(rhs_idx), P, n_out, src, dim,
-                               rad, ptr(ws), ws.numel(), ctypes.byref(n_seg), stream_ptr()),
+    check(lib.ej_segment_count(ptr(lhs_coords), lhs_coords.shape[0], lhs_coords.shape[1],
+                               ptr(rhs_coords), rhs_coords.shape[0], rhs_coords.shape[1],
+                               ptr(lhs_idx), ptr(rhs_idx), P, n_out, src, dim, rad, ptr(ws),
+                               ws.numel(), ctypes.byref(n_seg), stream_ptr()),
           "ej_segment_count")
     U = n_seg.value
     out_coords = torch.empty((U, n_out), dtype=torch.int32, device=dev)

@@ -64,11 +64,11 @@ SIGNATURES = {
     "ej_join_count": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32, _P_i64, _i32,
                              _vp, _sz, _P_i64, _vp]),
     "ej_join_fill": (_i32, [_i64, _i64, _i32, _i32, _vp, _sz, _i64, _vp, _vp, _i64, _vp]),
-    "ej_output_coords": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _P_i32, _P_i32, _vp,
-                                _vp]),
+    "ej_output_coords": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i64, _i32, _P_i32,
+                                _P_i32, _vp, _vp]),
     "ej_segment_workspace_size": (_i32, [_i64, _P_sz]),
-    "ej_segment_count": (_i32, [_vp, _i32, _vp, _i32, _vp, _vp, _i64, _i32, _P_i32, _P_i32,
-                                _P_i64, _vp, _sz, _P_i64, _vp]),
+    "ej_segment_count": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i64, _i32, _P_i32,
+                                _P_i32, _P_i64, _vp, _sz, _P_i64, _vp]),
     "ej_segment_fill": (_i32, [_i64, _i64, _i32, _P_i64, _vp, _sz, _vp, _vp, _vp, _vp, _i64,
                                _vp]),
     "ej_gather_tiles": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),

@@ -69,6 +69,12 @@ def build(verbose: bool = True) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    try:  # every symbol must resolve (a kernel whose host stub was not emitted would not)
+        import ctypes
+
+        ctypes.CDLL(str(tmp), mode=os.RTLD_NOW)
+    except OSError as e:
+        raise RuntimeError(f"built library does not load: {e}") from e
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH} from {len(srcs)} sources")

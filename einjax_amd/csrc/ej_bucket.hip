@@ -114,8 +114,10 @@ __global__ void slot_map_kernel(const int64_t *flags, const int64_t *excl, int64
 template <typename T, typename U>
 __global__ __launch_bounds__(256) void tile_copy_kernel(const T *__restrict__ dense, BucketGeom g,
                                                         const int64_t *tile_of_slot,
-                                                        int32_t *coords, U *__restrict__ values) {
+                                                        const int64_t *counted, int32_t *coords,
+                                                        U *__restrict__ values) {
   const int64_t slot = blockIdx.x;
+  if (slot >= *counted) return;  // only slots the count filled in
   int64_t t = tile_of_slot[slot];
   if (threadIdx.x == 0) {
     int64_t tt = t;
@@ -252,15 +254,15 @@ extern "C" int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t nd
   if (dtype == EJ_F64)
     hipLaunchKernelGGL((tile_copy_kernel<double, float>), dim3(static_cast<unsigned>(n_tiles)),
                        dim3(256), 0, stream, static_cast<const double *>(dense), g,
-                       w.tile_of_slot, coords, static_cast<float *>(values));
+                       w.tile_of_slot, w.scalars, coords, static_cast<float *>(values));
   else if (dtype == EJ_F32)
     hipLaunchKernelGGL((tile_copy_kernel<float, float>), dim3(static_cast<unsigned>(n_tiles)),
                        dim3(256), 0, stream, static_cast<const float *>(dense), g,
-                       w.tile_of_slot, coords, static_cast<float *>(values));
+                       w.tile_of_slot, w.scalars, coords, static_cast<float *>(values));
   else
     hipLaunchKernelGGL((tile_copy_kernel<uint16_t, uint16_t>), dim3(static_cast<unsigned>(n_tiles)),
                        dim3(256), 0, stream, static_cast<const uint16_t *>(dense), g,
-                       w.tile_of_slot, coords, static_cast<uint16_t *>(values));
+                       w.tile_of_slot, w.scalars, coords, static_cast<uint16_t *>(values));
   EJ_LAUNCH_CHECK();
   return EJ_OK;
 }

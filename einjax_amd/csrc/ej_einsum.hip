@@ -273,12 +273,14 @@ __device__ inline int64_t xcd_logical_block() {
 //
 // One workgroup (4 waves, 2x2) computes a BM x BN block of one output tile
 // (segment) for one batch index, iterating the segment's pairs and the K
-// dimension in BK chunks.  Operands are staged through LDS as [rows][k]
-// (k contiguous, the layout both MFMA operands read); an operand whose free
-// dimension is contiguous in HBM is transposed in registers before the LDS
-// store.  The next chunk's global loads are issued before the current
-// chunk's MFMAs, so HBM/L2 latency overlaps the math.  Accumulation is fp32
-// in registers; each output block is written once.
+// dimension in BK chunks ("stages").  Operands are staged through LDS as
+// [rows][k] (k contiguous, the layout both MFMA operands read); an operand
+// whose free dimension is contiguous in HBM is transposed in registers
+// before its LDS store.  LDS is double-buffered: the global loads of stage
+// s+1 are issued before the MFMAs of stage s and written to the other buffer
+// after them, so one barrier per stage suffices and HBM/L2 latency overlaps
+// the math.  The tile indices of the next pair are fetched one pair ahead.
+// Accumulation is fp32 in registers; each output block is written once.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -290,11 +292,28 @@ struct GemmGeom {
   int64_t mblocks, nblocks;
 };
 
+// LDS placement of a [rows][BK] operand chunk in 16-byte chunks of VEC
+// elements.  With 128-byte rows (8 chunks) the chunk index is XOR-swizzled
+// by (row & 7) ^ ((row >> 3) & 7): the MFMA operand reads (16 consecutive
+// rows, one chunk) and the transposed stores (rows 8 apart, one chunk) then
+// touch distinct bank groups.  Other row widths use a 16-byte pad.
+template <typename T, int BK>
+struct LdsLayout {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int CH = BK / VEC;
+  static constexpr bool SWZ = CH == 8;
+  static constexpr int LDK = SWZ ? BK : BK + VEC;
+  __device__ static inline int off(int row, int chunk) {
+    const int p = SWZ ? (chunk ^ ((row & 7) ^ ((row >> 3) & 7))) : chunk;
+    return row * LDK + p * VEC;
+  }
+};
+
 template <typename T, int ROWS, int BK, bool DIRECT>
 struct OperandStage {
-  static constexpr int VEC = 16 / sizeof(T);
-  static constexpr int LDK = BK + VEC;  // row pitch in LDS (elements)
-  // DIRECT: k contiguous in HBM; vectors along k.
+  using L = LdsLayout<T, BK>;
+  static constexpr int VEC = L::VEC;
+  // DIRECT: k contiguous in HBM; one 16-byte vector per (row, chunk).
   static constexpr int NVEC_D = ROWS * BK / VEC;
   static constexpr int PER_D = (NVEC_D + 255) / 256;
   // Transposed: rows contiguous in HBM; each thread owns KV k-rows x VEC rows.
@@ -302,6 +321,7 @@ struct OperandStage {
   static constexpr int KV = KV0 > 0 ? KV0 : 1;
   static constexpr int NBLK_T = (BK / KV) * (ROWS / VEC);
   static constexpr int NREG = DIRECT ? PER_D : KV;
+  static_assert(KV <= VEC, "a thread's k run must fit in one 16-byte chunk");
   uint4 r[NREG];
 
   // base points at element (row 0, k 0) of the chunk.
@@ -337,12 +357,13 @@ struct OperandStage {
         const int id = v * 256 + tid;
         if (id < NVEC_D) {
           const int row = id / (BK / VEC), kv = id % (BK / VEC);
-          *reinterpret_cast<uint4 *>(lds + row * LDK + kv * VEC) = r[v];
+          *reinterpret_cast<uint4 *>(lds + L::off(row, kv)) = r[v];
         }
       }
     } else {
       if (tid >= NBLK_T) return;
       const int rb = tid % (ROWS / VEC), kb = tid / (ROWS / VEC);
+      const int chunk = (kb * KV) / VEC, within = (kb * KV) % VEC;
       const uint32_t *w = reinterpret_cast<const uint32_t *>(r);
       if (sizeof(T) == 2) {
         // r[j] holds 8 bf16 of k-row j; emit, per row c, the KV values of k.
@@ -354,8 +375,15 @@ struct OperandStage {
             uint32_t word = w[j * 4 + c / 2];
             vals[j] = static_cast<uint16_t>((c & 1) ? (word >> 16) : (word & 0xffffu));
           }
-          T *dst = lds + (rb * VEC + c) * LDK + kb * KV;
-          if (KV == 4) {
+          T *dst = lds + L::off(rb * VEC + c, chunk) + within;
+          if (KV == 8) {
+            uint4 o;
+            o.x = vals[0] | (static_cast<uint32_t>(vals[1 % KV]) << 16);
+            o.y = vals[2 % KV] | (static_cast<uint32_t>(vals[3 % KV]) << 16);
+            o.z = vals[4 % KV] | (static_cast<uint32_t>(vals[5 % KV]) << 16);
+            o.w = vals[6 % KV] | (static_cast<uint32_t>(vals[7 % KV]) << 16);
+            *reinterpret_cast<uint4 *>(dst) = o;
+          } else if (KV == 4) {
             uint2 o;
             o.x = vals[0] | (static_cast<uint32_t>(vals[1 % KV]) << 16);
             o.y = vals[2 % KV] | (static_cast<uint32_t>(vals[3 % KV]) << 16);
@@ -370,14 +398,30 @@ struct OperandStage {
       } else {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          T *dst = lds + (rb * VEC + c) * LDK + kb * KV;
+          T *dst = lds + L::off(rb * VEC + c, chunk) + within;
+          if (KV == 4) {
+            *reinterpret_cast<uint4 *>(dst) = make_uint4(w[c], w[4 + c], w[8 + c], w[12 + c]);
+          } else {
 #pragma unroll
-          for (int j = 0; j < KV; ++j) reinterpret_cast<uint32_t *>(dst)[j] = w[j * 4 + c];
+            for (int j = 0; j < KV; ++j) reinterpret_cast<uint32_t *>(dst)[j] = w[j * 4 + c];
+          }
         }
       }
     }
   }
 };
+
+struct PairTiles {
+  int64_t at, bt;
+  bool ok;
+};
+
+__device__ inline PairTiles load_pair(const PairSrc &s, int64_t q) {
+  PairTiles t;
+  t.ok = pair_tiles(s, q, &t.at, &t.bt);
+  if (!t.ok) t.at = t.bt = 0;
+  return t;
+}
 
 template <typename T, int BM, int BN, int BK, bool A_DIRECT, bool B_DIRECT>
 __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
@@ -386,13 +430,14 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
                                                         GemmGeom g) {
   using SA = OperandStage<T, BM, BK, A_DIRECT>;
   using SB = OperandStage<T, BN, BK, B_DIRECT>;
-  constexpr int LDK = SA::LDK;
+  using L = LdsLayout<T, BK>;
+  constexpr int LDK = L::LDK;
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr bool BF16 = sizeof(T) == 2;
-  constexpr int KSTEP = BF16 ? 32 : 16;  // k consumed per inner step
-  __shared__ __align__(16) T As[BM * LDK];
-  __shared__ __align__(16) T Bs[BN * LDK];
+  constexpr int KSTEP = BF16 ? 32 : 16;  // k consumed per inner step (4 chunks)
+  __shared__ __align__(16) T As[2][BM * LDK];
+  __shared__ __align__(16) T Bs[2][BN * LDK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -419,37 +464,44 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
   SB sb;
   const int64_t a_off0 = bi * g.a_sb + mb * BM * g.a_sm;
   const int64_t b_off0 = bi * g.b_sb + nb * BN * g.b_sn;
-  // A chunk rows advance by a_sm (direct) and k by a_sk; see OperandStage.
-  auto issue = [&](int64_t st) {
-    const int64_t q = q0 + st / nkc;
-    const int kc = static_cast<int>(st % nkc);
-    int64_t at, bt;
-    const bool ok = pair_tiles(src, q, &at, &bt);
-    const T *ab = A + (ok ? at : 0) * g.a_elems + a_off0 + kc * BK * g.a_sk;
-    const T *bb = B + (ok ? bt : 0) * g.b_elems + b_off0 + kc * BK * g.b_sk;
-    sa.load(ab, g.a_sm, g.a_sk, ok, tid);
-    sb.load(bb, g.b_sn, g.b_sk, ok, tid);
+  auto issue = [&](const PairTiles &p, int kc) {
+    const T *ab = A + p.at * g.a_elems + a_off0 + kc * BK * g.a_sk;
+    const T *bb = B + p.bt * g.b_elems + b_off0 + kc * BK * g.b_sk;
+    sa.load(ab, g.a_sm, g.a_sk, p.ok, tid);
+    sb.load(bb, g.b_sn, g.b_sk, p.ok, tid);
   };
 
-  if (stages > 0) issue(0);
+  PairTiles cur{0, 0, false}, nxt{0, 0, false};
+  if (stages > 0) {
+    cur = load_pair(src, q0);
+    nxt = q0 + 1 < q1 ? load_pair(src, q0 + 1) : cur;
+    issue(cur, 0);
+    sa.store(As[0], tid);
+    sb.store(Bs[0], tid);
+  }
+  __syncthreads();
+  int kc = 0;
+  int64_t q = q0;
   for (int64_t st = 0; st < stages; ++st) {
-    __syncthreads();
-    sa.store(As, tid);
-    sb.store(Bs, tid);
-    __syncthreads();
-    if (st + 1 < stages) issue(st + 1);
+    const int buf = static_cast<int>(st & 1);
+    const bool more = st + 1 < stages;
+    if (more) {
+      if (kc + 1 < nkc) issue(cur, kc + 1);
+      else issue(nxt, 0);
+    }
+    const T *as = As[buf];
+    const T *bs = Bs[buf];
 #pragma unroll
     for (int ks = 0; ks < BK / KSTEP; ++ks) {
+      const int ch = ks * 4 + (lane >> 4);
       if constexpr (BF16) {
         bf16x8_t af[FM], bfr[FN];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
-          af[i] = *reinterpret_cast<const bf16x8_t *>(
-              As + (wm * WM + i * 16 + (lane & 15)) * LDK + ks * 32 + (lane >> 4) * 8);
+          af[i] = *reinterpret_cast<const bf16x8_t *>(as + L::off(wm * WM + i * 16 + (lane & 15), ch));
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8_t *>(
-              Bs + (wn * WN + j * 16 + (lane & 15)) * LDK + ks * 32 + (lane >> 4) * 8);
+          bfr[j] = *reinterpret_cast<const bf16x8_t *>(bs + L::off(wn * WN + j * 16 + (lane & 15), ch));
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -459,20 +511,271 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
         f32x4_t af[FM], bfr[FN];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
-          af[i] = *reinterpret_cast<const f32x4_t *>(
-              As + (wm * WM + i * 16 + (lane & 15)) * LDK + ks * 16 + (lane >> 4) * 4);
+          af[i] = *reinterpret_cast<const f32x4_t *>(as + L::off(wm * WM + i * 16 + (lane & 15), ch));
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          bfr[j] = *reinterpret_cast<const f32x4_t *>(
-              Bs + (wn * WN + j * 16 + (lane & 15)) * LDK + ks * 16 + (lane >> 4) * 4);
+          bfr[j] = *reinterpret_cast<const f32x4_t *>(bs + L::off(wn * WN + j * 16 + (lane & 15), ch));
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
           for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bfr[j][s], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s4], bfr[j][s4], acc[i][j], 0, 0, 0);
       }
+    }
+    if (++kc == nkc) {  // the stage just issued starts pair q + 1
+      kc = 0;
+      ++q;
+      cur = nxt;
+      if (q + 1 < q1) nxt = load_pair(src, q + 1);
+    }
+    if (more) {
+      sa.store(As[buf ^ 1], tid);
+      sb.store(Bs[buf ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  float *cb = C + seg * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = wm * WM + i * 16 + (lane >> 4) * 4 + r;
+        const int col = wn * WN + j * 16 + (lane & 15);
+        cb[row * g.c_sm + col * g.c_sn] = acc[i][j][r];
+      }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA grouped GEMM, bf16, streaming operands straight into an LDS ring.
+//
+// Used for the common layout: lhs tiles k-contiguous ([m][k]) and rhs tiles
+// n-contiguous ([k][n]), bf16.  Each stage (one pair's K-chunk of 64) is
+// copied HBM -> LDS with 16-byte direct loads (global_load_lds_dwordx4, no
+// register staging) into an NS-deep ring, so NS-1 stages are in flight while
+// the MFMAs of the current one run.  Both operands keep their HBM layout in
+// LDS; the per-lane source addresses are permuted so that 16-byte chunks
+// land XOR-swizzled:
+//   A [row][k]:  chunk c of row r at c ^ ((r & 7) ^ ((r >> 3) & 7)) (rows of
+//                128 B; the 16-row operand reads hit distinct bank groups);
+//   B [k][n]:    chunk j of k-row r at j ^ (2 * (r & 3)) (the 4-row reads of
+//                the transpose load hit distinct bank groups).
+// The B operand of v_mfma_f32_16x16x32_bf16 (8 consecutive k of one column
+// per lane) comes from two ds_read_b64_tr_b16: within each 16-lane group,
+// lane i receives element i % 4 of the 8 bytes read by lane 4t + i / 4
+// (t = 0..3), so lanes 4t..4t+3 read k-row t, columns 4q..4q+3.
+// The waits are explicit: s_waitcnt vmcnt(loads per stage x stages issued
+// later) then s_barrier (no fence), one barrier per stage.
+
+#define EJ_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 at LDS byte address `addr`.  Issued as inline asm: the
+// compiler would otherwise order it behind every LDS DMA in flight
+// (s_waitcnt vmcnt(0)), which defeats the ring.  Its completion is awaited
+// by lgkm_wait_all.
+__device__ inline i32x2_t ds_read_tr16_b64(uint32_t addr) {
+  i32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// s_waitcnt lgkmcnt(0), threaded through the values it guards so that their
+// consumers cannot be scheduled ahead of it.
+template <int N>
+__device__ inline void lgkm_wait_all(i32x4_t (&v)[N]) {
+  static_assert(N == 2 || N == 4, "operand count");
+  if constexpr (N == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]));
+}
+
+// Ring depth (stages) of the LDS-ring kernel per block shape.
+#ifndef EJ_DMA_STAGES_128
+#define EJ_DMA_STAGES_128 2
+#endif
+#ifndef EJ_DMA_STAGES_64
+#define EJ_DMA_STAGES_64 4
+#endif
+#ifndef EJ_USE_DMA_GEMM
+#define EJ_USE_DMA_GEMM 1
+#endif
+
+// Reads a workgroup-uniform element of a read-only index array through the
+// scalar cache, so the load does not occupy the vector memory counter that
+// paces the LDS ring.
+template <typename T>
+__device__ inline T ld_uniform(const T *p, int64_t i) {
+  return ((const __attribute__((address_space(4))) T *)(p))[i];
+}
+
+__device__ inline PairTiles load_pair_uniform(const PairSrc &s, int64_t q) {
+  const int32_t qq = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(q));
+  const int32_t p = s.perm ? ld_uniform(s.perm, qq) : qq;
+  PairTiles t;
+  t.at = s.lidx ? ld_uniform(s.lidx, p) : p;
+  t.bt = s.ridx ? ld_uniform(s.ridx, p) : p;
+  t.ok = t.at >= 0 && t.at < s.n_a_tiles && t.bt >= 0 && t.bt < s.n_b_tiles;
+  if (!t.ok) t.at = t.bt = 0;
+  return t;
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NS, int LPS>
+__device__ inline void wait_stage(int later) {
+  // later = number of stages issued after the one about to be consumed;
+  // each stage is LPS load instructions per wave.
+  if constexpr (NS >= 4) {
+    if (later >= 2) { wait_vmcnt<2 * LPS>(); return; }
+  }
+  if constexpr (NS >= 3) {
+    if (later >= 1) { wait_vmcnt<LPS>(); return; }
+  }
+  wait_vmcnt<0>();
+}
+
+template <int BM, int BN, int NS>
+__global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__restrict__ A,
+                                                            const uint16_t *__restrict__ B,
+                                                            float *__restrict__ C, PairSrc src,
+                                                            GemmGeom g) {
+#if defined(__HIP_DEVICE_COMPILE__)  // device-only body (LDS address-space casts, gfx950 asm)
+  constexpr int BK = 64;                       // k per stage (128 B per A row)
+  constexpr int A_BYTES = BM * BK * 2;         // [BM][64] bf16
+  constexpr int B_ROWB = BN * 2;               // bytes per k-row of B
+  constexpr int CHB = B_ROWB / 16;             // 16-byte chunks per B k-row
+  constexpr int B_BYTES = BK * B_ROWB;
+  constexpr int SLOT = A_BYTES + B_BYTES;
+  constexpr int A_BLOCKS = A_BYTES / 1024;     // 1 KB per wave-wide load
+  constexpr int B_BLOCKS = B_BYTES / 1024;
+  static_assert(A_BLOCKS % 4 == 0 && B_BLOCKS % 4 == 0, "blocks split over 4 waves");
+  constexpr int LPS = A_BLOCKS / 4 + B_BLOCKS / 4;  // load instructions per wave per stage
+  static_assert(NS >= 2 && NS <= 4 && 2 * LPS < 64, "ring depth / vmcnt range");
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  __shared__ __align__(1024) unsigned char ring[NS * SLOT];
+  const uint32_t ring_lds = static_cast<uint32_t>(
+      reinterpret_cast<size_t>((__attribute__((address_space(3))) unsigned char *)ring));
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int64_t lb = xcd_logical_block();
+  const int64_t nb = lb % g.nblocks;
+  lb /= g.nblocks;
+  const int64_t mb = lb % g.mblocks;
+  lb /= g.mblocks;
+  const int64_t bi = lb % g.batch;
+  const int64_t seg = lb / g.batch;
+  int64_t q0, q1;
+  seg_range(src, seg, &q0, &q1);
+  const int nkc = static_cast<int>(g.k / BK);
+  const int64_t stages = (q1 - q0) * nkc;
+
+  // Per-lane source offsets inside a stage (elements), fixed for the kernel.
+  int64_t a_src[A_BLOCKS / 4], b_src[B_BLOCKS / 4];
+#pragma unroll
+  for (int v = 0; v < A_BLOCKS / 4; ++v) {
+    const int blk = v * 4 + wave;
+    const int row = blk * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row & 7) ^ ((row >> 3) & 7));
+    a_src[v] = row * g.a_sm + c * 8;
+  }
+#pragma unroll
+  for (int v = 0; v < B_BLOCKS / 4; ++v) {
+    const int blk = v * 4 + wave;
+    const int krow = blk * (64 / CHB) + lane / CHB;
+    const int j = (lane % CHB) ^ (2 * (krow & 3));
+    b_src[v] = krow * g.b_sk + j * 8;
+  }
+  const int64_t a_off0 = bi * g.a_sb + mb * BM * g.a_sm;
+  const int64_t b_off0 = bi * g.b_sb + nb * BN;
+
+  // issue cursor (runs NS-1 stages ahead of the compute cursor)
+  int64_t iq = q0;
+  int ikc = 0;
+  PairTiles icur = stages > 0 ? load_pair_uniform(src, q0) : PairTiles{0, 0, false};
+  uint32_t okmask = 0;  // bit s % 32: stage s holds a valid pair
+  auto issue = [&](int64_t st) {
+    unsigned char *slot = ring + (st % NS) * SLOT;
+    const uint16_t *ab = A + icur.at * g.a_elems + a_off0 + ikc * BK;
+    const uint16_t *bb = B + icur.bt * g.b_elems + b_off0 + ikc * BK * g.b_sk;
+#pragma unroll
+    for (int v = 0; v < A_BLOCKS / 4; ++v)
+      __builtin_amdgcn_global_load_lds(ab + a_src[v], EJ_LDS(slot + (v * 4 + wave) * 1024), 16, 0,
+                                       0);
+#pragma unroll
+    for (int v = 0; v < B_BLOCKS / 4; ++v)
+      __builtin_amdgcn_global_load_lds(bb + b_src[v],
+                                       EJ_LDS(slot + A_BYTES + (v * 4 + wave) * 1024), 16, 0, 0);
+    okmask = (okmask & ~(1u << (st & 31))) | ((icur.ok ? 1u : 0u) << (st & 31));
+    if (++ikc == nkc) {
+      ikc = 0;
+      ++iq;
+      if (iq < q1) icur = load_pair_uniform(src, iq);
+    }
+  };
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s0 = 0; s0 < NS - 1; ++s0)
+    if (s0 < stages) issue(s0);
+
+  for (int64_t st = 0; st < stages; ++st) {
+    const int64_t later = stages - 1 - st < NS - 2 ? stages - 1 - st : NS - 2;
+    wait_stage<NS, LPS>(static_cast<int>(later));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (st + NS - 1 < stages) issue(st + NS - 1);
+    if (!((okmask >> (st & 31)) & 1u)) continue;  // uniform: the pair's index is invalid
+    const unsigned char *as = ring + (st % NS) * SLOT;
+    const uint32_t bs_lds = ring_lds + static_cast<uint32_t>((st % NS) * SLOT + A_BYTES);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8_t af[FM];
+      i32x4_t bq[FN];
+      const int ch = ks * 4 + (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int row = wm * WM + i * 16 + (lane & 15);
+        const int phys = ch ^ ((row & 7) ^ ((row >> 3) & 7));
+        af[i] = *reinterpret_cast<const bf16x8_t *>(as + row * 128 + phys * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n0 = wn * WN + j * 16;
+        const int t = (lane & 15) >> 2, qq = lane & 3;
+        const int jc = (n0 >> 3) + (qq >> 1);
+        i32x2_t h[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int krow = ks * 32 + (lane >> 4) * 8 + hh * 4 + t;
+          const int phys = jc ^ (2 * (krow & 3));
+          h[hh] = ds_read_tr16_b64(bs_lds + krow * B_ROWB + phys * 16 + (qq & 1) * 8);
+        }
+        bq[j] = i32x4_t{h[0][0], h[0][1], h[1][0], h[1][1]};
+      }
+      lgkm_wait_all<FN>(bq);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              af[i], __builtin_bit_cast(bf16x8_t, bq[j]), acc[i][j], 0, 0, 0);
     }
   }
 
@@ -487,6 +790,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
         const int col = wn * WN + j * 16 + (lane & 15);
         cb[row * g.c_sm + col * g.c_sn] = acc[i][j][r];
       }
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -616,6 +920,28 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
   g.nblocks = d->n / bn;
   const int64_t nblk = n_seg * g.batch * g.mblocks * g.nblocks;
   if (nblk >= (int64_t(1) << 32)) return false;
+  // bf16, k-contiguous lhs, n-contiguous rhs, K a multiple of 64: the LDS-ring
+  // kernel (direct HBM -> LDS loads, transpose reads for the rhs operand).
+  if (EJ_USE_DMA_GEMM && dtype == EJ_BF16 && ad && !bd && d->k % 64 == 0 && d->b_sn == 1 &&
+      d->b_sk % 8 == 0 &&
+      ((bm == 128 && bn == 128) || (bm == 64 && bn == 64))) {
+    const uint16_t *a = static_cast<const uint16_t *>(A);
+    const uint16_t *b = static_cast<const uint16_t *>(B);
+    if (bm == 128)
+      hipLaunchKernelGGL((tile_gemm_dma_kernel<128, 128, EJ_DMA_STAGES_128>),
+                         dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, a, b, C, src, g);
+    else
+      hipLaunchKernelGGL((tile_gemm_dma_kernel<64, 64, EJ_DMA_STAGES_64>),
+                         dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, a, b, C, src, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_error("tile_gemm_dma_kernel launch failed: %s", hipGetErrorString(e));
+      *status = EJ_E_HIP;
+    } else {
+      *status = EJ_OK;
+    }
+    return true;
+  }
   if (dtype == EJ_BF16) {
     *status = bk == 64 ? launch_gemm_bk<uint16_t, 64>(bm, bn, ad, bd, A, B, C, src, g, nblk, stream)
                        : launch_gemm_bk<uint16_t, 32>(bm, bn, ad, bd, A, B, C, src, g, nblk, stream);
@@ -665,6 +991,39 @@ int run_generic(const ej_einsum_desc *d, int32_t dtype, const void *A, const voi
   return EJ_OK;
 }
 
+// Every element a descriptor can address must lie inside its tile: the
+// kernels index tiles with these strides and no further checks.
+int check_desc(const ej_einsum_desc *d) {
+  int64_t a = 0, b = 0, c = 0, c_expect = 1;
+  for (int i = 0; i < d->n_out; ++i) {
+    EJ_CHECK_ARG(d->out_ext[i] >= 1 && d->out_a[i] >= 0 && d->out_b[i] >= 0,
+                 "malformed einsum descriptor");
+    a += (d->out_ext[i] - 1) * d->out_a[i];
+    b += (d->out_ext[i] - 1) * d->out_b[i];
+    c_expect *= d->out_ext[i];
+  }
+  for (int i = 0; i < d->n_red; ++i) {
+    EJ_CHECK_ARG(d->red_ext[i] >= 1 && d->red_a[i] >= 0 && d->red_b[i] >= 0,
+                 "malformed einsum descriptor");
+    a += (d->red_ext[i] - 1) * d->red_a[i];
+    b += (d->red_ext[i] - 1) * d->red_b[i];
+  }
+  EJ_CHECK_ARG(a < d->a_elems && b < d->b_elems && c_expect == d->c_elems,
+               "einsum descriptor addresses elements outside its tiles");
+  if (d->is_gemm) {
+    EJ_CHECK_ARG(d->batch >= 1 && d->m >= 1 && d->n >= 1 && d->k >= 1 && d->a_sb >= 0 &&
+                     d->a_sm >= 0 && d->a_sk >= 0 && d->b_sb >= 0 && d->b_sk >= 0 &&
+                     d->b_sn >= 0 && d->c_sb >= 0 && d->c_sm >= 0 && d->c_sn >= 0,
+                 "malformed GEMM descriptor");
+    a = (d->batch - 1) * d->a_sb + (d->m - 1) * d->a_sm + (d->k - 1) * d->a_sk;
+    b = (d->batch - 1) * d->b_sb + (d->k - 1) * d->b_sk + (d->n - 1) * d->b_sn;
+    c = (d->batch - 1) * d->c_sb + (d->m - 1) * d->c_sm + (d->n - 1) * d->c_sn;
+    EJ_CHECK_ARG(a < d->a_elems && b < d->b_elems && c < d->c_elems,
+                 "GEMM descriptor addresses elements outside its tiles");
+  }
+  return EJ_OK;
+}
+
 int einsum_common(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B,
                   const PairSrc &src, int64_t n_seg, float *C, hipStream_t stream) {
   EJ_CHECK_ARG(d, "desc is null");
@@ -676,6 +1035,7 @@ int einsum_common(const ej_einsum_desc *d, int32_t dtype, const void *A, const v
                "malformed einsum descriptor");
   if (n_seg == 0) return EJ_OK;
   EJ_CHECK_ARG(A && B && C, "null pointer argument");
+  EJ_TRY(check_desc(d));
   int status = EJ_OK;
   if (try_gemm(d, dtype, A, B, C, src, n_seg, stream, &status)) return status;
   return run_generic(d, dtype, A, B, C, src, n_seg, stream);

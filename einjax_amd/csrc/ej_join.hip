@@ -71,9 +71,10 @@ __global__ void probe_count_kernel(const uint64_t *probe_keys, int64_t n_probe,
 // EJ_ORDER_PROBE fill: pair q belongs to rhs row j = owner_of(offs, q).
 __global__ void fill_probe_order_kernel(const int64_t *offs, int64_t n_rhs, const int64_t *lo,
                                         const int32_t *lhs_perm, int64_t n_pairs,
-                                        int64_t *lhs_idx, int64_t *rhs_idx) {
+                                        const int64_t *counted, int64_t *lhs_idx,
+                                        int64_t *rhs_idx) {
   int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (q >= n_pairs) return;
+  if (q >= n_pairs || q >= *counted) return;
   int64_t j = owner_of(offs, n_rhs, q);
   int64_t t = q - offs[j];
   lhs_idx[q] = lhs_perm[lo[j] + t];
@@ -83,9 +84,10 @@ __global__ void fill_probe_order_kernel(const int64_t *offs, int64_t n_rhs, cons
 // EJ_ORDER_SORTED fill: pair q belongs to sorted lhs position p.
 __global__ void fill_sorted_order_kernel(const int64_t *offs, int64_t n_lhs, const int64_t *lo,
                                          const int32_t *lhs_perm, const int32_t *rhs_perm,
-                                         int64_t n_pairs, int64_t *lhs_idx, int64_t *rhs_idx) {
+                                         int64_t n_pairs, const int64_t *counted,
+                                         int64_t *lhs_idx, int64_t *rhs_idx) {
   int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (q >= n_pairs) return;
+  if (q >= n_pairs || q >= *counted) return;
   int64_t p = owner_of(offs, n_lhs, q);
   int64_t t = q - offs[p];
   lhs_idx[q] = lhs_perm[p];
@@ -260,10 +262,11 @@ extern "C" int ej_join_fill(int64_t n_lhs, int64_t n_rhs, int32_t n_keys, int32_
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
   if (order == EJ_ORDER_PROBE) {
     hipLaunchKernelGGL(fill_probe_order_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream,
-                       w.offs, n_rhs, w.lo, w.lperm, n_pairs, lhs_idx, rhs_idx);
+                       w.offs, n_rhs, w.lo, w.lperm, n_pairs, w.scalars, lhs_idx, rhs_idx);
   } else {
     hipLaunchKernelGGL(fill_sorted_order_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream,
-                       w.offs, n_lhs, w.lo, w.lperm, w.rperm, n_pairs, lhs_idx, rhs_idx);
+                       w.offs, n_lhs, w.lo, w.lperm, w.rperm, n_pairs, w.scalars, lhs_idx,
+                       rhs_idx);
   }
   EJ_LAUNCH_CHECK();
   return EJ_OK;
@@ -278,16 +281,22 @@ namespace {
 struct AggSpec {
   int32_t n;
   int32_t lncols, rncols;
+  int64_t n_lhs, n_rhs;
   int32_t src[EJ_MAX_KEYS];
   int32_t dim[EJ_MAX_KEYS];
   int64_t radix[EJ_MAX_KEYS];
 };
 
-int check_agg(int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim, int32_t lncols,
-              int32_t rncols, const int64_t *radices, AggSpec *a) {
+int check_agg(int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim, int64_t n_lhs,
+              int32_t lncols, int64_t n_rhs, int32_t rncols, const int64_t *radices, AggSpec *a) {
   EJ_CHECK_ARG(n_out >= 0 && n_out <= EJ_MAX_KEYS, "n_out=%d outside [0, %d]", n_out,
                EJ_MAX_KEYS);
+  EJ_CHECK_ARG(n_lhs >= 0 && n_rhs >= 0, "negative relation size");
+  EJ_CHECK_ARG(lncols >= 0 && lncols <= EJ_MAX_DIMS && rncols >= 0 && rncols <= EJ_MAX_DIMS,
+               "coordinate rank outside [0, %d]", EJ_MAX_DIMS);
   a->n = n_out;
+  a->n_lhs = n_lhs;
+  a->n_rhs = n_rhs;
   a->lncols = lncols;
   a->rncols = rncols;
   for (int d = 0; d < n_out; ++d) {
@@ -307,6 +316,10 @@ __global__ void output_coords_kernel(const int32_t *lc, const int32_t *rc, const
                                      const int64_t *ri, int64_t n, AggSpec a, int32_t *out) {
   int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n) return;
+  if (li[p] < 0 || li[p] >= a.n_lhs || ri[p] < 0 || ri[p] >= a.n_rhs) {
+    for (int d = 0; d < a.n; ++d) out[p * a.n + d] = -1;
+    return;
+  }
   const int32_t *lrow = lc + li[p] * a.lncols;
   const int32_t *rrow = rc + ri[p] * a.rncols;
   for (int d = 0; d < a.n; ++d) out[p * a.n + d] = a.src[d] == 0 ? lrow[a.dim[d]] : rrow[a.dim[d]];
@@ -317,6 +330,11 @@ __global__ void pair_keys_kernel(const int32_t *lc, const int32_t *rc, const int
                                  int *bad) {
   int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n) return;
+  if (li[p] < 0 || li[p] >= a.n_lhs || ri[p] < 0 || ri[p] >= a.n_rhs) {
+    keys[p] = 0;
+    atomicOr(bad, 1);
+    return;
+  }
   const int32_t *lrow = lc + li[p] * a.lncols;
   const int32_t *rrow = rc + ri[p] * a.rncols;
   uint64_t key = 0;
@@ -348,7 +366,7 @@ __global__ void seg_fill_kernel(const uint64_t *skeys, const int32_t *sperm, con
   const int64_t seg = excl[q] + flags[q] - 1;
   perm[q] = sperm[q];
   if (seg_ids) seg_ids[sperm[q]] = static_cast<int32_t>(seg);
-  if (flags[q]) {
+  if (flags[q] && seg < n_seg) {
     seg_offsets[seg] = static_cast<int32_t>(q);
     uint64_t key = skeys[q];
     for (int d = a.n - 1; d >= 0; --d) {
@@ -388,14 +406,14 @@ SegWs carve_seg(void *base, int64_t n) {
 }  // namespace
 }  // namespace ej
 
-extern "C" int ej_output_coords(const int32_t *lhs_coords, int32_t lhs_ncols,
-                                const int32_t *rhs_coords, int32_t rhs_ncols,
+extern "C" int ej_output_coords(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                                const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                                 const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
                                 int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
                                 int32_t *out, ej_stream_t stream_) {
   clear_error();
   AggSpec a;
-  EJ_TRY(check_agg(n_out, agg_src, agg_dim, lhs_ncols, rhs_ncols, nullptr, &a));
+  EJ_TRY(check_agg(n_out, agg_src, agg_dim, n_lhs, lhs_ncols, n_rhs, rhs_ncols, nullptr, &a));
   EJ_CHECK_ARG(n_pairs >= 0, "negative n_pairs");
   if (n_pairs == 0 || n_out == 0) return EJ_OK;
   EJ_CHECK_ARG(lhs_coords && rhs_coords && lhs_idx && rhs_idx && out, "null pointer argument");
@@ -412,8 +430,8 @@ extern "C" int ej_segment_workspace_size(int64_t n_pairs, size_t *bytes) {
   return EJ_OK;
 }
 
-extern "C" int ej_segment_count(const int32_t *lhs_coords, int32_t lhs_ncols,
-                                const int32_t *rhs_coords, int32_t rhs_ncols,
+extern "C" int ej_segment_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                                const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                                 const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
                                 int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
                                 const int64_t *radices, void *workspace, size_t workspace_bytes,
@@ -424,7 +442,7 @@ extern "C" int ej_segment_count(const int32_t *lhs_coords, int32_t lhs_ncols,
   EJ_CHECK_ARG(n_pairs >= 0 && n_pairs < (int64_t(1) << 31), "n_pairs must lie in [0, 2^31)");
   EJ_CHECK_ARG(radices || n_out == 0, "radices is null");
   AggSpec a;
-  EJ_TRY(check_agg(n_out, agg_src, agg_dim, lhs_ncols, rhs_ncols, radices, &a));
+  EJ_TRY(check_agg(n_out, agg_src, agg_dim, n_lhs, lhs_ncols, n_rhs, rhs_ncols, radices, &a));
   if (n_pairs == 0) {
     *n_segments = 0;
     return EJ_OK;
@@ -450,7 +468,7 @@ extern "C" int ej_segment_count(const int32_t *lhs_coords, int32_t lhs_ncols,
   EJ_HIP(hipMemcpyAsync(host, w.scalars, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   EJ_HIP(hipStreamSynchronize(stream));
   if (host[1] != 0) {
-    set_error("an output coordinate lies outside [0, radix)");
+    set_error("a pair index or an output coordinate lies outside [0, radix)");
     return EJ_E_RANGE;
   }
   *n_segments = host[0];

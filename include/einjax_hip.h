@@ -127,17 +127,21 @@ int ej_join_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                   int32_t order, void *workspace, size_t workspace_bytes, int64_t *n_pairs,
                   ej_stream_t stream);
 /* Writes the n_pairs matched pairs counted by ej_join_count.  capacity is
- * the length of lhs_idx / rhs_idx; capacity < n_pairs gives EJ_E_CAPACITY. */
+ * the length of lhs_idx / rhs_idx; capacity < n_pairs gives EJ_E_CAPACITY.
+ * Writes are clipped to the count stored in the workspace. */
 int ej_join_fill(int64_t n_lhs, int64_t n_rhs, int32_t n_keys, int32_t order,
                  const void *workspace, size_t workspace_bytes, int64_t n_pairs,
                  int64_t *lhs_idx, int64_t *rhs_idx, int64_t capacity, ej_stream_t stream);
 
 /* ---- output coordinates (reference: _compute_output_coords, :174-223) --- */
-/* out[p][d] = (agg_src[d] == 0 ? lhs : rhs).coords[idx[p]][agg_dim[d]] */
-int ej_output_coords(const int32_t *lhs_coords, int32_t lhs_ncols, const int32_t *rhs_coords,
-                     int32_t rhs_ncols, const int64_t *lhs_idx, const int64_t *rhs_idx,
-                     int64_t n_pairs, int32_t n_out, const int32_t *agg_src,
-                     const int32_t *agg_dim, int32_t *out, ej_stream_t stream);
+/* out[p][d] = (agg_src[d] == 0 ? lhs : rhs).coords[idx[p]][agg_dim[d]];
+ * a pair whose index lies outside [0, n_lhs) or [0, n_rhs) gets -1 in every
+ * column. */
+int ej_output_coords(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                     const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                     const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
+                     int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim, int32_t *out,
+                     ej_stream_t stream);
 
 /* ---- coordinate ranges -------------------------------------------------- */
 /* Per-column minimum and maximum of int32 coordinates [n, ncols]:
@@ -154,16 +158,21 @@ int ej_coords_range(const int32_t *coords, int64_t n, int32_t ncols, int32_t *lo
  * output coordinate in ascending lexicographic order (the reference's
  * sorted(coord_keys)); its pairs are perm[seg_offsets[u] .. seg_offsets[u+1])
  * in ascending pair index (the reference's accumulation order).
- * radices[d] bounds output dimension d.  Requires n_pairs < 2^31. */
+ * radices[d] bounds output dimension d.  Requires n_pairs < 2^31.  A pair
+ * index outside [0, n_lhs) / [0, n_rhs) or an output coordinate outside its
+ * radix gives EJ_E_RANGE. */
 int ej_segment_workspace_size(int64_t n_pairs, size_t *bytes);
-int ej_segment_count(const int32_t *lhs_coords, int32_t lhs_ncols, const int32_t *rhs_coords,
-                     int32_t rhs_ncols, const int64_t *lhs_idx, const int64_t *rhs_idx,
-                     int64_t n_pairs, int32_t n_out, const int32_t *agg_src,
-                     const int32_t *agg_dim, const int64_t *radices, void *workspace,
-                     size_t workspace_bytes, int64_t *n_segments, ej_stream_t stream);
+int ej_segment_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                     const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                     const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
+                     int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
+                     const int64_t *radices, void *workspace, size_t workspace_bytes,
+                     int64_t *n_segments, ej_stream_t stream);
 /* out_coords int32 [n_segments, n_out]; seg_offsets int32 [n_segments + 1];
  * perm int32 [n_pairs]; seg_ids int32 [n_pairs] (may be NULL): the segment of
- * each pair in pair order.  capacity bounds n_segments. */
+ * each pair in pair order.  capacity bounds n_segments.  n_pairs and
+ * n_segments must be the values of the matching ej_segment_count; writes are
+ * clipped to both. */
 int ej_segment_fill(int64_t n_pairs, int64_t n_segments, int32_t n_out, const int64_t *radices,
                     const void *workspace, size_t workspace_bytes, int32_t *out_coords,
                     int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids, int64_t capacity,
