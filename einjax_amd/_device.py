@@ -20,16 +20,23 @@ from ._lib import check, i32_array, i64_array
 _VALUE_DTYPES = {torch.float32: _lib.EJ_F32, torch.bfloat16: _lib.EJ_BF16}
 
 
+_gpu_checked = False
+
+
 def require_gpu() -> torch.device:
     """The current GPU; raises when none is visible (there is no CPU path)."""
-    if not torch.cuda.is_available():
-        raise RuntimeError("the sparse-einsum path runs on a ROCm GPU and none is visible")
-    _lib.load()
-    return torch.device("cuda", torch.cuda.current_device())
+    global _gpu_checked
+    if not _gpu_checked:
+        if not torch.cuda.is_available():
+            raise RuntimeError("the sparse-einsum path runs on a ROCm GPU and none is visible")
+        _lib.load()
+        _gpu_checked = True
+    return torch.device("cuda", torch._C._cuda_getDevice())
 
 
 def stream_ptr() -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    """hipStream_t of torch's current stream on the current device."""
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice()))
 
 
 def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:

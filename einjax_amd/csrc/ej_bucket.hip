@@ -105,6 +105,125 @@ __global__ __launch_bounds__(256) void tile_flags_kernel(const T *__restrict__ d
   if (threadIdx.x == 0) flags[t] = any ? 1 : 0;
 }
 
+// Vectorised forms for tiles whose rows are whole 16-byte vectors (vpr
+// vectors per row, vpr a power of two <= 256): thread t owns vector column
+// t % vpr and rows t / vpr, t / vpr + 256 / vpr, ...; a thread issues all its
+// loads before testing them, so the loads overlap.  MODE 0 = bf16, 1 = fp32,
+// 2 = fp64 input (fp32 tiles out).  ND2: rank-2 tensors (row offset = r *
+// row pitch); otherwise rows are decoded over the outer tile dimensions.
+template <int MODE>
+__device__ inline uint32_t nz_vec(uint4 x) {
+  if constexpr (MODE == 0) {
+    const uint32_t m = 0x7fff7fffu;
+    return (x.x & m) | (x.y & m) | (x.z & m) | (x.w & m);
+  } else if constexpr (MODE == 1) {
+    const uint32_t m = 0x7fffffffu;
+    return (x.x & m) | (x.y & m) | (x.z & m) | (x.w & m);
+  } else {
+    return (x.x | (x.y & 0x7fffffffu)) | (x.z | (x.w & 0x7fffffffu));
+  }
+}
+
+template <int MODE, bool ND2>
+__global__ __launch_bounds__(256) void tile_flags_vec_kernel(const unsigned char *__restrict__ dense,
+                                                             BucketGeom g, int vpr,
+                                                             int64_t row_pitch,
+                                                             int64_t *flags) {
+  constexpr int ESZ = MODE == 0 ? 2 : MODE == 1 ? 4 : 8;
+  constexpr int U = 8;
+  const int64_t t = blockIdx.x;
+  const unsigned char *base = dense + tile_origin(g, t) * ESZ;
+  const int c = threadIdx.x & (vpr - 1);
+  const int rstep = 256 / vpr;
+  uint32_t any = 0;
+  // The trip count is the same for every thread (the loop holds a barrier).
+  for (int64_t rb = 0; rb < g.rows; rb += static_cast<int64_t>(rstep) * U) {
+    const int64_t r0 = rb + threadIdx.x / vpr;
+    uint4 x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + static_cast<int64_t>(u) * rstep;
+      if (r < g.rows) {
+        const int64_t roff = ND2 ? r * row_pitch : row_offset(g, r) * ESZ;
+        x[u] = *reinterpret_cast<const uint4 *>(base + roff + c * 16);
+      } else {
+        x[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) any |= nz_vec<MODE>(x[u]);
+    if (__syncthreads_or(any != 0)) break;
+  }
+  any = __syncthreads_or(any != 0);
+  if (threadIdx.x == 0) flags[t] = any ? 1 : 0;
+}
+
+__device__ inline uint32_t zero_norm_bf16x2(uint32_t w) {
+  const uint32_t lo = (w & 0x7fffu) ? (w & 0xffffu) : 0u;
+  const uint32_t hi = (w & 0x7fff0000u) ? (w & 0xffff0000u) : 0u;
+  return lo | hi;
+}
+__device__ inline uint32_t zero_norm_f32(uint32_t w) { return (w & 0x7fffffffu) ? w : 0u; }
+
+template <int MODE, bool ND2>
+__global__ __launch_bounds__(256) void tile_copy_vec_kernel(const unsigned char *__restrict__ dense,
+                                                            BucketGeom g, int vpr,
+                                                            int64_t row_pitch,
+                                                            const int64_t *tile_of_slot,
+                                                            const int64_t *counted,
+                                                            int32_t *coords,
+                                                            unsigned char *__restrict__ values) {
+  constexpr int ESZ = MODE == 0 ? 2 : MODE == 1 ? 4 : 8;
+  constexpr int OSZ = MODE == 2 ? 4 : ESZ;  // stored element size
+  const int64_t slot = blockIdx.x;
+  if (slot >= *counted) return;
+  const int64_t t = tile_of_slot[slot];
+  if (threadIdx.x == 0) {
+    int64_t tt = t;
+    for (int d = g.nd - 1; d >= 0; --d) {
+      coords[slot * g.nd + d] = static_cast<int32_t>(tt % g.grid[d]);
+      tt /= g.grid[d];
+    }
+  }
+  const unsigned char *base = dense + tile_origin(g, t) * ESZ;
+  unsigned char *dst = values + slot * g.tile_elems * OSZ;
+  const int c = threadIdx.x & (vpr - 1);
+  const int rstep = 256 / vpr;
+  const int per_vec = 16 / ESZ;  // input elements per vector
+  for (int64_t r = threadIdx.x / vpr; r < g.rows; r += rstep) {
+    const int64_t roff = ND2 ? r * row_pitch : row_offset(g, r) * ESZ;
+    const uint4 x = *reinterpret_cast<const uint4 *>(base + roff + c * 16);
+    unsigned char *o = dst + (r * g.inner + static_cast<int64_t>(c) * per_vec) * OSZ;
+    if constexpr (MODE == 0) {
+      *reinterpret_cast<uint4 *>(o) = make_uint4(zero_norm_bf16x2(x.x), zero_norm_bf16x2(x.y),
+                                                 zero_norm_bf16x2(x.z), zero_norm_bf16x2(x.w));
+    } else if constexpr (MODE == 1) {
+      *reinterpret_cast<uint4 *>(o) = make_uint4(zero_norm_f32(x.x), zero_norm_f32(x.y),
+                                                 zero_norm_f32(x.z), zero_norm_f32(x.w));
+    } else {
+      const double d0 = __longlong_as_double(static_cast<long long>(x.x | (static_cast<uint64_t>(x.y) << 32)));
+      const double d1 = __longlong_as_double(static_cast<long long>(x.z | (static_cast<uint64_t>(x.w) << 32)));
+      float f0 = static_cast<float>(d0), f1 = static_cast<float>(d1);
+      if (f0 == 0.0f) f0 = 0.0f;
+      if (f1 == 0.0f) f1 = 0.0f;
+      *reinterpret_cast<float2 *>(o) = make_float2(f0, f1);
+    }
+  }
+}
+
+// Vector geometry: vectors per tile row, or 0 when the vector kernels do
+// not apply (row not a whole number of 16-byte vectors, misaligned pitch).
+int vec_shape(const BucketGeom &g, int esz, const void *dense, int64_t *row_pitch) {
+  const int64_t inner_b = g.inner * esz;
+  if (inner_b % 16 != 0 || (reinterpret_cast<uintptr_t>(dense) & 15u) != 0) return 0;
+  const int64_t vpr = inner_b / 16;
+  if (vpr > 256 || (vpr & (vpr - 1)) != 0) return 0;
+  const int64_t pitch = g.nd >= 2 ? g.dstride[g.nd - 2] * esz : 0;
+  if (pitch % 16 != 0) return 0;
+  *row_pitch = pitch;
+  return static_cast<int>(vpr);
+}
+
 __global__ void slot_map_kernel(const int64_t *flags, const int64_t *excl, int64_t n,
                                 int64_t *tile_of_slot) {
   int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -211,15 +330,29 @@ extern "C" int ej_bucket_dense_count(const void *dense, int32_t dtype, int32_t n
   BucketWs w = carve_bucket(workspace, g.n_tiles);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
-  if (dtype == EJ_F64)
-    hipLaunchKernelGGL(tile_flags_kernel<double>, dim3(static_cast<unsigned>(g.n_tiles)),
-                       dim3(256), 0, stream, static_cast<const double *>(dense), g, w.flags);
+  const int esz = dtype == EJ_F64 ? 8 : dtype == EJ_F32 ? 4 : 2;
+  const int mode = dtype == EJ_F64 ? 2 : dtype == EJ_F32 ? 1 : 0;
+  int64_t pitch = 0;
+  const int vpr = vec_shape(g, esz, dense, &pitch);
+  const dim3 grid(static_cast<unsigned>(g.n_tiles));
+  const unsigned char *db = static_cast<const unsigned char *>(dense);
+  if (vpr > 0) {
+#define EJ_FLAGS(M, N2) hipLaunchKernelGGL((tile_flags_vec_kernel<M, N2>), grid, dim3(256), 0, stream, db, g, vpr, pitch, w.flags)
+    if (g.nd == 2) {
+      if (mode == 0) EJ_FLAGS(0, true); else if (mode == 1) EJ_FLAGS(1, true); else EJ_FLAGS(2, true);
+    } else {
+      if (mode == 0) EJ_FLAGS(0, false); else if (mode == 1) EJ_FLAGS(1, false); else EJ_FLAGS(2, false);
+    }
+#undef EJ_FLAGS
+  } else if (dtype == EJ_F64)
+    hipLaunchKernelGGL(tile_flags_kernel<double>, grid, dim3(256), 0, stream,
+                       static_cast<const double *>(dense), g, w.flags);
   else if (dtype == EJ_F32)
-    hipLaunchKernelGGL(tile_flags_kernel<float>, dim3(static_cast<unsigned>(g.n_tiles)), dim3(256),
-                       0, stream, static_cast<const float *>(dense), g, w.flags);
+    hipLaunchKernelGGL(tile_flags_kernel<float>, grid, dim3(256), 0, stream,
+                       static_cast<const float *>(dense), g, w.flags);
   else
-    hipLaunchKernelGGL(tile_flags_kernel<uint16_t>, dim3(static_cast<unsigned>(g.n_tiles)),
-                       dim3(256), 0, stream, static_cast<const uint16_t *>(dense), g, w.flags);
+    hipLaunchKernelGGL(tile_flags_kernel<uint16_t>, grid, dim3(256), 0, stream,
+                       static_cast<const uint16_t *>(dense), g, w.flags);
   EJ_LAUNCH_CHECK();
   EJ_TRY(scan_exclusive_i64(w.flags, w.excl, g.n_tiles, w.scalars, w.scan_ws, stream));
   hipLaunchKernelGGL(slot_map_kernel, dim3(grid_for(g.n_tiles)), dim3(kBlock), 0, stream, w.flags,
@@ -251,18 +384,34 @@ extern "C" int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t nd
   EJ_CHECK_ARG(dense && coords && values, "null pointer argument");
   BucketWs w = carve_bucket(const_cast<void *>(workspace), g.n_tiles);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
-  if (dtype == EJ_F64)
-    hipLaunchKernelGGL((tile_copy_kernel<double, float>), dim3(static_cast<unsigned>(n_tiles)),
-                       dim3(256), 0, stream, static_cast<const double *>(dense), g,
-                       w.tile_of_slot, w.scalars, coords, static_cast<float *>(values));
+  const int esz = dtype == EJ_F64 ? 8 : dtype == EJ_F32 ? 4 : 2;
+  const int mode = dtype == EJ_F64 ? 2 : dtype == EJ_F32 ? 1 : 0;
+  int64_t pitch = 0;
+  const int vpr = vec_shape(g, esz, dense, &pitch);
+  const dim3 grid(static_cast<unsigned>(n_tiles));
+  const bool out_aligned = (reinterpret_cast<uintptr_t>(values) & 15u) == 0;
+  if (vpr > 0 && out_aligned) {
+    const unsigned char *db = static_cast<const unsigned char *>(dense);
+    unsigned char *vb = static_cast<unsigned char *>(values);
+#define EJ_COPY(M, N2) hipLaunchKernelGGL((tile_copy_vec_kernel<M, N2>), grid, dim3(256), 0, stream, db, g, vpr, pitch, w.tile_of_slot, w.scalars, coords, vb)
+    if (g.nd == 2) {
+      if (mode == 0) EJ_COPY(0, true); else if (mode == 1) EJ_COPY(1, true); else EJ_COPY(2, true);
+    } else {
+      if (mode == 0) EJ_COPY(0, false); else if (mode == 1) EJ_COPY(1, false); else EJ_COPY(2, false);
+    }
+#undef EJ_COPY
+  } else if (dtype == EJ_F64)
+    hipLaunchKernelGGL((tile_copy_kernel<double, float>), grid, dim3(256), 0, stream,
+                       static_cast<const double *>(dense), g, w.tile_of_slot, w.scalars, coords,
+                       static_cast<float *>(values));
   else if (dtype == EJ_F32)
-    hipLaunchKernelGGL((tile_copy_kernel<float, float>), dim3(static_cast<unsigned>(n_tiles)),
-                       dim3(256), 0, stream, static_cast<const float *>(dense), g,
-                       w.tile_of_slot, w.scalars, coords, static_cast<float *>(values));
+    hipLaunchKernelGGL((tile_copy_kernel<float, float>), grid, dim3(256), 0, stream,
+                       static_cast<const float *>(dense), g, w.tile_of_slot, w.scalars, coords,
+                       static_cast<float *>(values));
   else
-    hipLaunchKernelGGL((tile_copy_kernel<uint16_t, uint16_t>), dim3(static_cast<unsigned>(n_tiles)),
-                       dim3(256), 0, stream, static_cast<const uint16_t *>(dense), g,
-                       w.tile_of_slot, w.scalars, coords, static_cast<uint16_t *>(values));
+    hipLaunchKernelGGL((tile_copy_kernel<uint16_t, uint16_t>), grid, dim3(256), 0, stream,
+                       static_cast<const uint16_t *>(dense), g, w.tile_of_slot, w.scalars, coords,
+                       static_cast<uint16_t *>(values));
   EJ_LAUNCH_CHECK();
   return EJ_OK;
 }

@@ -603,6 +603,9 @@ __device__ inline void lgkm_wait_all(i32x4_t (&v)[N]) {
 #ifndef EJ_DMA_STAGES_64
 #define EJ_DMA_STAGES_64 4
 #endif
+#ifndef EJ_DMA_BK_128
+#define EJ_DMA_BK_128 64
+#endif
 #ifndef EJ_USE_DMA_GEMM
 #define EJ_USE_DMA_GEMM 1
 #endif
@@ -635,6 +638,13 @@ template <int NS, int LPS>
 __device__ inline void wait_stage(int later) {
   // later = number of stages issued after the one about to be consumed;
   // each stage is LPS load instructions per wave.
+  static_assert(NS >= 2 && NS <= 6, "ring depth");
+  if constexpr (NS >= 6) {
+    if (later >= 4) { wait_vmcnt<4 * LPS>(); return; }
+  }
+  if constexpr (NS >= 5) {
+    if (later >= 3) { wait_vmcnt<3 * LPS>(); return; }
+  }
   if constexpr (NS >= 4) {
     if (later >= 2) { wait_vmcnt<2 * LPS>(); return; }
   }
@@ -644,14 +654,27 @@ __device__ inline void wait_stage(int later) {
   wait_vmcnt<0>();
 }
 
-template <int BM, int BN, int NS>
+// XOR swizzles of 16-byte chunks (see the kernel comment).
+template <int CHA>
+__device__ inline int swz_a(int row) {
+  if constexpr (CHA == 8) return (row & 7) ^ ((row >> 3) & 7);
+  else return (row >> 2) & 3;
+}
+template <int CHB>
+__device__ inline int swz_b(int krow) {
+  if constexpr (CHB == 16) return (2 * (krow & 3)) ^ (8 * ((krow >> 3) & 1));
+  else return 2 * (krow & 3);
+}
+
+template <int BM, int BN, int BK, int NS>
 __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__restrict__ A,
                                                             const uint16_t *__restrict__ B,
                                                             float *__restrict__ C, PairSrc src,
                                                             GemmGeom g) {
 #if defined(__HIP_DEVICE_COMPILE__)  // device-only body (LDS address-space casts, gfx950 asm)
-  constexpr int BK = 64;                       // k per stage (128 B per A row)
-  constexpr int A_BYTES = BM * BK * 2;         // [BM][64] bf16
+  constexpr int A_ROWB = BK * 2;               // bytes per A row of a stage
+  constexpr int CHA = A_ROWB / 16;             // 16-byte chunks per A row
+  constexpr int A_BYTES = BM * A_ROWB;         // [BM][BK] bf16
   constexpr int B_ROWB = BN * 2;               // bytes per k-row of B
   constexpr int CHB = B_ROWB / 16;             // 16-byte chunks per B k-row
   constexpr int B_BYTES = BK * B_ROWB;
@@ -660,7 +683,8 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
   constexpr int B_BLOCKS = B_BYTES / 1024;
   static_assert(A_BLOCKS % 4 == 0 && B_BLOCKS % 4 == 0, "blocks split over 4 waves");
   constexpr int LPS = A_BLOCKS / 4 + B_BLOCKS / 4;  // load instructions per wave per stage
-  static_assert(NS >= 2 && NS <= 4 && 2 * LPS < 64, "ring depth / vmcnt range");
+  static_assert(NS >= 2 && NS <= 6 && (NS - 2) * LPS < 64, "ring depth / vmcnt range");
+  static_assert(BK == 32 || BK == 64, "stage depth");
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int FM = WM / 16, FN = WN / 16;
   __shared__ __align__(1024) unsigned char ring[NS * SLOT];
@@ -686,15 +710,15 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 #pragma unroll
   for (int v = 0; v < A_BLOCKS / 4; ++v) {
     const int blk = v * 4 + wave;
-    const int row = blk * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ ((row & 7) ^ ((row >> 3) & 7));
+    const int row = blk * (1024 / A_ROWB) + lane / CHA;
+    const int c = (lane % CHA) ^ swz_a<CHA>(row);
     a_src[v] = row * g.a_sm + c * 8;
   }
 #pragma unroll
   for (int v = 0; v < B_BLOCKS / 4; ++v) {
     const int blk = v * 4 + wave;
     const int krow = blk * (64 / CHB) + lane / CHB;
-    const int j = (lane % CHB) ^ (2 * (krow & 3));
+    const int j = (lane % CHB) ^ swz_b<CHB>(krow);
     b_src[v] = krow * g.b_sk + j * 8;
   }
   const int64_t a_off0 = bi * g.a_sb + mb * BM * g.a_sm;
@@ -752,8 +776,8 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const int row = wm * WM + i * 16 + (lane & 15);
-        const int phys = ch ^ ((row & 7) ^ ((row >> 3) & 7));
-        af[i] = *reinterpret_cast<const bf16x8_t *>(as + row * 128 + phys * 16);
+        const int phys = ch ^ swz_a<CHA>(row);
+        af[i] = *reinterpret_cast<const bf16x8_t *>(as + row * A_ROWB + phys * 16);
       }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -764,7 +788,7 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const int krow = ks * 32 + (lane >> 4) * 8 + hh * 4 + t;
-          const int phys = jc ^ (2 * (krow & 3));
+          const int phys = jc ^ swz_b<CHB>(krow);
           h[hh] = ds_read_tr16_b64(bs_lds + krow * B_ROWB + phys * 16 + (qq & 1) * 8);
         }
         bq[j] = i32x4_t{h[0][0], h[0][1], h[1][0], h[1][1]};
@@ -928,10 +952,10 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
     const uint16_t *a = static_cast<const uint16_t *>(A);
     const uint16_t *b = static_cast<const uint16_t *>(B);
     if (bm == 128)
-      hipLaunchKernelGGL((tile_gemm_dma_kernel<128, 128, EJ_DMA_STAGES_128>),
+      hipLaunchKernelGGL((tile_gemm_dma_kernel<128, 128, EJ_DMA_BK_128, EJ_DMA_STAGES_128>),
                          dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, a, b, C, src, g);
     else
-      hipLaunchKernelGGL((tile_gemm_dma_kernel<64, 64, EJ_DMA_STAGES_64>),
+      hipLaunchKernelGGL((tile_gemm_dma_kernel<64, 64, 64, EJ_DMA_STAGES_64>),
                          dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, a, b, C, src, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
