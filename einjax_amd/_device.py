@@ -4,12 +4,14 @@ Every function takes and returns torch tensors resident on the current
 GPU; torch supplies the memory and the current stream, all arithmetic runs
 in the library's kernels.  Sizes that depend on the data (pairs, segments,
 tiles) come back through the library's *_count calls, one host
-synchronisation each.
+synchronisation each, or, in queued_segment_einsum, through pinned host
+memory read at an event while the einsum is already queued.
 """
 
 from __future__ import annotations
 
 import ctypes
+import threading
 from math import prod
 
 import torch
@@ -195,6 +197,101 @@ def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_off
                                         ptr(lhs_idx), ptr(rhs_idx), ptr(perm), ptr(seg_offsets),
                                         U, ptr(out), stream_ptr()), "ej_segment_einsum")
     return out
+
+
+class _Counts(threading.local):
+    """Per-thread pinned count buffer [P, join range flag, U, plan range
+    flag] and the event that marks when the queued counts have landed."""
+
+    buf: torch.Tensor | None = None
+    event: torch.cuda.Event | None = None
+
+
+_counts = _Counts()
+
+
+def _count_buffer() -> tuple[torch.Tensor, torch.cuda.Event]:
+    if _counts.buf is None:
+        _counts.buf = torch.zeros(4, dtype=torch.int64, pin_memory=True)
+        _counts.event = torch.cuda.Event()
+    return _counts.buf, _counts.event
+
+
+def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys,
+                          agg_radices, desc, lhs_values, rhs_values, pair_bound: int):
+    """Join, segment plan and fused segment einsum queued back to back on the
+    current stream, with the pair count bounded by pair_bound instead of
+    read first.  The host waits only for an event recorded after the plan's
+    count (the einsum is already queued behind it), then checks the counts.
+
+    Returns (status, result).  status "ok": result = (P, coords [U, n_out],
+    seg_offsets, perm, values [U, *out_tile], li, ri), views clipped to the
+    counts.  "bound": P exceeded pair_bound (result[0] = P); "range": a
+    coordinate fell outside its radix.  Either way the caller runs the exact
+    path; every kernel clips its work to the device-side counts, so an
+    exceeded bound costs a rerun, never a stray access."""
+    lib = _lib.load()
+    dev = lhs_coords.device
+    code = value_code(lhs_values)
+    if rhs_values.dtype != lhs_values.dtype:
+        raise TypeError("both operands must have the same value dtype")
+    n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
+    nk = len(join_keys)
+    cap_p = max(int(pair_bound), 1)
+    cap_u = max(1, min(cap_p, prod(agg_radices)))
+    buf, event = _count_buffer()
+    base = buf.data_ptr()
+    stream = stream_ptr()
+    order = _lib.EJ_ORDER_PROBE
+
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_join_workspace_size(n_l, n_r, order, ctypes.byref(nbytes)),
+          "ej_join_workspace_size")
+    jws = workspace(nbytes.value, dev)
+    check(lib.ej_join_count_async(
+        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
+        i32_array([k[0] for k in join_keys]), i32_array([k[1] for k in join_keys]),
+        i64_array(join_radices), order, ptr(jws), jws.numel(), ctypes.c_void_p(base), stream),
+        "ej_join_count_async")
+    li = torch.empty(cap_p, dtype=torch.int64, device=dev)
+    ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
+    check(lib.ej_join_fill(n_l, n_r, nk, order, ptr(jws), jws.numel(), cap_p, ptr(li), ptr(ri),
+                           cap_p, stream), "ej_join_fill")
+
+    n_out = len(agg_keys)
+    src = i32_array([s for s, _ in agg_keys])
+    dim = i32_array([d for _, d in agg_keys])
+    rad = i64_array(agg_radices)
+    check(lib.ej_segment_workspace_size(cap_p, ctypes.byref(nbytes)),
+          "ej_segment_workspace_size")
+    sws = workspace(nbytes.value, dev)
+    check(lib.ej_segment_count_async(
+        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1],
+        ptr(li), ptr(ri), cap_p, ptr(jws), n_out, src, dim, rad, ptr(sws), sws.numel(),
+        ctypes.c_void_p(base + 16), stream), "ej_segment_count_async")
+    event.record()
+    coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
+    offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
+    check(lib.ej_segment_fill_async(cap_p, n_out, rad, ptr(sws), sws.numel(), ptr(coords),
+                                    ptr(offsets), ptr(perm), None, cap_u, stream),
+          "ej_segment_fill_async")
+    out = torch.empty((cap_u, *_out_tile(desc)), dtype=torch.float32, device=dev)
+    check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
+                                      lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
+                                      ptr(perm), ptr(offsets), cap_u, ptr(sws), ptr(out), stream),
+          "ej_segment_einsum_async")
+    event.synchronize()
+    P, bad_join, U, bad_plan = (int(x) for x in buf.tolist())
+    if bad_join:
+        return "range", None
+    if P > cap_p:
+        return "bound", (P,)
+    if bad_plan:
+        return "range", None
+    if U > cap_u:  # cannot happen: U <= min(P, prod(agg_radices))
+        raise RuntimeError(f"segment count {U} exceeds its bound {cap_u}")
+    return "ok", (P, coords[:U], offsets[:U + 1], perm[:P], out[:U], li[:P], ri[:P])
 
 
 def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:

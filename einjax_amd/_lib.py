@@ -63,6 +63,8 @@ SIGNATURES = {
     "ej_join_workspace_size": (_i32, [_i64, _i64, _i32, _P_sz]),
     "ej_join_count": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32, _P_i64, _i32,
                              _vp, _sz, _P_i64, _vp]),
+    "ej_join_count_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32,
+                                   _P_i64, _i32, _vp, _sz, _vp, _vp]),
     "ej_join_fill": (_i32, [_i64, _i64, _i32, _i32, _vp, _sz, _i64, _vp, _vp, _i64, _vp]),
     "ej_output_coords": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i64, _i32, _P_i32,
                                 _P_i32, _vp, _vp]),
@@ -71,11 +73,17 @@ SIGNATURES = {
                                 _P_i32, _P_i64, _vp, _sz, _P_i64, _vp]),
     "ej_segment_fill": (_i32, [_i64, _i64, _i32, _P_i64, _vp, _sz, _vp, _vp, _vp, _vp, _i64,
                                _vp]),
+    "ej_segment_count_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i64, _vp,
+                                      _i32, _P_i32, _P_i32, _P_i64, _vp, _sz, _vp, _vp]),
+    "ej_segment_fill_async": (_i32, [_i64, _i32, _P_i64, _vp, _sz, _vp, _vp, _vp, _vp, _i64,
+                                     _vp]),
     "ej_gather_tiles": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "ej_pair_einsum": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64, _vp, _vp,
                               _i64, _vp, _vp]),
     "ej_segment_einsum": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64, _vp,
                                  _vp, _vp, _vp, _i64, _vp, _vp]),
+    "ej_segment_einsum_async": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64,
+                                       _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "ej_segment_sum": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _vp]),
     "ej_bucket_workspace_size": (_i32, [_i32, _P_i64, _P_i64, _P_sz]),
     "ej_bucket_dense_count": (_i32, [_vp, _i32, _i32, _P_i64, _P_i64, _vp, _sz, _P_i64, _vp]),

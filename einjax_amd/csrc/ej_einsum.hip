@@ -235,7 +235,13 @@ struct PairSrc {
   const int32_t *perm;         // null: identity
   const int32_t *seg_off;      // null: one pair per segment
   int64_t n_a_tiles, n_b_tiles;
+  const int64_t *n_live;       // non-null: segments >= *n_live are skipped (grid is a bound)
 };
+
+// Whether the workgroup's segment lies beyond the device-side segment count.
+__device__ inline bool seg_dead(const PairSrc &s, int64_t seg) {
+  return s.n_live && seg >= *s.n_live;
+}
 
 __device__ inline void seg_range(const PairSrc &s, int64_t seg, int64_t *q0, int64_t *q1) {
   if (s.seg_off) {
@@ -448,6 +454,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
   lb /= g.mblocks;
   const int64_t bi = lb % g.batch;
   const int64_t seg = lb / g.batch;
+  if (seg_dead(src, seg)) return;
 
   int64_t q0, q1;
   seg_range(src, seg, &q0, &q1);
@@ -700,6 +707,7 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
   lb /= g.mblocks;
   const int64_t bi = lb % g.batch;
   const int64_t seg = lb / g.batch;
+  if (seg_dead(src, seg)) return;
   int64_t q0, q1;
   seg_range(src, seg, &q0, &q1);
   const int nkc = static_cast<int>(g.k / BK);
@@ -836,7 +844,7 @@ __global__ __launch_bounds__(256) void generic_einsum_kernel(const T *__restrict
                                                              GenDesc d) {
   const int64_t seg = blockIdx.x / d.eblocks;
   const int64_t e = (blockIdx.x % d.eblocks) * 256 + threadIdx.x;
-  if (e >= d.c_elems) return;
+  if (e >= d.c_elems || seg_dead(src, seg)) return;
   int64_t rem = e, aoff = 0, boff = 0;
   for (int i = d.n_out - 1; i >= 0; --i) {
     int64_t x = rem % d.out_ext[i];
@@ -1133,7 +1141,7 @@ extern "C" int ej_pair_einsum(const ej_einsum_desc *desc, int32_t dtype, const v
                               const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
                               float *out, ej_stream_t stream) {
   clear_error();
-  PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles};
+  PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles, nullptr};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_pairs, out, as_stream(stream));
 }
 
@@ -1145,8 +1153,23 @@ extern "C" int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, cons
                                  ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || n_segments == 0, "seg_offsets is null");
-  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles};
+  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, nullptr};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_segments, out,
+                       as_stream(stream));
+}
+
+extern "C" int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype,
+                                       const void *lhs_values, const void *rhs_values,
+                                       int64_t n_lhs_tiles, int64_t n_rhs_tiles,
+                                       const int64_t *lhs_idx, const int64_t *rhs_idx,
+                                       const int32_t *perm, const int32_t *seg_offsets,
+                                       int64_t max_segments, const int64_t *n_segments_dev,
+                                       float *out, ej_stream_t stream) {
+  clear_error();
+  EJ_CHECK_ARG(seg_offsets || max_segments == 0, "seg_offsets is null");
+  EJ_CHECK_ARG(n_segments_dev, "n_segments_dev is null");
+  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, n_segments_dev};
+  return einsum_common(desc, dtype, lhs_values, rhs_values, src, max_segments, out,
                        as_stream(stream));
 }
 

@@ -73,17 +73,21 @@ int key_bits(const int64_t *radix, int n, int *bits);
 
 // ---- device-wide primitives (ej_scan_sort.hip) ----------------------------
 // Exclusive scan of n int64 values; total (device scalar) may be null.
+// n_dev (optional): device-side count clipping n.
 size_t scan_workspace_bytes(int64_t n);
 int scan_exclusive_i64(const int64_t *in, int64_t *out, int64_t n, int64_t *total,
-                       void *ws, hipStream_t stream);
+                       void *ws, hipStream_t stream, const int64_t *n_dev = nullptr);
 
 // Stable LSD radix sort of (key, value) pairs on the low `bits` key bits.
-// The result ends in keys/vals; keys_alt/vals_alt are scratch of length n.
+// The input lies in keys/vals, or in keys_alt/vals_alt when input_in_alt;
+// the result always ends in keys/vals.  A caller that packs its input into
+// the alt buffers when radix_passes(bits) is odd saves the final copy.
 size_t sort_workspace_bytes(int64_t n);
+int radix_passes(int bits);
+// n_dev (optional): device-side count clipping n (keys beyond it stay put).
 int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *vals_alt,
-                   int64_t n, int bits, void *ws, hipStream_t stream);
-
-int fill_iota_i32(int32_t *v, int64_t n, hipStream_t stream);
+                   int64_t n, int bits, void *ws, hipStream_t stream,
+                   bool input_in_alt = false, const int64_t *n_dev = nullptr);
 
 // ---- device helpers --------------------------------------------------------
 __device__ inline uint64_t pack_key(const int32_t *row, const KeySpec &ks, int *bad) {
@@ -100,6 +104,138 @@ __device__ inline uint64_t pack_key(const int32_t *row, const KeySpec &ks, int *
 }
 
 constexpr int kBlock = 256;   // threads per block for the integer kernels
+
+// Live length of a sequence with host-side bound cap whose device-side count,
+// if dev is non-null, is *dev: min(cap, max(*dev, 0)).  Kernels launched on a
+// bound before the exact count reaches the host clip their work with it.
+__device__ inline int64_t live_count(int64_t cap, const int64_t *dev) {
+  if (!dev) return cap;
+  const int64_t v = *dev;
+  return v < 0 ? 0 : (v < cap ? v : cap);
+}
+
+// ---- block-level scans ------------------------------------------------------
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ inline int64_t wave_inclusive_sum(int64_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int64_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Exclusive prefix of v across a block of NT threads; *block_total receives
+// the sum.  Every thread of the block must call it.
+template <int NT>
+__device__ inline int64_t block_exclusive_sum(int64_t v, int64_t *block_total) {
+  __shared__ int64_t wave_tot[NT / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t inc = wave_inclusive_sum(v);
+  if (lane == 63) wave_tot[wave] = inc;
+  __syncthreads();
+  int64_t wave_off = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    int64_t t = wave_tot[w];
+    if (w < wave) wave_off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *block_total = tot;
+  return wave_off + inc - v;
+}
+
+// ---- two-launch exclusive scan ---------------------------------------------
+// Sequences of up to kFastScanBlocks tiles of kScanTile values are scanned by
+// two launches: scan_reduce (each block sums its tile) and scan_apply (each
+// block adds up the sums of the blocks before it, scans its tile and writes
+// the prefixes).  Values come from a functor load(i) -> int64 so callers can
+// generate them (flags from sorted keys, say) instead of materialising them;
+// emit(i, value) runs once per index in scan_apply.
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kBlock * kScanItems;
+constexpr int64_t kFastScanBlocks = kBlock;
+constexpr int64_t kFastScanMax = kFastScanBlocks * kScanTile;
+
+template <class Load>
+__global__ __launch_bounds__(kBlock) void scan_reduce_kernel(Load load, int64_t n,
+                                                             const int64_t *n_dev,
+                                                             int64_t *block_sums) {
+  n = live_count(n, n_dev);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  int64_t s = 0;
+#pragma unroll
+  for (int r = 0; r < kScanItems; ++r) {
+    const int64_t i = base + r * kBlock + threadIdx.x;
+    s += i < n ? load(i) : 0;
+  }
+  int64_t tot;
+  block_exclusive_sum<kBlock>(s, &tot);
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = tot;
+}
+
+template <class Load, class Emit>
+__global__ __launch_bounds__(kBlock) void scan_apply_kernel(Load load, Emit emit, int64_t n,
+                                                            const int64_t *n_dev,
+                                                            const int64_t *block_sums,
+                                                            int64_t nblocks, int64_t *out,
+                                                            int64_t *total) {
+  n = live_count(n, n_dev);
+  // Offset of this block: sum of the block sums before it (nblocks <= kBlock).
+  const int64_t bs = threadIdx.x < nblocks ? block_sums[threadIdx.x] : 0;
+  int64_t offset;
+  block_exclusive_sum<kBlock>(threadIdx.x < blockIdx.x ? bs : 0, &offset);
+  if (blockIdx.x == 0 && total) {
+    int64_t grand;
+    block_exclusive_sum<kBlock>(bs, &grand);
+    if (threadIdx.x == 0) *total = grand;
+  }
+  // Blocked layout inside the tile: thread t owns kScanItems consecutive values.
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
+                       static_cast<int64_t>(threadIdx.x) * kScanItems;
+  int64_t v[kScanItems];
+  int64_t s = 0;
+#pragma unroll
+  for (int r = 0; r < kScanItems; ++r) {
+    v[r] = base + r < n ? load(base + r) : 0;
+    s += v[r];
+  }
+  int64_t tile_tot;
+  int64_t run = offset + block_exclusive_sum<kBlock>(s, &tile_tot);
+#pragma unroll
+  for (int r = 0; r < kScanItems; ++r) {
+    if (base + r < n) {
+      out[base + r] = run;
+      emit(base + r, v[r]);
+    }
+    run += v[r];
+  }
+}
+
+struct LoadI64 {
+  const int64_t *in;
+  __device__ int64_t operator()(int64_t i) const { return in[i]; }
+};
+
+struct NoEmit {
+  __device__ void operator()(int64_t, int64_t) const {}
+};
+
+// Launches the two kernels for n in [1, kFastScanMax] (n_dev: optional
+// device-side count clipping n); block_sums holds ceil(n / kScanTile) values.
+template <class Load, class Emit>
+inline void launch_fast_scan(Load load, Emit emit, int64_t n, const int64_t *n_dev,
+                             int64_t *block_sums, int64_t *out, int64_t *total,
+                             hipStream_t stream) {
+  const int64_t nblocks = (n + kScanTile - 1) / kScanTile;
+  hipLaunchKernelGGL(scan_reduce_kernel<Load>, dim3(static_cast<unsigned>(nblocks)),
+                     dim3(kBlock), 0, stream, load, n, n_dev, block_sums);
+  hipLaunchKernelGGL((scan_apply_kernel<Load, Emit>), dim3(static_cast<unsigned>(nblocks)),
+                     dim3(kBlock), 0, stream, load, emit, n, n_dev, block_sums, nblocks, out,
+                     total);
+}
 
 inline unsigned grid_for(int64_t n, int per_block = kBlock) {
   int64_t g = ceil_div(n, per_block);

@@ -19,12 +19,22 @@ namespace ej {
 
 namespace {
 
-__global__ void pack_keys_kernel(const int32_t *coords, int64_t n, KeySpec ks, uint64_t *keys,
-                                 int *bad) {
+// Packs the join keys of both relations in one launch: threads [0, n_lhs)
+// take lhs rows, the rest rhs rows.  A non-null perm gets the identity
+// permutation the stable sort starts from.
+__global__ void pack_keys_kernel(const int32_t *lc, int64_t n_lhs, KeySpec lks, uint64_t *lkeys,
+                                 int32_t *lperm, const int32_t *rc, int64_t n_rhs, KeySpec rks,
+                                 uint64_t *rkeys, int32_t *rperm, int *bad) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
   int b = 0;
-  keys[i] = pack_key(coords + i * ks.ncols, ks, &b);
+  if (i < n_lhs) {
+    lkeys[i] = pack_key(lc + i * lks.ncols, lks, &b);
+    if (lperm) lperm[i] = static_cast<int32_t>(i);
+  } else if (i - n_lhs < n_rhs) {
+    const int64_t j = i - n_lhs;
+    rkeys[j] = pack_key(rc + j * rks.ncols, rks, &b);
+    if (rperm) rperm[j] = static_cast<int32_t>(j);
+  }
   if (b) atomicOr(bad, 1);
 }
 
@@ -66,6 +76,67 @@ __global__ void probe_count_kernel(const uint64_t *probe_keys, int64_t n_probe,
   int64_t hi = upper_bound_u64(build_sorted, n_build, k);
   lo_out[j] = lo;
   cnt_out[j] = hi - lo;
+}
+
+// Probe count and scan in one workgroup, for build sides that fit in LDS:
+// lo_out[j] = first build position equal to probe key j, offs = exclusive
+// scan of the equal-range sizes, *total = P.  The build keys are staged in
+// LDS and each thread runs kProbeBatch branch-free equal-range searches side
+// by side (fixed trip count ceil(log2 n_build)), so their LDS reads overlap.
+constexpr int kProbeThreads = 1024;
+constexpr int kProbeLdsKeys = 8192;
+constexpr int64_t kProbeSmallMax = 8192;
+constexpr int kProbeBatch = 4;
+
+__global__ __launch_bounds__(kProbeThreads) void probe_scan_small_kernel(
+    const uint64_t *__restrict__ probe_keys, int64_t n_probe,
+    const uint64_t *__restrict__ build_sorted, int n_build, int64_t *__restrict__ lo_out,
+    int64_t *__restrict__ offs, int64_t *__restrict__ total) {
+  __shared__ uint64_t bk[kProbeLdsKeys];
+  for (int i = threadIdx.x; i < n_build; i += kProbeThreads) bk[i] = build_sorted[i];
+  __syncthreads();
+  const int64_t c = (n_probe + kProbeThreads - 1) / kProbeThreads;
+  const int64_t lo = min(n_probe, static_cast<int64_t>(threadIdx.x) * c);
+  const int64_t hi = min(n_probe, lo + c);
+  int64_t s = 0;
+  for (int64_t j0 = lo; j0 < hi; j0 += kProbeBatch) {
+    uint64_t k[kProbeBatch];
+    int lb[kProbeBatch], ub[kProbeBatch];
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      k[u] = j0 + u < hi ? probe_keys[j0 + u] : 0;
+      lb[u] = 0;
+      ub[u] = 0;
+    }
+    // Invariant: the answer lies in [base, base + len]; base + len <= n_build.
+    for (int len = n_build; len > 1;) {
+      const int half = len >> 1;
+#pragma unroll
+      for (int u = 0; u < kProbeBatch; ++u) {
+        lb[u] += bk[lb[u] + half] < k[u] ? half : 0;
+        ub[u] += bk[ub[u] + half] <= k[u] ? half : 0;
+      }
+      len -= half;
+    }
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      lb[u] += bk[lb[u]] < k[u] ? 1 : 0;
+      ub[u] += bk[ub[u]] <= k[u] ? 1 : 0;
+      if (j0 + u < hi) {
+        lo_out[j0 + u] = lb[u];
+        offs[j0 + u] = ub[u] - lb[u];
+        s += ub[u] - lb[u];
+      }
+    }
+  }
+  int64_t tot;
+  int64_t run = block_exclusive_sum<kProbeThreads>(s, &tot);
+  for (int64_t j = lo; j < hi; ++j) {
+    const int64_t v = offs[j];
+    offs[j] = run;
+    run += v;
+  }
+  if (threadIdx.x == 0) *total = tot;
 }
 
 // EJ_ORDER_PROBE fill: pair q belongs to rhs row j = owner_of(offs, q).
@@ -168,14 +239,19 @@ extern "C" int ej_join_workspace_size(int64_t n_lhs, int64_t n_rhs, int32_t orde
   return EJ_OK;
 }
 
-extern "C" int ej_join_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
-                             const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
-                             int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
-                             const int64_t *radices, int32_t order, void *workspace,
-                             size_t workspace_bytes, int64_t *n_pairs, ej_stream_t stream_) {
-  clear_error();
-  hipStream_t stream = as_stream(stream_);
-  EJ_CHECK_ARG(n_pairs, "n_pairs is null");
+namespace ej {
+namespace {
+
+// Enqueues the join count.  *host_known >= 0 on return: the pair count is
+// known on the host (cross product or an empty side) and nothing was
+// enqueued; otherwise (-1) the count and a range flag land in w.scalars[0..1].
+int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                       const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                       int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                       const int64_t *radices, int32_t order, void *workspace,
+                       size_t workspace_bytes, int64_t *host_known, int64_t **dev_scalars,
+                       hipStream_t stream) {
+  *host_known = -1;
   EJ_CHECK_ARG(n_lhs >= 0 && n_rhs >= 0, "negative relation size");
   EJ_CHECK_ARG(n_lhs < (int64_t(1) << 31) && n_rhs < (int64_t(1) << 31),
                "relations are limited to 2^31 - 1 tiles");
@@ -191,7 +267,7 @@ extern "C" int ej_join_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t l
       set_error("cross product too large");
       return EJ_E_UNSUPPORTED;
     }
-    *n_pairs = static_cast<int64_t>(p);
+    *host_known = static_cast<int64_t>(p);
     return EJ_OK;
   }
   EJ_CHECK_ARG(lhs_coords && rhs_coords, "coordinate pointer is null");
@@ -200,41 +276,98 @@ extern "C" int ej_join_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t l
   JoinWs w = carve_join(workspace, n_lhs, n_rhs, order);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
+  *dev_scalars = w.scalars;
 
   EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
   int *bad = reinterpret_cast<int *>(w.scalars + 1);
-  hipLaunchKernelGGL(pack_keys_kernel, dim3(grid_for(n_lhs)), dim3(kBlock), 0, stream, lhs_coords,
-                     n_lhs, lks, w.lkeys, bad);
+  // Sorted sides are packed where an odd number of radix passes leaves them
+  // in the primary buffers.
+  const bool sort_rhs = order == EJ_ORDER_SORTED;
+  const bool l_alt = n_lhs > 1 && (radix_passes(bits) & 1);
+  const bool r_alt = sort_rhs && n_rhs > 1 && (radix_passes(bits) & 1);
+  hipLaunchKernelGGL(pack_keys_kernel, dim3(grid_for(n_lhs + n_rhs)), dim3(kBlock), 0, stream,
+                     lhs_coords, n_lhs, lks, l_alt ? w.lkeys_alt : w.lkeys,
+                     l_alt ? w.lperm_alt : w.lperm, rhs_coords, n_rhs, rks,
+                     r_alt ? w.rkeys_alt : w.rkeys,
+                     sort_rhs ? (r_alt ? w.rperm_alt : w.rperm) : nullptr, bad);
   EJ_LAUNCH_CHECK();
-  hipLaunchKernelGGL(pack_keys_kernel, dim3(grid_for(n_rhs)), dim3(kBlock), 0, stream, rhs_coords,
-                     n_rhs, rks, w.rkeys, bad);
-  EJ_LAUNCH_CHECK();
-  EJ_TRY(fill_iota_i32(w.lperm, n_lhs, stream));
   EJ_TRY(sort_pairs_u64(w.lkeys, w.lperm, w.lkeys_alt, w.lperm_alt, n_lhs, bits, w.sort_ws,
-                        stream));
-  int64_t n_probe;
-  if (order == EJ_ORDER_PROBE) {
-    n_probe = n_rhs;
-    hipLaunchKernelGGL(probe_count_kernel, dim3(grid_for(n_rhs)), dim3(kBlock), 0, stream,
-                       w.rkeys, n_rhs, w.lkeys, n_lhs, w.lo, w.cnt);
-  } else {
-    EJ_TRY(fill_iota_i32(w.rperm, n_rhs, stream));
+                        stream, l_alt));
+  if (sort_rhs)
     EJ_TRY(sort_pairs_u64(w.rkeys, w.rperm, w.rkeys_alt, w.rperm_alt, n_rhs, bits, w.sort_ws,
-                          stream));
-    n_probe = n_lhs;
-    hipLaunchKernelGGL(probe_count_kernel, dim3(grid_for(n_lhs)), dim3(kBlock), 0, stream,
-                       w.lkeys, n_lhs, w.rkeys, n_rhs, w.lo, w.cnt);
+                          stream, r_alt));
+  const int64_t n_probe = sort_rhs ? n_lhs : n_rhs;
+  const int64_t n_build = sort_rhs ? n_rhs : n_lhs;
+  const uint64_t *probe = sort_rhs ? w.lkeys : w.rkeys;
+  const uint64_t *build = sort_rhs ? w.rkeys : w.lkeys;
+  if (n_probe <= kProbeSmallMax && n_build <= kProbeLdsKeys) {
+    hipLaunchKernelGGL(probe_scan_small_kernel, dim3(1), dim3(kProbeThreads), 0, stream, probe,
+                       n_probe, build, static_cast<int>(n_build), w.lo, w.offs, w.scalars);
+    EJ_LAUNCH_CHECK();
+  } else {
+    hipLaunchKernelGGL(probe_count_kernel, dim3(grid_for(n_probe)), dim3(kBlock), 0, stream,
+                       probe, n_probe, build, n_build, w.lo, w.cnt);
+    EJ_LAUNCH_CHECK();
+    EJ_TRY(scan_exclusive_i64(w.cnt, w.offs, n_probe, w.scalars, w.scan_ws, stream));
   }
-  EJ_LAUNCH_CHECK();
-  EJ_TRY(scan_exclusive_i64(w.cnt, w.offs, n_probe, w.scalars, w.scan_ws, stream));
+  return EJ_OK;
+}
+
+}  // namespace
+}  // namespace ej
+
+extern "C" int ej_join_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                             const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                             int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                             const int64_t *radices, int32_t order, void *workspace,
+                             size_t workspace_bytes, int64_t *n_pairs, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(n_pairs, "n_pairs is null");
+  int64_t known = -1;
+  int64_t *scal = nullptr;
+  EJ_TRY(join_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
+                            lhs_dims, rhs_dims, radices, order, workspace, workspace_bytes,
+                            &known, &scal, stream));
+  if (known >= 0) {
+    *n_pairs = known;
+    return EJ_OK;
+  }
   int64_t host[2] = {0, 0};
-  EJ_HIP(hipMemcpyAsync(host, w.scalars, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  EJ_HIP(hipMemcpyAsync(host, scal, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   EJ_HIP(hipStreamSynchronize(stream));
   if (host[1] != 0) {
     set_error("a join-key coordinate lies outside [0, radix)");
     return EJ_E_RANGE;
   }
   *n_pairs = host[0];
+  return EJ_OK;
+}
+
+extern "C" int ej_join_count_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                                   const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                                   int32_t n_keys, const int32_t *lhs_dims,
+                                   const int32_t *rhs_dims, const int64_t *radices,
+                                   int32_t order, void *workspace, size_t workspace_bytes,
+                                   int64_t *counts, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(counts, "counts is null");
+  int64_t known = -1;
+  int64_t *scal = nullptr;
+  EJ_TRY(join_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
+                            lhs_dims, rhs_dims, radices, order, workspace, workspace_bytes,
+                            &known, &scal, stream));
+  if (known >= 0) {
+    // Nothing was enqueued: hand the host-known count over in stream order
+    // through the workspace so that device-side consumers see it too.
+    JoinWs w = carve_join(workspace, n_lhs, n_rhs, order);
+    EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+    const int64_t v[2] = {known, 0};
+    EJ_HIP(hipMemcpyAsync(w.scalars, v, sizeof(v), hipMemcpyHostToDevice, stream));
+    scal = w.scalars;
+  }
+  EJ_HIP(hipMemcpyAsync(counts, scal, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   return EJ_OK;
 }
 
@@ -325,11 +458,16 @@ __global__ void output_coords_kernel(const int32_t *lc, const int32_t *rc, const
   for (int d = 0; d < a.n; ++d) out[p * a.n + d] = a.src[d] == 0 ? lrow[a.dim[d]] : rrow[a.dim[d]];
 }
 
+// scal[2] receives the live pair count (n clipped by *n_dev).
 __global__ void pair_keys_kernel(const int32_t *lc, const int32_t *rc, const int64_t *li,
-                                 const int64_t *ri, int64_t n, AggSpec a, uint64_t *keys,
-                                 int *bad) {
+                                 const int64_t *ri, int64_t n, const int64_t *n_dev, AggSpec a,
+                                 uint64_t *keys, int32_t *perm, int64_t *scal) {
+  n = live_count(n, n_dev);
   int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p == 0) scal[2] = n;
+  int *bad = reinterpret_cast<int *>(scal + 1);
   if (p >= n) return;
+  perm[p] = static_cast<int32_t>(p);
   if (li[p] < 0 || li[p] >= a.n_lhs || ri[p] < 0 || ri[p] >= a.n_rhs) {
     keys[p] = 0;
     atomicOr(bad, 1);
@@ -351,16 +489,40 @@ __global__ void pair_keys_kernel(const int32_t *lc, const int32_t *rc, const int
   if (b) atomicOr(bad, 1);
 }
 
-__global__ void seg_flags_kernel(const uint64_t *skeys, int64_t n, int64_t *flags) {
+__global__ void seg_flags_kernel(const uint64_t *skeys, int64_t n, const int64_t *n_dev,
+                                 int64_t *flags) {
+  n = live_count(n, n_dev);
   int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (q >= n) return;
   flags[q] = (q == 0 || skeys[q] != skeys[q - 1]) ? 1 : 0;
 }
 
+// Segment-start flag of sorted position q, generated inside the scan.
+struct SegFlagLoad {
+  const uint64_t *skeys;
+  __device__ int64_t operator()(int64_t q) const {
+    return (q == 0 || skeys[q] != skeys[q - 1]) ? 1 : 0;
+  }
+};
+
+struct StoreFlag {
+  int64_t *flags;
+  __device__ void operator()(int64_t q, int64_t f) const { flags[q] = f; }
+};
+
+// dev_counts (optional): the workspace scalars; the live pair count is
+// dev_counts[2] and the segment count dev_counts[0] (then n_seg is the
+// capacity of out_coords / seg_offsets).
 __global__ void seg_fill_kernel(const uint64_t *skeys, const int32_t *sperm, const int64_t *flags,
-                                const int64_t *excl, int64_t n, int64_t n_seg, AggSpec a,
-                                int32_t *out_coords, int32_t *seg_offsets, int32_t *perm,
-                                int32_t *seg_ids) {
+                                const int64_t *excl, int64_t n, int64_t n_seg,
+                                const int64_t *dev_counts, AggSpec a, int32_t *out_coords,
+                                int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids) {
+  if (dev_counts) {
+    n = live_count(n, dev_counts + 2);
+    const int64_t u = dev_counts[0];
+    if (u > n_seg) return;  // capacity exceeded: the host sees the count and rejects
+    n_seg = u;
+  }
   int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (q >= n) return;
   const int64_t seg = excl[q] + flags[q] - 1;
@@ -430,6 +592,61 @@ extern "C" int ej_segment_workspace_size(int64_t n_pairs, size_t *bytes) {
   return EJ_OK;
 }
 
+namespace ej {
+namespace {
+
+// Enqueues the segment count; *known_empty on return: no pairs, nothing
+// enqueued.  Otherwise U and a range flag land in w.scalars[0..1] and the
+// live pair count in w.scalars[2].
+int segment_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                          const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                          const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
+                          const int64_t *n_pairs_dev, int32_t n_out, const int32_t *agg_src,
+                          const int32_t *agg_dim, const int64_t *radices, void *workspace,
+                          size_t workspace_bytes, bool *known_empty, int64_t **dev_scalars,
+                          hipStream_t stream) {
+  *known_empty = false;
+  EJ_CHECK_ARG(n_pairs >= 0 && n_pairs < (int64_t(1) << 31), "n_pairs must lie in [0, 2^31)");
+  EJ_CHECK_ARG(radices || n_out == 0, "radices is null");
+  AggSpec a;
+  EJ_TRY(check_agg(n_out, agg_src, agg_dim, n_lhs, lhs_ncols, n_rhs, rhs_ncols, radices, &a));
+  if (n_pairs == 0) {
+    *known_empty = true;
+    return EJ_OK;
+  }
+  EJ_CHECK_ARG(lhs_coords && rhs_coords && lhs_idx && rhs_idx, "null pointer argument");
+  int bits = 0;
+  EJ_TRY(key_bits(a.radix, n_out, &bits));
+  SegWs w = carve_seg(workspace, n_pairs);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  *dev_scalars = w.scalars;
+  EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
+  const bool alt = n_pairs > 1 && (radix_passes(bits) & 1);
+  hipLaunchKernelGGL(pair_keys_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream,
+                     lhs_coords, rhs_coords, lhs_idx, rhs_idx, n_pairs, n_pairs_dev, a,
+                     alt ? w.keys_alt : w.keys, alt ? w.perm_alt : w.perm, w.scalars);
+  EJ_LAUNCH_CHECK();
+  // From here on the live pair count is w.scalars[2] (n_pairs clipped).
+  const int64_t *live = n_pairs_dev ? w.scalars + 2 : nullptr;
+  EJ_TRY(sort_pairs_u64(w.keys, w.perm, w.keys_alt, w.perm_alt, n_pairs, bits, w.sort_ws, stream,
+                        alt, live));
+  if (n_pairs <= kFastScanMax) {
+    launch_fast_scan(SegFlagLoad{w.keys}, StoreFlag{w.flags}, n_pairs, live,
+                     static_cast<int64_t *>(w.scan_ws), w.excl, w.scalars, stream);
+    EJ_LAUNCH_CHECK();
+  } else {
+    hipLaunchKernelGGL(seg_flags_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream, w.keys,
+                       n_pairs, live, w.flags);
+    EJ_LAUNCH_CHECK();
+    EJ_TRY(scan_exclusive_i64(w.flags, w.excl, n_pairs, w.scalars, w.scan_ws, stream, live));
+  }
+  return EJ_OK;
+}
+
+}  // namespace
+}  // namespace ej
+
 extern "C" int ej_segment_count(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                                 const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                                 const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
@@ -439,39 +656,50 @@ extern "C" int ej_segment_count(const int32_t *lhs_coords, int64_t n_lhs, int32_
   clear_error();
   hipStream_t stream = as_stream(stream_);
   EJ_CHECK_ARG(n_segments, "n_segments is null");
-  EJ_CHECK_ARG(n_pairs >= 0 && n_pairs < (int64_t(1) << 31), "n_pairs must lie in [0, 2^31)");
-  EJ_CHECK_ARG(radices || n_out == 0, "radices is null");
-  AggSpec a;
-  EJ_TRY(check_agg(n_out, agg_src, agg_dim, n_lhs, lhs_ncols, n_rhs, rhs_ncols, radices, &a));
-  if (n_pairs == 0) {
+  bool empty = false;
+  int64_t *scal = nullptr;
+  EJ_TRY(segment_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols,
+                               lhs_idx, rhs_idx, n_pairs, nullptr, n_out, agg_src, agg_dim,
+                               radices, workspace, workspace_bytes, &empty, &scal, stream));
+  if (empty) {
     *n_segments = 0;
     return EJ_OK;
   }
-  EJ_CHECK_ARG(lhs_coords && rhs_coords && lhs_idx && rhs_idx, "null pointer argument");
-  int bits = 0;
-  EJ_TRY(key_bits(a.radix, n_out, &bits));
-  SegWs w = carve_seg(workspace, n_pairs);
-  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
-               workspace_bytes, w.bytes);
-  EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
-  int *bad = reinterpret_cast<int *>(w.scalars + 1);
-  hipLaunchKernelGGL(pair_keys_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream,
-                     lhs_coords, rhs_coords, lhs_idx, rhs_idx, n_pairs, a, w.keys, bad);
-  EJ_LAUNCH_CHECK();
-  EJ_TRY(fill_iota_i32(w.perm, n_pairs, stream));
-  EJ_TRY(sort_pairs_u64(w.keys, w.perm, w.keys_alt, w.perm_alt, n_pairs, bits, w.sort_ws, stream));
-  hipLaunchKernelGGL(seg_flags_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream, w.keys,
-                     n_pairs, w.flags);
-  EJ_LAUNCH_CHECK();
-  EJ_TRY(scan_exclusive_i64(w.flags, w.excl, n_pairs, w.scalars, w.scan_ws, stream));
   int64_t host[2] = {0, 0};
-  EJ_HIP(hipMemcpyAsync(host, w.scalars, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  EJ_HIP(hipMemcpyAsync(host, scal, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   EJ_HIP(hipStreamSynchronize(stream));
   if (host[1] != 0) {
     set_error("a pair index or an output coordinate lies outside [0, radix)");
     return EJ_E_RANGE;
   }
   *n_segments = host[0];
+  return EJ_OK;
+}
+
+extern "C" int ej_segment_count_async(const int32_t *lhs_coords, int64_t n_lhs,
+                                      int32_t lhs_ncols, const int32_t *rhs_coords,
+                                      int64_t n_rhs, int32_t rhs_ncols, const int64_t *lhs_idx,
+                                      const int64_t *rhs_idx, int64_t n_pairs,
+                                      const int64_t *n_pairs_dev, int32_t n_out,
+                                      const int32_t *agg_src, const int32_t *agg_dim,
+                                      const int64_t *radices, void *workspace,
+                                      size_t workspace_bytes, int64_t *counts,
+                                      ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(counts, "counts is null");
+  bool empty = false;
+  int64_t *scal = nullptr;
+  EJ_TRY(segment_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols,
+                               lhs_idx, rhs_idx, n_pairs, n_pairs_dev, n_out, agg_src, agg_dim,
+                               radices, workspace, workspace_bytes, &empty, &scal, stream));
+  if (empty) {
+    SegWs w = carve_seg(workspace, 0);
+    EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+    EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
+    scal = w.scalars;
+  }
+  EJ_HIP(hipMemcpyAsync(counts, scal, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   return EJ_OK;
 }
 
@@ -500,8 +728,30 @@ extern "C" int ej_segment_fill(int64_t n_pairs, int64_t n_segments, int32_t n_ou
   SegWs w = carve_seg(const_cast<void *>(workspace), n_pairs);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
   hipLaunchKernelGGL(seg_fill_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream, w.keys,
-                     w.perm, w.flags, w.excl, n_pairs, n_segments, a, out_coords, seg_offsets,
-                     perm, seg_ids);
+                     w.perm, w.flags, w.excl, n_pairs, n_segments, nullptr, a, out_coords,
+                     seg_offsets, perm, seg_ids);
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+extern "C" int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices,
+                                     const void *workspace, size_t workspace_bytes,
+                                     int32_t *out_coords, int32_t *seg_offsets, int32_t *perm,
+                                     int32_t *seg_ids, int64_t capacity, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(n_pairs >= 0 && capacity >= 0, "bad sizes");
+  if (n_pairs == 0) return EJ_OK;
+  EJ_CHECK_ARG(seg_offsets && perm && (out_coords || n_out == 0), "null output pointer");
+  EJ_CHECK_ARG(n_out >= 0 && n_out <= EJ_MAX_KEYS && (radices || n_out == 0), "bad n_out");
+  AggSpec a;
+  a.n = n_out;
+  for (int d = 0; d < n_out; ++d) a.radix[d] = radices[d];
+  SegWs w = carve_seg(const_cast<void *>(workspace), n_pairs);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+  hipLaunchKernelGGL(seg_fill_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream, w.keys,
+                     w.perm, w.flags, w.excl, n_pairs, capacity, w.scalars, a, out_coords,
+                     seg_offsets, perm, seg_ids);
   EJ_LAUNCH_CHECK();
   return EJ_OK;
 }

@@ -41,43 +41,13 @@ int key_bits(const int64_t *radix, int n, int *bits) {
 }
 
 // ---------------------------------------------------------------------------
-// Scan: each block scans kScanTile consecutive values (8 per thread), writes
-// the block total, the totals are scanned recursively and added back.
-constexpr int kScanItems = 8;
-constexpr int kScanTile = kBlock * kScanItems;
-
-// Inclusive prefix sum across the 64 lanes of a wave.
-__device__ inline int64_t wave_inclusive_sum(int64_t v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int64_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
-  return v;
-}
-
-// Exclusive prefix of v across the block; *block_total receives the sum.
-__device__ inline int64_t block_exclusive_sum(int64_t v, int64_t *block_total) {
-  __shared__ int64_t wave_tot[kBlock / 64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int64_t inc = wave_inclusive_sum(v);
-  if (lane == 63) wave_tot[wave] = inc;
-  __syncthreads();
-  int64_t wave_off = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < kBlock / 64; ++w) {
-    int64_t t = wave_tot[w];
-    if (w < wave) wave_off += t;
-    tot += t;
-  }
-  __syncthreads();
-  *block_total = tot;
-  return wave_off + inc - v;
-}
-
+// Scan.  Up to kFastScanMax values: the two-launch reduce-then-scan.  Longer:
+// each block scans kScanTile consecutive values (8 per thread), writes the
+// block total, the totals are scanned recursively and added back.
 __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(const int64_t *in, int64_t *out,
-                                                            int64_t *tile_sums, int64_t n) {
+                                                            int64_t *tile_sums, int64_t n,
+                                                            const int64_t *n_dev) {
+  n = live_count(n, n_dev);
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
                        static_cast<int64_t>(threadIdx.x) * kScanItems;
   int64_t v[kScanItems];
@@ -89,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(const int64_t *in, i
     s += v[i];
   }
   int64_t tot;
-  int64_t run = block_exclusive_sum(s, &tot);
+  int64_t run = block_exclusive_sum<kBlock>(s, &tot);
 #pragma unroll
   for (int i = 0; i < kScanItems; ++i) {
     int64_t idx = base + i;
@@ -100,7 +70,8 @@ __global__ __launch_bounds__(kBlock) void scan_tiles_kernel(const int64_t *in, i
 }
 
 __global__ __launch_bounds__(kBlock) void scan_add_kernel(int64_t *out, const int64_t *tile_offs,
-                                                          int64_t n) {
+                                                          int64_t n, const int64_t *n_dev) {
+  n = live_count(n, n_dev);
   const int64_t off = tile_offs[blockIdx.x];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
   for (int i = threadIdx.x; i < kScanTile; i += kBlock) {
@@ -110,7 +81,8 @@ __global__ __launch_bounds__(kBlock) void scan_add_kernel(int64_t *out, const in
 }
 
 __global__ void scan_total_kernel(const int64_t *in, const int64_t *out, int64_t n,
-                                  int64_t *total) {
+                                  const int64_t *n_dev, int64_t *total) {
+  n = live_count(n, n_dev);
   *total = n > 0 ? out[n - 1] + in[n - 1] : 0;
 }
 
@@ -126,9 +98,15 @@ size_t scan_workspace_bytes(int64_t n) {
 }
 
 int scan_exclusive_i64(const int64_t *in, int64_t *out, int64_t n, int64_t *total, void *ws,
-                       hipStream_t stream) {
+                       hipStream_t stream, const int64_t *n_dev) {
   if (n <= 0) {
     if (total) EJ_HIP(hipMemsetAsync(total, 0, sizeof(int64_t), stream));
+    return EJ_OK;
+  }
+  if (n <= kFastScanMax) {
+    launch_fast_scan(LoadI64{in}, NoEmit{}, n, n_dev, static_cast<int64_t *>(ws), out, total,
+                     stream);
+    EJ_LAUNCH_CHECK();
     return EJ_OK;
   }
   const int64_t tiles = ceil_div(n, kScanTile);
@@ -137,70 +115,113 @@ int scan_exclusive_i64(const int64_t *in, int64_t *out, int64_t n, int64_t *tota
   int64_t *sums_scanned = sums + tiles;
   char *rest = w + align_up(sizeof(int64_t) * tiles * 2, 256);
   hipLaunchKernelGGL(scan_tiles_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0,
-                     stream, in, out, sums, n);
+                     stream, in, out, sums, n, n_dev);
   EJ_LAUNCH_CHECK();
   if (tiles > 1) {
     EJ_TRY(scan_exclusive_i64(sums, sums_scanned, tiles, nullptr, rest, stream));
     hipLaunchKernelGGL(scan_add_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kBlock), 0,
-                       stream, out, sums_scanned, n);
+                       stream, out, sums_scanned, n, n_dev);
     EJ_LAUNCH_CHECK();
   }
   if (total) {
-    hipLaunchKernelGGL(scan_total_kernel, dim3(1), dim3(1), 0, stream, in, out, n, total);
+    hipLaunchKernelGGL(scan_total_kernel, dim3(1), dim3(1), 0, stream, in, out, n, n_dev,
+                       total);
     EJ_LAUNCH_CHECK();
   }
   return EJ_OK;
 }
 
 // ---------------------------------------------------------------------------
-// Radix sort: 8-bit digits, tiles of kSortTile keys per block.
-//   pass 1: per-block digit histogram, stored digit-major so that one
-//           exclusive scan yields every block's starting offset per digit;
-//   pass 2: scan;
-//   pass 3: stable scatter.  Ranks inside a round of 256 keys come from
-//           wave64 ballots (peer mask of equal digits + popcount of lower
-//           lanes) and a per-digit prefix over the four waves in LDS.
+// Radix sort: 8-bit digits; each block takes a tile of kBlock * ITEMS keys,
+// ITEMS in {1, 2, 4, 8} chosen per sort so that short sequences spread over
+// many blocks (fewer serial rounds per block).
+//   pass 1: per-block digit histogram;
+//   pass 2: stable scatter.  Each block first derives its starting offset
+//           per digit.  Up to kInlineOffsetBlocks blocks: the histogram is
+//           stored block-major (hist[block][digit]) and every block reads it
+//           directly (digit totals scanned across the 256 digits plus the
+//           counts of earlier blocks).  More blocks: it is stored digit-major
+//           (hist[digit][block]) and one device-wide exclusive scan of it
+//           supplies the offsets.
+//           Ranks inside a round of 256 keys come from wave64 ballots (peer
+//           mask of equal digits + popcount of lower lanes) and a per-digit
+//           prefix over the four waves in LDS.
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
-constexpr int kSortItems = 8;
-constexpr int kSortTile = kBlock * kSortItems;
+constexpr int kMaxSortItems = 8;
+constexpr int64_t kInlineOffsetBlocks = 128;
 static_assert(kRadix == kBlock, "one thread per digit in the scatter bookkeeping");
 
+template <int ITEMS>
 __global__ __launch_bounds__(kBlock) void radix_hist_kernel(const uint64_t *keys, int64_t n,
-                                                            int shift, int64_t *hist,
-                                                            int64_t nblocks) {
+                                                            const int64_t *n_dev, int shift,
+                                                            int64_t *hist, int64_t nblocks,
+                                                            bool digit_major) {
+  n = live_count(n, n_dev);
   __shared__ int counts[kRadix];
   counts[threadIdx.x] = 0;
-  __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kBlock * ITEMS;
+  uint64_t k[ITEMS];
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
+  for (int r = 0; r < ITEMS; ++r) {
     int64_t i = base + r * kBlock + threadIdx.x;
-    if (i < n) atomicAdd(&counts[(keys[i] >> shift) & (kRadix - 1)], 1);
+    k[r] = i < n ? keys[i] : 0;
   }
   __syncthreads();
-  hist[static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x] = counts[threadIdx.x];
+#pragma unroll
+  for (int r = 0; r < ITEMS; ++r) {
+    int64_t i = base + r * kBlock + threadIdx.x;
+    if (i < n) atomicAdd(&counts[(k[r] >> shift) & (kRadix - 1)], 1);
+  }
+  __syncthreads();
+  const int64_t at = digit_major ? static_cast<int64_t>(threadIdx.x) * nblocks + blockIdx.x
+                                 : static_cast<int64_t>(blockIdx.x) * kRadix + threadIdx.x;
+  hist[at] = counts[threadIdx.x];
 }
 
+// offs == nullptr: offsets are derived from the block-major hist.
+template <int ITEMS>
 __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
-    const uint64_t *kin, const int32_t *vin, uint64_t *kout, int32_t *vout, int64_t n, int shift,
-    const int64_t *offs, int64_t nblocks) {
+    const uint64_t *__restrict__ kin, const int32_t *__restrict__ vin, uint64_t *__restrict__ kout,
+    int32_t *__restrict__ vout, int64_t n, const int64_t *n_dev, int shift,
+    const int64_t *__restrict__ hist, const int64_t *__restrict__ offs, int64_t nblocks) {
+  n = live_count(n, n_dev);
   __shared__ int64_t base_off[kRadix];
   __shared__ int wcount[kBlock / 64][kRadix];
   __shared__ int wprefix[kBlock / 64][kRadix];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  base_off[tid] = offs[static_cast<int64_t>(tid) * nblocks + blockIdx.x];
-  const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kSortTile;
-  for (int r = 0; r < kSortItems; ++r) {
+  const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kBlock * ITEMS;
+  uint64_t kk[ITEMS];
+  int32_t vv[ITEMS];
+#pragma unroll
+  for (int r = 0; r < ITEMS; ++r) {
+    const int64_t i = tile0 + r * kBlock + tid;
+    kk[r] = i < n ? kin[i] : 0;
+    vv[r] = i < n ? vin[i] : 0;
+  }
+  if (offs) {
+    base_off[tid] = offs[static_cast<int64_t>(tid) * nblocks + blockIdx.x];
+  } else {
+    int64_t before = 0, digit_total = 0;
+#pragma unroll 8
+    for (int64_t b = 0; b < nblocks; ++b) {
+      const int64_t c = hist[b * kRadix + tid];
+      digit_total += c;
+      before += b < static_cast<int64_t>(blockIdx.x) ? c : 0;
+    }
+    int64_t all;
+    base_off[tid] = block_exclusive_sum<kBlock>(digit_total, &all) + before;
+  }
+#pragma unroll
+  for (int r = 0; r < ITEMS; ++r) {
 #pragma unroll
     for (int w = 0; w < kBlock / 64; ++w) wcount[w][tid] = 0;
     __syncthreads();
     const int64_t i = tile0 + r * kBlock + tid;
     const bool valid = i < n;
-    uint64_t k = valid ? kin[i] : 0;
-    int32_t v = valid ? vin[i] : 0;
-    int d = static_cast<int>((k >> shift) & (kRadix - 1));
+    const uint64_t k = kk[r];
+    const int d = static_cast<int>((k >> shift) & (kRadix - 1));
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
@@ -221,20 +242,16 @@ __global__ __launch_bounds__(kBlock) void radix_scatter_kernel(
     if (valid) {
       int64_t pos = base_off[d] + wprefix[wave][d] + rank;
       kout[pos] = k;
-      vout[pos] = v;
+      vout[pos] = vv[r];
     }
     __syncthreads();
     base_off[tid] += run;
   }
 }
 
-__global__ void iota_kernel(int32_t *v, int64_t n) {
-  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) v[i] = static_cast<int32_t>(i);
-}
-
 __global__ void copy_pairs_kernel(const uint64_t *ks, const int32_t *vs, uint64_t *kd,
-                                  int32_t *vd, int64_t n) {
+                                  int32_t *vd, int64_t n, const int64_t *n_dev) {
+  n = live_count(n, n_dev);
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) {
     kd[i] = ks[i];
@@ -242,44 +259,68 @@ __global__ void copy_pairs_kernel(const uint64_t *ks, const int32_t *vs, uint64_
   }
 }
 
-int fill_iota_i32(int32_t *v, int64_t n, hipStream_t stream) {
-  if (n <= 0) return EJ_OK;
-  hipLaunchKernelGGL(iota_kernel, dim3(grid_for(n)), dim3(kBlock), 0, stream, v, n);
-  EJ_LAUNCH_CHECK();
-  return EJ_OK;
+// Keys per thread for a sort of n keys: the fewest rounds per block that keep
+// the grid within kInlineOffsetBlocks blocks, else the largest tile.
+int sort_items(int64_t n) {
+  for (int items = 1; items < kMaxSortItems; items *= 2)
+    if (ceil_div(n, static_cast<int64_t>(kBlock) * items) <= kInlineOffsetBlocks) return items;
+  return kMaxSortItems;
 }
 
+// Covers every sort of up to n keys: below 8 * kBlock * kInlineOffsetBlocks
+// keys a sort uses at most kInlineOffsetBlocks blocks, above it the block
+// count grows with n.
 size_t sort_workspace_bytes(int64_t n) {
-  int64_t nblocks = ceil_div(n > 0 ? n : 1, kSortTile);
+  int64_t nblocks = ceil_div(n > 0 ? n : 1, static_cast<int64_t>(kBlock) * sort_items(n));
+  if (nblocks < kInlineOffsetBlocks) nblocks = kInlineOffsetBlocks;
   int64_t h = nblocks * kRadix;
   return align_up(sizeof(int64_t) * h * 2, 256) + scan_workspace_bytes(h);
 }
 
-int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *vals_alt,
-                   int64_t n, int bits, void *ws, hipStream_t stream) {
-  if (n <= 1 || bits <= 0) return EJ_OK;
-  const int64_t nblocks = ceil_div(n, kSortTile);
+int radix_passes(int bits) { return bits <= 0 ? 0 : (bits + kRadixBits - 1) / kRadixBits; }
+
+template <int ITEMS>
+int sort_passes(uint64_t *&ks, int32_t *&vs, uint64_t *&kd, int32_t *&vd, int64_t n, int bits,
+                void *ws, hipStream_t stream, const int64_t *n_dev) {
+  const int64_t nblocks = ceil_div(n, static_cast<int64_t>(kBlock) * ITEMS);
   const int64_t h = nblocks * kRadix;
   char *w = static_cast<char *>(ws);
   int64_t *hist = reinterpret_cast<int64_t *>(w);
   int64_t *offs = hist + h;
   void *scan_ws = w + align_up(sizeof(int64_t) * h * 2, 256);
-  uint64_t *ks = keys, *kd = keys_alt;
-  int32_t *vs = vals, *vd = vals_alt;
+  const bool inline_offs = nblocks <= kInlineOffsetBlocks;
   for (int shift = 0; shift < bits; shift += kRadixBits) {
-    hipLaunchKernelGGL(radix_hist_kernel, dim3(static_cast<unsigned>(nblocks)), dim3(kBlock), 0,
-                       stream, ks, n, shift, hist, nblocks);
+    hipLaunchKernelGGL(radix_hist_kernel<ITEMS>, dim3(static_cast<unsigned>(nblocks)),
+                       dim3(kBlock), 0, stream, ks, n, n_dev, shift, hist, nblocks,
+                       !inline_offs);
     EJ_LAUNCH_CHECK();
-    EJ_TRY(scan_exclusive_i64(hist, offs, h, nullptr, scan_ws, stream));
-    hipLaunchKernelGGL(radix_scatter_kernel, dim3(static_cast<unsigned>(nblocks)), dim3(kBlock),
-                       0, stream, ks, vs, kd, vd, n, shift, offs, nblocks);
+    if (!inline_offs) EJ_TRY(scan_exclusive_i64(hist, offs, h, nullptr, scan_ws, stream));
+    hipLaunchKernelGGL(radix_scatter_kernel<ITEMS>, dim3(static_cast<unsigned>(nblocks)),
+                       dim3(kBlock), 0, stream, ks, vs, kd, vd, n, n_dev, shift, hist,
+                       inline_offs ? nullptr : offs, nblocks);
     EJ_LAUNCH_CHECK();
     uint64_t *tk = ks; ks = kd; kd = tk;
     int32_t *tv = vs; vs = vd; vd = tv;
   }
-  if (ks != keys) {
+  return EJ_OK;
+}
+
+int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *vals_alt,
+                   int64_t n, int bits, void *ws, hipStream_t stream, bool input_in_alt,
+                   const int64_t *n_dev) {
+  uint64_t *ks = input_in_alt ? keys_alt : keys, *kd = input_in_alt ? keys : keys_alt;
+  int32_t *vs = input_in_alt ? vals_alt : vals, *vd = input_in_alt ? vals : vals_alt;
+  if (n > 1 && bits > 0) {
+    switch (sort_items(n)) {
+      case 1: EJ_TRY(sort_passes<1>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
+      case 2: EJ_TRY(sort_passes<2>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
+      case 4: EJ_TRY(sort_passes<4>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
+      default: EJ_TRY(sort_passes<8>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
+    }
+  }
+  if (ks != keys && n > 0) {
     hipLaunchKernelGGL(copy_pairs_kernel, dim3(grid_for(n)), dim3(kBlock), 0, stream, ks, vs,
-                       keys, vals, n);
+                       keys, vals, n, n_dev);
     EJ_LAUNCH_CHECK();
   }
   return EJ_OK;

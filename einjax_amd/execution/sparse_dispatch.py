@@ -121,22 +121,39 @@ def _retry_radices(fn, make_radices, cols):
 # ---------------------------------------------------------------------------
 # Phase 1: join.
 
+def _join_radices(lhs: SparseTensorRelation, rhs: SparseTensorRelation, keys, maxima):
+    """Key radices from grid metadata (and, if given, the data's column maxima)."""
+    out = []
+    for i, (a, b) in enumerate(keys):
+        r = max(_grid(lhs, a), _grid(rhs, b), _host_col_max(lhs.coords, a),
+                _host_col_max(rhs.coords, b))
+        if maxima is not None:
+            r = max(r, maxima[2 * i], maxima[2 * i + 1])
+        out.append(r)
+    return out
+
+
 def _join_dev(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys, lc, rc,
               order=_lib.EJ_ORDER_PROBE):
     keys = [tuple(k) for k in join_keys]
-
-    def radices(maxima):
-        out = []
-        for i, (a, b) in enumerate(keys):
-            r = max(_grid(lhs, a), _grid(rhs, b), _host_col_max(lhs.coords, a),
-                    _host_col_max(rhs.coords, b))
-            if maxima is not None:
-                r = max(r, maxima[2 * i], maxima[2 * i + 1])
-            out.append(r)
-        return out
-
     cols = [c for a, b in keys for c in ((lc, a), (rc, b))]
-    return _retry_radices(lambda r: _device.join(lc, rc, keys, r, order), radices, cols)
+    return _retry_radices(lambda r: _device.join(lc, rc, keys, r, order),
+                          lambda m: _join_radices(lhs, rhs, keys, m), cols)
+
+
+# Pair counts of recent joins, keyed by the coordinate buffers, their shapes,
+# the keys and the radices: a bound for the next execute_sparse on the same
+# relations, which can then queue its whole step without waiting for the
+# count (a wrong bound is detected and costs one rerun).  -1: the queued
+# path found a coordinate outside the metadata radices; do not retry it.
+_pair_hints: dict = {}
+_PAIR_HINTS_MAX = 256
+
+
+def _remember_pairs(key, n_pairs: int):
+    if key not in _pair_hints and len(_pair_hints) >= _PAIR_HINTS_MAX:
+        _pair_hints.pop(next(iter(_pair_hints)))
+    _pair_hints[key] = int(n_pairs)
 
 
 def coordinate_join(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys):
@@ -315,9 +332,11 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
 
     lc = _dev_coords(lhs.coords, lhs.ndim)
     rc = _dev_coords(rhs.coords, rhs.ndim)
-    li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
-    if li.numel() == 0:
-        return _empty_result(lhs, len(output_tile_shape), output_tile_shape, output_shape, host)
+    n_out = len(output_tile_shape)
+
+    def operands():
+        desc = _device.describe(kernel_string, lhs.tile_shape, rhs.tile_shape)
+        return (desc, *_same_dtype(_dev_values(lhs.values), _dev_values(rhs.values)))
 
     def radices(maxima):
         out = []
@@ -329,17 +348,42 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
             out.append(r)
         return out
 
-    cols = [((lc if s == 0 else rc), dim) for s, dim in agg]
-    coords, offsets, perm, _ = _retry_radices(
-        lambda r: _device.segment_plan(lc, rc, li, ri, agg, r), radices, cols)
-    desc = _device.describe(kernel_string, lhs.tile_shape, rhs.tile_shape)
-    a, b = _same_dtype(_dev_values(lhs.values), _dev_values(rhs.values))
-    if fused:
-        vals = _device.segment_einsum(desc, a, b, li, ri, perm, offsets)
+    keys = [tuple(k) for k in join_keys]
+    hint_key = None
+    queued = None
+    if fused and keys and lc.shape[0] and rc.shape[0]:
+        j_rad = _join_radices(lhs, rhs, keys, None)
+        hint_key = (lc.data_ptr(), rc.data_ptr(), tuple(lc.shape), tuple(rc.shape), tuple(keys),
+                    tuple(j_rad), tuple(agg))
+        bound = _pair_hints.get(hint_key)
+        if bound is not None and bound > 0:
+            desc, a, b = operands()
+            status, res = _device.queued_segment_einsum(lc, rc, keys, j_rad, agg, radices(None),
+                                                        desc, a, b, bound)
+            if status == "ok":
+                queued = res
+                _pair_hints[hint_key] = res[0]
+            else:
+                _pair_hints[hint_key] = res[0] if status == "bound" else -1
+    if queued is not None:
+        P, coords, offsets, perm, vals, li, ri = queued
+        if P == 0:
+            return _empty_result(lhs, n_out, output_tile_shape, output_shape, host)
     else:
-        pair_vals = _device.pair_einsum(desc, a, b, li, ri)
-        vals = _device.segment_sum(pair_vals, perm, offsets)
-    n_out = len(output_tile_shape)
+        li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
+        if hint_key is not None and _pair_hints.get(hint_key, 0) >= 0:
+            _remember_pairs(hint_key, li.numel())
+        if li.numel() == 0:
+            return _empty_result(lhs, n_out, output_tile_shape, output_shape, host)
+        cols = [((lc if s == 0 else rc), dim) for s, dim in agg]
+        coords, offsets, perm, _ = _retry_radices(
+            lambda r: _device.segment_plan(lc, rc, li, ri, agg, r), radices, cols)
+        desc, a, b = operands()
+        if fused:
+            vals = _device.segment_einsum(desc, a, b, li, ri, perm, offsets)
+        else:
+            pair_vals = _device.pair_einsum(desc, a, b, li, ri)
+            vals = _device.segment_sum(pair_vals, perm, offsets)
     if coords.shape[1] != n_out:
         import torch
 

@@ -20,6 +20,11 @@
  *   tile einsum   ej_einsum_describe / ej_pair_einsum / ej_segment_einsum
  *                 (replaces jnp.einsum(_add_batch_dim(kernel_string)),
  *                  execution/sparse_dispatch.py:121-126)
+ *   queued step   ej_join_count_async / ej_segment_count_async /
+ *                 ej_segment_fill_async / ej_segment_einsum_async
+ *                 (the same phases with the counts kept on the device, so a
+ *                  caller can queue a whole execute_sparse,
+ *                  execution/sparse_dispatch.py:226-297, without waiting)
  *   segment sum   ej_segment_sum
  *                 (the accumulation half of segment_sum, execution/sparse_dispatch.py:164-171)
  *
@@ -27,11 +32,12 @@
  *   - Every pointer argument named *_coords, *_values, *_idx, *keys, perm,
  *     seg_*, out*, dense and workspace is a DEVICE pointer.  Small descriptor
  *     arrays (dims, radices, shapes, agg_*) and the scalar outputs n_pairs,
- *     n_segments, n_tiles are HOST pointers.
+ *     n_segments, n_tiles are HOST pointers; `counts` of the *_async
+ *     functions is PINNED host memory (hipHostMalloc).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
  *     Functions whose name ends in _count synchronize `stream` because they
- *     return a data-dependent size to the host; every other function is
- *     asynchronous.
+ *     return a data-dependent size to the host; every other function,
+ *     including the *_count_async forms, is asynchronous.
  *   - A *_count call leaves its state in the caller's workspace; the matching
  *     *_fill call must receive the same workspace, unmodified.
  *   - Return value: EJ_OK (0) or a negative EJ_E_* status.  ej_last_error()
@@ -53,7 +59,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 1
+#define EJ_ABI_VERSION 2
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -133,6 +139,22 @@ int ej_join_fill(int64_t n_lhs, int64_t n_rhs, int32_t n_keys, int32_t order,
                  const void *workspace, size_t workspace_bytes, int64_t n_pairs,
                  int64_t *lhs_idx, int64_t *rhs_idx, int64_t capacity, ej_stream_t stream);
 
+/* Asynchronous form of ej_join_count.  No counterpart in the reference, whose
+ * join runs on the host inside execute_sparse (sparse_dispatch.py:226-297);
+ * it lets a caller queue the whole sparse einsum without waiting for the
+ * pair count.  Enqueues the count on `stream` and copies, in stream order,
+ * counts[0] = P and counts[1] = a range flag (nonzero: a join-key coordinate
+ * lies outside [0, radix), what ej_join_count reports as EJ_E_RANGE) to
+ * `counts`, host memory allocated pinned, valid once the stream has passed
+ * this call.  P also stays on the device as the first int64 of the
+ * workspace: ej_join_fill called with n_pairs = capacity = any bound clips
+ * its writes to it, and ej_segment_count_async takes it as n_pairs_dev. */
+int ej_join_count_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                        const int64_t *radices, int32_t order, void *workspace,
+                        size_t workspace_bytes, int64_t *counts, ej_stream_t stream);
+
 /* ---- output coordinates (reference: _compute_output_coords, :174-223) --- */
 /* out[p][d] = (agg_src[d] == 0 ? lhs : rhs).coords[idx[p]][agg_dim[d]];
  * a pair whose index lies outside [0, n_lhs) or [0, n_rhs) gets -1 in every
@@ -178,6 +200,29 @@ int ej_segment_fill(int64_t n_pairs, int64_t n_segments, int32_t n_out, const in
                     int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids, int64_t capacity,
                     ej_stream_t stream);
 
+/* Asynchronous forms of the segment plan (no counterpart in the reference,
+ * whose grouping runs on the host; see ej_join_count_async).
+ * ej_segment_count_async: n_pairs bounds lhs_idx / rhs_idx (and sizes the
+ * workspace); n_pairs_dev (may be NULL) is the live pair count on the
+ * device, e.g. the first int64 of a join workspace after
+ * ej_join_count_async.  counts[0] = U and counts[1] = a range flag are
+ * copied in stream order to pinned host memory; U also stays on the device
+ * as the first int64 of the workspace.
+ * ej_segment_fill_async: ej_segment_fill on those device-side counts;
+ * capacity bounds out_coords [capacity, n_out] and seg_offsets
+ * [capacity + 1]; if U exceeds it nothing is written (the caller sees U in
+ * counts[0]). */
+int ej_segment_count_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                           const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                           const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
+                           const int64_t *n_pairs_dev, int32_t n_out, const int32_t *agg_src,
+                           const int32_t *agg_dim, const int64_t *radices, void *workspace,
+                           size_t workspace_bytes, int64_t *counts, ej_stream_t stream);
+int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices,
+                          const void *workspace, size_t workspace_bytes, int32_t *out_coords,
+                          int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids,
+                          int64_t capacity, ej_stream_t stream);
+
 /* ---- gather (reference: values[indices], sparse_dispatch.py:118-119) ---- */
 /* out[i] = values[idx[i]] for whole tiles of tile_bytes each.  Indices
  * outside [0, n_tiles) produce a zero tile. */
@@ -205,6 +250,18 @@ int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs
                       const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
                       const int32_t *seg_offsets, int64_t n_segments, float *out,
                       ej_stream_t stream);
+
+/* ej_segment_einsum with the segment count read on the device from
+ * *n_segments_dev (e.g. the first int64 of a segment workspace after
+ * ej_segment_count_async): the grid covers max_segments, seg_offsets holds
+ * at least min(U, max_segments) + 1 entries and out max_segments tiles, of
+ * which the first U are written.  No counterpart in the reference (see
+ * ej_join_count_async). */
+int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
+                            const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
+                            const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
+                            const int32_t *seg_offsets, int64_t max_segments,
+                            const int64_t *n_segments_dev, float *out, ej_stream_t stream);
 
 /* ---- segment sum (reference: segment_sum accumulation, :164-171) -------- */
 /* out[u] = sum_{q in [seg_offsets[u], seg_offsets[u+1])} pair_values[perm[q]],

@@ -86,6 +86,57 @@ def test_join_and_plan_full_size(gpu, name):
     npt.assert_array_equal(seg.cpu().numpy(), seg_o)
 
 
+# Sizes straddling the sort's tile choices (1, 2, 4, 8 keys per thread; up
+# to 128 blocks with offsets read inline, more with a scanned histogram), the
+# two-launch scan limit (524288) and odd/even radix pass counts.
+PLAN_SIZES = [1, 2, 255, 257, 32768, 32769, 65537, 262145, 600000]
+
+
+@pytest.mark.parametrize("P", PLAN_SIZES)
+@pytest.mark.parametrize("radix", [(64, 64), (4096, 64)])
+def test_segment_plan_sizes(gpu, P, radix):
+    """Segment plan of P random pairs (12-bit keys: two radix passes; 18-bit
+    keys: three) bit-exact against the oracle's stable sort."""
+    note("segment plan", P, radix)
+    rng = np.random.default_rng(P)
+    nl, nr = 3000, 2000
+    lc = rng.integers(0, radix[0], (nl, 2), dtype=np.int32)
+    rc = rng.integers(0, radix[1], (nr, 2), dtype=np.int32)
+    li = rng.integers(0, nl, P).astype(np.int64)
+    ri = rng.integers(0, nr, P).astype(np.int64)
+    agg = [(0, 0), (1, 1)]
+    oc_o = R.compute_output_coords(lc, rc, li, ri, agg)
+    uc_o, perm_o, off_o, seg_o = R.segment_plan(oc_o)
+    from einjax_amd import _device
+
+    t = lambda a: torch.from_numpy(a).cuda()
+    coords, off, perm, seg = _device.segment_plan(t(lc), t(rc), t(li), t(ri), agg, list(radix))
+    npt.assert_array_equal(coords.cpu().numpy(), uc_o)
+    npt.assert_array_equal(off.cpu().numpy(), off_o)
+    npt.assert_array_equal(perm.cpu().numpy(), perm_o)
+    npt.assert_array_equal(seg.cpu().numpy(), seg_o)
+
+
+@pytest.mark.parametrize("n_lhs,n_rhs", [(1, 1), (8192, 8192), (8193, 100), (100, 8193),
+                                         (20000, 30000)])
+def test_join_sizes(gpu, n_lhs, n_rhs):
+    """Both join orders around the single-workgroup probe limits (8192 build
+    keys in LDS, 8192 probe keys), bit-exact against the oracle."""
+    note("join sizes", n_lhs, n_rhs)
+    rng = np.random.default_rng(n_lhs * 7 + n_rhs)
+    lc = rng.integers(0, 2000, (n_lhs, 2), dtype=np.int32)
+    rc = rng.integers(0, 2000, (n_rhs, 2), dtype=np.int32)
+    keys = [(1, 0)]
+    hl, hr = ej.coordinate_join_hash(lc, rc, keys)
+    li_o, ri_o = R.coordinate_join(lc, rc, keys)
+    npt.assert_array_equal(hl, li_o)
+    npt.assert_array_equal(hr, ri_o)
+    sl, sr = ej.coordinate_join_sorted(lc, rc, keys)
+    sl_o, sr_o = R.coordinate_join_sorted(lc, rc, keys)
+    npt.assert_array_equal(sl, sl_o)
+    npt.assert_array_equal(sr, sr_o)
+
+
 def test_join_edge_cases(gpu):
     note("join edge cases")
     e = np.zeros((0, 2), np.int32)
@@ -330,6 +381,83 @@ def test_workload_end_to_end(gpu, name, fused):
         assert isinstance(h.values, np.ndarray) and h.values.dtype == np.float32
         npt.assert_array_equal(h.coords, want.coords)
         npt.assert_array_equal(h.values, got.values.cpu().numpy())
+
+
+@pytest.mark.parametrize("name", ["blocksparse_1k", "order3_small", "zipf_small"])
+def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
+    """A repeated execute_sparse on the same relations queues its whole step
+    on the pair count remembered from the previous call.  Its output must be
+    bit-identical to the exact path's, with the remembered bound equal to,
+    below (falls back to the exact path) and far above the true count."""
+    note("queued step", name)
+    if name == "blocksparse_1k":
+        w = G.workload_blocksparse_1k()
+    elif name == "order3_small":
+        w = G.workload_order3(n=512, l=128, density=0.02)
+    else:
+        w = G.workload_sparse_sparse_zipf(n=4096)
+    statuses = []
+    real = _device_mod().queued_segment_einsum
+
+    def spy(*a, **k):
+        st, res = real(*a, **k)
+        statuses.append(st)
+        return st, res
+
+    monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    sd._pair_hints.clear()
+    lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
+    run = lambda: ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    exact = run()
+    assert statuses == [] and len(sd._pair_hints) == 1
+    key, P = next(iter(sd._pair_hints.items()))
+    ref_c, ref_v = exact.coords.cpu().numpy(), exact.values.cpu().numpy()
+    want = R.execute_sparse(w["lhs"], w["rhs"], w["join_keys"], w["kernel_string"],
+                            w["agg_keys"], precision="fp64")
+    npt.assert_array_equal(ref_c, want.coords)
+    assert R.rel_l2(ref_v, want.values) <= TOL[w["dtype"]]
+    for bound, status in [(P, "ok"), (max(P - 1, 1), "bound"), (3 * P + 7, "ok")]:
+        sd._pair_hints[key] = bound
+        got = run()
+        assert statuses[-1] == status, (bound, statuses)
+        npt.assert_array_equal(got.coords.cpu().numpy(), ref_c)
+        npt.assert_array_equal(got.values.cpu().numpy(), ref_v)
+        assert got.values.shape == exact.values.shape
+        assert sd._pair_hints[key] == P
+
+
+def test_queued_step_range_fallback(gpu, monkeypatch):
+    """Relations whose shape metadata understates their coordinates: the
+    queued step detects the out-of-range keys, the exact path (radices from
+    the data) answers, and the queued path is not tried again."""
+    note("queued step range fallback")
+    w = G.workload_blocksparse_1k()
+    statuses = []
+    real = _device_mod().queued_segment_einsum
+
+    def spy(*a, **k):
+        st, res = real(*a, **k)
+        statuses.append(st)
+        return st, res
+
+    monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    sd._pair_hints.clear()
+    L, Rr = w["lhs"], w["rhs"]
+    small = lambda r: R.Rel(r.coords, r.values, r.tile_shape, r.tile_shape)
+    lhs, rhs = dev_rel(small(L), w["dtype"]), dev_rel(small(Rr), w["dtype"])
+    want = R.execute_sparse(L, Rr, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                            precision="fp64")
+    for _ in range(3):
+        got = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+        npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+        assert R.rel_l2(got.values.cpu().numpy(), want.values) <= TOL[w["dtype"]]
+    assert statuses == ["range"]
+
+
+def _device_mod():
+    from einjax_amd import _device
+
+    return _device
 
 
 def test_headline_workload_full_size(gpu):
