@@ -184,6 +184,7 @@ def main():
     coords, offs, perm, _ = _device.segment_plan(lc, rc, li, ri, ak, radices)
     U = coords.shape[0]
     desc = _device.describe(ks, L.tile_shape, Rr.tile_shape)
+    desc.seg_group = sd._segment_run(rhs, jk, ak)  # as execute_sparse sets it
     reps = 10
     t_join = wall_time_ms(lambda: sd._join_dev(lhs, rhs, jk, lc, rc), reps)
     t_plan = wall_time_ms(lambda: _device.segment_plan(lc, rc, li, ri, ak, radices), reps)
@@ -214,7 +215,7 @@ def main():
                             (L.tile_shape[0], Rr.tile_shape[1]), 2)
     jgs_gbs = (B_join + B_gather + B_segsum) / ((t_join + t_gather + t_segsum) * 1e-3) / 1e9
     fused_tflops = F / (t_fused * 1e-3) / 1e12
-    kernel_name = "tile_gemm_dma_kernel<128,128,64,2>"
+    kernel_name = "seg_gemm_bf16_kernel<128,128,4,4,2,8>"
     traffic = load_traffic(kernel_name)
 
     res = {

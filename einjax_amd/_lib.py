@@ -46,7 +46,7 @@ class EinsumDesc(ctypes.Structure):
         ("out_b", _i64 * EJ_MAX_LABELS), ("red_ext", _i64 * EJ_MAX_LABELS),
         ("red_a", _i64 * EJ_MAX_LABELS), ("red_b", _i64 * EJ_MAX_LABELS),
         ("a_elems", _i64), ("b_elems", _i64), ("c_elems", _i64),
-        ("is_gemm", _i32), ("pad_", _i32),
+        ("is_gemm", _i32), ("seg_group", _i32),
         ("batch", _i64), ("m", _i64), ("n", _i64), ("k", _i64),
         ("a_sb", _i64), ("a_sm", _i64), ("a_sk", _i64),
         ("b_sb", _i64), ("b_sk", _i64), ("b_sn", _i64),

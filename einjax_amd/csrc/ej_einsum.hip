@@ -596,11 +596,9 @@ __device__ inline i32x2_t ds_read_tr16_b64(uint32_t addr) {
 // consumers cannot be scheduled ahead of it.
 template <int N>
 __device__ inline void lgkm_wait_all(i32x4_t (&v)[N]) {
-  static_assert(N == 2 || N == 4, "operand count");
-  if constexpr (N == 4)
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
-  else
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]));
+  asm volatile("s_waitcnt lgkmcnt(0)");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
 }
 
 // Ring depth (stages) of the LDS-ring kernel per block shape.
@@ -826,6 +824,300 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 }
 
 // ---------------------------------------------------------------------------
+// Grouped segment GEMM, bf16: G consecutive output segments per workgroup.
+//
+// Consecutive segments often contract the same sequence of lhs tiles: an
+// lhs row against a dense rhs gives segments (i, k), (i, k+1), ... that all
+// pair A(i, j) with B(j, k), B(j, k+1), ... over the same j.  One workgroup
+// then computes G of them at once: every stage streams one lhs K-chunk and
+// G rhs K-chunks into the LDS ring, so an lhs chunk is fetched once per G
+// output tiles, and the workgroup holds G output tiles of accumulators.
+// The workgroup checks that property on its own pairs.  A group without it
+// (different lengths or lhs tiles, fewer than G live segments, an invalid
+// index) runs pair by pair in plan order, each stage feeding only the waves
+// of that pair's segment, so every plan gives the results of G = 1.
+//
+// The tile indices of the group's pairs are read once, one pair per lane,
+// and passed to the issue loop with readlane, so issuing a stage waits on
+// nothing but the ring.  LDS layout and the rhs transpose reads are those
+// of tile_gemm_dma_kernel.  Four waves tile the group's BM x (G * BN)
+// output as WGM x (4 / WGM); each wave's columns lie in one segment.
+
+__device__ inline void pair_tile_idx(const PairSrc &s, int64_t q, int32_t *a, int32_t *b) {
+  const int64_t p = s.perm ? s.perm[q] : q;
+  const int64_t at = s.lidx ? s.lidx[p] : p;
+  const int64_t bt = s.ridx ? s.ridx[p] : p;
+  const bool ok = at >= 0 && at < s.n_a_tiles && bt >= 0 && bt < s.n_b_tiles;
+  *a = ok ? static_cast<int32_t>(at) : -1;
+  *b = ok ? static_cast<int32_t>(bt) : -1;
+}
+
+__device__ inline int32_t lane_value(int32_t v, int lane) {
+  return __builtin_amdgcn_readlane(v, lane);
+}
+
+template <int BM, int BN, int NS, int G, int WGM, int NW>
+__global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *__restrict__ A,
+                                                           const uint16_t *__restrict__ B,
+                                                           float *__restrict__ C, PairSrc src,
+                                                           GemmGeom g, int64_t n_seg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int BK = 32;  // one MFMA K step per stage
+  constexpr int WGN = NW / WGM;
+  constexpr int WM = BM / WGM, WN = G * BN / WGN;
+  static_assert(WGM * WGN == NW && WM % 16 == 0 && WN % 16 == 0 && BN % WN == 0, "wave tiling");
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int A_ROWB = BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
+  constexpr int B_ROWB = BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
+  constexpr int SLOT = A_BYTES + G * B_BYTES;
+  constexpr int LPA = A_BYTES / (1024 * NW), LPB = B_BYTES / (1024 * NW);  // 1 KB loads per wave
+  static_assert(LPA * 1024 * NW == A_BYTES && LPB * 1024 * NW == B_BYTES, "chunks split over waves");
+  constexpr int LPS = LPA + G * LPB;
+  static_assert(NS >= 2 && NS <= 6 && (NS - 2) * LPS < 64, "ring depth / vmcnt range");
+  static_assert(G == 1 || G == 2 || G == 4, "group size");
+  static_assert(CHA == 4 && (CHB == 8 || CHB == 16), "row widths");
+  constexpr uint32_t ALL = 0xF, SKIP = 0xE;  // stage codes (else: the one segment fed)
+  __shared__ __align__(1024) unsigned char ring[NS * SLOT];
+  const uint32_t ring_lds = static_cast<uint32_t>(
+      reinterpret_cast<size_t>((__attribute__((address_space(3))) unsigned char *)ring));
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int wseg = (wn * WN) / BN;  // segment (inside the group) of this wave's columns
+  const int wcol = (wn * WN) % BN;  // its first column inside that segment's tile
+  int64_t lb = xcd_logical_block();
+  const int64_t nb = lb % g.nblocks;
+  lb /= g.nblocks;
+  const int64_t mb = lb % g.mblocks;
+  lb /= g.mblocks;
+  const int64_t bi = lb % g.batch;
+  const int64_t seg0 = (lb / g.batch) * G;
+  int64_t nseg = n_seg;
+  if (src.n_live) {
+    const int64_t live = ld_uniform(src.n_live, 0);
+    nseg = live < nseg ? live : nseg;
+  }
+  if (seg0 >= nseg) return;
+  const int nls = nseg - seg0 < G ? static_cast<int>(nseg - seg0) : G;  // live segments
+  int32_t off[G + 1];  // off[s] = off[nls] for s > nls
+#pragma unroll
+  for (int s = 0; s <= G; ++s) {
+    const int64_t ss = seg0 + (s <= nls ? s : nls);
+    off[s] = src.seg_off ? ld_uniform(src.seg_off, ss) : static_cast<int32_t>(ss);
+  }
+  const int32_t len = off[1] - off[0];
+  bool uni = G > 1 && nls == G;
+#pragma unroll
+  for (int s = 1; s < G; ++s) uni = uni && off[s + 1] - off[s] == len;
+
+  // Pair table, one pair per lane, 64 pairs per chunk.  Shared mode: lane t
+  // holds pair t of every segment (ta = its lhs tile, tb[s] = segment s's rhs
+  // tile).  Sequential mode: lane r holds the r-th pair of the group's plan
+  // range (ta, tb[0]) and, for G > 1, its segment in tb[1].
+  int32_t ta = -1, tb[G];
+#pragma unroll
+  for (int s = 0; s < G; ++s) tb[s] = -1;
+  int chunk = -1;
+  auto load_shared = [&](int c) -> bool {  // whether the chunk's pairs share their lhs tiles
+    const int t = c * 64 + lane;
+    bool bad = false;
+    if (t < len) {  // loads batched per level: plan -> pair -> tiles
+      int64_t p[G], a[G], b[G];
+#pragma unroll
+      for (int s = 0; s < G; ++s) p[s] = off[s] + t;
+      if (src.perm) {
+#pragma unroll
+        for (int s = 0; s < G; ++s) p[s] = src.perm[p[s]];
+      }
+#pragma unroll
+      for (int s = 0; s < G; ++s) a[s] = src.lidx ? src.lidx[p[s]] : p[s];
+#pragma unroll
+      for (int s = 0; s < G; ++s) b[s] = src.ridx ? src.ridx[p[s]] : p[s];
+#pragma unroll
+      for (int s = 0; s < G; ++s) {
+        const bool ok = a[s] >= 0 && a[s] < src.n_a_tiles && b[s] >= 0 && b[s] < src.n_b_tiles;
+        bad = bad || !ok || a[s] != a[0];
+        tb[s] = ok ? static_cast<int32_t>(b[s]) : -1;
+      }
+      ta = static_cast<int32_t>(a[0]);
+    }
+    chunk = c;
+    return __builtin_amdgcn_ballot_w64(bad) == 0;
+  };
+  auto load_seq = [&](int c) {
+    const int r = c * 64 + lane;
+    if (off[0] + r < off[G]) {
+      int32_t a, b;
+      pair_tile_idx(src, off[0] + r, &a, &b);
+      ta = a;
+      tb[0] = b;
+      if constexpr (G > 1) {
+        int s = 0;
+#pragma unroll
+        for (int u = 1; u < G; ++u) s += off[0] + r >= off[u] ? 1 : 0;
+        tb[1] = s;
+      }
+    }
+    chunk = c;
+  };
+  if (uni) {
+    for (int c = (len + 63) / 64 - 1; c >= 0 && uni; --c) uni = load_shared(c);
+  }
+  if (!uni) load_seq(0);
+  const int nkc = static_cast<int>(g.k / BK);
+  const int64_t npos = uni ? len : off[G] - off[0];
+  const int64_t stages = npos * nkc;
+
+  // Per-lane source offsets inside a stage (elements), fixed for the kernel;
+  // 32-bit so that the loads take a scalar base plus a vector offset.
+  uint32_t a_src[LPA], b_src[LPB];
+#pragma unroll
+  for (int v = 0; v < LPA; ++v) {
+    const int blk = v * NW + wave;
+    const int row = blk * (1024 / A_ROWB) + lane / CHA;
+    const int c = (lane % CHA) ^ swz_a<CHA>(row);
+    a_src[v] = static_cast<uint32_t>(row * g.a_sm + c * 8);
+  }
+#pragma unroll
+  for (int v = 0; v < LPB; ++v) {
+    const int blk = v * NW + wave;
+    const int krow = blk * (64 / CHB) + lane / CHB;
+    const int j = (lane % CHB) ^ swz_b<CHB>(krow);
+    b_src[v] = static_cast<uint32_t>(krow * g.b_sk + j * 8);
+  }
+  const int64_t a_off0 = bi * g.a_sb + mb * BM * g.a_sm;
+  const int64_t b_off0 = bi * g.b_sb + nb * BN;
+
+  // Per-lane LDS read offsets inside a slot (bytes).  A: 16 rows x one
+  // 16-byte k chunk per fragment; the row swizzle depends on the lane only,
+  // so fragment i is a constant away from fragment 0.  B: two transpose
+  // reads per fragment (k rows 0-3 and 4-7 of the lane group's 8).
+  const uint32_t a_rd = static_cast<uint32_t>(
+      (wm * WM + (lane & 15)) * A_ROWB + (((lane >> 4) ^ swz_a<CHA>(lane & 15)) * 16));
+  uint32_t b_rd[FN][2];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n0 = wcol + j * 16;
+    const int t = (lane & 15) >> 2, qq = lane & 3;
+    const int jc = (n0 >> 3) + (qq >> 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int krow = (lane >> 4) * 8 + hh * 4 + t;
+      const int phys = jc ^ swz_b<CHB>(krow);
+      b_rd[j][hh] = static_cast<uint32_t>(A_BYTES + wseg * B_BYTES + krow * B_ROWB + phys * 16 +
+                                          (qq & 1) * 8);
+    }
+  }
+
+  int64_t ipos = 0;
+  int ikc = 0;
+  uint32_t codes = 0;  // 4 bits per ring slot
+  auto issue = [&](int64_t st) {
+    if ((ipos >> 6) != chunk) {  // groups of more than 64 pairs only
+      if (uni) load_shared(static_cast<int>(ipos >> 6));
+      else load_seq(static_cast<int>(ipos >> 6));
+    }
+    const int li = static_cast<int>(ipos & 63);
+    const int32_t at = lane_value(ta, li);
+    int32_t bt[G];
+    uint32_t code;
+    if (uni) {
+#pragma unroll
+      for (int s = 0; s < G; ++s) bt[s] = lane_value(tb[s], li);
+      code = ALL;
+    } else {
+      const int32_t b0 = lane_value(tb[0], li);
+#pragma unroll
+      for (int s = 0; s < G; ++s) bt[s] = b0;
+      code = at < 0 ? SKIP : (G > 1 ? static_cast<uint32_t>(lane_value(tb[1], li)) : ALL);
+    }
+    const int64_t a_tile = at < 0 ? 0 : at;
+    unsigned char *slot = ring + (st % NS) * SLOT;
+    const uint16_t *ab = A + a_tile * g.a_elems + a_off0 + ikc * BK;
+#pragma unroll
+    for (int v = 0; v < LPA; ++v)
+      __builtin_amdgcn_global_load_lds(ab + a_src[v], EJ_LDS(slot + (v * NW + wave) * 1024), 16,
+                                       0, 0);
+#pragma unroll
+    for (int s = 0; s < G; ++s) {
+      const int64_t b_tile = bt[s] < 0 ? 0 : bt[s];
+      const uint16_t *bb = B + b_tile * g.b_elems + b_off0 + ikc * BK * g.b_sk;
+#pragma unroll
+      for (int v = 0; v < LPB; ++v)
+        __builtin_amdgcn_global_load_lds(
+            bb + b_src[v], EJ_LDS(slot + A_BYTES + s * B_BYTES + (v * NW + wave) * 1024), 16, 0,
+            0);
+    }
+    const int sh = static_cast<int>(st % NS) * 4;
+    codes = (codes & ~(0xFu << sh)) | (code << sh);
+    if (++ikc == nkc) {
+      ikc = 0;
+      ++ipos;
+    }
+  };
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s0 = 0; s0 < NS - 1; ++s0)
+    if (s0 < stages) issue(s0);
+
+  for (int64_t st = 0; st < stages; ++st) {
+    const int64_t later = stages - 1 - st < NS - 2 ? stages - 1 - st : NS - 2;
+    wait_stage<NS, LPS>(static_cast<int>(later));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int slot = static_cast<int>(st % NS);
+    const uint32_t code = (codes >> (slot * 4)) & 0xFu;
+    if (st + NS - 1 < stages) issue(st + NS - 1);
+    if (code != ALL && code != static_cast<uint32_t>(wseg)) continue;  // wave-uniform
+    uint32_t base = ring_lds + static_cast<uint32_t>(slot * SLOT);
+    asm volatile("" : "+s"(base));  // keeps the read addresses per stage, not per slot
+    bf16x8_t af[FM];
+    i32x4_t bq[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[i] = *reinterpret_cast<const bf16x8_t *>(
+          (const __attribute__((address_space(3))) unsigned char *)(size_t)(base + a_rd) +
+          i * 16 * A_ROWB);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const i32x2_t h0 = ds_read_tr16_b64(base + b_rd[j][0]);
+      const i32x2_t h1 = ds_read_tr16_b64(base + b_rd[j][1]);
+      bq[j] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
+    }
+    lgkm_wait_all<FN>(bq);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            af[i], __builtin_bit_cast(bf16x8_t, bq[j]), acc[i][j], 0, 0, 0);
+  }
+
+  if (wseg < nls) {
+    float *cb = C + (seg0 + wseg) * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+    const uint32_t row0 = static_cast<uint32_t>(wm * WM + (lane >> 4) * 4);
+    const uint32_t col0 = static_cast<uint32_t>(wcol + (lane & 15));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t o = static_cast<uint32_t>((row0 + i * 16 + r) * g.c_sm +
+                                                   (col0 + j * 16) * g.c_sn);
+          cb[o] = acc[i][j][r];
+        }
+  }
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // Generic strided tile einsum (any binary string the describer accepts).
 // One thread per output element; the per-pair sum is formed in fp32 and
 // added to the segment total in plan order.
@@ -915,6 +1207,41 @@ int launch_gemm_bk(int bm, int bn, bool ad, bool bd, const void *A, const void *
   return EJ_E_UNSUPPORTED;
 }
 
+// Ring depth of the grouped kernel (LDS: NS x (BM*32 + G*32*BN) x 2 bytes).
+#ifndef EJ_SEG_NS1
+#define EJ_SEG_NS1 4
+#endif
+#ifndef EJ_SEG_NS4
+#define EJ_SEG_NS4 4
+#endif
+
+template <int BM, int G, int NS, int WGM, int NW>
+int launch_seg_gemm_t(const uint16_t *A, const uint16_t *B, float *C, const PairSrc &src,
+                      const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
+  const int64_t nblk = ceil_div(n_seg, G) * g.batch * g.mblocks * g.nblocks;
+  if (nblk >= (int64_t(1) << 32)) {
+    set_error("einsum launch too large");
+    return EJ_E_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((seg_gemm_bf16_kernel<BM, BM, NS, G, WGM, NW>),
+                     dim3(static_cast<unsigned>(nblk)), dim3(NW * 64), 0, stream, A, B, C, src, g,
+                     n_seg);
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+// Group of 4: 128 x 128 tiles on 8 waves (2 x 4, one segment per wave
+// column), 64 x 64 tiles on 4 waves (one segment per wave).
+int launch_seg_gemm(int bm, int grp, const uint16_t *A, const uint16_t *B, float *C,
+                    const PairSrc &src, const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
+  if (bm == 128) {
+    if (grp == 4) return launch_seg_gemm_t<128, 4, EJ_SEG_NS4, 2, 8>(A, B, C, src, g, n_seg, stream);
+    return launch_seg_gemm_t<128, 1, EJ_SEG_NS1, 2, 4>(A, B, C, src, g, n_seg, stream);
+  }
+  if (grp == 4) return launch_seg_gemm_t<64, 4, EJ_SEG_NS4, 1, 4>(A, B, C, src, g, n_seg, stream);
+  return launch_seg_gemm_t<64, 1, EJ_SEG_NS1, 2, 4>(A, B, C, src, g, n_seg, stream);
+}
+
 int pick_block(int64_t x) { return x % 128 == 0 ? 128 : x % 64 == 0 ? 64 : x % 32 == 0 ? 32 : 0; }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -952,13 +1279,20 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
   g.nblocks = d->n / bn;
   const int64_t nblk = n_seg * g.batch * g.mblocks * g.nblocks;
   if (nblk >= (int64_t(1) << 32)) return false;
-  // bf16, k-contiguous lhs, n-contiguous rhs, K a multiple of 64: the LDS-ring
-  // kernel (direct HBM -> LDS loads, transpose reads for the rhs operand).
-  if (EJ_USE_DMA_GEMM && dtype == EJ_BF16 && ad && !bd && d->k % 64 == 0 && d->b_sn == 1 &&
-      d->b_sk % 8 == 0 &&
-      ((bm == 128 && bn == 128) || (bm == 64 && bn == 64))) {
+  // bf16, k-contiguous lhs, n-contiguous rhs: the LDS-ring kernels (direct
+  // HBM -> LDS loads, transpose reads for the rhs operand).  Segments the
+  // caller marks as sharing their lhs tiles in runs of 4 go four to a
+  // workgroup; otherwise one segment per workgroup with 64-deep K stages.
+  if (dtype == EJ_BF16 && ad && !bd && d->k % 32 == 0 && d->b_sn == 1 && d->b_sk % 8 == 0 &&
+      bm == bn && (bm == 128 || bm == 64) && src.n_a_tiles < (int64_t(1) << 31) &&
+      src.n_b_tiles < (int64_t(1) << 31)) {
     const uint16_t *a = static_cast<const uint16_t *>(A);
     const uint16_t *b = static_cast<const uint16_t *>(B);
+    const bool grouped = src.seg_off && d->seg_group > 0 && d->seg_group % 4 == 0;
+    if (grouped || d->k % 64 != 0) {
+      *status = launch_seg_gemm(bm, grouped ? 4 : 1, a, b, C, src, g, n_seg, stream);
+      return true;
+    }
     if (bm == 128)
       hipLaunchKernelGGL((tile_gemm_dma_kernel<128, 128, EJ_DMA_BK_128, EJ_DMA_STAGES_128>),
                          dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, a, b, C, src, g);

@@ -141,6 +141,30 @@ def _join_dev(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys, l
                           lambda m: _join_radices(lhs, rhs, keys, m), cols)
 
 
+def _segment_run(rhs: SparseTensorRelation, join_keys, agg_keys) -> int:
+    """Length of the runs of consecutive output segments that contract the
+    same lhs tiles in the same order, or 0 when the relations do not show
+    one.  With the last output dimension taken from the rhs, the earlier ones
+    from the lhs, and every rhs tile present (a dense rhs whose only other
+    dimensions are join dimensions), the segments of one lhs-derived output
+    prefix are consecutive, one per rhs grid step along that dimension, and
+    each pairs the same lhs tiles with a different rhs tile.  The einsum
+    kernels use it to read each lhs tile once for several output tiles; they
+    check it on the data, so a wrong value costs speed only."""
+    if not agg_keys or agg_keys[-1][0] != 1 or any(s != 0 for s, _ in agg_keys[:-1]):
+        return 0
+    d = agg_keys[-1][1]
+    rdims = {b for _, b in join_keys}
+    if d in rdims or len(rdims) + 1 != rhs.ndim:
+        return 0
+    full = 1
+    for x in range(rhs.ndim):
+        full *= _grid(rhs, x)
+    if rhs.num_tuples != full:
+        return 0
+    return _grid(rhs, d)
+
+
 # Pair counts of recent joins, keyed by the coordinate buffers, their shapes,
 # the keys and the radices: a bound for the next execute_sparse on the same
 # relations, which can then queue its whole step without waiting for the
@@ -336,6 +360,7 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
 
     def operands():
         desc = _device.describe(kernel_string, lhs.tile_shape, rhs.tile_shape)
+        desc.seg_group = _segment_run(rhs, [tuple(k) for k in join_keys], agg)
         return (desc, *_same_dtype(_dev_values(lhs.values), _dev_values(rhs.values)))
 
     def radices(maxima):

@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 2
+#define EJ_ABI_VERSION 3
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -102,7 +102,14 @@ typedef struct ej_einsum_desc {
   int64_t a_elems, b_elems, c_elems; /* elements per lhs / rhs / output tile */
   /* GEMM form (valid when is_gemm == 1): C[b][m][n] = sum_k A[b][m][k] B[b][k][n] */
   int32_t is_gemm;
-  int32_t pad_;
+  /* Scheduling hint set by the caller (ej_einsum_describe writes 0): the
+   * output segments come in aligned runs of this many consecutive segments
+   * that contract the same lhs tiles in the same order, as an lhs row does
+   * against a dense rhs.  The segment einsum then computes up to that many
+   * segments per workgroup, reading each lhs tile once for all of them.  A
+   * wrong hint costs speed, never correctness: each workgroup checks its
+   * segments and falls back to pair-by-pair accumulation. */
+  int32_t seg_group;
   int64_t batch, m, n, k;
   int64_t a_sb, a_sm, a_sk;
   int64_t b_sb, b_sk, b_sn;

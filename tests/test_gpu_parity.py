@@ -263,6 +263,96 @@ def test_gemm_index_out_of_range_contributes_nothing(gpu):
 
 
 # ---------------------------------------------------------------------------
+# grouped segment einsum: several output segments per workgroup when the
+# segments contract the same lhs tiles (an lhs row against a dense rhs)
+
+def _matmul_rels(rng, tile, rows, inner, cols, lhs_density, rhs_density=1.0):
+    """bf16 'ij,jk->ik' relations: lhs [rows x inner] tiles at lhs_density,
+    rhs [inner x cols] tiles at rhs_density (1.0: dense)."""
+    def pick(grid, dens):
+        n = grid[0] * grid[1]
+        k = max(1, int(round(dens * n)))
+        flat = np.sort(rng.choice(n, size=k, replace=False))
+        return np.stack(np.unravel_index(flat, grid), axis=1).astype(np.int32)
+
+    ac, bc = pick((rows, inner), lhs_density), pick((inner, cols), rhs_density)
+    av = R.bf16_round(rng.standard_normal((len(ac), tile, tile)).astype(np.float32))
+    bv = R.bf16_round(rng.standard_normal((len(bc), tile, tile)).astype(np.float32))
+    return (R.Rel(ac, av, (rows * tile, inner * tile), (tile, tile)),
+            R.Rel(bc, bv, (inner * tile, cols * tile), (tile, tile)))
+
+
+def _segment_einsum_groups(lhs, rhs, groups, li_override=None):
+    """Runs the device join, plan and fused einsum with each seg_group hint;
+    returns the plan's output coordinates and {hint: values}."""
+    from einjax_amd import _device
+
+    L, Rr = dev_rel(lhs, "bf16"), dev_rel(rhs, "bf16")
+    li, ri = sd._join_dev(L, Rr, [(1, 0)], L.coords, Rr.coords)
+    coords, offs, perm, _ = _device.segment_plan(L.coords, Rr.coords, li, ri, [(0, 0), (1, 1)],
+                                                  [sd._grid(L, 0), sd._grid(Rr, 1)])
+    if li_override is not None:
+        li = li_override(li)
+    desc = _device.describe("ij,jk->ik", lhs.tile_shape, rhs.tile_shape)
+    out = {}
+    for gsz in groups:
+        desc.seg_group = gsz
+        out[gsz] = _device.segment_einsum(desc, L.values, Rr.values, li, ri, perm,
+                                          offs).cpu().numpy()
+    return coords.cpu().numpy(), out
+
+
+@pytest.mark.parametrize("tile,rows,inner,cols,dens", [
+    (128, 6, 5, 8, 0.5),    # uniform groups of 4 on 128 x 128 tiles (8 waves)
+    (64, 5, 7, 12, 0.4),    # 64 x 64 tiles (4 waves)
+    (64, 2, 70, 4, 1.0),    # 70 pairs per segment: pair table in two chunks
+])
+def test_grouped_segment_einsum(gpu, tile, rows, inner, cols, dens):
+    note("grouped segment einsum", tile, rows, inner, cols, dens)
+    rng = np.random.default_rng(tile + rows + inner)
+    lhs, rhs = _matmul_rels(rng, tile, rows, inner, cols, dens)
+    assert sd._segment_run(host_rel(rhs), [(1, 0)], [(0, 0), (1, 1)]) == cols
+    coords, out = _segment_einsum_groups(lhs, rhs, (0, cols))
+    want = R.execute_sparse(lhs, rhs, [(1, 0)], "ij,jk->ik", [(0, 0), (1, 1)], precision="fp64")
+    npt.assert_array_equal(coords, want.coords)
+    # same accumulation order per output tile: bitwise equal to one segment per workgroup
+    npt.assert_array_equal(out[cols], out[0])
+    assert R.rel_l2(out[cols], want.values) <= TOL["bf16"]
+
+
+@pytest.mark.parametrize("cols,rhs_dens", [(6, 1.0), (8, 0.6), (5, 1.0)])
+def test_grouped_segment_einsum_wrong_hint(gpu, cols, rhs_dens):
+    """A hint the data does not bear out (groups straddling rows, sparse rhs,
+    a segment count that is not a multiple of 4) costs speed, not results."""
+    note("grouped segment einsum, wrong hint", cols, rhs_dens)
+    rng = np.random.default_rng(cols)
+    lhs, rhs = _matmul_rels(rng, 128, 5, 6, cols, 0.5, rhs_dens)
+    coords, out = _segment_einsum_groups(lhs, rhs, (0, 4, 8))
+    want = R.execute_sparse(lhs, rhs, [(1, 0)], "ij,jk->ik", [(0, 0), (1, 1)], precision="fp64")
+    npt.assert_array_equal(coords, want.coords)
+    npt.assert_array_equal(out[4], out[0])
+    npt.assert_array_equal(out[8], out[0])
+    assert R.rel_l2(out[0], want.values) <= TOL["bf16"]
+
+
+def test_grouped_segment_einsum_invalid_index(gpu):
+    """An out-of-range lhs index inside a group contributes nothing there,
+    as it does with one segment per workgroup."""
+    note("grouped segment einsum, invalid index")
+    rng = np.random.default_rng(11)
+    lhs, rhs = _matmul_rels(rng, 128, 4, 5, 8, 0.6)
+
+    def corrupt(li):
+        li = li.clone()
+        li[3] = -1
+        li[10] = 10 ** 6
+        return li
+
+    _, out = _segment_einsum_groups(lhs, rhs, (0, 8), li_override=corrupt)
+    npt.assert_array_equal(out[8], out[0])
+
+
+# ---------------------------------------------------------------------------
 # segment sum
 
 def test_segment_sum_known_answers_and_order(gpu):
