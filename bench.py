@@ -18,7 +18,7 @@ GEMM, segment sum; plus tiling), achieved GB/s against HBM for
 join+gather+segment-sum, the roofline of the dominant kernel, and the CPU
 oracle timed on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--all-configs]
 """
 
 from __future__ import annotations
@@ -127,12 +127,97 @@ def cpu_baseline(w, band_tiles: int, min_seconds: float = 10.0):
     }
 
 
+CONFIG_NAMES = ["blocksparse_1k", "blocksparse_16k_bf16", "sparse_sparse_zipf",
+                "batched_banded_bf16", "order3"]
+
+
+def measure_config(name: str, reps: int = 5) -> dict:
+    """One workload at full size: the execute_sparse step (wall clock) and
+    the fused segment einsum alone (HIP events), with the effective TFLOP/s,
+    the MFMA fraction and the compulsory-byte rate of the fused kernel.
+    Coordinates come from the seeded generator; tile values are drawn on the
+    GPU (N(0,1), or U(-1,1) for the Zipf workload) since only timing is
+    reported here (parity at these shapes is the test suite's job)."""
+    import torch
+
+    from einjax_amd import SparseTensorRelation, _device, execute_sparse
+    from einjax_amd.execution import sparse_dispatch as sd
+    from oracle import generators as G
+    from oracle import workload as W
+
+    w = G.WORKLOADS[name](values=False)
+    L, Rr = w["lhs"], w["rhs"]
+    bf16 = w["dtype"] == "bf16"
+    dt = torch.bfloat16 if bf16 else torch.float32
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    uniform = name == "sparse_sparse_zipf"
+
+    def dev(r):
+        shape = (r.coords.shape[0], *r.tile_shape)
+        v = torch.rand(shape, generator=gen, device="cuda") * 2 - 1 if uniform else \
+            torch.randn(shape, generator=gen, device="cuda")
+        return SparseTensorRelation(torch.from_numpy(r.coords).cuda(), v.to(dt), r.shape,
+                                    r.tile_shape)
+
+    lhs, rhs = dev(L), dev(Rr)
+    jk, ak, ks = w["join_keys"], w["agg_keys"], w["kernel_string"]
+
+    def step():
+        return execute_sparse(lhs, rhs, jk, ks, ak)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / reps
+    lc, rc = lhs.coords, rhs.coords
+    li, ri = sd._join_dev(lhs, rhs, jk, lc, rc)
+    P = li.numel()
+    radices = [sd._grid(lhs if s == 0 else rhs, d) for s, d in ak]
+    coords, offs, perm, _ = _device.segment_plan(lc, rc, li, ri, ak, radices)
+    U = coords.shape[0]
+    desc = _device.describe(ks, L.tile_shape, Rr.tile_shape)
+    run = sd._segment_run(rhs, jk, ak)
+    desc.seg_group = run
+    fused = lambda: _device.segment_einsum(desc, lhs.values, rhs.values, li, ri, perm, offs)
+    t_fused = event_time_ms(fused, reps)
+    t_fused_single = None
+    if run:
+        desc.seg_group = 0
+        t_fused_single = event_time_ms(fused, reps)
+    F = W.flops_gemm(ks, L.tile_shape, Rr.tile_shape, P)
+    e = 2 if bf16 else 4
+    out_tile = sd._infer_output_tile_shape(ks, L.tile_shape, Rr.tile_shape)
+    B_fused = W.bytes_fused(int(torch.unique(li).numel()), int(torch.unique(ri).numel()),
+                            L.tile_shape, Rr.tile_shape, e, U, out_tile, len(ak))
+    peak = MFMA_PEAK_TFLOPS["bf16" if bf16 else "fp32"]
+    res = {
+        "workload": w["name"], "dtype": w["dtype"], "pairs": P, "output_tiles": U,
+        "lhs_tiles": int(L.coords.shape[0]), "rhs_tiles": int(Rr.coords.shape[0]),
+        "gflop": F / 1e9, "ms_per_step": ms_step, "tflops_step": F / ms_step / 1e9,
+        "segment_run": run, "fused_ms": t_fused, "fused_tflops": F / t_fused / 1e9,
+        "fused_mfma_frac": F / t_fused / 1e9 / peak, "fused_compulsory_bytes": B_fused,
+        "fused_compulsory_gbs": B_fused / t_fused / 1e6,
+        "fused_compulsory_hbm_frac": B_fused / t_fused / 1e6 / HBM_PEAK_GBS,
+    }
+    if t_fused_single is not None:
+        res["fused_ms_one_segment_per_workgroup"] = t_fused_single
+    del lhs, rhs, li, ri, coords, offs, perm
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--all-configs", action="store_true",
+                    help="also time every workload configuration at full size (adds 'configs')")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path runs "
@@ -174,7 +259,6 @@ def main():
         out = step()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    P_pairs = None
 
     # ---- stages ----------------------------------------------------------
     lc, rc = lhs.coords, rhs.coords
@@ -266,6 +350,13 @@ def main():
         res["cpu_baseline"] = cpu_baseline(w, band_tiles=16)
     else:
         res["cpu_baseline"] = None
+    if args.all_configs:
+        del lhs, rhs, li, ri, coords, offs, perm, out
+        torch.cuda.empty_cache()
+        res["configs"] = {}
+        for name in CONFIG_NAMES:
+            log(f"config {name} ...")
+            res["configs"][name] = measure_config(name)
     print(json.dumps(res), flush=True)
 
 
