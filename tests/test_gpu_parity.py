@@ -118,10 +118,11 @@ def test_segment_plan_sizes(gpu, P, radix):
 
 
 @pytest.mark.parametrize("n_lhs,n_rhs", [(1, 1), (8192, 8192), (8193, 100), (100, 8193),
-                                         (20000, 30000)])
+                                         (300, 65536), (300, 65537), (20000, 30000)])
 def test_join_sizes(gpu, n_lhs, n_rhs):
     """Both join orders around the single-workgroup probe limits (8192 build
-    keys in LDS, 8192 probe keys), bit-exact against the oracle."""
+    keys in LDS, 8192 probe keys) and at a large probe side, bit-exact
+    against the oracle."""
     note("join sizes", n_lhs, n_rhs)
     rng = np.random.default_rng(n_lhs * 7 + n_rhs)
     lc = rng.integers(0, 2000, (n_lhs, 2), dtype=np.int32)
