@@ -592,6 +592,15 @@ __device__ inline i32x2_t ds_read_tr16_b64(uint32_t addr) {
   return v;
 }
 
+// The same at LDS byte address addr + OFF (the instruction's offset field).
+template <int OFF>
+__device__ inline i32x2_t ds_read_tr16_b64_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "LDS offset field");
+  i32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+  return v;
+}
+
 // s_waitcnt lgkmcnt(0), threaded through the values it guards so that their
 // consumers cannot be scheduled ahead of it.
 template <int N>
@@ -824,7 +833,8 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 }
 
 // ---------------------------------------------------------------------------
-// Grouped segment GEMM, bf16: G consecutive output segments per workgroup.
+// Grouped segment GEMM: G consecutive output segments per workgroup,
+// operands streamed HBM -> LDS ring (bf16 or fp32).
 //
 // Consecutive segments often contract the same sequence of lhs tiles: an
 // lhs row against a dense rhs gives segments (i, k), (i, k+1), ... that all
@@ -839,9 +849,12 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 //
 // The tile indices of the group's pairs are read once, one pair per lane,
 // and passed to the issue loop with readlane, so issuing a stage waits on
-// nothing but the ring.  LDS layout and the rhs transpose reads are those
-// of tile_gemm_dma_kernel.  Four waves tile the group's BM x (G * BN)
-// output as WGM x (4 / WGM); each wave's columns lie in one segment.
+// nothing but the ring.  Every stage is one K-chunk of 32 of both operands,
+// copied with 16-byte direct loads (global_load_lds_dwordx4) whose per-lane
+// source addresses are permuted so that the chunks land swizzled in LDS.
+// NW waves tile the group's BM x (G * BN) output as WGM x (NW / WGM); each
+// wave's columns lie in one segment.  The operand policy (SegOpBf16,
+// SegOpF32) fixes the LDS layout, the swizzles and the MFMA loop.
 
 __device__ inline void pair_tile_idx(const PairSrc &s, int64_t q, int32_t *a, int32_t *b) {
   const int64_t p = s.perm ? s.perm[q] : q;
@@ -856,52 +869,176 @@ __device__ inline int32_t lane_value(int32_t v, int lane) {
   return __builtin_amdgcn_readlane(v, lane);
 }
 
-template <int BM, int BN, int NS, int G, int WGM, int NW>
-__global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *__restrict__ A,
-                                                           const uint16_t *__restrict__ B,
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// bf16 operands, lhs [m][k] and rhs [k][n] tiles, v_mfma_f32_16x16x32_bf16.
+// LDS: lhs chunk [BM][32] (64-byte rows, 16-byte chunk c of row r at
+// c ^ ((r >> 2) & 3)), rhs chunk [32][BN] as tile_gemm_dma_kernel lays it
+// out (read with ds_read_b64_tr_b16).
+template <int BM_, int BN_>
+struct SegOpBf16 {
+  using elem = uint16_t;
+  static constexpr bool kBf16 = true;
+  static constexpr int BM = BM_, BN = BN_, BK = 32;
+  static constexpr int A_ROWB = BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
+  static constexpr int B_ROWB = BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
+  static_assert(CHA == 4 && (CHB == 8 || CHB == 16), "row widths");
+
+  // Element offset (inside a stage) of the 16 bytes that `lane` copies into
+  // LDS block `blk` (1 KB) of the lhs / rhs chunk.
+  __device__ static uint32_t a_src(int blk, int lane, const GemmGeom &g) {
+    const int row = blk * (1024 / A_ROWB) + lane / CHA;
+    const int c = (lane % CHA) ^ swz_a<CHA>(row);
+    return static_cast<uint32_t>(row * g.a_sm + c * 8);
+  }
+  __device__ static uint32_t b_src(int blk, int lane, const GemmGeom &g) {
+    const int krow = blk * (64 / CHB) + lane / CHB;
+    const int j = (lane % CHB) ^ swz_b<CHB>(krow);
+    return static_cast<uint32_t>(krow * g.b_sk + j * 8);
+  }
+
+  // Per-lane LDS read offsets of one wave (bytes inside a slot; rd[0] for
+  // the lhs, rd[1 + j] for rhs fragment j).  The lhs swizzle depends on the
+  // lane only, so fragment i sits a constant away from fragment 0.  Of the
+  // two rhs transpose reads of a fragment (k rows t and 4 + t of the lane
+  // group's 8) the second has the same swizzle, 4 rows further: an
+  // immediate offset.  The MFMA loop is seg_gemm_kernel's.
+  template <int FN>
+  static constexpr int n_rd = 1 + FN;
+
+  template <int FM, int FN>
+  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FN>], int row0, int wcol,
+                                      uint32_t b_region, int lane) {
+    rd[0] = static_cast<uint32_t>((row0 + (lane & 15)) * A_ROWB +
+                                  (((lane >> 4) ^ swz_a<CHA>(lane & 15)) * 16));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n0 = wcol + j * 16;
+      const int t = (lane & 15) >> 2, qq = lane & 3;
+      const int jc = (n0 >> 3) + (qq >> 1);
+      const int krow = (lane >> 4) * 8 + t;
+      const int phys = jc ^ swz_b<CHB>(krow);
+      rd[1 + j] = b_region + static_cast<uint32_t>(krow * B_ROWB + phys * 16 + (qq & 1) * 8);
+    }
+  }
+};
+
+// fp32 operands, lhs [m][k] and rhs [k][n] tiles, v_mfma_f32_16x16x4f32.
+// The 32 k of a stage are split over 8 MFMAs so that lane group g = lane / 16
+// of MFMA 4h + c takes k = 16h + 4g + c: each lane then reads its lhs values
+// of four MFMAs with one 16-byte read (chunk 4h + g of its row), and its rhs
+// values as four 4-byte reads of rows 16h + 4g + c.  The order of the k terms
+// inside the fp32 sum differs from k-major by construction; the contraction
+// is the same.
+// LDS: lhs chunk [BM][32] (128-byte rows, chunk c of row r at
+// c ^ (r & 7) ^ ((r >> 3) & 1)); rhs chunk [32][BN] (chunk c of k-row r at
+// c ^ 4 ((r >> 2) & 3), so the four lane groups of a read hit four bank
+// quarters).
+template <int BM_, int BN_>
+struct SegOpF32 {
+  using elem = float;
+  static constexpr bool kBf16 = false;
+  static constexpr int BM = BM_, BN = BN_, BK = 32;
+  static constexpr int A_ROWB = BK * 4, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
+  static constexpr int B_ROWB = BN * 4, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
+  static_assert(CHA == 8 && CHB >= 8, "row widths");
+
+  __device__ static int swa(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+  __device__ static int swb(int krow) { return CHB >= 16 ? 4 * ((krow >> 2) & 3) : 4 * ((krow >> 2) & 1); }
+
+  __device__ static uint32_t a_src(int blk, int lane, const GemmGeom &g) {
+    const int row = blk * (1024 / A_ROWB) + lane / CHA;
+    const int c = (lane % CHA) ^ swa(row);
+    return static_cast<uint32_t>(row * g.a_sm + c * 4);
+  }
+  __device__ static uint32_t b_src(int blk, int lane, const GemmGeom &g) {
+    const int krow = blk * (1024 / B_ROWB) + lane / CHB;
+    const int c = (lane % CHB) ^ swb(krow);
+    return static_cast<uint32_t>(krow * g.b_sk + c * 4);
+  }
+
+  // Per-lane LDS read offsets (rd[h], h = 0, 1: lhs chunk 4h + g of row
+  // row0 + (lane & 15); rd[2 + j]: column wcol + 16j + (lane & 15) of k-row
+  // 4g).  The MFMA loop is seg_gemm_kernel's.
+  template <int FN>
+  static constexpr int n_rd = 2 + FN;
+
+  template <int FM, int FN>
+  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FN>], int row0, int wcol,
+                                      uint32_t b_region, int lane) {
+    const int row = row0 + (lane & 15), g = lane >> 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      rd[h] = static_cast<uint32_t>(row * A_ROWB + (((4 * h + g) ^ swa(row)) * 16));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = wcol + j * 16 + (lane & 15);
+      const int krow = 4 * g;  // rows 16h + 4g + c share this swizzle
+      rd[2 + j] = b_region + static_cast<uint32_t>(krow * B_ROWB +
+                                                   (((col >> 2) ^ swb(krow)) * 16) + (col & 3) * 4);
+    }
+  }
+};
+
+template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
+__global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
+                                                           const typename Op::elem *__restrict__ B,
                                                            float *__restrict__ C, PairSrc src,
-                                                           GemmGeom g, int64_t n_seg) {
+                                                           GemmGeom g, int64_t n_seg, int spw,
+                                                           int mb_loop) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int BK = 32;  // one MFMA K step per stage
+  using T = typename Op::elem;
+  constexpr int BM = Op::BM, BN = Op::BN, BK = Op::BK;
   constexpr int WGN = NW / WGM;
   constexpr int WM = BM / WGM, WN = G * BN / WGN;
   static_assert(WGM * WGN == NW && WM % 16 == 0 && WN % 16 == 0 && BN % WN == 0, "wave tiling");
   constexpr int FM = WM / 16, FN = WN / 16;
-  constexpr int A_ROWB = BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
-  constexpr int B_ROWB = BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
+  constexpr int A_BYTES = Op::A_BYTES, B_BYTES = Op::B_BYTES;
   constexpr int SLOT = A_BYTES + G * B_BYTES;
   constexpr int LPA = A_BYTES / (1024 * NW), LPB = B_BYTES / (1024 * NW);  // 1 KB loads per wave
   static_assert(LPA * 1024 * NW == A_BYTES && LPB * 1024 * NW == B_BYTES, "chunks split over waves");
   constexpr int LPS = LPA + G * LPB;
   static_assert(NS >= 2 && NS <= 6 && (NS - 2) * LPS < 64, "ring depth / vmcnt range");
   static_assert(G == 1 || G == 2 || G == 4, "group size");
-  static_assert(CHA == 4 && (CHB == 8 || CHB == 16), "row widths");
-  constexpr uint32_t ALL = 0xF, SKIP = 0xE;  // stage codes (else: the one segment fed)
+  // Segments one workgroup covers: a group of G, or (G == 1) up to SMAX
+  // consecutive segments computed one after another.
+  constexpr int SMAX = G > 1 || !MULTI ? G : 8;
+  // Stage codes, 8 bits per ring slot: the segment (inside the workgroup's
+  // range) the stage feeds, kAll for a stage shared by the whole group, or
+  // with kSkip set for a pair whose tile index is invalid.
+  constexpr uint32_t kAll = 0x20, kSkip = 0x10;
   __shared__ __align__(1024) unsigned char ring[NS * SLOT];
   const uint32_t ring_lds = static_cast<uint32_t>(
       reinterpret_cast<size_t>((__attribute__((address_space(3))) unsigned char *)ring));
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
-  const int wseg = (wn * WN) / BN;  // segment (inside the group) of this wave's columns
+  const int wseg = (wn * WN) / BN;  // segment (inside a group) of this wave's columns
   const int wcol = (wn * WN) % BN;  // its first column inside that segment's tile
+  // Work of this workgroup: m-blocks [mb0, mb0 + nmb) of segments
+  // [seg0, seg0 + nls) for one n-block and one batch index.
   int64_t lb = xcd_logical_block();
   const int64_t nb = lb % g.nblocks;
   lb /= g.nblocks;
-  const int64_t mb = lb % g.mblocks;
-  lb /= g.mblocks;
+  int64_t mb0 = 0, nmb = g.mblocks;
+  if (!MULTI || !mb_loop) {
+    mb0 = lb % g.mblocks;
+    lb /= g.mblocks;
+    nmb = 1;
+  }
   const int64_t bi = lb % g.batch;
-  const int64_t seg0 = (lb / g.batch) * G;
+  const int segs = G > 1 || !MULTI ? G : spw;
+  const int64_t seg0 = (lb / g.batch) * segs;
   int64_t nseg = n_seg;
   if (src.n_live) {
     const int64_t live = ld_uniform(src.n_live, 0);
     nseg = live < nseg ? live : nseg;
   }
   if (seg0 >= nseg) return;
-  const int nls = nseg - seg0 < G ? static_cast<int>(nseg - seg0) : G;  // live segments
-  int32_t off[G + 1];  // off[s] = off[nls] for s > nls
+  const int nls = nseg - seg0 < segs ? static_cast<int>(nseg - seg0) : segs;  // live segments
+  int32_t off[SMAX + 1];  // off[s] = off[nls] for s > nls
 #pragma unroll
-  for (int s = 0; s <= G; ++s) {
+  for (int s = 0; s <= SMAX; ++s) {
     const int64_t ss = seg0 + (s <= nls ? s : nls);
     off[s] = src.seg_off ? ld_uniform(src.seg_off, ss) : static_cast<int32_t>(ss);
   }
@@ -912,52 +1049,72 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *
 
   // Pair table, one pair per lane, 64 pairs per chunk.  Shared mode: lane t
   // holds pair t of every segment (ta = its lhs tile, tb[s] = segment s's rhs
-  // tile).  Sequential mode: lane r holds the r-th pair of the group's plan
-  // range (ta, tb[0]) and, for G > 1, its segment in tb[1].
-  int32_t ta = -1, tb[G];
+  // tile).  Sequential mode: lane r holds the r-th pair of the workgroup's plan
+  // range (ta, tb[0]) and its segment in tsg.
+  // (The pair arrays are copied out of src so that no lambda refers to the
+  // kernel argument itself, which would keep it in scratch memory.)
+  const int32_t *const s_perm = src.perm;
+  const int64_t *const s_lidx = src.lidx, *const s_ridx = src.ridx;
+  const int64_t n_at = src.n_a_tiles, n_bt = src.n_b_tiles;
+  int32_t ta = -1, tb[G], tsg = 0;
 #pragma unroll
   for (int s = 0; s < G; ++s) tb[s] = -1;
   int chunk = -1;
+  // Both loaders assign every table variable, in the same order, whatever
+  // the lane holds (the compiler otherwise merges their stores through a
+  // selected pointer and moves the table to scratch memory).
   auto load_shared = [&](int c) -> bool {  // whether the chunk's pairs share their lhs tiles
     const int t = c * 64 + lane;
     bool bad = false;
+    int32_t na = -1, nb[G];
+#pragma unroll
+    for (int s = 0; s < G; ++s) nb[s] = -1;
     if (t < len) {  // loads batched per level: plan -> pair -> tiles
       int64_t p[G], a[G], b[G];
 #pragma unroll
       for (int s = 0; s < G; ++s) p[s] = off[s] + t;
-      if (src.perm) {
+      if (s_perm) {
 #pragma unroll
-        for (int s = 0; s < G; ++s) p[s] = src.perm[p[s]];
+        for (int s = 0; s < G; ++s) p[s] = s_perm[p[s]];
       }
 #pragma unroll
-      for (int s = 0; s < G; ++s) a[s] = src.lidx ? src.lidx[p[s]] : p[s];
+      for (int s = 0; s < G; ++s) a[s] = s_lidx ? s_lidx[p[s]] : p[s];
 #pragma unroll
-      for (int s = 0; s < G; ++s) b[s] = src.ridx ? src.ridx[p[s]] : p[s];
+      for (int s = 0; s < G; ++s) b[s] = s_ridx ? s_ridx[p[s]] : p[s];
 #pragma unroll
       for (int s = 0; s < G; ++s) {
-        const bool ok = a[s] >= 0 && a[s] < src.n_a_tiles && b[s] >= 0 && b[s] < src.n_b_tiles;
+        const bool ok = a[s] >= 0 && a[s] < n_at && b[s] >= 0 && b[s] < n_bt;
         bad = bad || !ok || a[s] != a[0];
-        tb[s] = ok ? static_cast<int32_t>(b[s]) : -1;
+        nb[s] = ok ? static_cast<int32_t>(b[s]) : -1;
       }
-      ta = static_cast<int32_t>(a[0]);
+      na = static_cast<int32_t>(a[0]);
     }
+    ta = na;
+#pragma unroll
+    for (int s = 0; s < G; ++s) tb[s] = nb[s];
+    tsg = 0;
     chunk = c;
     return __builtin_amdgcn_ballot_w64(bad) == 0;
   };
   auto load_seq = [&](int c) {
     const int r = c * 64 + lane;
-    if (off[0] + r < off[G]) {
-      int32_t a, b;
-      pair_tile_idx(src, off[0] + r, &a, &b);
-      ta = a;
-      tb[0] = b;
-      if constexpr (G > 1) {
-        int s = 0;
+    int32_t na = -1, nb = -1, ns = 0;
+    if (off[0] + r < off[SMAX]) {
+      const int64_t q = off[0] + r;
+      const int64_t p = s_perm ? s_perm[q] : q;
+      const int64_t a = s_lidx ? s_lidx[p] : p;
+      const int64_t b = s_ridx ? s_ridx[p] : p;
+      const bool ok = a >= 0 && a < n_at && b >= 0 && b < n_bt;
+      na = ok ? static_cast<int32_t>(a) : -1;
+      nb = ok ? static_cast<int32_t>(b) : -1;
 #pragma unroll
-        for (int u = 1; u < G; ++u) s += off[0] + r >= off[u] ? 1 : 0;
-        tb[1] = s;
-      }
+      for (int u = 1; u < SMAX; ++u) ns += q >= off[u] ? 1 : 0;
     }
+    ta = na;
+    tb[0] = nb;
+#pragma unroll
+    for (int s = 1; s < G; ++s) tb[s] = -1;
+    tsg = ns;
     chunk = c;
   };
   if (uni) {
@@ -965,55 +1122,25 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *
   }
   if (!uni) load_seq(0);
   const int nkc = static_cast<int>(g.k / BK);
-  const int64_t npos = uni ? len : off[G] - off[0];
-  const int64_t stages = npos * nkc;
+  const int64_t npos = uni ? len : off[SMAX] - off[0];  // pairs per m-block
+  const int64_t per_mb = npos * nkc;                    // stages per m-block
+  const int64_t stages = per_mb * nmb;
 
   // Per-lane source offsets inside a stage (elements), fixed for the kernel;
   // 32-bit so that the loads take a scalar base plus a vector offset.
   uint32_t a_src[LPA], b_src[LPB];
 #pragma unroll
-  for (int v = 0; v < LPA; ++v) {
-    const int blk = v * NW + wave;
-    const int row = blk * (1024 / A_ROWB) + lane / CHA;
-    const int c = (lane % CHA) ^ swz_a<CHA>(row);
-    a_src[v] = static_cast<uint32_t>(row * g.a_sm + c * 8);
-  }
+  for (int v = 0; v < LPA; ++v) a_src[v] = Op::a_src(v * NW + wave, lane, g);
 #pragma unroll
-  for (int v = 0; v < LPB; ++v) {
-    const int blk = v * NW + wave;
-    const int krow = blk * (64 / CHB) + lane / CHB;
-    const int j = (lane % CHB) ^ swz_b<CHB>(krow);
-    b_src[v] = static_cast<uint32_t>(krow * g.b_sk + j * 8);
-  }
-  const int64_t a_off0 = bi * g.a_sb + mb * BM * g.a_sm;
+  for (int v = 0; v < LPB; ++v) b_src[v] = Op::b_src(v * NW + wave, lane, g);
   const int64_t b_off0 = bi * g.b_sb + nb * BN;
 
-  // Per-lane LDS read offsets inside a slot (bytes).  A: 16 rows x one
-  // 16-byte k chunk per fragment; the row swizzle depends on the lane only,
-  // so fragment i is a constant away from fragment 0.  B: two transpose
-  // reads per fragment (k rows 0-3 and 4-7 of the lane group's 8).
-  const uint32_t a_rd = static_cast<uint32_t>(
-      (wm * WM + (lane & 15)) * A_ROWB + (((lane >> 4) ^ swz_a<CHA>(lane & 15)) * 16));
-  uint32_t b_rd[FN][2];
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n0 = wcol + j * 16;
-    const int t = (lane & 15) >> 2, qq = lane & 3;
-    const int jc = (n0 >> 3) + (qq >> 1);
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int krow = (lane >> 4) * 8 + hh * 4 + t;
-      const int phys = jc ^ swz_b<CHB>(krow);
-      b_rd[j][hh] = static_cast<uint32_t>(A_BYTES + wseg * B_BYTES + krow * B_ROWB + phys * 16 +
-                                          (qq & 1) * 8);
-    }
-  }
-
-  int64_t ipos = 0;
+  // Issue cursor: m-block imb, pair ipos, K-chunk ikc.
+  int64_t imb = mb0, ipos = 0;
   int ikc = 0;
-  uint32_t codes = 0;  // 4 bits per ring slot
+  uint64_t codes = 0;  // 8 bits per ring slot
   auto issue = [&](int64_t st) {
-    if ((ipos >> 6) != chunk) {  // groups of more than 64 pairs only
+    if ((ipos >> 6) != chunk) {  // more than 64 pairs per m-block only
       if (uni) load_shared(static_cast<int>(ipos >> 6));
       else load_seq(static_cast<int>(ipos >> 6));
     }
@@ -1024,16 +1151,16 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *
     if (uni) {
 #pragma unroll
       for (int s = 0; s < G; ++s) bt[s] = lane_value(tb[s], li);
-      code = ALL;
+      code = kAll;
     } else {
       const int32_t b0 = lane_value(tb[0], li);
 #pragma unroll
       for (int s = 0; s < G; ++s) bt[s] = b0;
-      code = at < 0 ? SKIP : (G > 1 ? static_cast<uint32_t>(lane_value(tb[1], li)) : ALL);
+      code = static_cast<uint32_t>(lane_value(tsg, li)) | (at < 0 ? kSkip : 0u);
     }
     const int64_t a_tile = at < 0 ? 0 : at;
     unsigned char *slot = ring + (st % NS) * SLOT;
-    const uint16_t *ab = A + a_tile * g.a_elems + a_off0 + ikc * BK;
+    const T *ab = A + a_tile * g.a_elems + bi * g.a_sb + imb * BM * g.a_sm + ikc * BK;
 #pragma unroll
     for (int v = 0; v < LPA; ++v)
       __builtin_amdgcn_global_load_lds(ab + a_src[v], EJ_LDS(slot + (v * NW + wave) * 1024), 16,
@@ -1041,18 +1168,21 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *
 #pragma unroll
     for (int s = 0; s < G; ++s) {
       const int64_t b_tile = bt[s] < 0 ? 0 : bt[s];
-      const uint16_t *bb = B + b_tile * g.b_elems + b_off0 + ikc * BK * g.b_sk;
+      const T *bb = B + b_tile * g.b_elems + b_off0 + ikc * BK * g.b_sk;
 #pragma unroll
       for (int v = 0; v < LPB; ++v)
         __builtin_amdgcn_global_load_lds(
             bb + b_src[v], EJ_LDS(slot + A_BYTES + s * B_BYTES + (v * NW + wave) * 1024), 16, 0,
             0);
     }
-    const int sh = static_cast<int>(st % NS) * 4;
-    codes = (codes & ~(0xFu << sh)) | (code << sh);
+    const int sh = static_cast<int>(st % NS) * 8;
+    codes = (codes & ~(uint64_t(0xFF) << sh)) | (uint64_t(code) << sh);
     if (++ikc == nkc) {
       ikc = 0;
-      ++ipos;
+      if (++ipos == npos) {
+        ipos = 0;
+        ++imb;
+      }
     }
   };
 
@@ -1061,58 +1191,166 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_bf16_kernel(const uint16_t *
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // This wave's part of output block (segment seg0 + sseg, m-block mb):
+  // the accumulators, or zeros.  (Stores issued mid-loop count in vmcnt and
+  // retire in order with the ring's loads, so the next stage wait also
+  // covers them; measured, that beats both an exact allowance for them and
+  // fewer, wider stores after an in-quad transpose.)
+  const uint32_t row0 = static_cast<uint32_t>(wm * WM + (lane >> 4) * 4);
+  const uint32_t col0 = static_cast<uint32_t>(wcol + (lane & 15));
+  auto block_ptr = [&](int sseg, int64_t mb) -> float * {
+    return C + (seg0 + sseg) * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+  };
+  auto store_zero = [&](int sseg, int64_t mb) {
+    if (sseg >= nls) return;
+    float *cb = block_ptr(sseg, mb);
+    for (int i = 0; i < FM; ++i)
+      for (int j = 0; j < FN; ++j)
+        for (int r = 0; r < 4; ++r)
+          cb[(row0 + i * 16 + r) * g.c_sm + (col0 + j * 16) * g.c_sn] = 0.f;
+  };
 
 #pragma unroll
   for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < stages) issue(s0);
 
+  uint32_t rd[Op::template n_rd<FN>];
+  Op::template read_offsets<FM, FN>(rd, wm * WM, wcol,
+                                    static_cast<uint32_t>(A_BYTES + wseg * B_BYTES), lane);
+  int64_t cmb = mb0;      // compute cursor's m-block
+  int64_t cleft = per_mb;  // stages left in it
   for (int64_t st = 0; st < stages; ++st) {
     const int64_t later = stages - 1 - st < NS - 2 ? stages - 1 - st : NS - 2;
+    const int slot = static_cast<int>(st % NS);
     wait_stage<NS, LPS>(static_cast<int>(later));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    const int slot = static_cast<int>(st % NS);
-    const uint32_t code = (codes >> (slot * 4)) & 0xFu;
+    const uint32_t code = static_cast<uint32_t>(codes >> (slot * 8)) & 0xFFu;
     if (st + NS - 1 < stages) issue(st + NS - 1);
-    if (code != ALL && code != static_cast<uint32_t>(wseg)) continue;  // wave-uniform
-    uint32_t base = ring_lds + static_cast<uint32_t>(slot * SLOT);
-    asm volatile("" : "+s"(base));  // keeps the read addresses per stage, not per slot
-    bf16x8_t af[FM];
-    i32x4_t bq[FN];
+    // Whether this wave takes part: every wave for a shared stage or (one
+    // segment per wave column group) any valid stage of a lone segment;
+    // with G > 1, only the waves of the stage's segment.  Wave-uniform.
+    const bool feed = !(code & kSkip) && (code == kAll || G == 1 ||
+                                          (code & 0xFu) == static_cast<uint32_t>(wseg));
+    if (feed) {
+      uint32_t base = ring_lds + static_cast<uint32_t>(slot * SLOT);
+      asm volatile("" : "+s"(base));  // keeps the read addresses per stage, not per slot
+      // The stage's MFMAs (written out here: as a separate function taking the
+      // accumulators by reference the compiler kept extra copies of them).
+      typedef const __attribute__((address_space(3))) unsigned char *lds_ptr;
+      if constexpr (Op::kBf16) {
+        constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
+        bf16x8_t af[FM];
+        i32x4_t bq[FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[i] = *reinterpret_cast<const bf16x8_t *>(
-          (const __attribute__((address_space(3))) unsigned char *)(size_t)(base + a_rd) +
-          i * 16 * A_ROWB);
+        for (int i = 0; i < FM; ++i)
+          af[i] = *reinterpret_cast<const bf16x8_t *>((lds_ptr)(size_t)(base + rd[0]) +
+                                                     i * 16 * A_ROWB);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const i32x2_t h0 = ds_read_tr16_b64(base + b_rd[j][0]);
-      const i32x2_t h1 = ds_read_tr16_b64(base + b_rd[j][1]);
-      bq[j] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
-    }
-    lgkm_wait_all<FN>(bq);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            af[i], __builtin_bit_cast(bf16x8_t, bq[j]), acc[i][j], 0, 0, 0);
-  }
-
-  if (wseg < nls) {
-    float *cb = C + (seg0 + wseg) * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
-    const uint32_t row0 = static_cast<uint32_t>(wm * WM + (lane >> 4) * 4);
-    const uint32_t col0 = static_cast<uint32_t>(wcol + (lane & 15));
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t o = static_cast<uint32_t>((row0 + i * 16 + r) * g.c_sm +
-                                                   (col0 + j * 16) * g.c_sn);
-          cb[o] = acc[i][j][r];
+        for (int j = 0; j < FN; ++j) {
+          const i32x2_t h0 = ds_read_tr16_b64(base + rd[1 + j]);
+          const i32x2_t h1 = ds_read_tr16_b64_at<4 * B_ROWB>(base + rd[1 + j]);
+          bq[j] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
         }
+        lgkm_wait_all<FN>(bq);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                af[i], __builtin_bit_cast(bf16x8_t, bq[j]), acc[i][j], 0, 0, 0);
+      } else {
+        constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          f32x4_t af[FM];
+          float bv[FN][4];
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+            af[i] = *reinterpret_cast<const f32x4_t *>((lds_ptr)(size_t)(base + rd[h]) +
+                                                      i * 16 * A_ROWB);
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              bv[j][c] = *reinterpret_cast<const float *>((lds_ptr)(size_t)(base + rd[2 + j]) +
+                                                         (16 * h + c) * B_ROWB);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+              for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][c], bv[j][c], acc[i][j],
+                                                                 0, 0, 0);
+        }
+      }
+    }
+    // Output after the last stage of an output block: the end of an m-block,
+    // or (one segment per wave column group) the end of a segment's stages.
+    // A single-unit workgroup (!MULTI) writes once, after the loop.
+    if constexpr (!MULTI) continue;
+    bool done = --cleft == 0;
+    if constexpr (G == 1) {
+      if (!done && !uni) {
+        const uint32_t nxt = static_cast<uint32_t>(codes >> (((st + 1) % NS) * 8)) & 0xFu;
+        done = nxt != (code & 0xFu);
+      }
+    }
+    if (done) {
+      const int sseg = G > 1 ? wseg : static_cast<int>(code & 0xFu);
+      if (sseg < nls) {
+        float *cb = block_ptr(sseg, cmb);
+        // Strides made opaque here, so that the store offsets are formed at
+        // the store and not hoisted out of the stage loop into registers.
+        int32_t csm = static_cast<int32_t>(g.c_sm), csn = static_cast<int32_t>(g.c_sn);
+        asm volatile("" : "+s"(csm), "+s"(csn));
+        const uint32_t o0 = row0 * csm + col0 * csn;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              cb[o0 + (i * 16 + r) * csm + j * 16 * csn] = acc[i][j][r];
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (cleft == 0) {
+        ++cmb;
+        cleft = per_mb;
+      }
+    }
+  }
+  if constexpr (!MULTI) {
+    if (wseg < nls) {
+      float *cb = block_ptr(wseg, mb0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t o = static_cast<uint32_t>((row0 + i * 16 + r) * g.c_sm +
+                                                     (col0 + j * 16) * g.c_sn);
+            cb[o] = acc[i][j][r];
+          }
+    }
+    return;
+  }
+  // Every output block is written once, also where no stage fed it: a
+  // segment without pairs (a caller's plan may hold one) or a workgroup with
+  // no stages at all gets zeros.
+  if constexpr (G == 1) {
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s)
+      if (s < nls && off[s + 1] == off[s])
+        for (int64_t mb = mb0; mb < mb0 + nmb; ++mb) store_zero(s, mb);
+  } else {
+    if (stages == 0)
+      for (int64_t mb = mb0; mb < mb0 + nmb; ++mb) store_zero(wseg, mb);
   }
 #endif
 }
@@ -1207,39 +1445,81 @@ int launch_gemm_bk(int bm, int bn, bool ad, bool bd, const void *A, const void *
   return EJ_E_UNSUPPORTED;
 }
 
-// Ring depth of the grouped kernel (LDS: NS x (BM*32 + G*32*BN) x 2 bytes).
-#ifndef EJ_SEG_NS1
-#define EJ_SEG_NS1 4
-#endif
-#ifndef EJ_SEG_NS4
-#define EJ_SEG_NS4 4
+// Ring depth of the grouped kernels: NS stages of (BM + G * BN) x 32 operand
+// elements, capped by the 160 KB of LDS.
+constexpr int seg_ring_depth(int slot_bytes, int want) {
+  return want * slot_bytes <= 163840 ? want : 163840 / slot_bytes;
+}
+#ifndef EJ_SEG_NS
+#define EJ_SEG_NS 4
 #endif
 
-template <int BM, int G, int NS, int WGM, int NW>
-int launch_seg_gemm_t(const uint16_t *A, const uint16_t *B, float *C, const PairSrc &src,
+// Work per workgroup.  Short work items leave a workgroup mostly filling and
+// draining its ring, so a workgroup takes every m-block of its segments, and
+// (G == 1) several consecutive segments, as long as the grid keeps at least
+// kSegMinBlocks workgroups.
+constexpr int64_t kSegMinBlocks = 1024;
+constexpr int kSegMaxRun = 8;  // segments per workgroup when G == 1 (SMAX)
+
+template <class Op, int G, int WGM, int NW>
+int launch_seg_gemm_t(const void *A, const void *B, float *C, const PairSrc &src,
                       const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
-  const int64_t nblk = ceil_div(n_seg, G) * g.batch * g.mblocks * g.nblocks;
+  constexpr int NS = seg_ring_depth(Op::A_BYTES + G * Op::B_BYTES, EJ_SEG_NS);
+  const int64_t groups = ceil_div(n_seg, G);
+  int64_t per_group = g.batch * g.nblocks;  // workgroups per group, m-blocks looped inside
+  const int mb_loop = g.mblocks > 1 && groups * per_group >= kSegMinBlocks ? 1 : 0;
+  if (!mb_loop) per_group *= g.mblocks;
+  int spw = 1;
+  if (G == 1 && src.seg_off)
+    while (spw < kSegMaxRun && ceil_div(n_seg, 2 * spw) * per_group >= kSegMinBlocks) spw *= 2;
+  const int64_t nblk = ceil_div(groups, spw) * per_group;
   if (nblk >= (int64_t(1) << 32)) {
     set_error("einsum launch too large");
     return EJ_E_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((seg_gemm_bf16_kernel<BM, BM, NS, G, WGM, NW>),
-                     dim3(static_cast<unsigned>(nblk)), dim3(NW * 64), 0, stream, A, B, C, src, g,
-                     n_seg);
+  using T = typename Op::elem;
+  if (mb_loop || spw > 1)
+    hipLaunchKernelGGL((seg_gemm_kernel<Op, NS, G, WGM, NW, true>),
+                       dim3(static_cast<unsigned>(nblk)), dim3(NW * 64), 0, stream,
+                       static_cast<const T *>(A), static_cast<const T *>(B), C, src, g, n_seg, spw,
+                       mb_loop);
+  else
+    hipLaunchKernelGGL((seg_gemm_kernel<Op, NS, G, WGM, NW, false>),
+                       dim3(static_cast<unsigned>(nblk)), dim3(NW * 64), 0, stream,
+                       static_cast<const T *>(A), static_cast<const T *>(B), C, src, g, n_seg, 1,
+                       0);
   EJ_LAUNCH_CHECK();
   return EJ_OK;
 }
 
-// Group of 4: 128 x 128 tiles on 8 waves (2 x 4, one segment per wave
-// column), 64 x 64 tiles on 4 waves (one segment per wave).
-int launch_seg_gemm(int bm, int grp, const uint16_t *A, const uint16_t *B, float *C,
-                    const PairSrc &src, const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
+// bf16: 128 x 128 tiles, a group of 4 on 8 waves (2 x 4, one segment per wave
+// column) or one segment on 4 waves (2 x 2); 64 x 64 tiles on 4 waves.
+int launch_seg_gemm_bf16(int bm, int grp, const void *A, const void *B, float *C,
+                         const PairSrc &src, const GemmGeom &g, int64_t n_seg,
+                         hipStream_t stream) {
   if (bm == 128) {
-    if (grp == 4) return launch_seg_gemm_t<128, 4, EJ_SEG_NS4, 2, 8>(A, B, C, src, g, n_seg, stream);
-    return launch_seg_gemm_t<128, 1, EJ_SEG_NS1, 2, 4>(A, B, C, src, g, n_seg, stream);
+    if (grp == 4) return launch_seg_gemm_t<SegOpBf16<128, 128>, 4, 2, 8>(A, B, C, src, g, n_seg, stream);
+    return launch_seg_gemm_t<SegOpBf16<128, 128>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
   }
-  if (grp == 4) return launch_seg_gemm_t<64, 4, EJ_SEG_NS4, 1, 4>(A, B, C, src, g, n_seg, stream);
-  return launch_seg_gemm_t<64, 1, EJ_SEG_NS1, 2, 4>(A, B, C, src, g, n_seg, stream);
+  if (grp == 4) return launch_seg_gemm_t<SegOpBf16<64, 64>, 4, 1, 4>(A, B, C, src, g, n_seg, stream);
+  return launch_seg_gemm_t<SegOpBf16<64, 64>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
+}
+
+// fp32 on 4 waves: a group of 4 puts one segment on each wave (WGM = 1);
+// one segment splits the tile into wave tiles of at least 16 x 16.
+int launch_seg_gemm_f32(int bm, int bn, int grp, const void *A, const void *B, float *C,
+                        const PairSrc &src, const GemmGeom &g, int64_t n_seg,
+                        hipStream_t stream) {
+#define EJ_F32_CASE(M_, N_, WGM1_)                                                             \
+  if (bm == M_ && bn == N_)                                                                    \
+    return grp == 4                                                                            \
+               ? launch_seg_gemm_t<SegOpF32<M_, N_>, 4, 1, 4>(A, B, C, src, g, n_seg, stream)  \
+               : launch_seg_gemm_t<SegOpF32<M_, N_>, 1, WGM1_, 4>(A, B, C, src, g, n_seg, stream);
+  EJ_F32_CASE(32, 32, 2) EJ_F32_CASE(32, 64, 2) EJ_F32_CASE(64, 32, 2)
+  EJ_F32_CASE(64, 64, 2) EJ_F32_CASE(128, 32, 4) EJ_F32_CASE(128, 64, 2)
+#undef EJ_F32_CASE
+  set_error("no fp32 segment GEMM configuration for %dx%d", bm, bn);
+  return EJ_E_UNSUPPORTED;
 }
 
 int pick_block(int64_t x) { return x % 128 == 0 ? 128 : x % 64 == 0 ? 64 : x % 32 == 0 ? 32 : 0; }
@@ -1290,7 +1570,7 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
     const uint16_t *b = static_cast<const uint16_t *>(B);
     const bool grouped = src.seg_off && d->seg_group > 0 && d->seg_group % 4 == 0;
     if (grouped || d->k % 64 != 0) {
-      *status = launch_seg_gemm(bm, grouped ? 4 : 1, a, b, C, src, g, n_seg, stream);
+      *status = launch_seg_gemm_bf16(bm, grouped ? 4 : 1, a, b, C, src, g, n_seg, stream);
       return true;
     }
     if (bm == 128)
@@ -1307,6 +1587,19 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
       *status = EJ_OK;
     }
     return true;
+  }
+  // fp32, k-contiguous lhs, n-contiguous rhs, K a multiple of 32, 16-byte
+  // rows: the LDS-ring kernel with fp32 MFMAs (grouped like the bf16 one).
+  if (dtype == EJ_F32 && ad && !bd && d->k % 32 == 0 && d->b_sn == 1 && d->b_sk % 4 == 0 &&
+      (bm == 32 || bm == 64 || bm == 128) && src.n_a_tiles < (int64_t(1) << 31) &&
+      src.n_b_tiles < (int64_t(1) << 31)) {
+    const int fbn = d->n % 64 == 0 ? 64 : 32;
+    if (d->n % fbn == 0) {
+      g.nblocks = d->n / fbn;
+      const bool grouped = src.seg_off && d->seg_group > 0 && d->seg_group % 4 == 0;
+      *status = launch_seg_gemm_f32(bm, fbn, grouped ? 4 : 1, A, B, C, src, g, n_seg, stream);
+      return true;
+    }
   }
   if (dtype == EJ_BF16) {
     *status = bk == 64 ? launch_gemm_bk<uint16_t, 64>(bm, bn, ad, bd, A, B, C, src, g, nblk, stream)

@@ -354,6 +354,105 @@ def test_grouped_segment_einsum_invalid_index(gpu):
 
 
 # ---------------------------------------------------------------------------
+# several output blocks per workgroup (every m-block of a group, or several
+# consecutive segments): used when the launch would otherwise have at least
+# 1024 workgroups of short work
+
+def _segments_fp64(lhs, rhs, li, ri, perm, off, spec, useg):
+    """float64 sums of the per-pair einsums of the segments useg, in plan
+    order (numpy on the host), for a spot check of large cases."""
+    out = []
+    for u in useg:
+        ps = perm[off[u]:off[u + 1]]
+        acc = None
+        for p in ps:
+            v = np.einsum(spec, lhs.values[li[p]].astype(np.float64),
+                          rhs.values[ri[p]].astype(np.float64))
+            acc = v if acc is None else acc + v
+        out.append(acc)
+    return np.stack(out)
+
+
+def test_multi_segment_workgroups_fp32(gpu):
+    """fp32 sparse x sparse with ~4,600 output tiles: four consecutive
+    segments per workgroup in the fused einsum.  Checked against the unfused
+    path (one pair per workgroup) and, on a sample, float64 sums."""
+    note("multi-segment workgroups fp32")
+    rng = np.random.default_rng(21)
+    g, t = 96, 64
+
+    def rel(n):
+        flat = np.sort(rng.choice(g * g, size=n, replace=False))
+        c = np.stack(np.unravel_index(flat, (g, g)), axis=1).astype(np.int32)
+        return R.Rel(c, rng.uniform(-1, 1, (n, t, t)).astype(np.float32), (g * t, g * t), (t, t))
+
+    lhs, rhs = rel(900), rel(900)
+    L, Rr = dev_rel(lhs), dev_rel(rhs)
+    fused = ej.execute_sparse(L, Rr, [(1, 0)], "ij,jk->ik", [(0, 0), (1, 1)])
+    split = ej.execute_sparse(L, Rr, [(1, 0)], "ij,jk->ik", [(0, 0), (1, 1)], fused=False)
+    U = fused.num_tuples
+    assert U >= 4096, U  # enough segments for the multi-segment launch
+    npt.assert_array_equal(fused.coords.cpu().numpy(), split.coords.cpu().numpy())
+    fv, sv = fused.values.cpu().numpy(), split.values.cpu().numpy()
+    assert R.rel_l2(fv, sv) <= 1e-6
+    li, ri = R.coordinate_join(lhs.coords, rhs.coords, [(1, 0)])
+    oc = R.compute_output_coords(lhs.coords, rhs.coords, li, ri, [(0, 0), (1, 1)])
+    _, perm, off, _ = R.segment_plan(oc)
+    sample = np.sort(rng.choice(U, 48, replace=False))
+    want = _segments_fp64(lhs, rhs, li, ri, perm, off, "ij,jk->ik", sample)
+    assert R.rel_l2(fv[sample], want) <= TOL["fp32"]
+
+
+def test_multi_mblock_workgroups_fp32(gpu):
+    """'ijk,kl->ijl' with 32^3 fp32 tiles (M = 1024 rows, 8 m-blocks of 128)
+    against a dense rhs, ~1,200 groups of 4 segments: every m-block of a group
+    in one workgroup.  Checked on a sample of output tiles in float64."""
+    note("multi-m-block workgroups fp32")
+    w = G.workload_order3(n=512, l=1024, density=0.1)
+    lhs, rhs = w["lhs"], w["rhs"]
+    got = ej.execute_sparse(dev_rel(lhs), dev_rel(rhs), w["join_keys"], w["kernel_string"],
+                            w["agg_keys"])
+    U = got.num_tuples
+    assert U // 4 >= 1024, U
+    li, ri = R.coordinate_join(lhs.coords, rhs.coords, w["join_keys"])
+    oc = R.compute_output_coords(lhs.coords, rhs.coords, li, ri, w["agg_keys"])
+    uc, perm, off, _ = R.segment_plan(oc)
+    npt.assert_array_equal(got.coords.cpu().numpy(), uc)
+    rng = np.random.default_rng(3)
+    sample = np.sort(rng.choice(U, 40, replace=False))
+    want = _segments_fp64(lhs, rhs, li, ri, perm, off, w["kernel_string"], sample)
+    assert R.rel_l2(got.values.cpu().numpy()[sample], want) <= TOL["fp32"]
+
+
+def test_multi_segment_workgroups_empty_segments(gpu):
+    """A caller's plan may hold segments without pairs: their output tiles
+    are zero, also when a workgroup covers several segments."""
+    note("multi-segment workgroups, empty segments")
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(8)
+    n_seg, t = 6000, 32
+    counts = rng.integers(0, 3, n_seg)  # 0, 1 or 2 pairs per segment
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    P = int(off[-1])
+    lv = rng.standard_normal((50, t, t)).astype(np.float32)
+    rv = rng.standard_normal((40, t, t)).astype(np.float32)
+    li = rng.integers(0, 50, P)
+    ri = rng.integers(0, 40, P)
+    perm = rng.permutation(P).astype(np.int32)
+    desc = _device.describe("ij,jk->ik", (t, t), (t, t))
+    c = lambda a: torch.from_numpy(a).cuda()
+    got = _device.segment_einsum(desc, c(lv), c(rv), c(li), c(ri), c(perm), c(off)).cpu().numpy()
+    pairs = np.einsum("pij,pjk->pik", lv[li].astype(np.float64), rv[ri].astype(np.float64))
+    want = np.zeros((n_seg, t, t))
+    for u in range(n_seg):
+        for q in range(off[u], off[u + 1]):
+            want[u] += pairs[perm[q]]
+    assert np.all(got[counts == 0] == 0)
+    assert R.rel_l2(got, want) <= TOL["fp32"]
+
+
+# ---------------------------------------------------------------------------
 # segment sum
 
 def test_segment_sum_known_answers_and_order(gpu):
