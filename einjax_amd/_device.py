@@ -340,3 +340,117 @@ def relation_to_dense(coords, values, shape, tile_shape) -> torch.Tensor:
                                            len(shape), i64_array(shape), i64_array(tile_shape),
                                            ptr(dense), stream_ptr()), "ej_relation_to_dense")
     return dense
+
+
+def _elem_code(t: torch.Tensor) -> int:
+    """Element dtype of a dense tensor or COO values: float64, float32 or bfloat16."""
+    if t.dtype == torch.float64:
+        return _lib.EJ_F64
+    return value_code(t)
+
+
+def _coo_count(dense: torch.Tensor):
+    lib = _lib.load()
+    code = _elem_code(dense)
+    nd = dense.dim()
+    shape = i64_array(dense.shape)
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_extract_coo_workspace_size(nd, shape, code, ctypes.byref(nbytes)),
+          "ej_extract_coo_workspace_size")
+    ws = workspace(nbytes.value, dense.device)
+    nnz = ctypes.c_int64()
+    check(lib.ej_extract_coo_count(ptr(dense), code, nd, shape, ptr(ws), ws.numel(),
+                                   ctypes.byref(nnz), stream_ptr()), "ej_extract_coo_count")
+    return nnz.value, ws, code, shape
+
+
+def count_nonzero(dense: torch.Tensor) -> int:
+    """Number of elements != 0 (NaN included) of a dense tensor."""
+    dense = dense.contiguous()
+    if dense.dim() == 0:
+        dense = dense.reshape(1)
+    return _coo_count(dense)[0]
+
+
+def extract_coo(dense: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense tensor -> (indices int32 [nnz, nd], values float64 [nnz]): the
+    elements != 0 in row-major order."""
+    lib = _lib.load()
+    dense = dense.contiguous()
+    nd = dense.dim()
+    n, ws, code, shape = _coo_count(dense)
+    idx = torch.empty((n, nd), dtype=torch.int32, device=dense.device)
+    vals = torch.empty((n,), dtype=torch.float64, device=dense.device)
+    check(lib.ej_extract_coo_fill(ptr(dense), code, nd, shape, ptr(ws), ws.numel(), n, ptr(idx),
+                                  ptr(vals), n, stream_ptr()), "ej_extract_coo_fill")
+    return idx, vals
+
+
+def bucket_coo(indices: torch.Tensor, values: torch.Tensor, shape,
+               tile_shape) -> tuple[torch.Tensor, torch.Tensor]:
+    """COO entries -> (coords int32 [T, nd], values [T, *tile_shape]).
+
+    float64 / float32 values give float32 tiles, bfloat16 values bfloat16
+    tiles.  Entries equal to zero are dropped; an element listed twice keeps
+    its last nonzero entry."""
+    lib = _lib.load()
+    nd = len(shape)
+    indices = indices.to(dtype=torch.int32).reshape(-1, nd).contiguous()
+    values = values.contiguous().reshape(-1)
+    code = _elem_code(values)
+    out_dtype = torch.bfloat16 if values.dtype == torch.bfloat16 else torch.float32
+    n = values.numel()
+    sh, ts = i64_array(shape), i64_array(tile_shape)
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_bucket_coo_workspace_size(n, ctypes.byref(nbytes)),
+          "ej_bucket_coo_workspace_size")
+    ws = workspace(nbytes.value, values.device)
+    n_tiles = ctypes.c_int64()
+    check(lib.ej_bucket_coo_count(ptr(indices), ptr(values), code, n, nd, sh, ts, ptr(ws),
+                                  ws.numel(), ctypes.byref(n_tiles), stream_ptr()),
+          "ej_bucket_coo_count")
+    T = n_tiles.value
+    coords = torch.empty((T, nd), dtype=torch.int32, device=values.device)
+    tiles = torch.empty((T, *tile_shape), dtype=out_dtype, device=values.device)
+    check(lib.ej_bucket_coo_fill(ptr(values), code, n, nd, sh, ts, ptr(ws), ws.numel(), T,
+                                 ptr(coords), ptr(tiles), T, stream_ptr()), "ej_bucket_coo_fill")
+    return coords, tiles
+
+
+def scheme_stats(tile_shapes, shape, dense: torch.Tensor | None = None,
+                 indices: torch.Tensor | None = None, values: torch.Tensor | None = None,
+                 bitmap_cap: int = 0):
+    """(num_tuples [S], value_count [S][nd]) as Python ints for each tile
+    shape, over the nonzero elements of a dense tensor or of COO entries."""
+    lib = _lib.load()
+    nd = len(shape)
+    tile_shapes = [tuple(int(t) for t in ts) for ts in tile_shapes]
+    S = len(tile_shapes)
+    if S == 0:
+        return [], []
+    sh = i64_array(shape)
+    flat = i64_array([t for ts in tile_shapes for t in ts])
+    nt = (ctypes.c_int64 * S)()
+    vc = (ctypes.c_int64 * (S * nd))()
+    nbytes = ctypes.c_size_t()
+    if dense is not None:
+        dense = dense.contiguous()
+        check(lib.ej_scheme_stats_workspace_size(nd, sh, S, flat, -1, 0, ctypes.byref(nbytes)),
+              "ej_scheme_stats_workspace_size")
+        ws = workspace(nbytes.value, dense.device)
+        check(lib.ej_scheme_stats_dense(ptr(dense), _elem_code(dense), nd, sh, S, flat, ptr(ws),
+                                        ws.numel(), nt, vc, stream_ptr()),
+              "ej_scheme_stats_dense")
+    else:
+        indices = indices.to(dtype=torch.int32).reshape(-1, nd).contiguous()
+        values = values.contiguous().reshape(-1)
+        n = values.numel()
+        check(lib.ej_scheme_stats_workspace_size(nd, sh, S, flat, n, bitmap_cap,
+                                                 ctypes.byref(nbytes)),
+              "ej_scheme_stats_workspace_size")
+        ws = workspace(nbytes.value, values.device)
+        check(lib.ej_scheme_stats_coo(ptr(indices), ptr(values), _elem_code(values), n, nd, sh,
+                                      S, flat, bitmap_cap, ptr(ws), ws.numel(), nt, vc,
+                                      stream_ptr()), "ej_scheme_stats_coo")
+    return ([int(nt[s]) for s in range(S)],
+            [tuple(int(vc[s * nd + l]) for l in range(nd)) for s in range(S)])

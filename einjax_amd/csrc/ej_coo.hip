@@ -1,0 +1,1153 @@
+// COO ingest, COO-to-tile bucketing and per-tile-shape occupancy statistics.
+//
+// Reference: SparseTensor (tensor/sparse.py:93-231).
+//   _extract_coo (:234-270): the elements != 0 of a dense array as int32
+//     indices in row-major order (np.nonzero) plus float64 values;
+//   to_relation (:160-219) for COO input: entries whose value is 0 are
+//     dropped (:184-187), the rest are grouped by tile coordinate in
+//     lexicographic order (np.unique(axis=0), :204-206) and scattered into
+//     zero tiles (:210-212); an element listed twice keeps its last entry,
+//     as numpy's fancy assignment leaves it;
+//   _compute_sparsity_metrics (:124-158) for the tile shapes of BaseTensor
+//     (tensor/base.py:39-49): num_tuples = number of distinct tile
+//     coordinates idx // tile_shape over the nonzero entries, value_count[l]
+//     = number of distinct idx[l] // tile_shape[l].
+//
+// Dense to COO: each wave owns a run of 64 * V * kCooRounds elements (V
+// elements = one 16-byte load per lane per round); a count pass, an
+// exclusive scan of the per-wave counts and a fill pass that compacts with
+// a wave prefix sum keep the row-major order without sorting.
+//
+// COO to tiles: one 64-bit key per entry, (tile index << wbits) | offset in
+// the tile, with dropped entries keyed past every tile; a stable radix sort
+// orders the entries by tile, then by element, then by input position;
+// tile-start flags and their scan number the tiles; the last entry of each
+// run of equal keys writes its value.
+//
+// Statistics: num_tuples of a tile shape is the number of set cells of its
+// occupancy map (one byte per tile of the grid).  The map of a tile shape
+// equals the map of a finer tile shape pooled by OR along one dimension:
+// every tile shape except (1, ..., 1) has a parent that divides its last
+// tile extent above 1 by that extent's smallest prime factor.  The maps are
+// built along that tree in depth-first order on a stack inside the
+// workspace, so the live maps are the ancestors of the current one (at most
+// about twice the finest map).  value_count[l] of a tile shape t is
+// num_tuples of the tile shape that equals the tensor shape in every
+// dimension except l, where it is t[l]: its grid is one tile wide in every
+// other dimension.  Those shapes join the tree.  For COO input, a tile
+// shape whose map would exceed bitmap_cap bytes is counted instead by
+// sorting the tile keys of the entries and counting distinct keys, and the
+// largest maps below the cap are built by marking the entries' tiles.
+#include "ej_internal.h"
+
+#include <algorithm>
+#include <array>
+#include <map>
+#include <vector>
+
+namespace ej {
+namespace {
+
+// ---- element access (T = double, float, or uint16_t holding bfloat16) ----
+__device__ inline bool nz(double x) { return x != 0.0; }  // NaN != 0 holds
+__device__ inline bool nz(float x) { return x != 0.0f; }
+__device__ inline bool nz(uint16_t x) { return (x & 0x7fffu) != 0; }  // +-0 are zero
+__device__ inline double as_f64(double x) { return x; }
+__device__ inline double as_f64(float x) { return static_cast<double>(x); }
+__device__ inline double as_f64(uint16_t x) {
+  return static_cast<double>(__uint_as_float(static_cast<uint32_t>(x) << 16));
+}
+// Tile element written for a nonzero entry: float64 rounds to fp32 (a value
+// that underflows is written as +0.0), fp32 and bf16 are kept.
+__device__ inline float tile_val(double x) {
+  const float f = static_cast<float>(x);
+  return f == 0.0f ? 0.0f : f;
+}
+__device__ inline float tile_val(float x) { return x; }
+__device__ inline uint16_t tile_val(uint16_t x) { return x; }
+
+int elem_size(int32_t dtype) { return dtype == EJ_F64 ? 8 : dtype == EJ_F32 ? 4 : 2; }
+
+__device__ inline int wave_sum_i32(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+__device__ inline int wave_incl_i32(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Adds the wave's total of v to *acc (one atomic per wave).
+__device__ inline void wave_add(unsigned long long *acc, int64_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  if ((threadIdx.x & 63) == 0 && v) atomicAdd(acc, static_cast<unsigned long long>(v));
+}
+
+// Number of bytes of w that are nonzero, for bytes holding 0 or 1.
+__device__ inline int bytes_set(uint32_t w) { return static_cast<int>((w * 0x01010101u) >> 24); }
+
+template <typename T>
+__global__ void fill_zero_kernel(T *p, int64_t n) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (; i < n; i += stride) p[i] = T(0);
+}
+
+inline unsigned stride_grid(int64_t work, int64_t cap_blocks = 8192) {
+  int64_t g = ceil_div(work > 0 ? work : 1, kBlock);
+  return static_cast<unsigned>(g < cap_blocks ? g : cap_blocks);
+}
+
+// ---------------------------------------------------------------------------
+// Dense to COO.
+constexpr int kCooRounds = 4;
+
+template <typename T> constexpr int vec_elems() { return 16 / static_cast<int>(sizeof(T)); }
+template <typename T> constexpr int64_t wave_run() {
+  return static_cast<int64_t>(kCooRounds) * 64 * vec_elems<T>();
+}
+
+struct DenseShape {
+  int32_t nd;
+  int64_t ext[EJ_MAX_DIMS];
+};
+
+// V consecutive elements from index i (a multiple of V); a 16-byte load when
+// the base is aligned and the group is whole.
+template <typename T>
+__device__ inline void load_group(const T *__restrict__ p, int64_t i, int64_t n, bool vec,
+                                  T (&v)[vec_elems<T>()]) {
+  constexpr int V = vec_elems<T>();
+  if (vec && i + V <= n) {
+    const uint4 w = *reinterpret_cast<const uint4 *>(p + i);
+    __builtin_memcpy(&v[0], &w, 16);
+  } else {
+#pragma unroll
+    for (int k = 0; k < V; ++k) v[k] = i + k < n ? p[i + k] : T(0);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_count_kernel(const T *__restrict__ dense, int64_t n,
+                                                        int64_t n_runs, bool vec,
+                                                        int64_t *__restrict__ counts) {
+  constexpr int V = vec_elems<T>();
+  const int lane = threadIdx.x & 63;
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (s >= n_runs) return;  // whole waves leave together
+  const int64_t base = s * wave_run<T>();
+  T v[kCooRounds][V];
+#pragma unroll
+  for (int r = 0; r < kCooRounds; ++r)
+    load_group(dense, base + static_cast<int64_t>(r * 64 + lane) * V, n, vec, v[r]);
+  int c = 0;
+#pragma unroll
+  for (int r = 0; r < kCooRounds; ++r)
+#pragma unroll
+    for (int k = 0; k < V; ++k) c += nz(v[r][k]) ? 1 : 0;
+  c = wave_sum_i32(c);
+  if (lane == 0) counts[s] = c;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_fill_kernel(const T *__restrict__ dense, int64_t n,
+                                                       int64_t n_runs, bool vec, DenseShape sh,
+                                                       const int64_t *__restrict__ excl,
+                                                       int64_t nnz_cap,
+                                                       int32_t *__restrict__ idx,
+                                                       double *__restrict__ vals) {
+  constexpr int V = vec_elems<T>();
+  const int lane = threadIdx.x & 63;
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (s >= n_runs) return;
+  const int64_t base = s * wave_run<T>();
+  int64_t off = excl[s];
+  for (int r = 0; r < kCooRounds; ++r) {
+    const int64_t i0 = base + static_cast<int64_t>(r * 64 + lane) * V;
+    T v[V];
+    load_group(dense, i0, n, vec, v);
+    int c = 0;
+#pragma unroll
+    for (int k = 0; k < V; ++k) c += nz(v[k]) ? 1 : 0;
+    const int incl = wave_incl_i32(c);
+    const int total = __shfl(incl, 63, 64);
+    if (c) {
+      int64_t pos = off + incl - c;
+      int64_t co[EJ_MAX_DIMS];
+      int64_t t = i0;
+#pragma unroll
+      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d) {
+        co[d] = 0;
+        if (d < sh.nd) {
+          co[d] = t % sh.ext[d];
+          t /= sh.ext[d];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        if (nz(v[k]) && pos < nnz_cap) {
+#pragma unroll
+          for (int d = 0; d < EJ_MAX_DIMS; ++d)
+            if (d < sh.nd) idx[pos * sh.nd + d] = static_cast<int32_t>(co[d]);
+          vals[pos] = as_f64(v[k]);
+          ++pos;
+        }
+        bool carry = true;  // next element in row-major order
+#pragma unroll
+        for (int d = EJ_MAX_DIMS - 1; d >= 0; --d) {
+          if (d < sh.nd && carry) {
+            if (++co[d] == sh.ext[d]) co[d] = 0;
+            else carry = false;
+          }
+        }
+      }
+    }
+    off += total;
+  }
+}
+
+struct ExtractWs {
+  int64_t *scalars, *counts, *excl;
+  void *scan_ws;
+  size_t bytes;
+};
+
+ExtractWs carve_extract(void *base, int64_t n_runs) {
+  Carver c(base);
+  ExtractWs w;
+  w.scalars = c.take<int64_t>(4);
+  w.counts = c.take<int64_t>(n_runs);
+  w.excl = c.take<int64_t>(n_runs);
+  w.scan_ws = c.take<char>(static_cast<int64_t>(scan_workspace_bytes(n_runs)));
+  w.bytes = c.off;
+  return w;
+}
+
+int dense_shape(int32_t ndim, const int64_t *shape, DenseShape *sh, int64_t *n) {
+  EJ_CHECK_ARG(ndim >= 1 && ndim <= EJ_MAX_DIMS, "ndim=%d outside [1, %d]", ndim, EJ_MAX_DIMS);
+  EJ_CHECK_ARG(shape, "shape is null");
+  sh->nd = ndim;
+  int64_t total = 1;
+  for (int d = 0; d < ndim; ++d) {
+    EJ_CHECK_ARG(shape[d] >= 0 && shape[d] <= INT32_MAX, "shape[%d]=%lld outside [0, 2^31)", d,
+                 (long long)shape[d]);
+    sh->ext[d] = shape[d];
+    total *= shape[d];
+  }
+  *n = total;
+  return EJ_OK;
+}
+
+int64_t extract_runs(int64_t n, int32_t dtype) {
+  const int64_t run = static_cast<int64_t>(kCooRounds) * 64 * (16 / elem_size(dtype));
+  return ceil_div(n, run);
+}
+
+// ---------------------------------------------------------------------------
+// COO to tiles.
+struct CooGeom {
+  int32_t nd;
+  int64_t shape[EJ_MAX_DIMS], tile[EJ_MAX_DIMS], grid[EJ_MAX_DIMS];
+  int64_t tile_elems, n_tiles;
+  int32_t wbits;      // bits of the offset inside a tile
+  int32_t bits;       // key bits the sort orders
+  uint64_t sentinel;  // key of a dropped entry: n_tiles << wbits
+};
+
+int bits_for(uint64_t values) {  // bits for keys in [0, values)
+  int b = 0;
+  while (b < 64 && (uint64_t(1) << b) < values) ++b;
+  return b;
+}
+
+int make_coo_geom(int32_t ndim, const int64_t *shape, const int64_t *tile, CooGeom *g) {
+  EJ_CHECK_ARG(ndim >= 1 && ndim <= EJ_MAX_DIMS, "ndim=%d outside [1, %d]", ndim, EJ_MAX_DIMS);
+  EJ_CHECK_ARG(shape && tile, "null shape");
+  g->nd = ndim;
+  unsigned __int128 tiles = 1, elems = 1;
+  for (int d = 0; d < ndim; ++d) {
+    EJ_CHECK_ARG(tile[d] >= 1 && shape[d] >= 0 && shape[d] <= INT32_MAX,
+                 "bad extent in dim %d", d);
+    EJ_CHECK_ARG(shape[d] % tile[d] == 0,
+                 "tile_shape[%d]=%lld does not evenly divide shape[%d]=%lld", d,
+                 (long long)tile[d], d, (long long)shape[d]);
+    g->shape[d] = shape[d];
+    g->tile[d] = tile[d];
+    g->grid[d] = shape[d] / tile[d];
+    tiles *= static_cast<uint64_t>(g->grid[d]);
+    elems *= static_cast<uint64_t>(tile[d]);
+  }
+  if (tiles >= (static_cast<unsigned __int128>(1) << 62) ||
+      elems >= (static_cast<unsigned __int128>(1) << 62)) {
+    set_error("tile grid or tile too large for 64-bit keys");
+    return EJ_E_UNSUPPORTED;
+  }
+  g->n_tiles = static_cast<int64_t>(tiles);
+  g->tile_elems = static_cast<int64_t>(elems);
+  g->wbits = bits_for(static_cast<uint64_t>(g->tile_elems));
+  const int tbits = bits_for(static_cast<uint64_t>(g->n_tiles) + 1);
+  if (tbits + g->wbits > 63) {
+    set_error("tile index and in-tile offset need %d bits; at most 63 are supported",
+              tbits + g->wbits);
+    return EJ_E_UNSUPPORTED;
+  }
+  g->bits = tbits + g->wbits;
+  g->sentinel = static_cast<uint64_t>(g->n_tiles) << g->wbits;
+  return EJ_OK;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_keys_kernel(const int32_t *__restrict__ idx,
+                                                       const T *__restrict__ vals, int64_t nnz,
+                                                       CooGeom g, uint64_t *__restrict__ keys,
+                                                       int32_t *__restrict__ order,
+                                                       int64_t *bad) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  uint64_t tkey = 0, wkey = 0;
+  bool ok = true;
+#pragma unroll
+  for (int d = 0; d < EJ_MAX_DIMS; ++d) {
+    if (d < g.nd) {
+      int64_t c = idx[i * g.nd + d];
+      if (c < 0 || c >= g.shape[d]) {
+        ok = false;
+        c = 0;
+      }
+      const uint32_t cu = static_cast<uint32_t>(c), tu = static_cast<uint32_t>(g.tile[d]);
+      tkey = tkey * static_cast<uint64_t>(g.grid[d]) + cu / tu;
+      wkey = wkey * static_cast<uint64_t>(tu) + cu % tu;
+    }
+  }
+  const bool keep = nz(vals[i]);
+  if (keep && !ok) *bad = 1;
+  keys[i] = keep && ok ? (tkey << g.wbits) | wkey : g.sentinel;
+  order[i] = static_cast<int32_t>(i);
+}
+
+__global__ __launch_bounds__(256) void coo_tile_flags_kernel(const uint64_t *__restrict__ keys,
+                                                             int64_t nnz, uint64_t sentinel,
+                                                             int wbits,
+                                                             int64_t *__restrict__ flags) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  const uint64_t k = keys[i];
+  flags[i] = k != sentinel && (i == 0 || (keys[i - 1] >> wbits) != (k >> wbits)) ? 1 : 0;
+}
+
+template <typename T, typename U>
+__global__ __launch_bounds__(256) void coo_scatter_kernel(
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ order,
+    const int64_t *__restrict__ flags, const int64_t *__restrict__ excl,
+    const T *__restrict__ vals, int64_t nnz, CooGeom g, int64_t n_tiles,
+    int32_t *__restrict__ coords, U *__restrict__ tiles) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  const uint64_t k = keys[i];
+  if (k == g.sentinel) return;
+  const int64_t slot = excl[i] + flags[i] - 1;
+  if (slot < 0 || slot >= n_tiles) return;
+  if (flags[i]) {
+    uint64_t t = k >> g.wbits;
+#pragma unroll
+    for (int d = EJ_MAX_DIMS - 1; d >= 0; --d) {
+      if (d < g.nd) {
+        const uint64_t gd = static_cast<uint64_t>(g.grid[d]);
+        coords[slot * g.nd + d] = static_cast<int32_t>(t % gd);
+        t /= gd;
+      }
+    }
+  }
+  if (i + 1 < nnz && keys[i + 1] == k) return;  // a later entry of this element wins
+  const uint64_t w = k & ((uint64_t(1) << g.wbits) - 1);
+  tiles[slot * g.tile_elems + static_cast<int64_t>(w)] = tile_val(vals[order[i]]);
+}
+
+struct CooWs {
+  int64_t *scalars;  // [0] tile count, [1] range flag
+  uint64_t *keys, *keys_alt;
+  int32_t *order, *order_alt;
+  int64_t *flags, *excl;
+  void *sort_ws, *scan_ws;
+  size_t bytes;
+};
+
+CooWs carve_coo(void *base, int64_t nnz) {
+  Carver c(base);
+  CooWs w;
+  w.scalars = c.take<int64_t>(4);
+  w.keys = c.take<uint64_t>(nnz);
+  w.keys_alt = c.take<uint64_t>(nnz);
+  w.order = c.take<int32_t>(nnz);
+  w.order_alt = c.take<int32_t>(nnz);
+  w.flags = c.take<int64_t>(nnz);
+  w.excl = c.take<int64_t>(nnz);
+  w.sort_ws = c.take<char>(static_cast<int64_t>(sort_workspace_bytes(nnz)));
+  w.scan_ws = c.take<char>(static_cast<int64_t>(scan_workspace_bytes(nnz)));
+  w.bytes = c.off;
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// Statistics.
+struct TileIdx {  // mixed-radix tile index of an element for one tile shape
+  int32_t nd;
+  int64_t shape[EJ_MAX_DIMS];
+  int64_t tile[EJ_MAX_DIMS];
+  int64_t grid[EJ_MAX_DIMS];
+  int64_t cells;  // tiles in the grid
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void dense_map_kernel(const T *__restrict__ dense, int64_t n,
+                                                        bool vec, uint8_t *__restrict__ map,
+                                                        unsigned long long *count) {
+  // One 4-element group per thread and iteration: one 32-bit store of flags.
+  const int64_t groups = (n + 3) / 4;
+  int64_t c = 0;
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < groups;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = q * 4;
+    T v[4];
+    if (vec && i + 4 <= n) {
+      if constexpr (sizeof(T) == 2) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(dense + i);
+        __builtin_memcpy(&v[0], &w, 8);
+      } else if constexpr (sizeof(T) == 4) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(dense + i);
+        __builtin_memcpy(&v[0], &w, 16);
+      } else {
+        const uint4 w0 = *reinterpret_cast<const uint4 *>(dense + i);
+        const uint4 w1 = *reinterpret_cast<const uint4 *>(dense + i + 2);
+        __builtin_memcpy(&v[0], &w0, 16);
+        __builtin_memcpy(&v[2], &w1, 16);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = i + k < n ? dense[i + k] : T(0);
+    }
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w |= (nz(v[k]) ? 1u : 0u) << (8 * k);
+    *reinterpret_cast<uint32_t *>(map + i) = w;  // map rows are padded to 256 bytes
+    c += bytes_set(w);
+  }
+  wave_add(count, c);
+}
+
+// Pooling by OR: in [outer][n_out * p][inner] -> out [outer][n_out][inner].
+struct PoolGeom {
+  int64_t outer, n_out, p, inner, total;  // total = outer * n_out * inner
+};
+
+// inner % 4 == 0: one 32-bit word of 4 outputs per thread.
+template <typename I>
+__global__ __launch_bounds__(256) void pool_words_kernel(const uint8_t *__restrict__ in,
+                                                         uint8_t *__restrict__ out, PoolGeom g,
+                                                         unsigned long long *count) {
+  const I words = static_cast<I>(g.total / 4);
+  const I inner = static_cast<I>(g.inner), n_out = static_cast<I>(g.n_out),
+          p = static_cast<I>(g.p);
+  int64_t c = 0;
+  for (I w = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
+       w += static_cast<I>(gridDim.x) * blockDim.x) {
+    const I o = w * 4;
+    const I r = o % inner, t = o / inner;
+    const I j = t % n_out, a = t / n_out;
+    const uint32_t *src =
+        reinterpret_cast<const uint32_t *>(in + ((a * n_out + j) * p * inner + r));
+    const I step = inner / 4;
+    uint32_t acc = 0;
+    for (I q = 0; q < p; ++q) acc |= src[q * step];
+    reinterpret_cast<uint32_t *>(out)[w] = acc;
+    c += bytes_set(acc);
+  }
+  wave_add(count, c);
+}
+
+// inner == 1, p == 2, total % 4 == 0: 8 input bytes -> 4 outputs per thread.
+__global__ __launch_bounds__(256) void pool_pairs_kernel(const uint8_t *__restrict__ in,
+                                                         uint8_t *__restrict__ out, int64_t total,
+                                                         unsigned long long *count) {
+  const int64_t words = total / 4;
+  int64_t c = 0;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
+       w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t x = reinterpret_cast<const uint64_t *>(in)[w];
+    const uint64_t y = x | (x >> 8);  // byte 2k holds the OR of input bytes 2k, 2k+1
+    const uint32_t acc = static_cast<uint32_t>((y & 0xff) | ((y >> 8) & 0xff00) |
+                                               ((y >> 16) & 0xff0000) |
+                                               ((y >> 24) & 0xff000000));
+    reinterpret_cast<uint32_t *>(out)[w] = acc;
+    c += bytes_set(acc);
+  }
+  wave_add(count, c);
+}
+
+// Any geometry: one output byte per thread.
+__global__ __launch_bounds__(256) void pool_bytes_kernel(const uint8_t *__restrict__ in,
+                                                         uint8_t *__restrict__ out, PoolGeom g,
+                                                         unsigned long long *count) {
+  int64_t c = 0;
+  for (int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; o < g.total;
+       o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = o % g.inner, t = o / g.inner;
+    const int64_t j = t % g.n_out, a = t / g.n_out;
+    const uint8_t *src = in + (a * g.n_out + j) * g.p * g.inner + r;
+    uint8_t acc = 0;
+    for (int64_t q = 0; q < g.p && !acc; ++q) acc |= src[q * g.inner];
+    out[o] = acc;
+    c += acc;
+  }
+  wave_add(count, c);
+}
+
+// Tile index of entry i for the tile shape in ti; false when the entry is
+// dropped (value 0) or lies outside the tensor (then *bad is set).
+template <typename T>
+__device__ inline bool entry_tile(const int32_t *__restrict__ idx, const T *__restrict__ vals,
+                                  int64_t i, const TileIdx &ti, int64_t *bad, uint64_t *tile) {
+  if (!nz(vals[i])) return false;
+  uint64_t t = 0;
+  bool ok = true;
+#pragma unroll
+  for (int d = 0; d < EJ_MAX_DIMS; ++d) {
+    if (d < ti.nd) {
+      const int64_t c = idx[i * ti.nd + d];
+      if (c < 0 || c >= ti.shape[d]) ok = false;
+      t = t * static_cast<uint64_t>(ti.grid[d]) +
+          static_cast<uint32_t>(c) / static_cast<uint32_t>(ti.tile[d]);
+    }
+  }
+  if (!ok) {
+    *bad = 1;
+    return false;
+  }
+  *tile = t;
+  return true;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_mark_kernel(const int32_t *__restrict__ idx,
+                                                       const T *__restrict__ vals, int64_t nnz,
+                                                       TileIdx ti, uint8_t *__restrict__ map,
+                                                       int64_t *bad) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  uint64_t t;
+  if (entry_tile(idx, vals, i, ti, bad, &t)) map[t] = 1;
+}
+
+__global__ __launch_bounds__(256) void map_count_kernel(const uint32_t *__restrict__ words,
+                                                        int64_t n_words,
+                                                        unsigned long long *count) {
+  int64_t c = 0;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < n_words;
+       w += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    c += bytes_set(words[w]);
+  wave_add(count, c);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void stat_keys_kernel(const int32_t *__restrict__ idx,
+                                                        const T *__restrict__ vals, int64_t nnz,
+                                                        TileIdx ti, uint64_t *__restrict__ keys,
+                                                        int64_t *bad) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  uint64_t t;
+  keys[i] = entry_tile(idx, vals, i, ti, bad, &t) ? t : static_cast<uint64_t>(ti.cells);
+}
+
+__global__ __launch_bounds__(256) void distinct_count_kernel(const uint64_t *__restrict__ keys,
+                                                             int64_t nnz, uint64_t sentinel,
+                                                             unsigned long long *count) {
+  int64_t c = 0;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nnz;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t k = keys[i];
+    c += k != sentinel && (i == 0 || keys[i - 1] != k) ? 1 : 0;
+  }
+  wave_add(count, c);
+}
+
+// ---- the plan --------------------------------------------------------------
+enum NodeKind { kDenseRoot, kCooRoot, kPool, kSorted };
+
+struct StatNode {
+  std::array<int64_t, EJ_MAX_DIMS> ts;
+  int64_t cells = 1;   // tiles in the grid
+  int parent = -1;
+  int pdim = -1;       // dimension pooled from the parent
+  int64_t pfac = 1;    // pooling factor
+  int kind = kPool;
+  std::vector<int> kids;
+  size_t off = 0;      // map offset on the stack
+};
+
+struct StatsPlan {
+  int nd = 0;
+  int64_t shape[EJ_MAX_DIMS] = {};
+  std::vector<StatNode> nodes;
+  std::vector<int> req;   // node of each requested tile shape
+  std::vector<int> proj;  // node of (scheme, dim): value_count source
+  std::vector<int> roots; // map roots in execution order
+  size_t stack_bytes = 0;
+  bool any_sorted = false;
+};
+
+// Ascending prime factors of n (trial division once per dimension).
+std::vector<int64_t> prime_factors(int64_t n) {
+  std::vector<int64_t> ps;
+  for (int64_t p = 2; p * p <= n; ++p) {
+    if (n % p == 0) {
+      ps.push_back(p);
+      while (n % p == 0) n /= p;
+    }
+  }
+  if (n > 1) ps.push_back(n);
+  return ps;
+}
+
+void layout(StatsPlan &pl, int v, size_t base) {
+  StatNode &nd = pl.nodes[v];
+  nd.off = base;
+  const size_t top = base + align_up(static_cast<size_t>(nd.cells), 256);
+  if (top > pl.stack_bytes) pl.stack_bytes = top;
+  for (int k : pl.nodes[v].kids) layout(pl, k, top);
+}
+
+// dense: nnz < 0.  cap: largest map in bytes for COO input (<= 0: default).
+int make_plan(int32_t ndim, const int64_t *shape, int64_t n_schemes, const int64_t *tile_shapes,
+              bool dense, int64_t cap, StatsPlan *pl) {
+  EJ_CHECK_ARG(ndim >= 1 && ndim <= EJ_MAX_DIMS, "ndim=%d outside [1, %d]", ndim, EJ_MAX_DIMS);
+  EJ_CHECK_ARG(shape, "shape is null");
+  EJ_CHECK_ARG(n_schemes >= 0, "n_schemes < 0");
+  EJ_CHECK_ARG(n_schemes == 0 || tile_shapes, "tile_shapes is null");
+  pl->nd = ndim;
+  unsigned __int128 total = 1;
+  for (int d = 0; d < ndim; ++d) {
+    EJ_CHECK_ARG(shape[d] >= 1 && shape[d] <= INT32_MAX, "shape[%d]=%lld outside [1, 2^31)", d,
+                 (long long)shape[d]);
+    pl->shape[d] = shape[d];
+    total *= static_cast<uint64_t>(shape[d]);
+  }
+  if (total >= (static_cast<unsigned __int128>(1) << 62)) {
+    set_error("tensor has 2^62 or more elements");
+    return EJ_E_UNSUPPORTED;
+  }
+  if (cap <= 0) cap = int64_t(1) << 32;
+  if (dense) cap = INT64_MAX;
+  std::vector<std::vector<int64_t>> primes(ndim);
+  for (int d = 0; d < ndim; ++d) primes[d] = prime_factors(shape[d]);
+
+  std::map<std::array<int64_t, EJ_MAX_DIMS>, int> ids;
+  auto insert = [&](const std::array<int64_t, EJ_MAX_DIMS> &ts) -> int {
+    auto it = ids.find(ts);
+    if (it != ids.end()) return it->second;
+    StatNode n;
+    n.ts = ts;
+    for (int d = 0; d < ndim; ++d) n.cells *= shape[d] / ts[d];
+    const int id = static_cast<int>(pl->nodes.size());
+    pl->nodes.push_back(std::move(n));
+    ids.emplace(ts, id);
+    return id;
+  };
+  pl->req.resize(static_cast<size_t>(n_schemes));
+  pl->proj.resize(static_cast<size_t>(n_schemes) * ndim);
+  for (int64_t s = 0; s < n_schemes; ++s) {
+    std::array<int64_t, EJ_MAX_DIMS> ts{};
+    for (int d = 0; d < EJ_MAX_DIMS; ++d) ts[d] = 1;
+    for (int d = 0; d < ndim; ++d) {
+      const int64_t t = tile_shapes[s * ndim + d];
+      EJ_CHECK_ARG(t >= 1 && shape[d] % t == 0,
+                   "tile shape %lld: extent %lld does not divide shape[%d]=%lld",
+                   (long long)s, (long long)t, d, (long long)shape[d]);
+      ts[d] = t;
+    }
+    pl->req[s] = insert(ts);
+    for (int l = 0; l < ndim; ++l) {
+      std::array<int64_t, EJ_MAX_DIMS> pj = ts;
+      for (int d = 0; d < ndim; ++d)
+        if (d != l) pj[d] = shape[d];
+      pl->proj[s * ndim + l] = insert(pj);
+    }
+  }
+  // Close under the parent relation (the vector grows while it is walked).
+  for (size_t v = 0; v < pl->nodes.size(); ++v) {
+    std::array<int64_t, EJ_MAX_DIMS> ts = pl->nodes[v].ts;
+    int d = ndim - 1;
+    while (d >= 0 && ts[d] == 1) --d;
+    if (d < 0) continue;  // (1, ..., 1)
+    int64_t p = ts[d];
+    for (int64_t q : primes[d])
+      if (ts[d] % q == 0) {
+        p = q;
+        break;
+      }
+    ts[d] /= p;
+    const int par = insert(ts);
+    pl->nodes[v].parent = par;
+    pl->nodes[v].pdim = d;
+    pl->nodes[v].pfac = p;
+  }
+  // Kinds, parents before children (a parent has more cells).
+  std::vector<int> order(pl->nodes.size());
+  for (size_t v = 0; v < order.size(); ++v) order[v] = static_cast<int>(v);
+  std::sort(order.begin(), order.end(), [&](int a, int b) {
+    return pl->nodes[a].cells != pl->nodes[b].cells ? pl->nodes[a].cells > pl->nodes[b].cells
+                                                    : a < b;
+  });
+  for (int v : order) {
+    StatNode &n = pl->nodes[v];
+    if (dense) {
+      n.kind = n.parent < 0 ? kDenseRoot : kPool;
+    } else if (n.cells > cap) {
+      n.kind = kSorted;
+      pl->any_sorted = true;
+    } else {
+      n.kind = n.parent < 0 || pl->nodes[n.parent].kind == kSorted ? kCooRoot : kPool;
+    }
+    if (n.kind == kPool) pl->nodes[n.parent].kids.push_back(v);
+    if (n.kind == kDenseRoot || n.kind == kCooRoot) pl->roots.push_back(v);
+  }
+  for (int r : pl->roots) layout(*pl, r, 0);
+  return EJ_OK;
+}
+
+struct StatsWs {
+  unsigned long long *counts;  // one per node, then the range flag
+  uint8_t *stack;
+  uint64_t *keys, *keys_alt;
+  int32_t *vals, *vals_alt;
+  void *sort_ws;
+  size_t bytes;
+};
+
+StatsWs carve_stats(void *base, const StatsPlan &pl, int64_t nnz) {
+  Carver c(base);
+  StatsWs w{};
+  w.counts = c.take<unsigned long long>(static_cast<int64_t>(pl.nodes.size()) + 1);
+  w.stack = c.take<uint8_t>(static_cast<int64_t>(pl.stack_bytes));
+  if (pl.any_sorted) {
+    w.keys = c.take<uint64_t>(nnz);
+    w.keys_alt = c.take<uint64_t>(nnz);
+    w.vals = c.take<int32_t>(nnz);
+    w.vals_alt = c.take<int32_t>(nnz);
+    w.sort_ws = c.take<char>(static_cast<int64_t>(sort_workspace_bytes(nnz)));
+  }
+  w.bytes = c.off;
+  return w;
+}
+
+TileIdx tile_idx(const StatsPlan &pl, const StatNode &n) {
+  TileIdx ti{};
+  ti.nd = pl.nd;
+  for (int d = 0; d < pl.nd; ++d) {
+    ti.shape[d] = pl.shape[d];
+    ti.tile[d] = n.ts[d];
+    ti.grid[d] = pl.shape[d] / n.ts[d];
+  }
+  ti.cells = n.cells;
+  return ti;
+}
+
+int launch_pool(const StatsPlan &pl, const StatNode &child, const uint8_t *in, uint8_t *out,
+                unsigned long long *count, hipStream_t stream) {
+  const StatNode &par = pl.nodes[child.parent];
+  PoolGeom g;
+  const int d = child.pdim;
+  g.p = child.pfac;
+  g.n_out = pl.shape[d] / child.ts[d];
+  g.outer = 1;
+  for (int e = 0; e < d; ++e) g.outer *= pl.shape[e] / child.ts[e];
+  g.inner = 1;
+  for (int e = d + 1; e < pl.nd; ++e) g.inner *= pl.shape[e] / child.ts[e];
+  g.total = child.cells;
+  (void)par;
+  if (g.inner % 4 == 0) {
+    const int64_t words = g.total / 4;
+    if (par.cells < (int64_t(1) << 31))
+      hipLaunchKernelGGL(pool_words_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
+                         stream, in, out, g, count);
+    else
+      hipLaunchKernelGGL(pool_words_kernel<int64_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
+                         stream, in, out, g, count);
+  } else if (g.inner == 1 && g.p == 2 && g.total % 4 == 0) {
+    hipLaunchKernelGGL(pool_pairs_kernel, dim3(stride_grid(g.total / 4)), dim3(kBlock), 0,
+                       stream, in, out, g.total, count);
+  } else {
+    hipLaunchKernelGGL(pool_bytes_kernel, dim3(stride_grid(g.total)), dim3(kBlock), 0, stream,
+                       in, out, g, count);
+  }
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream) {
+  const StatNode &n = pl.nodes[v];
+  for (int k : n.kids) {
+    const StatNode &kid = pl.nodes[k];
+    EJ_TRY(launch_pool(pl, kid, w.stack + n.off, w.stack + kid.off, w.counts + k, stream));
+    EJ_TRY(run_subtree(pl, k, w, stream));
+  }
+  return EJ_OK;
+}
+
+template <typename T>
+int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_dense,
+              const int32_t *idx, const T *vals, int64_t nnz, hipStream_t stream) {
+  const int64_t n_counts = static_cast<int64_t>(pl.nodes.size()) + 1;
+  int64_t *bad = reinterpret_cast<int64_t *>(w.counts + pl.nodes.size());
+  hipLaunchKernelGGL(fill_zero_kernel<unsigned long long>, dim3(stride_grid(n_counts)),
+                     dim3(kBlock), 0, stream, w.counts, n_counts);
+  EJ_LAUNCH_CHECK();
+  if (pl.any_sorted) {
+    for (size_t v = 0; v < pl.nodes.size(); ++v) {
+      const StatNode &n = pl.nodes[v];
+      if (n.kind != kSorted) continue;
+      const TileIdx ti = tile_idx(pl, n);
+      hipLaunchKernelGGL(stat_keys_kernel<T>, dim3(grid_for(nnz)), dim3(kBlock), 0, stream, idx,
+                         vals, nnz, ti, w.keys, bad);
+      EJ_LAUNCH_CHECK();
+      EJ_TRY(sort_pairs_u64(w.keys, w.vals, w.keys_alt, w.vals_alt, nnz,
+                            bits_for(static_cast<uint64_t>(n.cells) + 1), w.sort_ws, stream));
+      hipLaunchKernelGGL(distinct_count_kernel, dim3(stride_grid(nnz)), dim3(kBlock), 0, stream,
+                         w.keys, nnz, static_cast<uint64_t>(n.cells), w.counts + v);
+      EJ_LAUNCH_CHECK();
+    }
+  }
+  for (int r : pl.roots) {
+    const StatNode &n = pl.nodes[r];
+    uint8_t *map = w.stack + n.off;
+    if (n.kind == kDenseRoot) {
+      const bool vec = (reinterpret_cast<uintptr_t>(dense) % (4 * sizeof(T))) == 0;
+      hipLaunchKernelGGL(dense_map_kernel<T>, dim3(stride_grid(ceil_div(n_dense, 4))),
+                         dim3(kBlock), 0, stream, dense, n_dense, vec, map, w.counts + r);
+    } else {
+      const int64_t words = static_cast<int64_t>(align_up(static_cast<size_t>(n.cells), 256) / 4);
+      hipLaunchKernelGGL(fill_zero_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
+                         stream, reinterpret_cast<uint32_t *>(map), words);
+      EJ_LAUNCH_CHECK();
+      hipLaunchKernelGGL(coo_mark_kernel<T>, dim3(grid_for(nnz)), dim3(kBlock), 0, stream, idx,
+                         vals, nnz, tile_idx(pl, n), map, bad);
+      EJ_LAUNCH_CHECK();
+      hipLaunchKernelGGL(map_count_kernel, dim3(stride_grid(words)), dim3(kBlock), 0, stream,
+                         reinterpret_cast<const uint32_t *>(map), words, w.counts + r);
+    }
+    EJ_LAUNCH_CHECK();
+    EJ_TRY(run_subtree(pl, r, w, stream));
+  }
+  return EJ_OK;
+}
+
+int finish_stats(const StatsPlan &pl, const StatsWs &w, int64_t *num_tuples,
+                 int64_t *value_count, hipStream_t stream) {
+  std::vector<unsigned long long> host(pl.nodes.size() + 1);
+  EJ_HIP(hipMemcpyAsync(host.data(), w.counts, host.size() * sizeof(unsigned long long),
+                        hipMemcpyDeviceToHost, stream));
+  EJ_HIP(hipStreamSynchronize(stream));
+  if (host.back()) {
+    set_error("a nonzero entry has an index outside the tensor shape");
+    return EJ_E_RANGE;
+  }
+  for (size_t s = 0; s < pl.req.size(); ++s) {
+    num_tuples[s] = static_cast<int64_t>(host[pl.req[s]]);
+    for (int l = 0; l < pl.nd; ++l)
+      value_count[s * pl.nd + l] = static_cast<int64_t>(host[pl.proj[s * pl.nd + l]]);
+  }
+  return EJ_OK;
+}
+
+}  // namespace
+}  // namespace ej
+
+using namespace ej;
+
+// ---- dense to COO ------------------------------------------------------------
+extern "C" int ej_extract_coo_workspace_size(int32_t ndim, const int64_t *shape, int32_t dtype,
+                                             size_t *bytes) {
+  clear_error();
+  EJ_CHECK_ARG(bytes, "bytes is null");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  DenseShape sh;
+  int64_t n;
+  EJ_TRY(dense_shape(ndim, shape, &sh, &n));
+  *bytes = carve_extract(nullptr, extract_runs(n, dtype)).bytes;
+  return EJ_OK;
+}
+
+extern "C" int ej_extract_coo_count(const void *dense, int32_t dtype, int32_t ndim,
+                                    const int64_t *shape, void *workspace,
+                                    size_t workspace_bytes, int64_t *nnz, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(nnz, "nnz is null");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  DenseShape sh;
+  int64_t n;
+  EJ_TRY(dense_shape(ndim, shape, &sh, &n));
+  if (n == 0) {
+    *nnz = 0;
+    return EJ_OK;
+  }
+  EJ_CHECK_ARG(dense, "dense is null");
+  const int64_t runs = extract_runs(n, dtype);
+  ExtractWs w = carve_extract(workspace, runs);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  const bool vec = (reinterpret_cast<uintptr_t>(dense) & 15u) == 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(runs, 4)));
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL(coo_count_kernel<double>, grid, dim3(256), 0, stream,
+                       static_cast<const double *>(dense), n, runs, vec, w.counts);
+  else if (dtype == EJ_F32)
+    hipLaunchKernelGGL(coo_count_kernel<float>, grid, dim3(256), 0, stream,
+                       static_cast<const float *>(dense), n, runs, vec, w.counts);
+  else
+    hipLaunchKernelGGL(coo_count_kernel<uint16_t>, grid, dim3(256), 0, stream,
+                       static_cast<const uint16_t *>(dense), n, runs, vec, w.counts);
+  EJ_LAUNCH_CHECK();
+  EJ_TRY(scan_exclusive_i64(w.counts, w.excl, runs, w.scalars, w.scan_ws, stream));
+  int64_t host = 0;
+  EJ_HIP(hipMemcpyAsync(&host, w.scalars, sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  EJ_HIP(hipStreamSynchronize(stream));
+  *nnz = host;
+  return EJ_OK;
+}
+
+extern "C" int ej_extract_coo_fill(const void *dense, int32_t dtype, int32_t ndim,
+                                   const int64_t *shape, const void *workspace,
+                                   size_t workspace_bytes, int64_t nnz, int32_t *indices,
+                                   double *values, int64_t capacity, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  DenseShape sh;
+  int64_t n;
+  EJ_TRY(dense_shape(ndim, shape, &sh, &n));
+  EJ_CHECK_ARG(nnz >= 0 && nnz <= n, "nnz out of range");
+  if (capacity < nnz) {
+    set_error("capacity %lld < %lld nonzeros", (long long)capacity, (long long)nnz);
+    return EJ_E_CAPACITY;
+  }
+  if (nnz == 0) return EJ_OK;
+  EJ_CHECK_ARG(dense && indices && values, "null pointer argument");
+  const int64_t runs = extract_runs(n, dtype);
+  ExtractWs w = carve_extract(const_cast<void *>(workspace), runs);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+  const bool vec = (reinterpret_cast<uintptr_t>(dense) & 15u) == 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(runs, 4)));
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL(coo_fill_kernel<double>, grid, dim3(256), 0, stream,
+                       static_cast<const double *>(dense), n, runs, vec, sh, w.excl, nnz,
+                       indices, values);
+  else if (dtype == EJ_F32)
+    hipLaunchKernelGGL(coo_fill_kernel<float>, grid, dim3(256), 0, stream,
+                       static_cast<const float *>(dense), n, runs, vec, sh, w.excl, nnz,
+                       indices, values);
+  else
+    hipLaunchKernelGGL(coo_fill_kernel<uint16_t>, grid, dim3(256), 0, stream,
+                       static_cast<const uint16_t *>(dense), n, runs, vec, sh, w.excl, nnz,
+                       indices, values);
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+// ---- COO to tiles --------------------------------------------------------------
+extern "C" int ej_bucket_coo_workspace_size(int64_t nnz, size_t *bytes) {
+  clear_error();
+  EJ_CHECK_ARG(bytes, "bytes is null");
+  EJ_CHECK_ARG(nnz >= 0 && nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
+  *bytes = carve_coo(nullptr, nnz).bytes;
+  return EJ_OK;
+}
+
+extern "C" int ej_bucket_coo_count(const int32_t *indices, const void *values, int32_t dtype,
+                                   int64_t nnz, int32_t ndim, const int64_t *shape,
+                                   const int64_t *tile_shape, void *workspace,
+                                   size_t workspace_bytes, int64_t *n_tiles,
+                                   ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(n_tiles, "n_tiles is null");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(nnz >= 0 && nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
+  CooGeom g;
+  EJ_TRY(make_coo_geom(ndim, shape, tile_shape, &g));
+  if (nnz == 0 || g.n_tiles == 0) {
+    *n_tiles = 0;
+    return EJ_OK;
+  }
+  EJ_CHECK_ARG(indices && values, "null pointer argument");
+  CooWs w = carve_coo(workspace, nnz);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  hipLaunchKernelGGL(fill_zero_kernel<int64_t>, dim3(1), dim3(64), 0, stream, w.scalars,
+                     int64_t(4));
+  EJ_LAUNCH_CHECK();
+  const dim3 grid(grid_for(nnz));
+  // Keys go to the alternate buffers when the sort takes an odd number of
+  // passes, so the sorted result lands in keys / order without a copy.
+  const bool alt = radix_passes(g.bits) % 2 == 1;
+  uint64_t *k0 = alt ? w.keys_alt : w.keys;
+  int32_t *o0 = alt ? w.order_alt : w.order;
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL(coo_keys_kernel<double>, grid, dim3(kBlock), 0, stream, indices,
+                       static_cast<const double *>(values), nnz, g, k0, o0, w.scalars + 1);
+  else if (dtype == EJ_F32)
+    hipLaunchKernelGGL(coo_keys_kernel<float>, grid, dim3(kBlock), 0, stream, indices,
+                       static_cast<const float *>(values), nnz, g, k0, o0, w.scalars + 1);
+  else
+    hipLaunchKernelGGL(coo_keys_kernel<uint16_t>, grid, dim3(kBlock), 0, stream, indices,
+                       static_cast<const uint16_t *>(values), nnz, g, k0, o0, w.scalars + 1);
+  EJ_LAUNCH_CHECK();
+  EJ_TRY(sort_pairs_u64(w.keys, w.order, w.keys_alt, w.order_alt, nnz, g.bits, w.sort_ws, stream,
+                        alt));
+  hipLaunchKernelGGL(coo_tile_flags_kernel, grid, dim3(kBlock), 0, stream, w.keys, nnz,
+                     g.sentinel, g.wbits, w.flags);
+  EJ_LAUNCH_CHECK();
+  EJ_TRY(scan_exclusive_i64(w.flags, w.excl, nnz, w.scalars, w.scan_ws, stream));
+  int64_t host[2] = {0, 0};
+  EJ_HIP(hipMemcpyAsync(host, w.scalars, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  EJ_HIP(hipStreamSynchronize(stream));
+  if (host[1]) {
+    set_error("a nonzero entry has an index outside the tensor shape");
+    return EJ_E_RANGE;
+  }
+  *n_tiles = host[0];
+  return EJ_OK;
+}
+
+extern "C" int ej_bucket_coo_fill(const void *values, int32_t dtype, int64_t nnz, int32_t ndim,
+                                  const int64_t *shape, const int64_t *tile_shape,
+                                  const void *workspace, size_t workspace_bytes, int64_t n_tiles,
+                                  int32_t *coords, void *tiles, int64_t capacity,
+                                  ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(nnz >= 0 && nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
+  CooGeom g;
+  EJ_TRY(make_coo_geom(ndim, shape, tile_shape, &g));
+  EJ_CHECK_ARG(n_tiles >= 0 && n_tiles <= nnz && n_tiles <= g.n_tiles, "n_tiles out of range");
+  if (capacity < n_tiles) {
+    set_error("tile capacity %lld < %lld tiles", (long long)capacity, (long long)n_tiles);
+    return EJ_E_CAPACITY;
+  }
+  if (n_tiles == 0) return EJ_OK;
+  EJ_CHECK_ARG(values && coords && tiles, "null pointer argument");
+  CooWs w = carve_coo(const_cast<void *>(workspace), nnz);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+  const int64_t elems = n_tiles * g.tile_elems;
+  const dim3 grid(grid_for(nnz));
+  if (dtype == EJ_BF16) {
+    hipLaunchKernelGGL(fill_zero_kernel<uint16_t>, dim3(stride_grid(elems)), dim3(kBlock), 0,
+                       stream, static_cast<uint16_t *>(tiles), elems);
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL((coo_scatter_kernel<uint16_t, uint16_t>), grid, dim3(kBlock), 0, stream,
+                       w.keys, w.order, w.flags, w.excl, static_cast<const uint16_t *>(values),
+                       nnz, g, n_tiles, coords, static_cast<uint16_t *>(tiles));
+  } else {
+    hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(stride_grid(elems)), dim3(kBlock), 0,
+                       stream, static_cast<float *>(tiles), elems);
+    EJ_LAUNCH_CHECK();
+    if (dtype == EJ_F64)
+      hipLaunchKernelGGL((coo_scatter_kernel<double, float>), grid, dim3(kBlock), 0, stream,
+                         w.keys, w.order, w.flags, w.excl, static_cast<const double *>(values),
+                         nnz, g, n_tiles, coords, static_cast<float *>(tiles));
+    else
+      hipLaunchKernelGGL((coo_scatter_kernel<float, float>), grid, dim3(kBlock), 0, stream,
+                         w.keys, w.order, w.flags, w.excl, static_cast<const float *>(values),
+                         nnz, g, n_tiles, coords, static_cast<float *>(tiles));
+  }
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+// ---- statistics --------------------------------------------------------------
+extern "C" int ej_scheme_stats_workspace_size(int32_t ndim, const int64_t *shape,
+                                              int64_t n_schemes, const int64_t *tile_shapes,
+                                              int64_t nnz, int64_t bitmap_cap, size_t *bytes) {
+  clear_error();
+  EJ_CHECK_ARG(bytes, "bytes is null");
+  EJ_CHECK_ARG(nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
+  StatsPlan pl;
+  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, nnz < 0, bitmap_cap, &pl));
+  *bytes = carve_stats(nullptr, pl, nnz < 0 ? 0 : nnz).bytes;
+  return EJ_OK;
+}
+
+extern "C" int ej_scheme_stats_dense(const void *dense, int32_t dtype, int32_t ndim,
+                                     const int64_t *shape, int64_t n_schemes,
+                                     const int64_t *tile_shapes, void *workspace,
+                                     size_t workspace_bytes, int64_t *num_tuples,
+                                     int64_t *value_count, ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  StatsPlan pl;
+  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, true, 0, &pl));
+  if (n_schemes == 0) return EJ_OK;
+  EJ_CHECK_ARG(dense && num_tuples && value_count, "null pointer argument");
+  StatsWs w = carve_stats(workspace, pl, 0);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) n *= shape[d];
+  if (dtype == EJ_F64)
+    EJ_TRY(run_stats<double>(pl, w, static_cast<const double *>(dense), n, nullptr, nullptr, 0,
+                             stream));
+  else if (dtype == EJ_F32)
+    EJ_TRY(run_stats<float>(pl, w, static_cast<const float *>(dense), n, nullptr, nullptr, 0,
+                            stream));
+  else
+    EJ_TRY(run_stats<uint16_t>(pl, w, static_cast<const uint16_t *>(dense), n, nullptr, nullptr,
+                               0, stream));
+  return finish_stats(pl, w, num_tuples, value_count, stream);
+}
+
+extern "C" int ej_scheme_stats_coo(const int32_t *indices, const void *values, int32_t dtype,
+                                   int64_t nnz, int32_t ndim, const int64_t *shape,
+                                   int64_t n_schemes, const int64_t *tile_shapes,
+                                   int64_t bitmap_cap, void *workspace, size_t workspace_bytes,
+                                   int64_t *num_tuples, int64_t *value_count,
+                                   ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(nnz >= 0 && nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
+  StatsPlan pl;
+  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, false, bitmap_cap, &pl));
+  if (n_schemes == 0) return EJ_OK;
+  EJ_CHECK_ARG(num_tuples && value_count, "null pointer argument");
+  if (nnz == 0) {
+    for (int64_t s = 0; s < n_schemes; ++s) {
+      num_tuples[s] = 0;
+      for (int l = 0; l < ndim; ++l) value_count[s * ndim + l] = 0;
+    }
+    return EJ_OK;
+  }
+  EJ_CHECK_ARG(indices && values, "null pointer argument");
+  StatsWs w = carve_stats(workspace, pl, nnz);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  if (dtype == EJ_F64)
+    EJ_TRY(run_stats<double>(pl, w, nullptr, 0, indices, static_cast<const double *>(values), nnz,
+                             stream));
+  else if (dtype == EJ_F32)
+    EJ_TRY(run_stats<float>(pl, w, nullptr, 0, indices, static_cast<const float *>(values), nnz,
+                            stream));
+  else
+    EJ_TRY(run_stats<uint16_t>(pl, w, nullptr, 0, indices, static_cast<const uint16_t *>(values),
+                               nnz, stream));
+  return finish_stats(pl, w, num_tuples, value_count, stream);
+}

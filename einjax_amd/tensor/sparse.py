@@ -7,11 +7,10 @@ sparse path accepts both and answers in the residency it was given, so host
 callers see the reference's types while chained device calls never leave
 HBM.
 
-``SparseTensor`` (tensor/sparse.py:93-231) buckets its data on the GPU in
-``to_relation``.  Its per-scheme statistics (``schemes``, the reference's
-``_compute_sparsity_metrics``, :124-158) are computed lazily on first access
-rather than in the constructor, so building a relation does not pay for
-them.
+``SparseTensor`` (tensor/sparse.py:93-231) counts, buckets and measures its
+data on the GPU.  Its per-scheme statistics (``schemes``, the reference's
+``_compute_sparsity_metrics``, :124-158) are computed on first access rather
+than in the constructor, so building a relation does not pay for them.
 """
 
 from __future__ import annotations
@@ -135,80 +134,156 @@ class SparseTensorRelation:
         return out
 
 
-def _extract_coo(data: Any) -> tuple[np.ndarray, np.ndarray, tuple]:
-    """COO indices (int32 [nnz, nd]) and float64 values of host data
-    (sparse.py:234-270)."""
-    try:
-        import scipy.sparse as sp
+def _extract_coo(data: Any):
+    """COO indices (int32 [nnz, nd]) and float64 values of the data, with
+    its shape (reference: _extract_coo, tensor/sparse.py:234-270).
 
-        if sp.issparse(data):
-            coo = sp.coo_matrix(data) if data.ndim == 2 else data.tocoo()
-            idx = np.stack([coo.row, coo.col], axis=1).astype(np.int32)
-            return idx, np.asarray(coo.data, dtype=np.float64), tuple(coo.shape)
-    except ImportError:  # pragma: no cover
-        pass
-    arr = np.asarray(data, dtype=np.float64)
-    nz = np.nonzero(arr)
-    if len(nz[0]) == 0:
-        return np.zeros((0, arr.ndim), np.int32), np.zeros((0,), np.float64), tuple(arr.shape)
-    return np.stack(nz, axis=1).astype(np.int32), arr[nz], tuple(arr.shape)
+    A scipy sparse matrix gives its stored entries (scipy's own COO
+    conversion, explicit zeros and repeats included).  A dense array gives
+    its elements != 0 in row-major order, found on the GPU; host input
+    answers in NumPy, GPU input in torch tensors on the GPU."""
+    if _is_scipy(data):
+        coo = data.tocoo()
+        idx = np.stack([coo.row, coo.col], axis=1).astype(np.int32)
+        return idx, np.asarray(coo.data, dtype=np.float64), tuple(int(s) for s in coo.shape)
+    from .._device import extract_coo
+
+    dense, on_device = _dense_on_gpu(data)
+    shape = tuple(int(s) for s in dense.shape)
+    if dense.numel() == 0 or dense.dim() == 0:
+        import torch
+
+        flat = dense.reshape(-1)
+        keep = flat != 0
+        if on_device:  # a 0-d tensor: one element, no kernel needed
+            return (torch.zeros((int(keep.sum()), dense.dim()), dtype=torch.int32,
+                                device=dense.device), flat[keep].double(), shape)
+        return (np.zeros((int(keep.sum()), dense.dim()), np.int32),
+                flat[keep].double().cpu().numpy(), shape)
+    idx, vals = extract_coo(dense)
+    if on_device:
+        return idx, vals, shape
+    return idx.cpu().numpy(), vals.cpu().numpy(), shape
+
+
+def _dense_on_gpu(data):
+    """(dense torch tensor on the GPU, whether the input already was there).
+    float32 / bfloat16 / float64 stay as they are; other dtypes become
+    float64 on the host side (the reference's np.asarray(..., float64)) and
+    float32 on the GPU."""
+    import torch
+
+    from .._device import require_gpu
+
+    dev = require_gpu()
+    if _is_torch(data):
+        on_device = data.is_cuda
+        t = data
+        if t.dtype not in (torch.float32, torch.bfloat16, torch.float64):
+            t = t.to(torch.float32 if on_device else torch.float64)
+        return t.to(dev).contiguous(), on_device
+    arr = np.ascontiguousarray(np.asarray(data, dtype=np.float64))
+    return torch.from_numpy(arr).to(dev), False
 
 
 class SparseTensor:
     """Sparse tensor over dense or scipy-sparse data (sparse.py:93-231).
 
     ``data`` may be a NumPy array, a scipy sparse matrix, or a torch tensor
-    (CPU or GPU).  ``to_relation`` buckets on the GPU."""
+    (CPU or GPU).  Nonzero counting, the per-tile-shape statistics and
+    ``to_relation`` run on the GPU; the data is copied there once, on first
+    use, and kept (dense data as a dense tensor, scipy data as COO entries)."""
 
     def __init__(self, name: str, data: Any):
         self.name = name
         self.data = data
-        if _is_torch(data):
-            self.shape = tuple(int(s) for s in data.shape)
-        elif hasattr(data, "shape") and not isinstance(data, np.ndarray) and _is_scipy(data):
+        if _is_torch(data) or _is_scipy(data):
             self.shape = tuple(int(s) for s in data.shape)
         else:
             self.data = np.asarray(data, dtype=np.float64)
             self.shape = tuple(self.data.shape)
         self.tile_shapes = enumerate_tile_shapes(self.shape)
         self._schemes: dict | None = None
-        self._coo: tuple | None = None
+        self._gpu: tuple | None = None
+        self._nnz: int | None = None
+        self._coo_host: tuple | None = None
 
     @property
     def ndim(self) -> int:
         return len(self.shape)
 
-    def _host_coo(self):
-        if self._coo is None:
-            data = self.data.cpu().numpy() if _is_torch(self.data) else self.data
-            if _is_torch(self.data) and data.dtype != np.float64:
-                data = data.astype(np.float64)
-            self._coo = _extract_coo(data)
-        return self._coo
+    def _gpu_form(self) -> tuple:
+        """("dense", tensor) or ("coo", indices int32 [n, nd], values float64 [n]),
+        resident on the GPU."""
+        if self._gpu is None:
+            if _is_scipy(self.data):
+                import torch
+
+                from .._device import require_gpu
+
+                dev = require_gpu()
+                idx, vals, _ = _extract_coo(self.data)
+                self._gpu = ("coo", torch.from_numpy(idx).to(dev), torch.from_numpy(vals).to(dev))
+            else:
+                self._gpu = ("dense", _dense_on_gpu(self.data)[0])
+        return self._gpu
 
     @property
     def nnz(self) -> int:
-        return len(self._host_coo()[1])
+        """Stored entries: elements != 0 of dense data, stored entries of a
+        scipy matrix (sparse.py:119-122 over :234-270)."""
+        if self._nnz is None:
+            form = self._gpu_form()
+            if form[0] == "coo":
+                self._nnz = int(form[2].numel())
+            else:
+                from .._device import count_nonzero
+
+                self._nnz = count_nonzero(form[1]) if form[1].numel() else 0
+        return self._nnz
+
+    @property
+    def _indices(self) -> np.ndarray:
+        """Host COO indices int32 [nnz, nd] (the reference's attribute)."""
+        return self._host_coo()[0]
+
+    @property
+    def _values(self) -> np.ndarray:
+        """Host COO values float64 [nnz] (the reference's attribute)."""
+        return self._host_coo()[1]
+
+    def _host_coo(self):
+        if self._coo_host is None:
+            idx, vals, _ = _extract_coo(self.data)
+            if _is_torch(idx):
+                idx, vals = idx.cpu().numpy(), vals.cpu().numpy()
+            self._coo_host = (idx, vals)
+        return self._coo_host
 
     @property
     def schemes(self) -> dict:
         """tile_shape -> TilingScheme with num_tuples (non-empty tiles) and
         value_count (distinct tile coordinates per dimension), the reference's
-        per-scheme statistics (sparse.py:124-158), computed on first access."""
+        per-scheme statistics (sparse.py:124-158), computed on the GPU for
+        every tile shape at once on first access."""
         if self._schemes is None:
-            idx, vals, _ = self._host_coo()
-            nz = idx[vals != 0]
-            schemes = {}
-            for ts in self.tile_shapes:
-                sch = TilingScheme(self, self.shape, ts)
-                if len(nz) == 0:
-                    sch.num_tuples = 0
-                    sch.value_count = tuple(0 for _ in self.shape)
+            schemes = {ts: TilingScheme(self, self.shape, ts) for ts in self.tile_shapes}
+            if self.ndim == 0:
+                n = 1 if self.nnz else 0
+                for sch in schemes.values():
+                    sch.num_tuples, sch.value_count = n, ()
+            else:
+                from .._device import scheme_stats
+
+                form = self._gpu_form()
+                if form[0] == "coo":
+                    nt, vc = scheme_stats(self.tile_shapes, self.shape, indices=form[1],
+                                          values=form[2])
                 else:
-                    tc = nz // np.array(ts, dtype=np.int32)
-                    sch.value_count = tuple(len(np.unique(tc[:, d])) for d in range(self.ndim))
-                    sch.num_tuples = len(np.unique(tc, axis=0))
-                schemes[ts] = sch
+                    nt, vc = scheme_stats(self.tile_shapes, self.shape, dense=form[1])
+                for ts, n, v in zip(self.tile_shapes, nt, vc):
+                    schemes[ts].num_tuples = n
+                    schemes[ts].value_count = v
             self._schemes = schemes
         return self._schemes
 
@@ -220,6 +295,8 @@ class SparseTensor:
         gives a host relation (int32 coords, float32 tiles: occupancy is
         decided on the float64 values, tiles hold them rounded to float32);
         GPU float32 / bfloat16 data gives a device relation of that dtype.
+        scipy data is bucketed from its COO entries (a repeated entry keeps
+        its last nonzero value) without forming the dense matrix.
         Raises ValueError when a tile extent does not divide the shape."""
         tile_shape = tuple(int(t) for t in tile_shape)
         if len(tile_shape) != self.ndim:
@@ -231,33 +308,33 @@ class SparseTensor:
                                  f"shape[{d}]={self.shape[d]}")
         import torch
 
-        from .._device import bucket_dense, require_gpu
+        from .._device import bucket_coo, bucket_dense
 
-        dev = require_gpu()
         on_device = _is_torch(self.data) and self.data.is_cuda
-        if _is_torch(self.data):
-            dense = self.data
-            if dense.dtype not in (torch.float32, torch.bfloat16, torch.float64):
-                dense = dense.to(torch.float64 if not on_device else torch.float32)
-            dense = dense.to(dev)
-        elif _is_scipy(self.data):
-            dense = torch.from_numpy(np.asarray(self.data.toarray(), dtype=np.float64)).to(dev)
-        else:
-            dense = torch.from_numpy(np.ascontiguousarray(self.data)).to(dev)
+        form = self._gpu_form()
+        dev = form[1].device
         if prod(self.shape) == 0:
             coords = torch.zeros((0, self.ndim), dtype=torch.int32, device=dev)
             vals = torch.zeros((0, *tile_shape), dtype=torch.float32, device=dev)
+        elif form[0] == "coo":
+            coords, vals = bucket_coo(form[1], form[2], self.shape, tile_shape)
         else:
-            coords, vals = bucket_dense(dense, tile_shape)
+            coords, vals = bucket_dense(form[1], tile_shape)
         rel = SparseTensorRelation(coords, vals, self.shape, tile_shape)
         return rel if on_device else rel.to_host()
 
     def to_dense_array(self) -> np.ndarray:
-        """Dense float64 array of the data (sparse.py:221-231)."""
+        """Dense float64 array of the data (sparse.py:221-231); stored entries
+        of a scipy matrix are written in order, so a repeated entry keeps the
+        last value."""
         if _is_torch(self.data):
-            return self.data.float().cpu().numpy().astype(np.float64)
+            return self.data.double().cpu().numpy()
         if _is_scipy(self.data):
-            return np.asarray(self.data.toarray(), dtype=np.float64)
+            idx, vals, _ = _extract_coo(self.data)
+            out = np.zeros(self.shape, dtype=np.float64)
+            if len(vals):
+                out[tuple(idx[:, d] for d in range(self.ndim))] = vals
+            return out
         return np.array(self.data, dtype=np.float64)
 
 

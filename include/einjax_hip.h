@@ -5,8 +5,15 @@
  * (execution/sparse_dispatch.py:226-297).  This library replaces its phases
  * with HIP kernels behind plain C entry points:
  *
- *   tiling        ej_bucket_dense_count / ej_bucket_dense_fill
- *                 (replaces SparseTensor.to_relation, tensor/sparse.py:160-219)
+ *   tiling        ej_bucket_dense_count / ej_bucket_dense_fill,
+ *                 ej_bucket_coo_count / ej_bucket_coo_fill
+ *                 (replace SparseTensor.to_relation, tensor/sparse.py:160-219)
+ *   COO ingest    ej_extract_coo_count / ej_extract_coo_fill
+ *                 (replaces _extract_coo for dense input, tensor/sparse.py:234-270)
+ *   statistics    ej_scheme_stats_dense / ej_scheme_stats_coo
+ *                 (replace SparseTensor._compute_sparsity_metrics,
+ *                  tensor/sparse.py:124-158, over BaseTensor's tile shapes,
+ *                  tensor/base.py:39-49)
  *   join          ej_join_count / ej_join_fill
  *                 (replaces coordinate_join, execution/sparse_dispatch.py:29-82;
  *                  coordinate_join_hash / coordinate_join_sorted,
@@ -29,14 +36,16 @@
  *                 (the accumulation half of segment_sum, execution/sparse_dispatch.py:164-171)
  *
  * Conventions
- *   - Every pointer argument named *_coords, *_values, *_idx, *keys, perm,
- *     seg_*, out*, dense and workspace is a DEVICE pointer.  Small descriptor
- *     arrays (dims, radices, shapes, agg_*) and the scalar outputs n_pairs,
- *     n_segments, n_tiles are HOST pointers; `counts` of the *_async
- *     functions is PINNED host memory (hipHostMalloc).
+ *   - Every pointer argument named *coords, *values, *_idx, *keys, perm,
+ *     seg_*, out*, dense, indices, tiles and workspace is a DEVICE pointer.
+ *     Small descriptor arrays (dims, radices, shapes, tile_shapes, agg_*),
+ *     the scalar outputs n_pairs, n_segments, n_tiles, nnz and the
+ *     statistics num_tuples / value_count are HOST pointers; `counts` of the
+ *     *_async functions is PINNED host memory (hipHostMalloc).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
- *     Functions whose name ends in _count synchronize `stream` because they
- *     return a data-dependent size to the host; every other function,
+ *     Functions whose name ends in _count, and the ej_scheme_stats_*
+ *     functions, synchronize `stream` because they return data-dependent
+ *     values to the host; every other function,
  *     including the *_count_async forms, is asynchronous.
  *   - A *_count call leaves its state in the caller's workspace; the matching
  *     *_fill call must receive the same workspace, unmodified.
@@ -59,7 +68,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 3
+#define EJ_ABI_VERSION 4
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -298,6 +307,70 @@ int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t ndim, const i
                          const int64_t *tile_shape, const void *workspace,
                          size_t workspace_bytes, int64_t n_tiles, int32_t *coords, void *values,
                          int64_t capacity, ej_stream_t stream);
+
+/* ---- COO ingest (reference: _extract_coo, tensor/sparse.py:234-270) ----- */
+/* Dense row-major input (EJ_F32, EJ_BF16 or EJ_F64) to COO: the elements that
+ * compare != 0 (NaN included, -0.0 excluded) in row-major order, the order of
+ * np.nonzero; indices int32 [nnz, ndim], values float64 [nnz] (the
+ * reference's dtype, :246-260; the conversion is exact).  Extents must be
+ * below 2^31. */
+int ej_extract_coo_workspace_size(int32_t ndim, const int64_t *shape, int32_t dtype,
+                                  size_t *bytes);
+int ej_extract_coo_count(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
+                         void *workspace, size_t workspace_bytes, int64_t *nnz,
+                         ej_stream_t stream);
+int ej_extract_coo_fill(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
+                        const void *workspace, size_t workspace_bytes, int64_t nnz,
+                        int32_t *indices, double *values, int64_t capacity, ej_stream_t stream);
+
+/* ---- COO tiling (reference: SparseTensor.to_relation, tensor/sparse.py:160-219) */
+/* COO input: indices int32 [nnz, ndim] (device), values [nnz] of EJ_F64,
+ * EJ_F32 or EJ_BF16 (device), nnz < 2^31, in any order, repeats allowed.
+ * Entries whose value compares == 0 are dropped (:184-187); the tiles holding
+ * the others appear in ascending lexicographic coordinate order (:204-206);
+ * every other element of a kept tile is +0.0 (:210-212); an element listed
+ * more than once takes the value of its last nonzero entry, as the
+ * reference's fancy assignment leaves it.  A nonzero entry whose index lies
+ * outside shape gives EJ_E_RANGE; tile_shape must divide shape (EJ_E_INVAL).
+ * Tiles are fp32 for EJ_F64 / EJ_F32 values and bf16 for EJ_BF16 values. */
+int ej_bucket_coo_workspace_size(int64_t nnz, size_t *bytes);
+int ej_bucket_coo_count(const int32_t *indices, const void *values, int32_t dtype, int64_t nnz,
+                        int32_t ndim, const int64_t *shape, const int64_t *tile_shape,
+                        void *workspace, size_t workspace_bytes, int64_t *n_tiles,
+                        ej_stream_t stream);
+/* coords int32 [n_tiles, ndim]; tiles [n_tiles, *tile_shape]. */
+int ej_bucket_coo_fill(const void *values, int32_t dtype, int64_t nnz, int32_t ndim,
+                       const int64_t *shape, const int64_t *tile_shape, const void *workspace,
+                       size_t workspace_bytes, int64_t n_tiles, int32_t *coords, void *tiles,
+                       int64_t capacity, ej_stream_t stream);
+
+/* ---- statistics (reference: _compute_sparsity_metrics, tensor/sparse.py:124-158) */
+/* For each of n_schemes tile shapes (tile_shapes: HOST int64
+ * [n_schemes, ndim], each extent dividing shape), over the elements that
+ * compare != 0:
+ *   num_tuples[s]            = number of distinct tile coordinates idx // t_s;
+ *   value_count[s * ndim + l] = number of distinct idx[l] // t_s[l];
+ * all zero when no element is nonzero (:141-145).  num_tuples and
+ * value_count are HOST arrays; the calls synchronize `stream`.  Extents must
+ * lie in [1, 2^31).
+ * Dense input: nnz = -1 in the workspace query.  The workspace holds
+ * occupancy maps of about twice the tensor's element count in bytes.
+ * COO input (indices int32 [nnz, ndim], values [nnz], as ej_bucket_coo_*):
+ * tile shapes whose grid has more than bitmap_cap tiles (<= 0: 2^32) are
+ * counted by sorting the entries' tile keys instead of an occupancy map.  A
+ * nonzero entry outside shape gives EJ_E_RANGE. */
+int ej_scheme_stats_workspace_size(int32_t ndim, const int64_t *shape, int64_t n_schemes,
+                                   const int64_t *tile_shapes, int64_t nnz, int64_t bitmap_cap,
+                                   size_t *bytes);
+int ej_scheme_stats_dense(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
+                          int64_t n_schemes, const int64_t *tile_shapes, void *workspace,
+                          size_t workspace_bytes, int64_t *num_tuples, int64_t *value_count,
+                          ej_stream_t stream);
+int ej_scheme_stats_coo(const int32_t *indices, const void *values, int32_t dtype, int64_t nnz,
+                        int32_t ndim, const int64_t *shape, int64_t n_schemes,
+                        const int64_t *tile_shapes, int64_t bitmap_cap, void *workspace,
+                        size_t workspace_bytes, int64_t *num_tuples, int64_t *value_count,
+                        ej_stream_t stream);
 
 /* ---- relation to dense (reference: SparseTensorRelation.to_dense, :75-90) */
 /* Writes every tile of the relation into `dense` (row-major `shape`, fp32 or

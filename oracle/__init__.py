@@ -13,8 +13,15 @@ Modules
 
 Pinning (what checks each function; see tests/test_oracle.py):
   extract_coo, to_relation, relation_to_dense
-      reference known answers (tests/test_sparse.py:216-291), closed form
-      (round trip to_dense(to_relation(x)) == x), brute force on tiny inputs.
+      reference known answers (tests/test_sparse.py:216-291, :318-355),
+      closed form (round trip to_dense(to_relation(x)) == x), brute force on
+      tiny inputs (row-major nonzero order; a COO list with repeats equals a
+      sequential write of its nonzero entries).
+  divisors, all_tile_shapes, sparsity_metrics
+      reference known answers (tests/test_sparse.py:135-214,
+      tests/test_dense.py:41, :77-112, tests/test_rigorous.py:367-400) and
+      brute force: the occupancy of every tile shape by reducing the dense
+      blocks, value_count by projecting that occupancy.
   coordinate_join, coordinate_join_hash, coordinate_join_sorted
       match sets by brute force; counts from the reference tests
       (tests/test_sparse_dispatch.py:46-129, tests/test_pallas.py:235-338);

@@ -106,6 +106,41 @@ def dense_to_relation(dense: np.ndarray, tile_shape: tuple) -> Rel:
     return to_relation(idx, vals, shape, tile_shape)
 
 
+def divisors(n: int) -> list:
+    """Divisors of n ascending (core/notation.py:27-44); n <= 0 raises."""
+    if n <= 0:
+        raise ValueError(f"n must be positive, got {n}")
+    return [d for d in range(1, n + 1) if n % d == 0]
+
+
+def all_tile_shapes(shape: tuple) -> list:
+    """Every tile shape of a tensor, the product of the per-dimension
+    divisor lists in itertools.product order (tensor/base.py:39-49)."""
+    out = [()]
+    for n in shape:
+        out = [ts + (d,) for ts in out for d in divisors(n)]
+    return out
+
+
+def sparsity_metrics(indices: np.ndarray, values: np.ndarray, tile_shapes) -> dict:
+    """Per-tile-shape statistics (tensor/sparse.py:124-158): over the entries
+    with value != 0 (:139-141), num_tuples = number of distinct rows of
+    indices // tile_shape (np.unique(axis=0), :156-157) and value_count[d] =
+    number of distinct values in column d (:152-154); all zero when no entry
+    is nonzero (:143-147).  Returns {tile_shape: (num_tuples, value_count)}."""
+    nz = np.asarray(indices)[np.asarray(values) != 0]
+    out = {}
+    for ts in tile_shapes:
+        nd = len(ts)
+        if len(nz) == 0:
+            out[tuple(ts)] = (0, tuple(0 for _ in range(nd)))
+            continue
+        tc = nz // np.array(ts, dtype=np.int64)
+        vc = tuple(len(np.unique(tc[:, d])) for d in range(nd))
+        out[tuple(ts)] = (len(np.unique(tc, axis=0)), vc)
+    return out
+
+
 def relation_to_dense(rel: Rel) -> np.ndarray:
     """SparseTensorRelation.to_dense (tensor/sparse.py:75-90): tiles written in
     order into a zero array of the values' dtype."""

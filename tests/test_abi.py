@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 3
+    assert _lib.load().ej_version() == 4
 
 
 def describe(spec, lt, rt):
@@ -156,3 +156,60 @@ def test_error_status_mapping():
         _lib.check(_lib.EJ_E_CAPACITY, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.EJ_E_HIP, "x")
+
+
+def test_scheme_stats_workspace_and_validation():
+    lib = _lib.load()
+    shape = i64_array([16, 12])
+    shapes = [(a, b) for a in (1, 2, 4, 8, 16) for b in (1, 2, 3, 4, 6, 12)]
+    flat = i64_array([t for ts in shapes for t in ts])
+    dense, coo_map, coo_sort = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.ej_scheme_stats_workspace_size(2, shape, len(shapes), flat, -1, 0,
+                                              ctypes.byref(dense)) == 0
+    # the finest occupancy map alone is 16 * 12 bytes
+    assert dense.value >= 192
+    assert lib.ej_scheme_stats_workspace_size(2, shape, len(shapes), flat, 1000, 0,
+                                              ctypes.byref(coo_map)) == 0
+    # a cap of 8 cells sends the finer tile shapes to the sort path: key buffers
+    assert lib.ej_scheme_stats_workspace_size(2, shape, len(shapes), flat, 1000, 8,
+                                              ctypes.byref(coo_sort)) == 0
+    assert coo_sort.value > coo_map.value + 16 * 1000
+    bad = i64_array([16, 5])
+    assert lib.ej_scheme_stats_workspace_size(2, shape, 1, bad, -1, 0,
+                                              ctypes.byref(dense)) == _lib.EJ_E_INVAL
+    assert lib.ej_scheme_stats_workspace_size(2, i64_array([0, 4]), 1, i64_array([1, 1]), -1, 0,
+                                              ctypes.byref(dense)) == _lib.EJ_E_INVAL
+
+
+def test_scheme_stats_coo_without_entries_is_host_only():
+    lib = _lib.load()
+    nt = (ctypes.c_int64 * 2)(7, 7)
+    vc = (ctypes.c_int64 * 4)(7, 7, 7, 7)
+    st = lib.ej_scheme_stats_coo(None, None, _lib.EJ_F64, 0, 2, i64_array([4, 4]), 2,
+                                 i64_array([1, 1, 2, 4]), 0, None, 0, nt, vc, None)
+    assert st == 0 and list(nt) == [0, 0] and list(vc) == [0, 0, 0, 0]
+
+
+def test_coo_calls_host_paths():
+    lib = _lib.load()
+    n = ctypes.c_int64(-1)
+    a = ctypes.c_size_t()
+    assert lib.ej_extract_coo_count(None, _lib.EJ_F32, 2, i64_array([0, 5]), None, 0,
+                                    ctypes.byref(n), None) == 0 and n.value == 0
+    assert lib.ej_extract_coo_count(None, 9, 2, i64_array([2, 5]), None, 0, ctypes.byref(n),
+                                    None) == _lib.EJ_E_INVAL
+    assert lib.ej_extract_coo_workspace_size(2, i64_array([1024, 1024]), _lib.EJ_BF16,
+                                             ctypes.byref(a)) == 0 and a.value > 0
+    n.value = -1
+    assert lib.ej_bucket_coo_count(None, None, _lib.EJ_F64, 0, 2, i64_array([4, 4]),
+                                   i64_array([2, 2]), None, 0, ctypes.byref(n), None) == 0
+    assert n.value == 0
+    assert lib.ej_bucket_coo_count(None, None, _lib.EJ_F64, 3, 2, i64_array([4, 4]),
+                                   i64_array([3, 2]), None, 0, ctypes.byref(n),
+                                   None) == _lib.EJ_E_INVAL
+    assert lib.ej_bucket_coo_workspace_size(1 << 31, ctypes.byref(a)) == _lib.EJ_E_INVAL
+    assert lib.ej_bucket_coo_workspace_size(1000, ctypes.byref(a)) == 0 and a.value > 32000
+    assert lib.ej_bucket_coo_fill(None, _lib.EJ_F32, 10, 2, i64_array([4, 4]), i64_array([2, 2]),
+                                  None, 0, 3, None, None, 2, None) == _lib.EJ_E_CAPACITY
+    assert lib.ej_extract_coo_fill(None, _lib.EJ_F32, 2, i64_array([4, 4]), None, 0, 5, None,
+                                   None, 4, None) == _lib.EJ_E_CAPACITY

@@ -75,6 +75,122 @@ def test_to_relation_brute_force():
     npt.assert_array_equal(R.relation_to_dense(r), d)
 
 
+def test_extract_coo_known_answers():
+    # reference tests/test_sparse.py:318-355
+    idx, vals, shape = R.extract_coo(np.array([[1.0, 0.0], [0.0, 2.0]]))
+    assert shape == (2, 2) and idx.dtype == np.int32 and vals.dtype == np.float64
+    npt.assert_array_equal(idx, [[0, 0], [1, 1]])
+    npt.assert_array_equal(vals, [1.0, 2.0])
+    idx, vals, shape = R.extract_coo(np.zeros((3, 3)))
+    assert shape == (3, 3) and idx.shape == (0, 2) and len(vals) == 0
+    idx, vals, shape = R.extract_coo(np.array([0.0, 1.0, 0.0, 3.0]))
+    assert shape == (4,) and len(vals) == 2
+    import scipy.sparse as sp
+
+    idx, vals, shape = R.extract_coo(sp.csr_matrix(np.array([[1.0, 0.0], [0.0, 2.0]])))
+    assert shape == (2, 2) and len(vals) == 2
+
+
+def test_extract_coo_row_major_brute_force():
+    rng = np.random.default_rng(5)
+    d = rng.standard_normal((5, 7, 3)) * (rng.random((5, 7, 3)) < 0.3)
+    d[0, 0, 0] = np.nan  # NaN != 0: kept
+    d[1, 1, 1] = -0.0    # -0.0 == 0: dropped
+    idx, vals, _ = R.extract_coo(d)
+    want = [(i, j, k) for i in range(5) for j in range(7) for k in range(3)
+            if not (d[i, j, k] == 0)]
+    npt.assert_array_equal(idx, np.array(want))
+    npt.assert_array_equal(vals, np.array([d[w] for w in want]))
+
+
+def test_to_relation_from_coo_repeats_keep_last_entry():
+    # A COO list with repeated elements and explicit zeros: the tiles equal a
+    # sequential write of the nonzero entries in list order (the reference's
+    # to_dense_array loop, tensor/sparse.py:228-230, restricted to nonzeros).
+    rng = np.random.default_rng(9)
+    n = 400
+    idx = rng.integers(0, 12, size=(n, 2)).astype(np.int32)
+    vals = rng.standard_normal(n)
+    vals[rng.random(n) < 0.2] = 0.0
+    r = R.to_relation(idx, vals, (12, 12), (4, 3))
+    want = np.zeros((12, 12))
+    for (i, j), v in zip(idx, vals):
+        if v != 0:
+            want[i, j] = v
+    npt.assert_array_equal(R.relation_to_dense(r), want)
+    occupied = {(int(i) // 4, int(j) // 3) for (i, j), v in zip(idx, vals) if v != 0}
+    npt.assert_array_equal(r.coords, np.array(sorted(occupied)))
+
+
+# ---------------------------------------------------------------------------
+# tile shapes and statistics (reference tests/test_sparse.py:135-214,
+# tests/test_dense.py:77-112, tests/test_rigorous.py:367-400)
+
+def test_all_tile_shapes():
+    assert R.divisors(12) == [1, 2, 3, 4, 6, 12]
+    assert len(R.all_tile_shapes((3, 4, 5))) == 12   # test_dense.py:41
+    assert R.all_tile_shapes((3, 3)) == [(1, 1), (1, 3), (3, 1), (3, 3)]
+    assert R.all_tile_shapes((1, 1)) == [(1, 1)]     # test_rigorous.py:370-374
+    with pytest.raises(ValueError):
+        R.divisors(0)
+
+
+def metrics(data, shapes=None):
+    idx, vals, shape = R.extract_coo(np.asarray(data, dtype=np.float64))
+    return R.sparsity_metrics(idx, vals, shapes or R.all_tile_shapes(shape))
+
+
+def test_sparsity_metrics_known_answers():
+    m = metrics(np.array([[1.0, 0.0], [0.0, 2.0]]))
+    assert m[(2, 2)][0] == 1
+    m = metrics(np.diag([1.0, 2.0, 3.0]))
+    assert m[(1, 1)][0] == 3
+    m = metrics(np.diag([1.0, 2.0, 3.0, 4.0]))
+    assert m[(2, 2)] == (2, (2, 2))
+    d = np.zeros((4, 4))
+    d[0, 0], d[0, 3], d[1, 1] = 1.0, 2.0, 3.0
+    assert metrics(d)[(2, 2)] == (2, (1, 2))
+    assert metrics(np.zeros((3, 3)))[(1, 1)] == (0, (0, 0))
+    m = metrics(np.array([0.0, 1.0, 0.0, 3.0, 0.0, 0.0]))
+    assert m[(1,)][0] == 2 and m[(2,)][0] == 2 and m[(3,)][0] == 2
+    m = metrics(np.arange(1, 65).reshape(4, 4, 4).astype(float))
+    assert m[(2, 2, 2)][0] == 8
+    m = metrics(np.array([[1.0, 2, 0], [3.0, 4, 0], [5.0, 0, 0]]))
+    assert {ts: (n, vc) for ts, (n, vc) in m.items()} == {
+        (1, 1): (5, (3, 2)), (1, 3): (3, (3, 1)), (3, 1): (2, (1, 2)), (3, 3): (1, (1, 1))}
+    d = np.zeros((100, 100))
+    d[0, 0] = 1.0
+    m = metrics(d, [(1, 1), (100, 100)])
+    assert m[(1, 1)][0] == 1 and m[(100, 100)][0] == 1
+    assert metrics(np.ones((4, 4)), [(1, 1)])[(1, 1)][0] == 16
+    m = metrics(np.eye(4))
+    assert (m[(1, 1)][0], m[(1, 4)][0], m[(4, 1)][0], m[(2, 2)][0]) == (4, 4, 4, 2)
+
+
+def block_any(d, ts):
+    """Occupancy grid of tile shape ts by reducing the dense blocks."""
+    grid = tuple(n // t for n, t in zip(d.shape, ts))
+    inter = []
+    for g, t in zip(grid, ts):
+        inter += [g, t]
+    return (d.reshape(inter) != 0).any(axis=tuple(range(1, 2 * d.ndim, 2)))
+
+
+@pytest.mark.parametrize("shape,p", [((12, 18), 0.05), ((8, 6, 10), 0.02), ((30,), 0.2),
+                                     ((7, 4), 0.0)])
+def test_sparsity_metrics_brute_force(shape, p):
+    rng = np.random.default_rng(sum(shape))
+    d = rng.standard_normal(shape) * (rng.random(shape) < p)
+    m = metrics(d)
+    for ts, (n, vc) in m.items():
+        occ = block_any(d, ts)
+        assert n == int(occ.sum()), ts
+        for l in range(d.ndim):
+            other = tuple(a for a in range(d.ndim) if a != l)
+            assert vc[l] == int(occ.any(axis=other).sum()), (ts, l)
+    assert m[(1,) * d.ndim][0] == np.count_nonzero(d)
+
+
 # ---------------------------------------------------------------------------
 # joins
 
