@@ -19,6 +19,7 @@ join+gather+segment-sum, the roofline of the dominant kernel, and the CPU
 oracle timed on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--all-configs]
+                       [--ingest]
 """
 
 from __future__ import annotations
@@ -210,6 +211,78 @@ def measure_config(name: str, reps: int = 5) -> dict:
     return res
 
 
+def measure_ingest(cpu: bool = True) -> dict:
+    """Relation construction at full size: the per-tile-shape statistics of
+    every tile shape, nonzero counting, dense -> COO and COO -> tiles, for the
+    16384^2 bf16 block-sparse operand (225 tile shapes) and the statistics of
+    the 2048^3 fp32 order-3 operand (1728 tile shapes).  Each operand is
+    dense in HBM before timing; times are wall clock around each call,
+    including its host synchronisation.  The algorithmic bytes of the
+    statistics are one read of the dense operand; of dense -> COO that read
+    plus the COO written; of COO -> tiles the COO read plus the tiles
+    written."""
+    import torch
+
+    from einjax_amd import SparseTensorRelation, _device
+    from oracle import generators as G
+    from oracle import reference_path as R
+
+    out = {}
+    for name, gen, dt in (("blocksparse_16k_bf16_A", G.workload_blocksparse_16k, torch.bfloat16),
+                          ("order3_X", G.workload_order3, torch.float32)):
+        w = gen(values=False)
+        L = w["lhs"]
+        tile = L.tile_shape
+        nd = len(L.shape)
+        vals = (torch.rand((len(L.coords), *tile), device="cuda") + 0.5).to(dt)
+        rel = SparseTensorRelation(torch.from_numpy(L.coords).cuda(), vals, L.shape, tile)
+        dense = rel.to_dense()
+        del rel
+        shapes = R.all_tile_shapes(L.shape)
+        e = dense.element_size()
+        n_el = dense.numel()
+        t_stats = wall_time_ms(lambda: _device.scheme_stats(shapes, L.shape, dense=dense), 3)
+        B_stats = n_el * e
+        r = {"shape": list(L.shape), "dtype": str(dt).split(".")[-1], "tile_shapes": len(shapes),
+             "stats_ms": t_stats, "stats_gbs": B_stats / (t_stats * 1e-3) / 1e9,
+             "stats_hbm_frac": B_stats / (t_stats * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        t_cnt = wall_time_ms(lambda: _device.count_nonzero(dense), 3)
+        r["count_nonzero_ms"] = t_cnt
+        r["count_nonzero_gbs"] = B_stats / (t_cnt * 1e-3) / 1e9
+        if name.startswith("blocksparse"):
+            nnz = len(L.coords) * int(np.prod(tile))
+            t_ext = wall_time_ms(lambda: _device.extract_coo(dense), 3)
+            B_ext = n_el * e + nnz * (4 * nd + 8)
+            idx, v64 = _device.extract_coo(dense)
+            t_bc = wall_time_ms(lambda: _device.bucket_coo(idx, v64, L.shape, tile), 3)
+            B_bc = nnz * (4 * nd + 8) + len(L.coords) * int(np.prod(tile)) * 4
+            t_bd = wall_time_ms(lambda: _device.bucket_dense(dense, tile), 3)
+            r.update({"nnz": nnz, "extract_coo_ms": t_ext,
+                      "extract_coo_gbs": B_ext / (t_ext * 1e-3) / 1e9,
+                      "bucket_coo_ms": t_bc, "bucket_coo_gbs": B_bc / (t_bc * 1e-3) / 1e9,
+                      "bucket_dense_ms": t_bd})
+            if cpu:
+                # The oracle's statistics on the host COO: two tile shapes timed,
+                # scaled to all 225 (each tile shape costs one np.unique over
+                # every nonzero row).
+                hidx = idx.cpu().numpy()
+                hv = v64.cpu().numpy()
+                sample = [(128, 128), (64, 256)]
+                t0 = time.perf_counter()
+                R.sparsity_metrics(hidx, hv, sample)
+                t_cpu = time.perf_counter() - t0
+                r["cpu_baseline"] = {
+                    "value": t_cpu / len(sample) * len(shapes) * 1e3, "unit": "ms",
+                    "cores": 1, "kind": "port",
+                    "sample": f"oracle sparsity_metrics for {sample} on the {nnz} nonzeros "
+                              f"({t_cpu:.1f} s), scaled to {len(shapes)} tile shapes"}
+            del idx, v64
+        out[name] = r
+        del dense
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,6 +291,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all-configs", action="store_true",
                     help="also time every workload configuration at full size (adds 'configs')")
+    ap.add_argument("--ingest", action="store_true",
+                    help="also time relation construction at full size (adds 'ingest')")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path runs "
@@ -357,6 +432,10 @@ def main():
         for name in CONFIG_NAMES:
             log(f"config {name} ...")
             res["configs"][name] = measure_config(name)
+    if args.ingest:
+        torch.cuda.empty_cache()
+        log("relation construction ...")
+        res["ingest"] = measure_ingest(cpu=not args.no_cpu_baseline)
     print(json.dumps(res), flush=True)
 
 

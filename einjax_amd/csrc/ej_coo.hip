@@ -84,12 +84,23 @@ __device__ inline int wave_incl_i32(int v) {
   return v;
 }
 
-// Adds the wave's total of v to *acc (one atomic per wave).
-__device__ inline void wave_add(unsigned long long *acc, int64_t v) {
+// Adds the block's total of v to *acc: one atomic per 256-thread block.
+// Every thread of the block calls it.
+__device__ inline void block_add(unsigned long long *acc, int64_t v) {
+  __shared__ int64_t part[4];
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  if ((threadIdx.x & 63) == 0 && v) atomicAdd(acc, static_cast<unsigned long long>(v));
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int64_t t = part[0] + part[1] + part[2] + part[3];
+    if (t) atomicAdd(acc, static_cast<unsigned long long>(t));
+  }
 }
+
+// Counters of the statistics sit 128 bytes apart, so the atomics of
+// different tile shapes never contend for one cache line.
+constexpr int64_t kCountStride = 16;
 
 // Number of bytes of w that are nonzero, for bytes holding 0 or 1.
 __device__ inline int bytes_set(uint32_t w) { return static_cast<int>((w * 0x01010101u) >> 24); }
@@ -101,7 +112,9 @@ __global__ void fill_zero_kernel(T *p, int64_t n) {
   for (; i < n; i += stride) p[i] = T(0);
 }
 
-inline unsigned stride_grid(int64_t work, int64_t cap_blocks = 8192) {
+// Grid-stride launches: at most 8 blocks per CU, so the per-block atomics
+// stay few.
+inline unsigned stride_grid(int64_t work, int64_t cap_blocks = 2048) {
   int64_t g = ceil_div(work > 0 ? work : 1, kBlock);
   return static_cast<unsigned>(g < cap_blocks ? g : cap_blocks);
 }
@@ -410,43 +423,209 @@ template <typename T>
 __global__ __launch_bounds__(256) void dense_map_kernel(const T *__restrict__ dense, int64_t n,
                                                         bool vec, uint8_t *__restrict__ map,
                                                         unsigned long long *count) {
-  // One 4-element group per thread and iteration: one 32-bit store of flags.
-  const int64_t groups = (n + 3) / 4;
+  // 16 elements per thread and iteration: 16-byte loads, one 16-byte store of
+  // flags (the map is padded to 256 bytes, so the last store stays inside).
+  constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per load
+  constexpr int NL = 16 / E;                            // loads per group
+  const int64_t groups = (n + 15) / 16;
   int64_t c = 0;
   for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < groups;
        q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t i = q * 4;
-    T v[4];
-    if (vec && i + 4 <= n) {
-      if constexpr (sizeof(T) == 2) {
-        const uint2 w = *reinterpret_cast<const uint2 *>(dense + i);
-        __builtin_memcpy(&v[0], &w, 8);
-      } else if constexpr (sizeof(T) == 4) {
-        const uint4 w = *reinterpret_cast<const uint4 *>(dense + i);
-        __builtin_memcpy(&v[0], &w, 16);
-      } else {
-        const uint4 w0 = *reinterpret_cast<const uint4 *>(dense + i);
-        const uint4 w1 = *reinterpret_cast<const uint4 *>(dense + i + 2);
-        __builtin_memcpy(&v[0], &w0, 16);
-        __builtin_memcpy(&v[2], &w1, 16);
+    const int64_t i = q * 16;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (vec && i + 16 <= n) {
+      uint4 raw[NL];
+#pragma unroll
+      for (int l = 0; l < NL; ++l) raw[l] = reinterpret_cast<const uint4 *>(dense + i)[l];
+#pragma unroll
+      for (int l = 0; l < NL; ++l) {
+        T v[E];
+        __builtin_memcpy(&v[0], &raw[l], 16);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int k = l * E + e;
+          w[k >> 2] |= (nz(v[e]) ? 1u : 0u) << (8 * (k & 3));
+        }
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[k] = i + k < n ? dense[i + k] : T(0);
+      for (int k = 0; k < 16; ++k)
+        if (i + k < n && nz(dense[i + k])) w[k >> 2] |= 1u << (8 * (k & 3));
     }
-    uint32_t w = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w |= (nz(v[k]) ? 1u : 0u) << (8 * k);
-    *reinterpret_cast<uint32_t *>(map + i) = w;  // map rows are padded to 256 bytes
-    c += bytes_set(w);
+    *reinterpret_cast<uint4 *>(map + i) = make_uint4(w[0], w[1], w[2], w[3]);
+    c += bytes_set(w[0]) + bytes_set(w[1]) + bytes_set(w[2]) + bytes_set(w[3]);
   }
-  wave_add(count, c);
+  block_add(count, c);
 }
 
 // Pooling by OR: in [outer][n_out * p][inner] -> out [outer][n_out][inner].
 struct PoolGeom {
   int64_t outer, n_out, p, inner, total;  // total = outer * n_out * inner
 };
+
+// inner % 16 == 0: 16 outputs (one 16-byte word) per thread.
+template <typename I>
+__global__ __launch_bounds__(256) void pool_vec16_kernel(const uint8_t *__restrict__ in,
+                                                         uint8_t *__restrict__ out, PoolGeom g,
+                                                         unsigned long long *count) {
+  const I vecs = static_cast<I>(g.total / 16);
+  const I inner = static_cast<I>(g.inner), n_out = static_cast<I>(g.n_out),
+          p = static_cast<I>(g.p);
+  int64_t c = 0;
+  for (I w = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; w < vecs;
+       w += static_cast<I>(gridDim.x) * blockDim.x) {
+    const I o = w * 16;
+    const I r = o % inner, t = o / inner;
+    const I j = t % n_out, a = t / n_out;
+    const uint4 *src = reinterpret_cast<const uint4 *>(in + ((a * n_out + j) * p * inner + r));
+    const I step = inner / 16;
+    uint4 acc = make_uint4(0u, 0u, 0u, 0u);
+    for (I q = 0; q < p; ++q) {
+      const uint4 x = src[q * step];
+      acc.x |= x.x;
+      acc.y |= x.y;
+      acc.z |= x.z;
+      acc.w |= x.w;
+    }
+    reinterpret_cast<uint4 *>(out)[w] = acc;
+    c += bytes_set(acc.x) + bytes_set(acc.y) + bytes_set(acc.z) + bytes_set(acc.w);
+  }
+  block_add(count, c);
+}
+
+// Power-of-two pooling along the last dimension, counted without writing
+// the maps: a block reads 16384 consecutive map bytes, 64 per thread, and
+// counts the nonempty groups of 2^k bytes for k = 1 .. levels (<= 14) into
+// count[k - 1]; groups never cross a row because 2^levels divides the row
+// length.  Levels 1-6 are folded inside a thread's 64-bit mask of nonzero
+// bytes, 7-12 across the wave's ballot, 13-14 across the block's waves.
+// With write_level > 0 the map pooled by 2^write_level is written to out,
+// for the next kernel of a longer chain.
+constexpr int kChainMax = 14;
+constexpr int64_t kChainChunk = int64_t(256) * 64;
+
+struct ChainArgs {
+  int32_t levels;
+  int32_t write_level;
+  unsigned long long *count[kChainMax];
+};
+
+// Bits at positions that are multiples of 2^k, k = 1 .. 6.
+__device__ inline uint64_t level_mask(int k) {
+  switch (k) {
+    case 1: return 0x5555555555555555ull;
+    case 2: return 0x1111111111111111ull;
+    case 3: return 0x0101010101010101ull;
+    case 4: return 0x0001000100010001ull;
+    case 5: return 0x0000000100000001ull;
+    default: return 0x0000000000000001ull;
+  }
+}
+
+// 4 bits (one per byte) of a word whose bytes hold 0 or 1.
+__device__ inline uint32_t byte_bits(uint32_t w) {
+  return (w & 1u) | ((w >> 7) & 2u) | ((w >> 14) & 4u) | ((w >> 21) & 8u);
+}
+
+__global__ __launch_bounds__(256) void pool_chain_kernel(const uint8_t *__restrict__ in, int64_t S,
+                                                         ChainArgs a, uint8_t *__restrict__ out) {
+  __shared__ uint32_t wave_any[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t cnt[kChainMax];
+#pragma unroll
+  for (int k = 0; k < kChainMax; ++k) cnt[k] = 0;
+  const int64_t chunks = (S + kChainChunk - 1) / kChainChunk;
+  for (int64_t ch = blockIdx.x; ch < chunks; ch += gridDim.x) {
+    const int64_t base = ch * kChainChunk + static_cast<int64_t>(threadIdx.x) * 64;
+    uint64_t m = 0;
+    if (base + 64 <= S) {
+      const uint4 *src = reinterpret_cast<const uint4 *>(in + base);
+      uint4 v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = src[r];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        m |= static_cast<uint64_t>(byte_bits(v[r].x)) << (16 * r);
+        m |= static_cast<uint64_t>(byte_bits(v[r].y)) << (16 * r + 4);
+        m |= static_cast<uint64_t>(byte_bits(v[r].z)) << (16 * r + 8);
+        m |= static_cast<uint64_t>(byte_bits(v[r].w)) << (16 * r + 12);
+      }
+    } else if (base < S) {
+      for (int j = 0; j < 64 && base + j < S; ++j)
+        if (in[base + j]) m |= uint64_t(1) << j;
+    }
+    uint64_t g = m, gw = m;
+#pragma unroll
+    for (int k = 1; k <= 6; ++k) {
+      g = (g | (g >> (1 << (k - 1)))) & level_mask(k);
+      cnt[k - 1] += __popcll(g);
+      if (k == a.write_level) gw = g;
+    }
+    const uint64_t B = __ballot(m != 0);
+    uint64_t gb = B, gbw = B;
+#pragma unroll
+    for (int k = 7; k <= 12; ++k) {
+      gb = (gb | (gb >> (1 << (k - 7)))) & level_mask(k - 6);
+      if (lane == 0) cnt[k - 1] += __popcll(gb);
+      if (k == a.write_level) gbw = gb;
+    }
+    if (lane == 0) wave_any[wave] = B != 0 ? 1u : 0u;
+    __syncthreads();
+    const uint32_t w0 = wave_any[0], w1 = wave_any[1], w2 = wave_any[2], w3 = wave_any[3];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      cnt[12] += (w0 | w1) + (w2 | w3);
+      cnt[13] += w0 | w1 | w2 | w3;
+    }
+    const int W = a.write_level;
+    if (W > 0 && base < S) {
+      const int64_t ob = base >> W;  // first output byte of this thread's bytes
+      if (W <= 4) {
+        const int nw = (64 >> W) / 4;  // 32-bit words
+        for (int i = 0; i < nw; ++i) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            word |= static_cast<uint32_t>((gw >> ((4 * i + b) << W)) & 1u) << (8 * b);
+          reinterpret_cast<uint32_t *>(out + ob)[i] = word;
+        }
+      } else if (W == 5) {
+        out[ob] = static_cast<uint8_t>(gw & 1u);
+        out[ob + 1] = static_cast<uint8_t>((gw >> 32) & 1u);
+      } else if (W == 6) {
+        out[ob] = static_cast<uint8_t>(gw & 1u);
+      } else if (W <= 12) {
+        const int span = 1 << (W - 6);  // lanes per output byte
+        if ((lane & (span - 1)) == 0) out[ob] = static_cast<uint8_t>((gbw >> lane) & 1u);
+      } else if (threadIdx.x == 0) {
+        if (W == 13) {
+          out[ob] = static_cast<uint8_t>(w0 | w1);
+          if (base + 8192 < S) out[ob + 1] = static_cast<uint8_t>(w2 | w3);
+        } else {
+          out[ob] = static_cast<uint8_t>(w0 | w1 | w2 | w3);
+        }
+      }
+    }
+  }
+  // Block totals: the wave sums of levels 1-6, lane 0's sums of 7-12 and
+  // thread 0's of 13-14, then one atomic per level and block.
+  __shared__ int64_t part[4][kChainMax];
+#pragma unroll
+  for (int k = 0; k < kChainMax; ++k) {
+    int64_t v = cnt[k];
+    if (k < 6) {
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    }
+    if (lane == 0) part[wave][k] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < kChainMax && static_cast<int>(threadIdx.x) < a.levels) {
+    const int k = threadIdx.x;
+    const int64_t t = part[0][k] + part[1][k] + part[2][k] + part[3][k];
+    if (t) atomicAdd(a.count[k], static_cast<unsigned long long>(t));
+  }
+}
 
 // inner % 4 == 0: one 32-bit word of 4 outputs per thread.
 template <typename I>
@@ -470,7 +649,7 @@ __global__ __launch_bounds__(256) void pool_words_kernel(const uint8_t *__restri
     reinterpret_cast<uint32_t *>(out)[w] = acc;
     c += bytes_set(acc);
   }
-  wave_add(count, c);
+  block_add(count, c);
 }
 
 // inner == 1, p == 2, total % 4 == 0: 8 input bytes -> 4 outputs per thread.
@@ -489,7 +668,7 @@ __global__ __launch_bounds__(256) void pool_pairs_kernel(const uint8_t *__restri
     reinterpret_cast<uint32_t *>(out)[w] = acc;
     c += bytes_set(acc);
   }
-  wave_add(count, c);
+  block_add(count, c);
 }
 
 // Any geometry: one output byte per thread.
@@ -507,7 +686,7 @@ __global__ __launch_bounds__(256) void pool_bytes_kernel(const uint8_t *__restri
     out[o] = acc;
     c += acc;
   }
-  wave_add(count, c);
+  block_add(count, c);
 }
 
 // Tile index of entry i for the tile shape in ti; false when the entry is
@@ -553,7 +732,7 @@ __global__ __launch_bounds__(256) void map_count_kernel(const uint32_t *__restri
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < n_words;
        w += static_cast<int64_t>(gridDim.x) * blockDim.x)
     c += bytes_set(words[w]);
-  wave_add(count, c);
+  block_add(count, c);
 }
 
 template <typename T>
@@ -576,11 +755,14 @@ __global__ __launch_bounds__(256) void distinct_count_kernel(const uint64_t *__r
     const uint64_t k = keys[i];
     c += k != sentinel && (i == 0 || keys[i - 1] != k) ? 1 : 0;
   }
-  wave_add(count, c);
+  block_add(count, c);
 }
 
 // ---- the plan --------------------------------------------------------------
-enum NodeKind { kDenseRoot, kCooRoot, kPool, kSorted };
+// kChain: a power-of-two last tile extent pooled from its parent by 2 along
+// the last dimension; counted by pool_chain_kernel from the nearest
+// materialised ancestor, never materialised itself.
+enum NodeKind { kDenseRoot, kCooRoot, kPool, kSorted, kChain };
 
 struct StatNode {
   std::array<int64_t, EJ_MAX_DIMS> ts;
@@ -591,6 +773,7 @@ struct StatNode {
   int kind = kPool;
   std::vector<int> kids;
   size_t off = 0;      // map offset on the stack
+  size_t tmp_off = 0;  // chain maps of a chain longer than kChainMax levels
 };
 
 struct StatsPlan {
@@ -617,12 +800,36 @@ std::vector<int64_t> prime_factors(int64_t n) {
   return ps;
 }
 
+// Chain nodes below v, in level order.
+std::vector<int> chain_of(const StatsPlan &pl, int v) {
+  std::vector<int> c;
+  int cur = v;
+  for (;;) {
+    int next = -1;
+    for (int k : pl.nodes[cur].kids)
+      if (pl.nodes[k].kind == kChain) next = k;
+    if (next < 0) break;
+    c.push_back(next);
+    cur = next;
+  }
+  return c;
+}
+
 void layout(StatsPlan &pl, int v, size_t base) {
   StatNode &nd = pl.nodes[v];
   nd.off = base;
-  const size_t top = base + align_up(static_cast<size_t>(nd.cells), 256);
+  size_t top = base + align_up(static_cast<size_t>(nd.cells), 256);
+  // maps handed from one chain kernel to the next
+  nd.tmp_off = top;
+  const size_t levels = chain_of(pl, v).size();
+  int64_t cells = nd.cells;
+  for (size_t done = kChainMax; done < levels; done += kChainMax) {
+    cells >>= kChainMax;
+    top += align_up(static_cast<size_t>(cells), 256);
+  }
   if (top > pl.stack_bytes) pl.stack_bytes = top;
-  for (int k : pl.nodes[v].kids) layout(pl, k, top);
+  for (int k : pl.nodes[v].kids)
+    if (pl.nodes[k].kind != kChain) layout(pl, k, top);
 }
 
 // dense: nnz < 0.  cap: largest map in bytes for COO input (<= 0: default).
@@ -716,7 +923,10 @@ int make_plan(int32_t ndim, const int64_t *shape, int64_t n_schemes, const int64
     } else {
       n.kind = n.parent < 0 || pl->nodes[n.parent].kind == kSorted ? kCooRoot : kPool;
     }
-    if (n.kind == kPool) pl->nodes[n.parent].kids.push_back(v);
+    if (n.kind == kPool && n.pdim == ndim - 1 && n.pfac == 2 &&
+        (n.ts[ndim - 1] & (n.ts[ndim - 1] - 1)) == 0)
+      n.kind = kChain;
+    if (n.kind == kPool || n.kind == kChain) pl->nodes[n.parent].kids.push_back(v);
     if (n.kind == kDenseRoot || n.kind == kCooRoot) pl->roots.push_back(v);
   }
   for (int r : pl->roots) layout(*pl, r, 0);
@@ -735,7 +945,7 @@ struct StatsWs {
 StatsWs carve_stats(void *base, const StatsPlan &pl, int64_t nnz) {
   Carver c(base);
   StatsWs w{};
-  w.counts = c.take<unsigned long long>(static_cast<int64_t>(pl.nodes.size()) + 1);
+  w.counts = c.take<unsigned long long>((static_cast<int64_t>(pl.nodes.size()) + 1) * kCountStride);
   w.stack = c.take<uint8_t>(static_cast<int64_t>(pl.stack_bytes));
   if (pl.any_sorted) {
     w.keys = c.take<uint64_t>(nnz);
@@ -773,7 +983,15 @@ int launch_pool(const StatsPlan &pl, const StatNode &child, const uint8_t *in, u
   for (int e = d + 1; e < pl.nd; ++e) g.inner *= pl.shape[e] / child.ts[e];
   g.total = child.cells;
   (void)par;
-  if (g.inner % 4 == 0) {
+  if (g.inner % 16 == 0) {
+    const int64_t vecs = g.total / 16;
+    if (par.cells < (int64_t(1) << 31))
+      hipLaunchKernelGGL(pool_vec16_kernel<uint32_t>, dim3(stride_grid(vecs)), dim3(kBlock), 0,
+                         stream, in, out, g, count);
+    else
+      hipLaunchKernelGGL(pool_vec16_kernel<int64_t>, dim3(stride_grid(vecs)), dim3(kBlock), 0,
+                         stream, in, out, g, count);
+  } else if (g.inner % 4 == 0) {
     const int64_t words = g.total / 4;
     if (par.cells < (int64_t(1) << 31))
       hipLaunchKernelGGL(pool_words_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
@@ -792,11 +1010,43 @@ int launch_pool(const StatsPlan &pl, const StatNode &child, const uint8_t *in, u
   return EJ_OK;
 }
 
+int run_chain(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream) {
+  const std::vector<int> chain = chain_of(pl, v);
+  const StatNode &n = pl.nodes[v];
+  const uint8_t *src = w.stack + n.off;
+  int64_t S = n.cells;
+  uint8_t *tmp = w.stack + n.tmp_off;
+  for (size_t done = 0; done < chain.size(); done += kChainMax) {
+    ChainArgs a{};
+    a.levels = static_cast<int32_t>(std::min<size_t>(kChainMax, chain.size() - done));
+    const bool more = done + kChainMax < chain.size();
+    a.write_level = more ? kChainMax : 0;
+    for (int k = 0; k < a.levels; ++k) a.count[k] = w.counts + chain[done + k] * kCountStride;
+    const int64_t chunks = ceil_div(S, kChainChunk);
+    hipLaunchKernelGGL(pool_chain_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(chunks, 2048))),
+                       dim3(256), 0, stream, src, S, a, tmp);
+    EJ_LAUNCH_CHECK();
+    if (more) {
+      src = tmp;
+      S >>= kChainMax;
+      tmp += align_up(static_cast<size_t>(S), 256);
+    }
+  }
+  return EJ_OK;
+}
+
 int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream) {
   const StatNode &n = pl.nodes[v];
+  bool chained = false;
   for (int k : n.kids) {
     const StatNode &kid = pl.nodes[k];
-    EJ_TRY(launch_pool(pl, kid, w.stack + n.off, w.stack + kid.off, w.counts + k, stream));
+    if (kid.kind == kChain) {
+      if (!chained) EJ_TRY(run_chain(pl, v, w, stream));
+      chained = true;
+      continue;
+    }
+    EJ_TRY(launch_pool(pl, kid, w.stack + n.off, w.stack + kid.off, w.counts + k * kCountStride,
+                       stream));
     EJ_TRY(run_subtree(pl, k, w, stream));
   }
   return EJ_OK;
@@ -805,8 +1055,8 @@ int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream
 template <typename T>
 int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_dense,
               const int32_t *idx, const T *vals, int64_t nnz, hipStream_t stream) {
-  const int64_t n_counts = static_cast<int64_t>(pl.nodes.size()) + 1;
-  int64_t *bad = reinterpret_cast<int64_t *>(w.counts + pl.nodes.size());
+  const int64_t n_counts = (static_cast<int64_t>(pl.nodes.size()) + 1) * kCountStride;
+  int64_t *bad = reinterpret_cast<int64_t *>(w.counts + pl.nodes.size() * kCountStride);
   hipLaunchKernelGGL(fill_zero_kernel<unsigned long long>, dim3(stride_grid(n_counts)),
                      dim3(kBlock), 0, stream, w.counts, n_counts);
   EJ_LAUNCH_CHECK();
@@ -821,7 +1071,7 @@ int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_d
       EJ_TRY(sort_pairs_u64(w.keys, w.vals, w.keys_alt, w.vals_alt, nnz,
                             bits_for(static_cast<uint64_t>(n.cells) + 1), w.sort_ws, stream));
       hipLaunchKernelGGL(distinct_count_kernel, dim3(stride_grid(nnz)), dim3(kBlock), 0, stream,
-                         w.keys, nnz, static_cast<uint64_t>(n.cells), w.counts + v);
+                         w.keys, nnz, static_cast<uint64_t>(n.cells), w.counts + v * kCountStride);
       EJ_LAUNCH_CHECK();
     }
   }
@@ -829,9 +1079,9 @@ int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_d
     const StatNode &n = pl.nodes[r];
     uint8_t *map = w.stack + n.off;
     if (n.kind == kDenseRoot) {
-      const bool vec = (reinterpret_cast<uintptr_t>(dense) % (4 * sizeof(T))) == 0;
-      hipLaunchKernelGGL(dense_map_kernel<T>, dim3(stride_grid(ceil_div(n_dense, 4))),
-                         dim3(kBlock), 0, stream, dense, n_dense, vec, map, w.counts + r);
+      const bool vec = (reinterpret_cast<uintptr_t>(dense) % 16) == 0;
+      hipLaunchKernelGGL(dense_map_kernel<T>, dim3(stride_grid(ceil_div(n_dense, 16))),
+                         dim3(kBlock), 0, stream, dense, n_dense, vec, map, w.counts + r * kCountStride);
     } else {
       const int64_t words = static_cast<int64_t>(align_up(static_cast<size_t>(n.cells), 256) / 4);
       hipLaunchKernelGGL(fill_zero_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
@@ -841,7 +1091,7 @@ int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_d
                          vals, nnz, tile_idx(pl, n), map, bad);
       EJ_LAUNCH_CHECK();
       hipLaunchKernelGGL(map_count_kernel, dim3(stride_grid(words)), dim3(kBlock), 0, stream,
-                         reinterpret_cast<const uint32_t *>(map), words, w.counts + r);
+                         reinterpret_cast<const uint32_t *>(map), words, w.counts + r * kCountStride);
     }
     EJ_LAUNCH_CHECK();
     EJ_TRY(run_subtree(pl, r, w, stream));
@@ -851,18 +1101,19 @@ int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_d
 
 int finish_stats(const StatsPlan &pl, const StatsWs &w, int64_t *num_tuples,
                  int64_t *value_count, hipStream_t stream) {
-  std::vector<unsigned long long> host(pl.nodes.size() + 1);
+  std::vector<unsigned long long> host((pl.nodes.size() + 1) * kCountStride);
   EJ_HIP(hipMemcpyAsync(host.data(), w.counts, host.size() * sizeof(unsigned long long),
                         hipMemcpyDeviceToHost, stream));
   EJ_HIP(hipStreamSynchronize(stream));
-  if (host.back()) {
+  if (host[pl.nodes.size() * kCountStride]) {
     set_error("a nonzero entry has an index outside the tensor shape");
     return EJ_E_RANGE;
   }
   for (size_t s = 0; s < pl.req.size(); ++s) {
-    num_tuples[s] = static_cast<int64_t>(host[pl.req[s]]);
+    num_tuples[s] = static_cast<int64_t>(host[pl.req[s] * kCountStride]);
     for (int l = 0; l < pl.nd; ++l)
-      value_count[s * pl.nd + l] = static_cast<int64_t>(host[pl.proj[s * pl.nd + l]]);
+      value_count[s * pl.nd + l] =
+          static_cast<int64_t>(host[pl.proj[s * pl.nd + l] * kCountStride]);
   }
   return EJ_OK;
 }

@@ -172,8 +172,11 @@ def test_scipy_to_relation_without_densifying(gpu):
 # ---------------------------------------------------------------------------
 # statistics (reference: _compute_sparsity_metrics, tensor/sparse.py:124-158)
 
+# (3, 65536): last-dimension chains of 16 power-of-two levels, longer than one
+# counting pass; (4, 96, 32): chains from every (a, b, 1) map and odd factors.
 STAT_SHAPES = [((12, 18), 0.05), ((8, 6, 10), 0.02), ((30,), 0.2), ((7, 4), 0.3),
-               ((64, 48), 0.002), ((2, 3, 4, 5), 0.1), ((16, 16), 0.0), ((1, 1), 1.0)]
+               ((64, 48), 0.002), ((2, 3, 4, 5), 0.1), ((16, 16), 0.0), ((1, 1), 1.0),
+               ((3, 65536), 0.0005), ((4, 96, 32), 0.01)]
 
 
 @pytest.mark.parametrize("dtype", ["f64", "f32", "bf16"])
@@ -191,7 +194,7 @@ def test_scheme_stats_dense_parity(gpu, dtype, shape, p):
 
 @pytest.mark.parametrize("cap", [0, 40, 8, 1])
 @pytest.mark.parametrize("shape,n", [((12, 18), 40), ((8, 6, 10), 60), ((30,), 9),
-                                     ((64, 48), 500)])
+                                     ((64, 48), 500), ((131072,), 300)])
 def test_scheme_stats_coo_parity(gpu, cap, shape, n):
     """bitmap_cap moves tile shapes between the map path and the sort path;
     the counts must not change."""
