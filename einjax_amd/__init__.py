@@ -7,6 +7,7 @@ block-sparse matmul and the coordinate joins.  All computation runs in
 libejhip.so (HIP kernels behind a C ABI, include/einjax_hip.h).
 """
 
+from .autodiff import sparse_einsum, sparse_einsum_raw, sparse_einsum_raw_vjp
 from .execution.sparse_dispatch import (
     coordinate_join,
     execute_sharded_sparse,
@@ -38,5 +39,5 @@ __all__ = [
     "rank_schemes_by_sparsity", "select_best_sparse_tiling", "coordinate_join",
     "kernel_einsum", "segment_sum", "execute_sparse", "execute_sharded_sparse", "KernelRegistry",
     "KernelInfo", "block_sparse_matmul", "block_sparse_matmul_generic", "coordinate_join_hash",
-    "coordinate_join_sorted",
+    "coordinate_join_sorted", "sparse_einsum", "sparse_einsum_raw", "sparse_einsum_raw_vjp",
 ]

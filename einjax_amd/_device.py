@@ -454,3 +454,52 @@ def scheme_stats(tile_shapes, shape, dense: torch.Tensor | None = None,
                                       stream_ptr()), "ej_scheme_stats_coo")
     return ([int(nt[s]) for s in range(S)],
             [tuple(int(vc[s * nd + l]) for l in range(nd)) for s in range(S)])
+
+
+def index_plan(idx: torch.Tensor, n_targets: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(perm int32 [n], offsets int32 [n_targets + 1]): positions grouped by
+    target, ascending inside a target; out-of-range targets come last."""
+    lib = _lib.load()
+    idx = idx.to(dtype=torch.int64).contiguous().reshape(-1)
+    n = idx.numel()
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_index_plan_workspace_size(n, ctypes.byref(nbytes)),
+          "ej_index_plan_workspace_size")
+    ws = workspace(nbytes.value, idx.device)
+    perm = torch.empty((n,), dtype=torch.int32, device=idx.device)
+    offsets = torch.empty((n_targets + 1,), dtype=torch.int32, device=idx.device)
+    check(lib.ej_index_plan(ptr(idx), n, n_targets, ptr(perm), ptr(offsets), ptr(ws), ws.numel(),
+                            stream_ptr()), "ej_index_plan")
+    return perm, offsets
+
+
+def pair_einsum_vjp(kernel_string: str, lhs_values: torch.Tensor, rhs_values: torch.Tensor,
+                    lhs_idx: torch.Tensor, rhs_idx: torch.Tensor, grad_out: torch.Tensor,
+                    need_lhs: bool = True, need_rhs: bool = True):
+    """(grad_lhs, grad_rhs), fp32 with the operands' tile shapes (None when
+    not requested): the gradients of the per-pair tile einsum for the
+    cotangent grad_out [P, *out_tile]."""
+    lib = _lib.load()
+    code = value_code(lhs_values)
+    if rhs_values.dtype != lhs_values.dtype:
+        raise TypeError("both operands must have the same value dtype")
+    lt, rt = tuple(lhs_values.shape[1:]), tuple(rhs_values.shape[1:])
+    nl, nr = lhs_values.shape[0], rhs_values.shape[0]
+    li = lhs_idx.to(dtype=torch.int64).contiguous().reshape(-1)
+    ri = rhs_idx.to(dtype=torch.int64).contiguous().reshape(-1)
+    P = li.numel()
+    g = grad_out.to(dtype=torch.float32).contiguous()
+    dev = lhs_values.device
+    gl = torch.empty((nl, *lt), dtype=torch.float32, device=dev) if need_lhs else None
+    gr = torch.empty((nr, *rt), dtype=torch.float32, device=dev) if need_rhs else None
+    nbytes = ctypes.c_size_t()
+    check(lib.ej_pair_einsum_vjp_workspace_size(P, nl, nr, max(prod(lt), 1), max(prod(rt), 1),
+                                                code, ctypes.byref(nbytes)),
+          "ej_pair_einsum_vjp_workspace_size")
+    ws = workspace(nbytes.value, dev)
+    check(lib.ej_pair_einsum_vjp(kernel_string.encode(), i64_array(lt), len(lt), i64_array(rt),
+                                 len(rt), code, ptr(lhs_values.contiguous()), nl,
+                                 ptr(rhs_values.contiguous()), nr, ptr(li), ptr(ri), P, ptr(g),
+                                 ptr(gl), ptr(gr), ptr(ws), ws.numel(), stream_ptr()),
+          "ej_pair_einsum_vjp")
+    return gl, gr

@@ -1,0 +1,283 @@
+// Backward of the per-pair tile einsum.
+//
+// Reference: sparse_einsum_raw._bwd (autodiff/custom_vjp.py:254-275).  For
+// the forward out[p] = einsum("A,B->C", lhs[li[p]], rhs[ri[p]]) and the
+// cotangent g[p] of out[p]:
+//   grad_lhs[l] = sum over pairs p with li[p] == l of einsum("C,B->A", g[p], rhs[ri[p]])
+//   grad_rhs[r] = sum over pairs p with ri[p] == r of einsum("A,C->B", lhs[li[p]], g[p])
+// (the reversed strings of _reverse_einsum_string, custom_vjp.py:31-62; the
+// sums are the reference's .at[idx].add scatter, :271-272).
+//
+// The scatter becomes a segment sum keyed by operand tile: ej_index_plan
+// groups the pairs by target tile with a stable radix sort (positions
+// ascending inside a target), and the fused segment einsum computes every
+// gradient tile in one workgroup pass, written once, in a fixed order, with
+// no atomics.  Tiles that no pair touches get zeros.
+#include "ej_internal.h"
+
+#include <string.h>
+
+#include <string>
+
+namespace ej {
+namespace {
+
+__global__ __launch_bounds__(256) void plan_keys_kernel(const int64_t *__restrict__ idx, int64_t n,
+                                                        int64_t n_targets,
+                                                        uint64_t *__restrict__ keys,
+                                                        int32_t *__restrict__ pos) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t t = idx[i];
+  keys[i] = t >= 0 && t < n_targets ? static_cast<uint64_t>(t) : static_cast<uint64_t>(n_targets);
+  pos[i] = static_cast<int32_t>(i);
+}
+
+// offsets[t] = number of sorted keys below t, for t in [0, n_targets].
+__global__ __launch_bounds__(256) void plan_offsets_kernel(const uint64_t *__restrict__ keys,
+                                                           int64_t n, int64_t n_targets,
+                                                           int32_t *__restrict__ offsets) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t > n_targets) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < static_cast<uint64_t>(t)) lo = mid + 1;
+    else hi = mid;
+  }
+  offsets[t] = static_cast<int32_t>(lo);
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t *__restrict__ in,
+                                                          float *__restrict__ out, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    out[i] = __uint_as_float(static_cast<uint32_t>(in[i]) << 16);
+}
+
+__global__ void zero_f32_kernel(float *p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0.0f;
+}
+
+unsigned grid_capped(int64_t n) {
+  const int64_t g = ceil_div(n > 0 ? n : 1, kBlock);
+  return static_cast<unsigned>(g < 4096 ? g : 4096);
+}
+
+struct PlanWs {
+  uint64_t *keys, *keys_alt;
+  int32_t *pos_alt;
+  void *sort_ws;
+  size_t bytes;
+};
+
+PlanWs carve_plan(Carver &c, int64_t n) {
+  PlanWs w;
+  const size_t start = c.off;
+  w.keys = c.take<uint64_t>(n);
+  w.keys_alt = c.take<uint64_t>(n);
+  w.pos_alt = c.take<int32_t>(n);
+  w.sort_ws = c.take<char>(static_cast<int64_t>(sort_workspace_bytes(n)));
+  w.bytes = c.off - start;
+  return w;
+}
+
+int index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *perm, int32_t *offsets,
+               const PlanWs &w, hipStream_t stream) {
+  const int bits = [&] {
+    int b = 0;
+    while (b < 63 && (int64_t(1) << b) < n_targets + 1) ++b;
+    return b;
+  }();
+  if (n > 0) {
+    const bool alt = radix_passes(bits) % 2 == 1;
+    hipLaunchKernelGGL(plan_keys_kernel, dim3(grid_for(n)), dim3(kBlock), 0, stream, idx, n,
+                       n_targets, alt ? w.keys_alt : w.keys, alt ? w.pos_alt : perm);
+    EJ_LAUNCH_CHECK();
+    EJ_TRY(sort_pairs_u64(w.keys, perm, w.keys_alt, w.pos_alt, n, bits, w.sort_ws, stream, alt));
+  }
+  hipLaunchKernelGGL(plan_offsets_kernel, dim3(grid_for(n_targets + 1)), dim3(kBlock), 0, stream,
+                     w.keys, n, n_targets, offsets);
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+// "A,B->C" -> terms A, B, C (no validation beyond the separators; the
+// descriptor parser checks the labels).
+int split_terms(const char *ks, std::string *a, std::string *b, std::string *c) {
+  EJ_CHECK_ARG(ks, "kernel_string is null");
+  const char *arrow = strstr(ks, "->");
+  EJ_CHECK_ARG(arrow, "kernel_string must contain '->': %s", ks);
+  const char *comma = static_cast<const char *>(memchr(ks, ',', arrow - ks));
+  EJ_CHECK_ARG(comma, "kernel_string must have exactly two operands: %s", ks);
+  a->assign(ks, comma - ks);
+  b->assign(comma + 1, arrow - comma - 1);
+  c->assign(arrow + 2);
+  return EJ_OK;
+}
+
+struct VjpWs {
+  int32_t *perm_l, *off_l, *perm_r, *off_r;
+  float *lhs32, *rhs32;
+  PlanWs plan;
+  size_t bytes;
+};
+
+VjpWs carve_vjp(void *base, int64_t n_pairs, int64_t n_lhs, int64_t n_rhs, int64_t lhs_elems,
+                int64_t rhs_elems, int32_t dtype) {
+  Carver c(base);
+  VjpWs w{};
+  w.perm_l = c.take<int32_t>(n_pairs);
+  w.off_l = c.take<int32_t>(n_lhs + 1);
+  w.perm_r = c.take<int32_t>(n_pairs);
+  w.off_r = c.take<int32_t>(n_rhs + 1);
+  if (dtype == EJ_BF16) {
+    w.lhs32 = c.take<float>(n_lhs * lhs_elems);
+    w.rhs32 = c.take<float>(n_rhs * rhs_elems);
+  }
+  w.plan = carve_plan(c, n_pairs);
+  w.bytes = c.off;
+  return w;
+}
+
+}  // namespace
+}  // namespace ej
+
+using namespace ej;
+
+extern "C" int ej_index_plan_workspace_size(int64_t n, size_t *bytes) {
+  clear_error();
+  EJ_CHECK_ARG(bytes, "bytes is null");
+  EJ_CHECK_ARG(n >= 0 && n <= INT32_MAX, "n=%lld outside [0, 2^31)", (long long)n);
+  Carver c(nullptr);
+  *bytes = carve_plan(c, n).bytes;
+  return EJ_OK;
+}
+
+extern "C" int ej_index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *perm,
+                             int32_t *offsets, void *workspace, size_t workspace_bytes,
+                             ej_stream_t stream) {
+  clear_error();
+  EJ_CHECK_ARG(n >= 0 && n <= INT32_MAX, "n=%lld outside [0, 2^31)", (long long)n);
+  EJ_CHECK_ARG(n_targets >= 0 && n_targets < INT32_MAX, "n_targets out of range");
+  EJ_CHECK_ARG(offsets && (n == 0 || (idx && perm)), "null pointer argument");
+  Carver c(workspace);
+  PlanWs w = carve_plan(c, n);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  return index_plan(idx, n, n_targets, perm, offsets, w, as_stream(stream));
+}
+
+extern "C" int ej_pair_einsum_vjp_workspace_size(int64_t n_pairs, int64_t n_lhs_tiles,
+                                                 int64_t n_rhs_tiles, int64_t lhs_elems,
+                                                 int64_t rhs_elems, int32_t dtype,
+                                                 size_t *bytes) {
+  clear_error();
+  EJ_CHECK_ARG(bytes, "bytes is null");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(n_pairs >= 0 && n_pairs <= INT32_MAX, "n_pairs outside [0, 2^31)");
+  EJ_CHECK_ARG(n_lhs_tiles >= 0 && n_lhs_tiles < INT32_MAX && n_rhs_tiles >= 0 &&
+                   n_rhs_tiles < INT32_MAX && lhs_elems >= 1 && rhs_elems >= 1,
+               "bad sizes");
+  *bytes = carve_vjp(nullptr, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype).bytes;
+  return EJ_OK;
+}
+
+extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_tile,
+                                  int32_t lhs_ndim, const int64_t *rhs_tile, int32_t rhs_ndim,
+                                  int32_t dtype, const void *lhs_values, int64_t n_lhs_tiles,
+                                  const void *rhs_values, int64_t n_rhs_tiles,
+                                  const int64_t *lhs_idx, const int64_t *rhs_idx,
+                                  int64_t n_pairs, const float *grad_out, float *grad_lhs,
+                                  float *grad_rhs, void *workspace, size_t workspace_bytes,
+                                  ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(n_pairs >= 0 && n_pairs <= INT32_MAX, "n_pairs outside [0, 2^31)");
+  EJ_CHECK_ARG(n_lhs_tiles >= 0 && n_lhs_tiles < INT32_MAX && n_rhs_tiles >= 0 &&
+                   n_rhs_tiles < INT32_MAX,
+               "tile counts out of range");
+  std::string ta, tb, tc;
+  EJ_TRY(split_terms(kernel_string, &ta, &tb, &tc));
+  // Forward descriptor: validates the string against the tiles and gives
+  // the output tile extents (label order of the output term).
+  ej_einsum_desc fwd;
+  EJ_TRY(ej_einsum_describe(kernel_string, lhs_tile, lhs_ndim, rhs_tile, rhs_ndim, &fwd));
+  int64_t out_tile[EJ_MAX_LABELS];
+  for (int i = 0; i < fwd.n_out; ++i) out_tile[i] = fwd.out_ext[i];
+  int64_t lhs_elems = 1, rhs_elems = 1;
+  for (int i = 0; i < lhs_ndim; ++i) lhs_elems *= lhs_tile[i];
+  for (int i = 0; i < rhs_ndim; ++i) rhs_elems *= rhs_tile[i];
+  const std::string s_lhs = tc + "," + tb + "->" + ta;  // grad_lhs: "C,B->A"
+  const std::string s_rhs = ta + "," + tc + "->" + tb;  // grad_rhs: "A,C->B"
+  ej_einsum_desc dl, dr;
+  if (grad_lhs) {
+    const int st = ej_einsum_describe(s_lhs.c_str(), out_tile, fwd.n_out, rhs_tile, rhs_ndim, &dl);
+    if (st != EJ_OK) {
+      set_error("gradient string %s for the lhs is not a valid einsum of the output and rhs "
+                "tiles: %s", s_lhs.c_str(), ej_last_error());
+      return st;
+    }
+  }
+  if (grad_rhs) {
+    const int st = ej_einsum_describe(s_rhs.c_str(), lhs_tile, lhs_ndim, out_tile, fwd.n_out, &dr);
+    if (st != EJ_OK) {
+      set_error("gradient string %s for the rhs is not a valid einsum of the lhs and output "
+                "tiles: %s", s_rhs.c_str(), ej_last_error());
+      return st;
+    }
+  }
+  if (!grad_lhs && !grad_rhs) return EJ_OK;
+  VjpWs w = carve_vjp(workspace, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
+               workspace_bytes, w.bytes);
+  EJ_CHECK_ARG(n_pairs == 0 || (grad_out && lhs_idx && rhs_idx), "null pointer argument");
+  EJ_CHECK_ARG((!grad_lhs || n_rhs_tiles == 0 || rhs_values) &&
+                   (!grad_rhs || n_lhs_tiles == 0 || lhs_values),
+               "null operand values");
+  const void *lhs_v = lhs_values, *rhs_v = rhs_values;
+  if (dtype == EJ_BF16) {
+    // The cotangent is fp32; the operands are widened to fp32 once so the
+    // gradient einsums run in fp32 throughout.
+    if (grad_rhs && n_lhs_tiles > 0) {
+      hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_capped(n_lhs_tiles * lhs_elems)),
+                         dim3(kBlock), 0, stream, static_cast<const uint16_t *>(lhs_values),
+                         w.lhs32, n_lhs_tiles * lhs_elems);
+      EJ_LAUNCH_CHECK();
+      lhs_v = w.lhs32;
+    }
+    if (grad_lhs && n_rhs_tiles > 0) {
+      hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_capped(n_rhs_tiles * rhs_elems)),
+                         dim3(kBlock), 0, stream, static_cast<const uint16_t *>(rhs_values),
+                         w.rhs32, n_rhs_tiles * rhs_elems);
+      EJ_LAUNCH_CHECK();
+      rhs_v = w.rhs32;
+    }
+  }
+  if (grad_lhs && n_lhs_tiles > 0) {
+    if (n_pairs == 0 || n_rhs_tiles == 0) {
+      hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_capped(n_lhs_tiles * lhs_elems)),
+                         dim3(kBlock), 0, stream, grad_lhs, n_lhs_tiles * lhs_elems);
+      EJ_LAUNCH_CHECK();
+    } else {
+      EJ_TRY(index_plan(lhs_idx, n_pairs, n_lhs_tiles, w.perm_l, w.off_l, w.plan, stream));
+      EJ_TRY(ej_segment_einsum(&dl, EJ_F32, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
+                               rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, grad_lhs, stream_));
+    }
+  }
+  if (grad_rhs && n_rhs_tiles > 0) {
+    if (n_pairs == 0 || n_lhs_tiles == 0) {
+      hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_capped(n_rhs_tiles * rhs_elems)),
+                         dim3(kBlock), 0, stream, grad_rhs, n_rhs_tiles * rhs_elems);
+      EJ_LAUNCH_CHECK();
+    } else {
+      EJ_TRY(index_plan(rhs_idx, n_pairs, n_rhs_tiles, w.perm_r, w.off_r, w.plan, stream));
+      EJ_TRY(ej_segment_einsum(&dr, EJ_F32, lhs_v, grad_out, n_lhs_tiles, n_pairs, lhs_idx,
+                               nullptr, w.perm_r, w.off_r, n_rhs_tiles, grad_rhs, stream_));
+    }
+  }
+  return EJ_OK;
+}

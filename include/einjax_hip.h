@@ -34,10 +34,13 @@
  *                  execution/sparse_dispatch.py:226-297, without waiting)
  *   segment sum   ej_segment_sum
  *                 (the accumulation half of segment_sum, execution/sparse_dispatch.py:164-171)
+ *   backward      ej_index_plan / ej_pair_einsum_vjp
+ *                 (replace sparse_einsum_raw's backward, autodiff/custom_vjp.py:254-275)
  *
  * Conventions
  *   - Every pointer argument named *coords, *values, *_idx, *keys, perm,
- *     seg_*, out*, dense, indices, tiles and workspace is a DEVICE pointer.
+ *     seg_*, out*, dense, indices, tiles, idx, offsets, grad_* and workspace
+ *     is a DEVICE pointer.
  *     Small descriptor arrays (dims, radices, shapes, tile_shapes, agg_*),
  *     the scalar outputs n_pairs, n_segments, n_tiles, nnz and the
  *     statistics num_tuples / value_count are HOST pointers; `counts` of the
@@ -68,7 +71,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 4
+#define EJ_ABI_VERSION 5
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -371,6 +374,42 @@ int ej_scheme_stats_coo(const int32_t *indices, const void *values, int32_t dtyp
                         const int64_t *tile_shapes, int64_t bitmap_cap, void *workspace,
                         size_t workspace_bytes, int64_t *num_tuples, int64_t *value_count,
                         ej_stream_t stream);
+
+/* ---- backward (reference: sparse_einsum_raw._bwd, autodiff/custom_vjp.py:254-275) */
+/* Groups positions 0 .. n-1 by target idx[p] in [0, n_targets): perm int32
+ * [n] lists them target by target, ascending position within a target;
+ * offsets int32 [n_targets + 1] delimits the targets; positions whose target
+ * lies outside the range come last in perm, beyond offsets[n_targets].
+ * n < 2^31.  Asynchronous.  This is the grouping of the reference's
+ * .at[indices].add scatter (:271-272), made deterministic. */
+int ej_index_plan_workspace_size(int64_t n, size_t *bytes);
+int ej_index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *perm,
+                  int32_t *offsets, void *workspace, size_t workspace_bytes, ej_stream_t stream);
+
+/* Gradients of out[p] = einsum(kernel_string, lhs_values[lhs_idx[p]],
+ * rhs_values[rhs_idx[p]]) for the fp32 cotangent grad_out [n_pairs,
+ * *out_tile]:
+ *   grad_lhs[l] = sum_{p: lhs_idx[p] == l} einsum("C,B->A", grad_out[p], rhs_values[rhs_idx[p]])
+ *   grad_rhs[r] = sum_{p: rhs_idx[p] == r} einsum("A,C->B", lhs_values[lhs_idx[p]], grad_out[p])
+ * for kernel_string "A,B->C" (the reference's reversed strings,
+ * custom_vjp.py:31-62).  grad_lhs fp32 [n_lhs_tiles, *lhs_tile] and grad_rhs
+ * fp32 [n_rhs_tiles, *rhs_tile] are fully written (zeros where no pair
+ * contributes); either may be NULL to skip it.  Each gradient tile is summed
+ * in ascending pair order, without atomics, so results are reproducible.  A
+ * pair whose index lies outside its operand's tile count contributes
+ * nothing.  A reversed string that is not a valid einsum of its operands (a
+ * label of A found in neither C nor B) gives EJ_E_INVAL, as the reference's
+ * jnp.einsum raises.  dtype (EJ_F32 / EJ_BF16) is the dtype of the operand
+ * values; bf16 operands are widened to fp32 in the workspace. */
+int ej_pair_einsum_vjp_workspace_size(int64_t n_pairs, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
+                                      int64_t lhs_elems, int64_t rhs_elems, int32_t dtype,
+                                      size_t *bytes);
+int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_tile, int32_t lhs_ndim,
+                       const int64_t *rhs_tile, int32_t rhs_ndim, int32_t dtype,
+                       const void *lhs_values, int64_t n_lhs_tiles, const void *rhs_values,
+                       int64_t n_rhs_tiles, const int64_t *lhs_idx, const int64_t *rhs_idx,
+                       int64_t n_pairs, const float *grad_out, float *grad_lhs, float *grad_rhs,
+                       void *workspace, size_t workspace_bytes, ej_stream_t stream);
 
 /* ---- relation to dense (reference: SparseTensorRelation.to_dense, :75-90) */
 /* Writes every tile of the relation into `dense` (row-major `shape`, fp32 or

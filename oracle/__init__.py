@@ -37,6 +37,11 @@ Pinning (what checks each function; see tests/test_oracle.py):
   segment_sum, segment_plan
       reference known answers (tests/test_sparse_dispatch.py:204-252) and the
       closed form (sorted unique coordinates, per-segment sums), brute force.
+  reverse_einsum_string, pair_einsum_vjp
+      reference known answers (tests/test_autodiff.py:42-72 for the strings;
+      the gradients of :160-400 in closed form) and central finite
+      differences in float64 of the forward kernel_einsum, exact for this
+      bilinear map up to rounding.
   execute_sparse, block_sparse_matmul_generic, block_sparse_matmul
       to_dense(result) == einsum of the dense operands (the reference's own
       end-to-end tests, tests/test_sparse_dispatch.py:263-426,

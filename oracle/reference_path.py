@@ -283,6 +283,35 @@ def kernel_einsum(lhs_values, rhs_values, lhs_idx, rhs_idx, kernel_string, preci
     return batched_einsum(add_batch_dim(kernel_string), L, R).astype(dt, copy=False)
 
 
+def reverse_einsum_string(kernel_string: str) -> tuple:
+    """autodiff/custom_vjp.py:31-62: "A,B->C" -> ("C,B->A", "A,C->B");
+    ValueError without "->"."""
+    if "->" not in kernel_string:
+        raise ValueError(f"kernel_string must contain '->': {kernel_string}")
+    ins, out = kernel_string.split("->")
+    terms = ins.split(",")
+    return f"{out},{terms[1]}->{terms[0]}", f"{terms[0]},{out}->{terms[1]}"
+
+
+def pair_einsum_vjp(lhs_values, rhs_values, lhs_idx, rhs_idx, kernel_string, g):
+    """The backward of sparse_einsum_raw (autodiff/custom_vjp.py:254-275) in
+    float64: zero gradients shaped like the values (:259-260), per-pair
+    einsums with the reversed strings and the batch label (:266-270), summed
+    into the operand tiles with np.add.at, the restatement of
+    .at[indices].add (:271-272)."""
+    L = np.asarray(lhs_values, dtype=np.float64)
+    Rv = np.asarray(rhs_values, dtype=np.float64)
+    gl = np.zeros(L.shape, np.float64)
+    gr = np.zeros(Rv.shape, np.float64)
+    li, ri = np.asarray(lhs_idx, dtype=np.int64), np.asarray(rhs_idx, dtype=np.int64)
+    if len(li):
+        sl, sr = reverse_einsum_string(kernel_string)
+        G = np.asarray(g, dtype=np.float64)
+        np.add.at(gl, li, np.einsum(add_batch_dim(sl), G, Rv[ri]))
+        np.add.at(gr, ri, np.einsum(add_batch_dim(sr), L[li], G))
+    return gl, gr
+
+
 def batched_einsum(spec: str, L: np.ndarray, R: np.ndarray) -> np.ndarray:
     """np.einsum(spec, L, R), routed through np.matmul when the operands are
     in matmul layout: a common label prefix (batch), lhs = M + K,

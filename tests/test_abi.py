@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 4
+    assert _lib.load().ej_version() == 5
 
 
 def describe(spec, lt, rt):
@@ -213,3 +213,24 @@ def test_coo_calls_host_paths():
                                   None, 0, 3, None, None, 2, None) == _lib.EJ_E_CAPACITY
     assert lib.ej_extract_coo_fill(None, _lib.EJ_F32, 2, i64_array([4, 4]), None, 0, 5, None,
                                    None, 4, None) == _lib.EJ_E_CAPACITY
+
+
+def test_backward_host_validation():
+    lib = _lib.load()
+    a = ctypes.c_size_t()
+    assert lib.ej_index_plan_workspace_size(1000, ctypes.byref(a)) == 0 and a.value > 16000
+    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, _lib.EJ_BF16,
+                                                 ctypes.byref(a)) == 0
+    bf = a.value
+    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, _lib.EJ_F32,
+                                                 ctypes.byref(a)) == 0
+    assert bf >= a.value + 4 * 64 * 20  # bf16 operands are widened in the workspace
+    t = i64_array([2, 2])
+    fake = ctypes.c_void_p(16)
+    # "ij,jk->k": the lhs gradient string "k,jk->ij" names i, found in no operand
+    st = lib.ej_pair_einsum_vjp(b"ij,jk->k", t, 2, t, 2, _lib.EJ_F32, fake, 1, fake, 1, fake,
+                                fake, 1, fake, fake, None, None, 0, None)
+    assert st == _lib.EJ_E_INVAL and b"gradient string" in lib.ej_last_error()
+    st = lib.ej_pair_einsum_vjp(b"ij,jk", t, 2, t, 2, _lib.EJ_F32, fake, 1, fake, 1, fake,
+                                fake, 1, fake, fake, None, None, 0, None)
+    assert st == _lib.EJ_E_INVAL

@@ -467,3 +467,82 @@ def test_generator_sizes(name, n_l, n_r, P):
     c = w["lhs"].coords
     assert np.all(np.diff(np.ravel_multi_index(c.T, [s // t for s, t in zip(
         w["lhs"].shape, w["lhs"].tile_shape)])) > 0)  # lexicographic, distinct
+
+
+# ---------------------------------------------------------------------------
+# backward (reference autodiff/custom_vjp.py:31-62, :254-275;
+# tests/test_autodiff.py)
+
+def test_reverse_einsum_string_known_answers():
+    assert R.reverse_einsum_string("ij,jk->ik") == ("ik,jk->ij", "ij,ik->jk")
+    assert R.reverse_einsum_string("i,j->ij") == ("ij,j->i", "i,ij->j")
+    assert R.reverse_einsum_string("i,i->") == (",i->i", "i,->i")
+    assert R.reverse_einsum_string("bij,bjk->bik") == ("bik,bjk->bij", "bij,bik->bjk")
+    with pytest.raises(ValueError):
+        R.reverse_einsum_string("ij,jk")
+
+
+def test_pair_einsum_vjp_known_answers():
+    # tests/test_autodiff.py:160-224: loss = sum(A @ B) with one 2x2 tile each:
+    # dL/dA = ones @ B^T, dL/dB = A^T @ ones.
+    A = np.array([[1.0, 2.0], [3.0, 4.0]])
+    B = np.array([[5.0, 6.0], [7.0, 8.0]])
+    g = np.ones((1, 2, 2))
+    gl, gr = R.pair_einsum_vjp(A[None], B[None], [0], [0], "ij,jk->ik", g)
+    npt.assert_array_equal(gl[0], np.ones((2, 2)) @ B.T)
+    npt.assert_array_equal(gr[0], A.T @ np.ones((2, 2)))
+    # :335-373: an lhs tile matched twice accumulates both partners' terms.
+    A = np.zeros((4, 4)); A[0, 0], A[0, 2] = 1.0, 2.0
+    B = np.zeros((4, 4)); B[0, 0], B[2, 0] = 3.0, 4.0
+    lhs, rhs = R.dense_to_relation(A, (2, 2)), R.dense_to_relation(B, (2, 2))
+    li, ri = R.coordinate_join(lhs.coords, rhs.coords, [(1, 0)])
+    P = len(li)
+    gl, _ = R.pair_einsum_vjp(lhs.values, rhs.values, li, ri, "ij,jk->ik", np.ones((P, 2, 2)))
+    want = np.zeros_like(lhs.values)
+    for p in range(P):
+        want[li[p]] += np.ones((2, 2)) @ rhs.values[ri[p]].T
+    npt.assert_array_equal(gl, want)
+    # :441-476 outer product "ij,kl->ijkl", (1, 1) tiles: dL/da = sum of b
+    a, b = np.array([[[1.0]], [[2.0]]]), np.array([[[3.0]], [[4.0]]])
+    li, ri = np.repeat(np.arange(2), 2), np.tile(np.arange(2), 2)
+    gl, gr = R.pair_einsum_vjp(a, b, li, ri, "ij,kl->ijkl", np.ones((4, 1, 1, 1, 1)))
+    npt.assert_array_equal(gl.reshape(-1), [7.0, 7.0])
+    npt.assert_array_equal(gr.reshape(-1), [3.0, 3.0])
+
+
+@pytest.mark.parametrize("spec,lt,rt", [("ij,jk->ik", (3, 4), (4, 2)),
+                                        ("ij,kj->ik", (2, 3), (4, 3)),
+                                        ("bij,bjk->bik", (1, 2, 3), (1, 3, 2)),
+                                        ("ij,kl->ijkl", (2, 1), (1, 2)),
+                                        ("i,i->", (5,), (5,)),
+                                        ("ij,ij->ij", (2, 3), (2, 3)),
+                                        ("ijk,kl->ijl", (2, 2, 3), (3, 2))])
+def test_pair_einsum_vjp_finite_differences(spec, lt, rt):
+    """f(L, R) = sum_p <W_p, out_p> is linear in each operand, so central
+    differences in float64 give its gradient up to rounding."""
+    rng = np.random.default_rng(len(spec))
+    nl, nr, P = 4, 3, 9
+    L, Rv = rng.standard_normal((nl, *lt)), rng.standard_normal((nr, *rt))
+    li, ri = rng.integers(0, nl, P), rng.integers(0, nr, P)
+    li[0] = li[1]  # a tile in several pairs
+    out_shape = R.kernel_einsum(L, Rv, li, ri, spec, precision="fp64").shape
+    W = rng.standard_normal(out_shape)
+
+    def f(L_, R_):
+        return float(np.sum(W * R.kernel_einsum(L_, R_, li, ri, spec, precision="fp64")))
+
+    gl, gr = R.pair_einsum_vjp(L, Rv, li, ri, spec, W)
+    eps = 1e-3
+    for X, G, which in ((L, gl, 0), (Rv, gr, 1)):
+        fd = np.zeros_like(X)
+        for idx in np.ndindex(*X.shape):
+            Xp, Xm = X.copy(), X.copy()
+            Xp[idx] += eps
+            Xm[idx] -= eps
+            fp = f(Xp, Rv) if which == 0 else f(L, Xp)
+            fm = f(Xm, Rv) if which == 0 else f(L, Xm)
+            fd[idx] = (fp - fm) / (2 * eps)
+        npt.assert_allclose(G, fd, rtol=1e-9, atol=1e-9)
+    # tiles in no pair get zero gradient
+    unused = np.setdiff1d(np.arange(nl), li)
+    assert np.all(gl[unused] == 0)
