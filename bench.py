@@ -19,7 +19,7 @@ join+gather+segment-sum, the roofline of the dominant kernel, and the CPU
 oracle timed on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--all-configs]
-                       [--ingest]
+                       [--ingest] [--backward]
 """
 
 from __future__ import annotations
@@ -283,6 +283,33 @@ def measure_ingest(cpu: bool = True) -> dict:
     return out
 
 
+def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 5) -> dict:
+    """Backward of the headline's per-pair einsum (sparse_einsum_raw's
+    gradient): both operand gradients for an fp32 cotangent of every pair,
+    and each alone.  FLOPs: 2·M·N·K per pair per gradient."""
+    import torch
+
+    from einjax_amd import _device
+
+    g = torch.randn((li.numel(), lhs.tile_shape[0], rhs.tile_shape[1]), device="cuda")
+    run = {
+        "both": lambda: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri, g),
+        "lhs": lambda: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri, g,
+                                               need_rhs=False),
+        "rhs": lambda: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri, g,
+                                               need_lhs=False),
+    }
+    out = {}
+    for k, fn in run.items():
+        t = wall_time_ms(fn, reps)
+        flops = 2 * F if k == "both" else F
+        out[f"{k}_ms"] = t
+        out[f"{k}_tflops"] = flops / (t * 1e-3) / 1e12
+    del g
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,6 +318,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all-configs", action="store_true",
                     help="also time every workload configuration at full size (adds 'configs')")
+    ap.add_argument("--backward", action="store_true",
+                    help="also time the backward of the headline einsum (adds 'backward')")
     ap.add_argument("--ingest", action="store_true",
                     help="also time relation construction at full size (adds 'ingest')")
     args = ap.parse_args()
@@ -425,6 +454,9 @@ def main():
         res["cpu_baseline"] = cpu_baseline(w, band_tiles=16)
     else:
         res["cpu_baseline"] = None
+    if args.backward:
+        log("backward ...")
+        res["backward"] = measure_backward(lhs, rhs, li, ri, ks, F)
     if args.all_configs:
         del lhs, rhs, li, ri, coords, offs, perm, out
         torch.cuda.empty_cache()
