@@ -18,13 +18,14 @@ GEMM, segment sum; plus tiling), achieved GB/s against HBM for
 join+gather+segment-sum, the roofline of the dominant kernel, and the CPU
 oracle timed on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--all-configs]
-                       [--ingest] [--backward]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--all-configs]
+                       [--ingest] [--backward] [--copy-calibration]
 """
 
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -314,10 +315,13 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all-configs", action="store_true",
                     help="also time every workload configuration at full size (adds 'configs')")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy a 1 GiB device buffer 4 times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes) and exit")
     ap.add_argument("--backward", action="store_true",
                     help="also time the backward of the headline einsum (adds 'backward')")
     ap.add_argument("--ingest", action="store_true",
@@ -329,6 +333,15 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        a = torch.randn(2 ** 28, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": a.numel() * a.element_size(), "copies": 4}))
+        return
 
     sys.path.insert(0, str(ROOT))
     from einjax_amd import SparseTensorRelation, _device, execute_sparse
@@ -358,11 +371,14 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()  # no collector pause inside the timed steps
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    gc.enable()
 
     # ---- stages ----------------------------------------------------------
     lc, rc = lhs.coords, rhs.coords
@@ -403,7 +419,7 @@ def main():
                             (L.tile_shape[0], Rr.tile_shape[1]), 2)
     jgs_gbs = (B_join + B_gather + B_segsum) / ((t_join + t_gather + t_segsum) * 1e-3) / 1e9
     fused_tflops = F / (t_fused * 1e-3) / 1e12
-    kernel_name = "seg_gemm_bf16_kernel<128,128,4,4,2,8>"
+    kernel_name = "seg_gemm_kernel<SegOpBf16<128,128>,4,4,2,8,false>"
     traffic = load_traffic(kernel_name)
 
     res = {

@@ -239,44 +239,46 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     nk = len(join_keys)
     cap_p = max(int(pair_bound), 1)
     cap_u = max(1, min(cap_p, prod(agg_radices)))
+    n_out = len(agg_keys)
     buf, event = _count_buffer()
     base = buf.data_ptr()
     stream = stream_ptr()
     order = _lib.EJ_ORDER_PROBE
-
+    # Every buffer first, so that the launches below reach the GPU back to back.
     nbytes = ctypes.c_size_t()
     check(lib.ej_join_workspace_size(n_l, n_r, order, ctypes.byref(nbytes)),
           "ej_join_workspace_size")
     jws = workspace(nbytes.value, dev)
-    check(lib.ej_join_count_async(
-        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
-        i32_array([k[0] for k in join_keys]), i32_array([k[1] for k in join_keys]),
-        i64_array(join_radices), order, ptr(jws), jws.numel(), ctypes.c_void_p(base), stream),
-        "ej_join_count_async")
-    li = torch.empty(cap_p, dtype=torch.int64, device=dev)
-    ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
-    check(lib.ej_join_fill(n_l, n_r, nk, order, ptr(jws), jws.numel(), cap_p, ptr(li), ptr(ri),
-                           cap_p, stream), "ej_join_fill")
-
-    n_out = len(agg_keys)
-    src = i32_array([s for s, _ in agg_keys])
-    dim = i32_array([d for _, d in agg_keys])
-    rad = i64_array(agg_radices)
     check(lib.ej_segment_workspace_size(cap_p, ctypes.byref(nbytes)),
           "ej_segment_workspace_size")
     sws = workspace(nbytes.value, dev)
+    li = torch.empty(cap_p, dtype=torch.int64, device=dev)
+    ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
+    coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
+    offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
+    out = torch.empty((cap_u, *_out_tile(desc)), dtype=torch.float32, device=dev)
+    ldims = i32_array([k[0] for k in join_keys])
+    rdims = i32_array([k[1] for k in join_keys])
+    jrad = i64_array(join_radices)
+    src = i32_array([s for s, _ in agg_keys])
+    dim = i32_array([d for _, d in agg_keys])
+    rad = i64_array(agg_radices)
+
+    check(lib.ej_join_count_async(
+        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
+        ldims, rdims, jrad, order, ptr(jws), jws.numel(), ctypes.c_void_p(base), stream),
+        "ej_join_count_async")
+    check(lib.ej_join_fill(n_l, n_r, nk, order, ptr(jws), jws.numel(), cap_p, ptr(li), ptr(ri),
+                           cap_p, stream), "ej_join_fill")
     check(lib.ej_segment_count_async(
         ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1],
         ptr(li), ptr(ri), cap_p, ptr(jws), n_out, src, dim, rad, ptr(sws), sws.numel(),
         ctypes.c_void_p(base + 16), stream), "ej_segment_count_async")
     event.record()
-    coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
-    offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
-    perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
     check(lib.ej_segment_fill_async(cap_p, n_out, rad, ptr(sws), sws.numel(), ptr(coords),
                                     ptr(offsets), ptr(perm), None, cap_u, stream),
           "ej_segment_fill_async")
-    out = torch.empty((cap_u, *_out_tile(desc)), dtype=torch.float32, device=dev)
     check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                       lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
                                       ptr(perm), ptr(offsets), cap_u, ptr(sws), ptr(out), stream),
