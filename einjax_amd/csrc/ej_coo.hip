@@ -24,8 +24,8 @@
 // tile-start flags and their scan number the tiles; the last entry of each
 // run of equal keys writes its value.
 //
-// Statistics: num_tuples of a tile shape is the number of set cells of its
-// occupancy map (one byte per tile of the grid).  The map of a tile shape
+// Statistics: num_tuples of a tile shape is the number of set bits of its
+// occupancy map (one bit per tile of the grid).  The map of a tile shape
 // equals the map of a finer tile shape pooled by OR along one dimension:
 // every tile shape except (1, ..., 1) has a parent that divides its last
 // tile extent above 1 by that extent's smallest prime factor.  The maps are
@@ -35,7 +35,7 @@
 // num_tuples of the tile shape that equals the tensor shape in every
 // dimension except l, where it is t[l]: its grid is one tile wide in every
 // other dimension.  Those shapes join the tree.  For COO input, a tile
-// shape whose map would exceed bitmap_cap bytes is counted instead by
+// shape whose grid has more than bitmap_cap tiles is counted instead by
 // sorting the tile keys of the entries and counting distinct keys, and the
 // largest maps below the cap are built by marking the entries' tiles.
 #include "ej_internal.h"
@@ -112,9 +112,8 @@ __global__ void fill_zero_kernel(T *p, int64_t n) {
   for (; i < n; i += stride) p[i] = T(0);
 }
 
-// Grid-stride launches: at most 8 blocks per CU, so the per-block atomics
-// stay few.
-inline unsigned stride_grid(int64_t work, int64_t cap_blocks = 2048) {
+// Grid-stride launches: at most 32 blocks per CU (one atomic per block).
+inline unsigned stride_grid(int64_t work, int64_t cap_blocks = 8192) {
   int64_t g = ceil_div(work > 0 ? work : 1, kBlock);
   return static_cast<unsigned>(g < cap_blocks ? g : cap_blocks);
 }
@@ -419,66 +418,82 @@ struct TileIdx {  // mixed-radix tile index of an element for one tile shape
   int64_t cells;  // tiles in the grid
 };
 
+// Occupancy maps hold one bit per tile of a grid, row-major, packed into
+// 32-bit words (bit i of the map is bit i % 32 of word i / 32); bits past the
+// last tile are zero.
+
 template <typename T>
-__global__ __launch_bounds__(256) void dense_map_kernel(const T *__restrict__ dense, int64_t n,
-                                                        bool vec, uint8_t *__restrict__ map,
-                                                        unsigned long long *count) {
-  // 16 elements per thread and iteration: 16-byte loads, one 16-byte store of
-  // flags (the map is padded to 256 bytes, so the last store stays inside).
+__global__ __launch_bounds__(256) void dense_bits_kernel(const T *__restrict__ dense, int64_t n,
+                                                         bool vec, uint32_t *__restrict__ map,
+                                                         unsigned long long *count) {
+  // Each wave takes chunks of 4 rounds x 64 lanes x E elements, one 16-byte
+  // load per lane and round (consecutive lanes read consecutive bytes); the
+  // E flag bits of LPW neighbouring lanes are or-ed into one map word by
+  // shuffles and stored by the first of them.
   constexpr int E = 16 / static_cast<int>(sizeof(T));  // elements per load
-  constexpr int NL = 16 / E;                            // loads per group
-  const int64_t groups = (n + 15) / 16;
+  constexpr int LPW = 32 / E;                           // lanes per map word
+  constexpr int R = 4;
+  constexpr int64_t CHUNK = int64_t(R) * 64 * E;
+  const int lane = threadIdx.x & 63;
+  const int64_t words = (n + 31) / 32;
+  const int64_t chunks = (n + CHUNK - 1) / CHUNK;
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * 4;
   int64_t c = 0;
-  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < groups;
-       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t i = q * 16;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-    if (vec && i + 16 <= n) {
-      uint4 raw[NL];
+  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); ch < chunks;
+       ch += n_waves) {
+    const int64_t base = ch * CHUNK;
+    T v[R][E];
 #pragma unroll
-      for (int l = 0; l < NL; ++l) raw[l] = reinterpret_cast<const uint4 *>(dense + i)[l];
+    for (int r = 0; r < R; ++r) {
+      const int64_t i = base + static_cast<int64_t>(r * 64 + lane) * E;
+      if (vec && i + E <= n) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(dense + i);
+        __builtin_memcpy(&v[r][0], &x, 16);
+      } else {
 #pragma unroll
-      for (int l = 0; l < NL; ++l) {
-        T v[E];
-        __builtin_memcpy(&v[0], &raw[l], 16);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const int k = l * E + e;
-          w[k >> 2] |= (nz(v[e]) ? 1u : 0u) << (8 * (k & 3));
-        }
+        for (int k = 0; k < E; ++k) v[r][k] = i + k < n ? dense[i + k] : T(0);
       }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (i + k < n && nz(dense[i + k])) w[k >> 2] |= 1u << (8 * (k & 3));
     }
-    *reinterpret_cast<uint4 *>(map + i) = make_uint4(w[0], w[1], w[2], w[3]);
-    c += bytes_set(w[0]) + bytes_set(w[1]) + bytes_set(w[2]) + bytes_set(w[3]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint32_t b = 0;
+#pragma unroll
+      for (int k = 0; k < E; ++k) b |= (nz(v[r][k]) ? 1u : 0u) << k;
+      b <<= E * (lane % LPW);
+#pragma unroll
+      for (int d = 1; d < LPW; d <<= 1) b |= __shfl_xor(b, d, 64);
+      const int64_t widx = (base + static_cast<int64_t>(r * 64 + lane) * E) >> 5;
+      if (lane % LPW == 0 && widx < words) {
+        map[widx] = b;
+        c += __popc(b);
+      }
+    }
   }
   block_add(count, c);
 }
 
-// Pooling by OR: in [outer][n_out * p][inner] -> out [outer][n_out][inner].
+// Pooling by OR: in [outer][n_out * p][inner] -> out [outer][n_out][inner],
+// sizes in tiles (bits).
 struct PoolGeom {
   int64_t outer, n_out, p, inner, total;  // total = outer * n_out * inner
 };
 
-// inner % 16 == 0: 16 outputs (one 16-byte word) per thread.
+// inner % 128 == 0: 128 outputs (one 16-byte vector) per thread.
 template <typename I>
-__global__ __launch_bounds__(256) void pool_vec16_kernel(const uint8_t *__restrict__ in,
-                                                         uint8_t *__restrict__ out, PoolGeom g,
-                                                         unsigned long long *count) {
-  const I vecs = static_cast<I>(g.total / 16);
+__global__ __launch_bounds__(256) void pool_bits_vec_kernel(const uint32_t *__restrict__ in,
+                                                            uint32_t *__restrict__ out,
+                                                            PoolGeom g, unsigned long long *count) {
+  const I vecs = static_cast<I>(g.total / 128);
   const I inner = static_cast<I>(g.inner), n_out = static_cast<I>(g.n_out),
           p = static_cast<I>(g.p);
   int64_t c = 0;
   for (I w = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; w < vecs;
        w += static_cast<I>(gridDim.x) * blockDim.x) {
-    const I o = w * 16;
+    const I o = w * 128;
     const I r = o % inner, t = o / inner;
     const I j = t % n_out, a = t / n_out;
-    const uint4 *src = reinterpret_cast<const uint4 *>(in + ((a * n_out + j) * p * inner + r));
-    const I step = inner / 16;
+    const uint4 *src = reinterpret_cast<const uint4 *>(in) + ((a * n_out + j) * p * inner + r) / 128;
+    const I step = inner / 128;
     uint4 acc = make_uint4(0u, 0u, 0u, 0u);
     for (I q = 0; q < p; ++q) {
       const uint4 x = src[q * step];
@@ -488,21 +503,76 @@ __global__ __launch_bounds__(256) void pool_vec16_kernel(const uint8_t *__restri
       acc.w |= x.w;
     }
     reinterpret_cast<uint4 *>(out)[w] = acc;
-    c += bytes_set(acc.x) + bytes_set(acc.y) + bytes_set(acc.z) + bytes_set(acc.w);
+    c += __popc(acc.x) + __popc(acc.y) + __popc(acc.z) + __popc(acc.w);
+  }
+  block_add(count, c);
+}
+
+// inner % 32 == 0: one output word per thread.
+template <typename I>
+__global__ __launch_bounds__(256) void pool_bits_word_kernel(const uint32_t *__restrict__ in,
+                                                             uint32_t *__restrict__ out,
+                                                             PoolGeom g,
+                                                             unsigned long long *count) {
+  const I words = static_cast<I>(g.total / 32);
+  const I inner = static_cast<I>(g.inner), n_out = static_cast<I>(g.n_out),
+          p = static_cast<I>(g.p);
+  int64_t c = 0;
+  for (I w = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
+       w += static_cast<I>(gridDim.x) * blockDim.x) {
+    const I o = w * 32;
+    const I r = o % inner, t = o / inner;
+    const I j = t % n_out, a = t / n_out;
+    const uint32_t *src = in + ((a * n_out + j) * p * inner + r) / 32;
+    const I step = inner / 32;
+    uint32_t acc = 0;
+    for (I q = 0; q < p; ++q) acc |= src[q * step];
+    out[w] = acc;
+    c += __popc(acc);
+  }
+  block_add(count, c);
+}
+
+// Any geometry: one output word per thread, assembled bit by bit.
+__global__ __launch_bounds__(256) void pool_bits_any_kernel(const uint32_t *__restrict__ in,
+                                                            uint32_t *__restrict__ out,
+                                                            PoolGeom g,
+                                                            unsigned long long *count) {
+  const int64_t words = (g.total + 31) / 32;
+  int64_t c = 0;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
+       w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    uint32_t acc = 0;
+    for (int b = 0; b < 32; ++b) {
+      const int64_t o = w * 32 + b;
+      if (o >= g.total) break;
+      const int64_t r = o % g.inner, t = o / g.inner;
+      const int64_t j = t % g.n_out, a = t / g.n_out;
+      const int64_t i0 = (a * g.n_out + j) * g.p * g.inner + r;
+      uint32_t any = 0;
+      for (int64_t q = 0; q < g.p && !any; ++q) {
+        const int64_t i = i0 + q * g.inner;
+        any = (in[i >> 5] >> (i & 31)) & 1u;
+      }
+      acc |= any << b;
+    }
+    out[w] = acc;
+    c += __popc(acc);
   }
   block_add(count, c);
 }
 
 // Power-of-two pooling along the last dimension, counted without writing
-// the maps: a block reads 16384 consecutive map bytes, 64 per thread, and
-// counts the nonempty groups of 2^k bytes for k = 1 .. levels (<= 14) into
-// count[k - 1]; groups never cross a row because 2^levels divides the row
-// length.  Levels 1-6 are folded inside a thread's 64-bit mask of nonzero
-// bytes, 7-12 across the wave's ballot, 13-14 across the block's waves.
-// With write_level > 0 the map pooled by 2^write_level is written to out,
-// for the next kernel of a longer chain.
+// the maps: each wave reads 16384 consecutive map bits (256 per lane, four
+// 64-bit words) and counts the nonempty groups of 2^k bits for k = 1 ..
+// levels (<= 14) into count[k - 1]; groups never cross a row because
+// 2^levels divides the row length.  Levels 1-6 are folded inside each word,
+// 7-8 across a lane's four words, 9-14 across the wave's ballot; waves need
+// no barrier.  With write_level == 14 the map pooled by 2^14 (one bit per
+// wave chunk) is or-ed into out, which the caller zeroes, for the next pass
+// of a longer chain.
 constexpr int kChainMax = 14;
-constexpr int64_t kChainChunk = int64_t(256) * 64;
+constexpr int64_t kChainChunk = int64_t(64) * 256;  // bits per wave chunk
 
 struct ChainArgs {
   int32_t levels;
@@ -522,98 +592,68 @@ __device__ inline uint64_t level_mask(int k) {
   }
 }
 
-// 4 bits (one per byte) of a word whose bytes hold 0 or 1.
-__device__ inline uint32_t byte_bits(uint32_t w) {
-  return (w & 1u) | ((w >> 7) & 2u) | ((w >> 14) & 4u) | ((w >> 21) & 8u);
-}
-
-__global__ __launch_bounds__(256) void pool_chain_kernel(const uint8_t *__restrict__ in, int64_t S,
-                                                         ChainArgs a, uint8_t *__restrict__ out) {
-  __shared__ uint32_t wave_any[4];
+__global__ __launch_bounds__(256) void pool_chain_kernel(const uint32_t *__restrict__ in,
+                                                         int64_t S, ChainArgs a,
+                                                         uint32_t *__restrict__ out) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int64_t cnt[kChainMax];
 #pragma unroll
   for (int k = 0; k < kChainMax; ++k) cnt[k] = 0;
   const int64_t chunks = (S + kChainChunk - 1) / kChainChunk;
-  for (int64_t ch = blockIdx.x; ch < chunks; ch += gridDim.x) {
-    const int64_t base = ch * kChainChunk + static_cast<int64_t>(threadIdx.x) * 64;
-    uint64_t m = 0;
-    if (base + 64 <= S) {
-      const uint4 *src = reinterpret_cast<const uint4 *>(in + base);
-      uint4 v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = src[r];
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * 4;
+  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * 4 + wave; ch < chunks; ch += n_waves) {
+    const int64_t base = ch * kChainChunk + static_cast<int64_t>(lane) * 256;
+    uint64_t m[4] = {0, 0, 0, 0};
+    if (base + 256 <= S) {
+      const uint4 *src = reinterpret_cast<const uint4 *>(in) + (base >> 7);
+      const uint4 v0 = src[0], v1 = src[1];
+      m[0] = static_cast<uint64_t>(v0.x) | static_cast<uint64_t>(v0.y) << 32;
+      m[1] = static_cast<uint64_t>(v0.z) | static_cast<uint64_t>(v0.w) << 32;
+      m[2] = static_cast<uint64_t>(v1.x) | static_cast<uint64_t>(v1.y) << 32;
+      m[3] = static_cast<uint64_t>(v1.z) | static_cast<uint64_t>(v1.w) << 32;
+    } else if (base < S) {
+      // the map allocation is padded to 256 bytes: these words are inside it
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        m |= static_cast<uint64_t>(byte_bits(v[r].x)) << (16 * r);
-        m |= static_cast<uint64_t>(byte_bits(v[r].y)) << (16 * r + 4);
-        m |= static_cast<uint64_t>(byte_bits(v[r].z)) << (16 * r + 8);
-        m |= static_cast<uint64_t>(byte_bits(v[r].w)) << (16 * r + 12);
+        const int64_t b = base + 64 * r;
+        if (b < S) {
+          m[r] = reinterpret_cast<const uint64_t *>(in)[b >> 6];
+          if (S - b < 64) m[r] &= (uint64_t(1) << (S - b)) - 1;
+        }
       }
-    } else if (base < S) {
-      for (int j = 0; j < 64 && base + j < S; ++j)
-        if (in[base + j]) m |= uint64_t(1) << j;
     }
-    uint64_t g = m, gw = m;
+    uint64_t g[4] = {m[0], m[1], m[2], m[3]};
 #pragma unroll
     for (int k = 1; k <= 6; ++k) {
-      g = (g | (g >> (1 << (k - 1)))) & level_mask(k);
-      cnt[k - 1] += __popcll(g);
-      if (k == a.write_level) gw = g;
-    }
-    const uint64_t B = __ballot(m != 0);
-    uint64_t gb = B, gbw = B;
+      int c = 0;
 #pragma unroll
-    for (int k = 7; k <= 12; ++k) {
-      gb = (gb | (gb >> (1 << (k - 7)))) & level_mask(k - 6);
-      if (lane == 0) cnt[k - 1] += __popcll(gb);
-      if (k == a.write_level) gbw = gb;
-    }
-    if (lane == 0) wave_any[wave] = B != 0 ? 1u : 0u;
-    __syncthreads();
-    const uint32_t w0 = wave_any[0], w1 = wave_any[1], w2 = wave_any[2], w3 = wave_any[3];
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      cnt[12] += (w0 | w1) + (w2 | w3);
-      cnt[13] += w0 | w1 | w2 | w3;
-    }
-    const int W = a.write_level;
-    if (W > 0 && base < S) {
-      const int64_t ob = base >> W;  // first output byte of this thread's bytes
-      if (W <= 4) {
-        const int nw = (64 >> W) / 4;  // 32-bit words
-        for (int i = 0; i < nw; ++i) {
-          uint32_t word = 0;
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            word |= static_cast<uint32_t>((gw >> ((4 * i + b) << W)) & 1u) << (8 * b);
-          reinterpret_cast<uint32_t *>(out + ob)[i] = word;
-        }
-      } else if (W == 5) {
-        out[ob] = static_cast<uint8_t>(gw & 1u);
-        out[ob + 1] = static_cast<uint8_t>((gw >> 32) & 1u);
-      } else if (W == 6) {
-        out[ob] = static_cast<uint8_t>(gw & 1u);
-      } else if (W <= 12) {
-        const int span = 1 << (W - 6);  // lanes per output byte
-        if ((lane & (span - 1)) == 0) out[ob] = static_cast<uint8_t>((gbw >> lane) & 1u);
-      } else if (threadIdx.x == 0) {
-        if (W == 13) {
-          out[ob] = static_cast<uint8_t>(w0 | w1);
-          if (base + 8192 < S) out[ob + 1] = static_cast<uint8_t>(w2 | w3);
-        } else {
-          out[ob] = static_cast<uint8_t>(w0 | w1 | w2 | w3);
-        }
+      for (int r = 0; r < 4; ++r) {
+        g[r] = (g[r] | (g[r] >> (1 << (k - 1)))) & level_mask(k);
+        c += __popcll(g[r]);
       }
+      cnt[k - 1] += c;
     }
+    // g[r] now holds bit 0 = word r nonempty
+    cnt[6] += (g[0] | g[1]) + (g[2] | g[3]);
+    const bool any = (g[0] | g[1] | g[2] | g[3]) != 0;
+    cnt[7] += any ? 1 : 0;
+    const uint64_t B = __ballot(any);
+    uint64_t gb = B;
+#pragma unroll
+    for (int k = 9; k <= 14; ++k) {
+      gb = (gb | (gb >> (1 << (k - 9)))) & level_mask(k - 8);
+      if (lane == 0) cnt[k - 1] += __popcll(gb);
+    }
+    if (a.write_level == kChainMax && lane == 0 && B != 0)
+      atomicOr(&out[ch >> 5], 1u << (ch & 31));
   }
-  // Block totals: the wave sums of levels 1-6, lane 0's sums of 7-12 and
-  // thread 0's of 13-14, then one atomic per level and block.
+  // Block totals (levels 1-8 summed over the lanes, 9-14 held by lane 0),
+  // then one atomic per level and block.
   __shared__ int64_t part[4][kChainMax];
 #pragma unroll
   for (int k = 0; k < kChainMax; ++k) {
     int64_t v = cnt[k];
-    if (k < 6) {
+    if (k < 8) {
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
     }
@@ -625,68 +665,6 @@ __global__ __launch_bounds__(256) void pool_chain_kernel(const uint8_t *__restri
     const int64_t t = part[0][k] + part[1][k] + part[2][k] + part[3][k];
     if (t) atomicAdd(a.count[k], static_cast<unsigned long long>(t));
   }
-}
-
-// inner % 4 == 0: one 32-bit word of 4 outputs per thread.
-template <typename I>
-__global__ __launch_bounds__(256) void pool_words_kernel(const uint8_t *__restrict__ in,
-                                                         uint8_t *__restrict__ out, PoolGeom g,
-                                                         unsigned long long *count) {
-  const I words = static_cast<I>(g.total / 4);
-  const I inner = static_cast<I>(g.inner), n_out = static_cast<I>(g.n_out),
-          p = static_cast<I>(g.p);
-  int64_t c = 0;
-  for (I w = static_cast<I>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
-       w += static_cast<I>(gridDim.x) * blockDim.x) {
-    const I o = w * 4;
-    const I r = o % inner, t = o / inner;
-    const I j = t % n_out, a = t / n_out;
-    const uint32_t *src =
-        reinterpret_cast<const uint32_t *>(in + ((a * n_out + j) * p * inner + r));
-    const I step = inner / 4;
-    uint32_t acc = 0;
-    for (I q = 0; q < p; ++q) acc |= src[q * step];
-    reinterpret_cast<uint32_t *>(out)[w] = acc;
-    c += bytes_set(acc);
-  }
-  block_add(count, c);
-}
-
-// inner == 1, p == 2, total % 4 == 0: 8 input bytes -> 4 outputs per thread.
-__global__ __launch_bounds__(256) void pool_pairs_kernel(const uint8_t *__restrict__ in,
-                                                         uint8_t *__restrict__ out, int64_t total,
-                                                         unsigned long long *count) {
-  const int64_t words = total / 4;
-  int64_t c = 0;
-  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words;
-       w += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const uint64_t x = reinterpret_cast<const uint64_t *>(in)[w];
-    const uint64_t y = x | (x >> 8);  // byte 2k holds the OR of input bytes 2k, 2k+1
-    const uint32_t acc = static_cast<uint32_t>((y & 0xff) | ((y >> 8) & 0xff00) |
-                                               ((y >> 16) & 0xff0000) |
-                                               ((y >> 24) & 0xff000000));
-    reinterpret_cast<uint32_t *>(out)[w] = acc;
-    c += bytes_set(acc);
-  }
-  block_add(count, c);
-}
-
-// Any geometry: one output byte per thread.
-__global__ __launch_bounds__(256) void pool_bytes_kernel(const uint8_t *__restrict__ in,
-                                                         uint8_t *__restrict__ out, PoolGeom g,
-                                                         unsigned long long *count) {
-  int64_t c = 0;
-  for (int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; o < g.total;
-       o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t r = o % g.inner, t = o / g.inner;
-    const int64_t j = t % g.n_out, a = t / g.n_out;
-    const uint8_t *src = in + (a * g.n_out + j) * g.p * g.inner + r;
-    uint8_t acc = 0;
-    for (int64_t q = 0; q < g.p && !acc; ++q) acc |= src[q * g.inner];
-    out[o] = acc;
-    c += acc;
-  }
-  block_add(count, c);
 }
 
 // Tile index of entry i for the tile shape in ti; false when the entry is
@@ -717,12 +695,12 @@ __device__ inline bool entry_tile(const int32_t *__restrict__ idx, const T *__re
 template <typename T>
 __global__ __launch_bounds__(256) void coo_mark_kernel(const int32_t *__restrict__ idx,
                                                        const T *__restrict__ vals, int64_t nnz,
-                                                       TileIdx ti, uint8_t *__restrict__ map,
+                                                       TileIdx ti, uint32_t *__restrict__ map,
                                                        int64_t *bad) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= nnz) return;
   uint64_t t;
-  if (entry_tile(idx, vals, i, ti, bad, &t)) map[t] = 1;
+  if (entry_tile(idx, vals, i, ti, bad, &t)) atomicOr(&map[t >> 5], 1u << (t & 31));
 }
 
 __global__ __launch_bounds__(256) void map_count_kernel(const uint32_t *__restrict__ words,
@@ -731,7 +709,7 @@ __global__ __launch_bounds__(256) void map_count_kernel(const uint32_t *__restri
   int64_t c = 0;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < n_words;
        w += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    c += bytes_set(words[w]);
+    c += __popc(words[w]);
   block_add(count, c);
 }
 
@@ -815,17 +793,22 @@ std::vector<int> chain_of(const StatsPlan &pl, int v) {
   return c;
 }
 
+// Bytes of a map of `cells` bits: whole 32-bit words, padded to 256 bytes.
+size_t map_bytes(int64_t cells) {
+  return align_up(static_cast<size_t>((cells + 31) / 32) * 4, 256);
+}
+
 void layout(StatsPlan &pl, int v, size_t base) {
   StatNode &nd = pl.nodes[v];
   nd.off = base;
-  size_t top = base + align_up(static_cast<size_t>(nd.cells), 256);
+  size_t top = base + map_bytes(nd.cells);
   // maps handed from one chain kernel to the next
   nd.tmp_off = top;
   const size_t levels = chain_of(pl, v).size();
   int64_t cells = nd.cells;
   for (size_t done = kChainMax; done < levels; done += kChainMax) {
     cells >>= kChainMax;
-    top += align_up(static_cast<size_t>(cells), 256);
+    top += map_bytes(cells);
   }
   if (top > pl.stack_bytes) pl.stack_bytes = top;
   for (int k : pl.nodes[v].kids)
@@ -933,9 +916,44 @@ int make_plan(int32_t ndim, const int64_t *shape, int64_t n_schemes, const int64
   return EJ_OK;
 }
 
+// The plan of the last statistics request on this thread: a workspace query
+// and the call that follows it with the same arguments build it once.
+struct PlanCache {
+  bool valid = false;
+  std::vector<int64_t> key;
+  StatsPlan plan;
+};
+thread_local PlanCache g_plan_cache;
+
+int cached_plan(int32_t ndim, const int64_t *shape, int64_t n_schemes,
+                const int64_t *tile_shapes, bool dense, int64_t cap, const StatsPlan **out) {
+  std::vector<int64_t> key;
+  if (ndim >= 1 && ndim <= EJ_MAX_DIMS && shape && n_schemes >= 0 &&
+      (n_schemes == 0 || tile_shapes)) {
+    key.reserve(static_cast<size_t>(4 + ndim + n_schemes * ndim));
+    key.push_back(ndim);
+    key.push_back(dense ? 1 : 0);
+    key.push_back(dense ? 0 : cap);
+    key.push_back(n_schemes);
+    key.insert(key.end(), shape, shape + ndim);
+    key.insert(key.end(), tile_shapes, tile_shapes + n_schemes * ndim);
+    if (g_plan_cache.valid && g_plan_cache.key == key) {
+      *out = &g_plan_cache.plan;
+      return EJ_OK;
+    }
+  }
+  g_plan_cache.valid = false;
+  g_plan_cache.plan = StatsPlan();
+  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, dense, cap, &g_plan_cache.plan));
+  g_plan_cache.key = std::move(key);
+  g_plan_cache.valid = true;
+  *out = &g_plan_cache.plan;
+  return EJ_OK;
+}
+
 struct StatsWs {
   unsigned long long *counts;  // one per node, then the range flag
-  uint8_t *stack;
+  uint32_t *stack;
   uint64_t *keys, *keys_alt;
   int32_t *vals, *vals_alt;
   void *sort_ws;
@@ -946,7 +964,7 @@ StatsWs carve_stats(void *base, const StatsPlan &pl, int64_t nnz) {
   Carver c(base);
   StatsWs w{};
   w.counts = c.take<unsigned long long>((static_cast<int64_t>(pl.nodes.size()) + 1) * kCountStride);
-  w.stack = c.take<uint8_t>(static_cast<int64_t>(pl.stack_bytes));
+  w.stack = c.take<uint32_t>(static_cast<int64_t>(pl.stack_bytes / 4));
   if (pl.any_sorted) {
     w.keys = c.take<uint64_t>(nnz);
     w.keys_alt = c.take<uint64_t>(nnz);
@@ -970,7 +988,7 @@ TileIdx tile_idx(const StatsPlan &pl, const StatNode &n) {
   return ti;
 }
 
-int launch_pool(const StatsPlan &pl, const StatNode &child, const uint8_t *in, uint8_t *out,
+int launch_pool(const StatsPlan &pl, const StatNode &child, const uint32_t *in, uint32_t *out,
                 unsigned long long *count, hipStream_t stream) {
   const StatNode &par = pl.nodes[child.parent];
   PoolGeom g;
@@ -982,29 +1000,26 @@ int launch_pool(const StatsPlan &pl, const StatNode &child, const uint8_t *in, u
   g.inner = 1;
   for (int e = d + 1; e < pl.nd; ++e) g.inner *= pl.shape[e] / child.ts[e];
   g.total = child.cells;
-  (void)par;
-  if (g.inner % 16 == 0) {
-    const int64_t vecs = g.total / 16;
-    if (par.cells < (int64_t(1) << 31))
-      hipLaunchKernelGGL(pool_vec16_kernel<uint32_t>, dim3(stride_grid(vecs)), dim3(kBlock), 0,
+  const bool small = par.cells < (int64_t(1) << 31);
+  if (g.inner % 128 == 0) {
+    const int64_t vecs = g.total / 128;
+    if (small)
+      hipLaunchKernelGGL(pool_bits_vec_kernel<uint32_t>, dim3(stride_grid(vecs)), dim3(kBlock), 0,
                          stream, in, out, g, count);
     else
-      hipLaunchKernelGGL(pool_vec16_kernel<int64_t>, dim3(stride_grid(vecs)), dim3(kBlock), 0,
+      hipLaunchKernelGGL(pool_bits_vec_kernel<int64_t>, dim3(stride_grid(vecs)), dim3(kBlock), 0,
                          stream, in, out, g, count);
-  } else if (g.inner % 4 == 0) {
-    const int64_t words = g.total / 4;
-    if (par.cells < (int64_t(1) << 31))
-      hipLaunchKernelGGL(pool_words_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
-                         stream, in, out, g, count);
+  } else if (g.inner % 32 == 0) {
+    const int64_t words = g.total / 32;
+    if (small)
+      hipLaunchKernelGGL(pool_bits_word_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock),
+                         0, stream, in, out, g, count);
     else
-      hipLaunchKernelGGL(pool_words_kernel<int64_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
+      hipLaunchKernelGGL(pool_bits_word_kernel<int64_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
                          stream, in, out, g, count);
-  } else if (g.inner == 1 && g.p == 2 && g.total % 4 == 0) {
-    hipLaunchKernelGGL(pool_pairs_kernel, dim3(stride_grid(g.total / 4)), dim3(kBlock), 0,
-                       stream, in, out, g.total, count);
   } else {
-    hipLaunchKernelGGL(pool_bytes_kernel, dim3(stride_grid(g.total)), dim3(kBlock), 0, stream,
-                       in, out, g, count);
+    hipLaunchKernelGGL(pool_bits_any_kernel, dim3(stride_grid(ceil_div(g.total, 32))),
+                       dim3(kBlock), 0, stream, in, out, g, count);
   }
   EJ_LAUNCH_CHECK();
   return EJ_OK;
@@ -1013,23 +1028,30 @@ int launch_pool(const StatsPlan &pl, const StatNode &child, const uint8_t *in, u
 int run_chain(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream) {
   const std::vector<int> chain = chain_of(pl, v);
   const StatNode &n = pl.nodes[v];
-  const uint8_t *src = w.stack + n.off;
+  const uint32_t *src = w.stack + n.off / 4;
   int64_t S = n.cells;
-  uint8_t *tmp = w.stack + n.tmp_off;
+  uint32_t *tmp = w.stack + n.tmp_off / 4;
   for (size_t done = 0; done < chain.size(); done += kChainMax) {
     ChainArgs a{};
     a.levels = static_cast<int32_t>(std::min<size_t>(kChainMax, chain.size() - done));
     const bool more = done + kChainMax < chain.size();
     a.write_level = more ? kChainMax : 0;
     for (int k = 0; k < a.levels; ++k) a.count[k] = w.counts + chain[done + k] * kCountStride;
-    const int64_t chunks = ceil_div(S, kChainChunk);
-    hipLaunchKernelGGL(pool_chain_kernel, dim3(static_cast<unsigned>(std::min<int64_t>(chunks, 2048))),
-                       dim3(256), 0, stream, src, S, a, tmp);
+    if (more) {  // the next pass's map is or-ed together: start from zero
+      const int64_t words = static_cast<int64_t>(map_bytes(S >> kChainMax) / 4);
+      hipLaunchKernelGGL(fill_zero_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
+                         stream, tmp, words);
+      EJ_LAUNCH_CHECK();
+    }
+    const int64_t blocks = ceil_div(ceil_div(S, kChainChunk), 4);
+    hipLaunchKernelGGL(pool_chain_kernel,
+                       dim3(static_cast<unsigned>(std::min<int64_t>(blocks, 4096))), dim3(256), 0,
+                       stream, src, S, a, tmp);
     EJ_LAUNCH_CHECK();
     if (more) {
       src = tmp;
       S >>= kChainMax;
-      tmp += align_up(static_cast<size_t>(S), 256);
+      tmp += map_bytes(S) / 4;
     }
   }
   return EJ_OK;
@@ -1045,8 +1067,8 @@ int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream
       chained = true;
       continue;
     }
-    EJ_TRY(launch_pool(pl, kid, w.stack + n.off, w.stack + kid.off, w.counts + k * kCountStride,
-                       stream));
+    EJ_TRY(launch_pool(pl, kid, w.stack + n.off / 4, w.stack + kid.off / 4,
+                       w.counts + k * kCountStride, stream));
     EJ_TRY(run_subtree(pl, k, w, stream));
   }
   return EJ_OK;
@@ -1077,21 +1099,25 @@ int run_stats(const StatsPlan &pl, const StatsWs &w, const T *dense, int64_t n_d
   }
   for (int r : pl.roots) {
     const StatNode &n = pl.nodes[r];
-    uint8_t *map = w.stack + n.off;
+    uint32_t *map = w.stack + n.off / 4;
     if (n.kind == kDenseRoot) {
       const bool vec = (reinterpret_cast<uintptr_t>(dense) % 16) == 0;
-      hipLaunchKernelGGL(dense_map_kernel<T>, dim3(stride_grid(ceil_div(n_dense, 16))),
-                         dim3(kBlock), 0, stream, dense, n_dense, vec, map, w.counts + r * kCountStride);
+      const int64_t chunk = 4 * 64 * (16 / static_cast<int64_t>(sizeof(T)));
+      hipLaunchKernelGGL(dense_bits_kernel<T>,
+                         dim3(static_cast<unsigned>(std::min<int64_t>(
+                             std::max<int64_t>(ceil_div(ceil_div(n_dense, chunk), 4), 1), 8192))),
+                         dim3(kBlock), 0, stream, dense, n_dense, vec, map,
+                         w.counts + r * kCountStride);
     } else {
-      const int64_t words = static_cast<int64_t>(align_up(static_cast<size_t>(n.cells), 256) / 4);
+      const int64_t words = static_cast<int64_t>(map_bytes(n.cells) / 4);
       hipLaunchKernelGGL(fill_zero_kernel<uint32_t>, dim3(stride_grid(words)), dim3(kBlock), 0,
-                         stream, reinterpret_cast<uint32_t *>(map), words);
+                         stream, map, words);
       EJ_LAUNCH_CHECK();
       hipLaunchKernelGGL(coo_mark_kernel<T>, dim3(grid_for(nnz)), dim3(kBlock), 0, stream, idx,
                          vals, nnz, tile_idx(pl, n), map, bad);
       EJ_LAUNCH_CHECK();
       hipLaunchKernelGGL(map_count_kernel, dim3(stride_grid(words)), dim3(kBlock), 0, stream,
-                         reinterpret_cast<const uint32_t *>(map), words, w.counts + r * kCountStride);
+                         map, words, w.counts + r * kCountStride);
     }
     EJ_LAUNCH_CHECK();
     EJ_TRY(run_subtree(pl, r, w, stream));
@@ -1331,8 +1357,9 @@ extern "C" int ej_scheme_stats_workspace_size(int32_t ndim, const int64_t *shape
   clear_error();
   EJ_CHECK_ARG(bytes, "bytes is null");
   EJ_CHECK_ARG(nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
-  StatsPlan pl;
-  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, nnz < 0, bitmap_cap, &pl));
+  const StatsPlan *pp = nullptr;
+  EJ_TRY(cached_plan(ndim, shape, n_schemes, tile_shapes, nnz < 0, bitmap_cap, &pp));
+  const StatsPlan &pl = *pp;
   *bytes = carve_stats(nullptr, pl, nnz < 0 ? 0 : nnz).bytes;
   return EJ_OK;
 }
@@ -1345,8 +1372,9 @@ extern "C" int ej_scheme_stats_dense(const void *dense, int32_t dtype, int32_t n
   clear_error();
   hipStream_t stream = as_stream(stream_);
   EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
-  StatsPlan pl;
-  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, true, 0, &pl));
+  const StatsPlan *pp = nullptr;
+  EJ_TRY(cached_plan(ndim, shape, n_schemes, tile_shapes, true, 0, &pp));
+  const StatsPlan &pl = *pp;
   if (n_schemes == 0) return EJ_OK;
   EJ_CHECK_ARG(dense && num_tuples && value_count, "null pointer argument");
   StatsWs w = carve_stats(workspace, pl, 0);
@@ -1376,8 +1404,9 @@ extern "C" int ej_scheme_stats_coo(const int32_t *indices, const void *values, i
   hipStream_t stream = as_stream(stream_);
   EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
   EJ_CHECK_ARG(nnz >= 0 && nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
-  StatsPlan pl;
-  EJ_TRY(make_plan(ndim, shape, n_schemes, tile_shapes, false, bitmap_cap, &pl));
+  const StatsPlan *pp = nullptr;
+  EJ_TRY(cached_plan(ndim, shape, n_schemes, tile_shapes, false, bitmap_cap, &pp));
+  const StatsPlan &pl = *pp;
   if (n_schemes == 0) return EJ_OK;
   EJ_CHECK_ARG(num_tuples && value_count, "null pointer argument");
   if (nnz == 0) {
