@@ -404,7 +404,7 @@ def bucket_coo(indices: torch.Tensor, values: torch.Tensor, shape,
     n = values.numel()
     sh, ts = i64_array(shape), i64_array(tile_shape)
     nbytes = ctypes.c_size_t()
-    check(lib.ej_bucket_coo_workspace_size(n, ctypes.byref(nbytes)),
+    check(lib.ej_bucket_coo_workspace_size(n, code, nd, sh, ts, ctypes.byref(nbytes)),
           "ej_bucket_coo_workspace_size")
     ws = workspace(nbytes.value, values.device)
     n_tiles = ctypes.c_int64()
@@ -414,8 +414,9 @@ def bucket_coo(indices: torch.Tensor, values: torch.Tensor, shape,
     T = n_tiles.value
     coords = torch.empty((T, nd), dtype=torch.int32, device=values.device)
     tiles = torch.empty((T, *tile_shape), dtype=out_dtype, device=values.device)
-    check(lib.ej_bucket_coo_fill(ptr(values), code, n, nd, sh, ts, ptr(ws), ws.numel(), T,
-                                 ptr(coords), ptr(tiles), T, stream_ptr()), "ej_bucket_coo_fill")
+    check(lib.ej_bucket_coo_fill(ptr(indices), ptr(values), code, n, nd, sh, ts, ptr(ws),
+                                 ws.numel(), T, ptr(coords), ptr(tiles), T, stream_ptr()),
+          "ej_bucket_coo_fill")
     return coords, tiles
 
 

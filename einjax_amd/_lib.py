@@ -95,11 +95,11 @@ SIGNATURES = {
     "ej_extract_coo_count": (_i32, [_vp, _i32, _i32, _P_i64, _vp, _sz, _P_i64, _vp]),
     "ej_extract_coo_fill": (_i32, [_vp, _i32, _i32, _P_i64, _vp, _sz, _i64, _vp, _vp, _i64,
                                    _vp]),
-    "ej_bucket_coo_workspace_size": (_i32, [_i64, _P_sz]),
+    "ej_bucket_coo_workspace_size": (_i32, [_i64, _i32, _i32, _P_i64, _P_i64, _P_sz]),
     "ej_bucket_coo_count": (_i32, [_vp, _vp, _i32, _i64, _i32, _P_i64, _P_i64, _vp, _sz, _P_i64,
                                    _vp]),
-    "ej_bucket_coo_fill": (_i32, [_vp, _i32, _i64, _i32, _P_i64, _P_i64, _vp, _sz, _i64, _vp,
-                                  _vp, _i64, _vp]),
+    "ej_bucket_coo_fill": (_i32, [_vp, _vp, _i32, _i64, _i32, _P_i64, _P_i64, _vp, _sz, _i64,
+                                  _vp, _vp, _i64, _vp]),
     "ej_scheme_stats_workspace_size": (_i32, [_i32, _P_i64, _i64, _P_i64, _i64, _i64, _P_sz]),
     "ej_scheme_stats_dense": (_i32, [_vp, _i32, _i32, _P_i64, _i64, _P_i64, _vp, _sz, _P_i64,
                                      _P_i64, _vp]),

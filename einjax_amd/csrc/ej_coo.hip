@@ -105,6 +105,28 @@ constexpr int64_t kCountStride = 16;
 // Number of bytes of w that are nonzero, for bytes holding 0 or 1.
 __device__ inline int bytes_set(uint32_t w) { return static_cast<int>((w * 0x01010101u) >> 24); }
 
+// Sets bit t of a bit map for every lane with valid set, with one atomic per
+// distinct map word of the wave (skipped when its bits are already set):
+// neighbouring entries mostly fall in the same word, which would otherwise
+// take one contended atomic per entry.  Every lane of the wave calls it.
+__device__ inline void wave_set_bit(uint32_t *map, uint64_t t, bool valid) {
+  const int lane = threadIdx.x & 63;
+  uint64_t my_word = valid ? (t >> 5) : ~uint64_t(0);
+  const uint32_t my_bit = valid ? 1u << (t & 31) : 0u;
+  for (;;) {
+    const uint64_t active = __ballot(my_word != ~uint64_t(0));
+    if (!active) break;
+    const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
+    const uint64_t lw = __shfl(my_word, leader, 64);
+    const bool same = my_word == lw;
+    uint32_t bits = same ? my_bit : 0u;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) bits |= __shfl_xor(bits, d, 64);
+    if (lane == leader && (map[lw] & bits) != bits) atomicOr(&map[lw], bits);
+    if (same) my_word = ~uint64_t(0);
+  }
+}
+
 template <typename T>
 __global__ void fill_zero_kernel(T *p, int64_t n) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -408,6 +430,167 @@ CooWs carve_coo(void *base, int64_t nnz) {
   return w;
 }
 
+// COO to tiles without sorting, for fp32 tiles on grids of at most 2^30
+// tiles: every entry marks its tile in a byte-per-tile flag array with a
+// plain store (concurrent stores write the same value, and no two tiles
+// share a byte, so no atomics); the flags are packed into a bit map whose
+// word popcounts are scanned, so a tile's slot is the number of occupied
+// tiles before it and slots follow the lexicographic tile order; each
+// element of the output takes the value of the largest entry index that
+// names it (atomicMax of the index, kept in the output buffer until the
+// values are resolved), which is the last entry, as the sorted path keeps it.
+constexpr int64_t kCooMapMaxTiles = int64_t(1) << 30;
+
+bool coo_map_path(int32_t dtype, const CooGeom &g) {
+  return dtype != EJ_BF16 && g.n_tiles <= kCooMapMaxTiles;
+}
+
+struct CooMapWs {
+  int64_t *scalars;  // [0] tile count, [1] range flag
+  uint8_t *flags;    // one byte per tile, padded to whole map words
+  uint32_t *map;
+  int64_t *cnt, *prefix;
+  void *scan_ws;
+  size_t bytes;
+};
+
+CooMapWs carve_coo_map(void *base, int64_t n_tiles) {
+  const int64_t words = (n_tiles + 31) / 32;
+  Carver c(base);
+  CooMapWs w;
+  w.scalars = c.take<int64_t>(4);
+  w.flags = c.take<uint8_t>(words * 32);
+  w.map = c.take<uint32_t>(words);
+  w.cnt = c.take<int64_t>(words);
+  w.prefix = c.take<int64_t>(words);
+  w.scan_ws = c.take<char>(static_cast<int64_t>(scan_workspace_bytes(words)));
+  w.bytes = c.off;
+  return w;
+}
+
+// Tile index and in-tile offset of entry i; false for an entry whose value
+// is 0, or that lies outside the tensor (then *bad is set).
+template <typename T>
+__device__ inline bool coo_entry(const int32_t *__restrict__ idx, const T *__restrict__ vals,
+                                 int64_t i, const CooGeom &g, int64_t *bad, uint64_t *tile,
+                                 uint64_t *within) {
+  if (!nz(vals[i])) return false;
+  uint64_t tkey = 0, wkey = 0;
+  bool ok = true;
+#pragma unroll
+  for (int d = 0; d < EJ_MAX_DIMS; ++d) {
+    if (d < g.nd) {
+      const int64_t c = idx[i * g.nd + d];
+      if (c < 0 || c >= g.shape[d]) ok = false;
+      const uint32_t cu = static_cast<uint32_t>(c), tu = static_cast<uint32_t>(g.tile[d]);
+      tkey = tkey * static_cast<uint64_t>(g.grid[d]) + cu / tu;
+      wkey = wkey * static_cast<uint64_t>(tu) + cu % tu;
+    }
+  }
+  if (!ok) {
+    *bad = 1;
+    return false;
+  }
+  *tile = tkey;
+  *within = wkey;
+  return true;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_tile_mark_kernel(const int32_t *__restrict__ idx,
+                                                            const T *__restrict__ vals,
+                                                            int64_t nnz, CooGeom g,
+                                                            uint8_t *__restrict__ flags,
+                                                            int64_t *bad) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  uint64_t t, w;
+  if (coo_entry(idx, vals, i, g, bad, &t, &w) && !flags[t]) flags[t] = 1;
+}
+
+// Map word j from flags [32j, 32j + 32), and its popcount.
+__global__ __launch_bounds__(256) void pack_flags_kernel(const uint8_t *__restrict__ flags,
+                                                         int64_t words,
+                                                         uint32_t *__restrict__ map,
+                                                         int64_t *__restrict__ cnt) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= words) return;
+  const uint4 *src = reinterpret_cast<const uint4 *>(flags + j * 32);
+  const uint4 a = src[0], b = src[1];
+  const uint32_t f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t bits = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if ((f[q] >> (8 * k)) & 0xffu) bits |= 1u << (4 * q + k);
+  }
+  map[j] = bits;
+  cnt[j] = __popc(bits);
+}
+
+__global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void coo_winner_kernel(const int32_t *__restrict__ idx,
+                                                         const T *__restrict__ vals, int64_t nnz,
+                                                         CooGeom g,
+                                                         const uint32_t *__restrict__ map,
+                                                         const int64_t *__restrict__ prefix,
+                                                         int64_t n_slots, int64_t *bad,
+                                                         int32_t *__restrict__ win) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= nnz) return;
+  uint64_t t, w;
+  if (!coo_entry(idx, vals, i, g, bad, &t, &w)) return;
+  const uint32_t word = map[t >> 5];
+  const int64_t slot = prefix[t >> 5] + __popc(word & ((1u << (t & 31)) - 1u));
+  if (slot < n_slots) atomicMax(&win[slot * g.tile_elems + static_cast<int64_t>(w)], int32_t(i));
+}
+
+// In place: the entry index each element holds becomes that entry's value
+// (fp32), or +0.0 where no entry names the element.
+template <typename T>
+__global__ __launch_bounds__(256) void coo_resolve_kernel(const T *__restrict__ vals,
+                                                          int32_t *__restrict__ tiles,
+                                                          int64_t elems) {
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < elems;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t wi = tiles[e];
+    const float f = wi >= 0 ? tile_val(vals[wi]) : 0.0f;
+    tiles[e] = __float_as_int(f);
+  }
+}
+
+__global__ __launch_bounds__(256) void coo_map_coords_kernel(const uint32_t *__restrict__ map,
+                                                             const int64_t *__restrict__ prefix,
+                                                             int64_t words, CooGeom g,
+                                                             int64_t n_slots,
+                                                             int32_t *__restrict__ coords) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= words) return;
+  uint32_t bits = map[j];
+  int64_t slot = prefix[j];
+  while (bits && slot < n_slots) {
+    const int k = __ffs(bits) - 1;
+    uint64_t t = static_cast<uint64_t>(j) * 32 + k;
+#pragma unroll
+    for (int d = EJ_MAX_DIMS - 1; d >= 0; --d) {
+      if (d < g.nd) {
+        const uint64_t gd = static_cast<uint64_t>(g.grid[d]);
+        coords[slot * g.nd + d] = static_cast<int32_t>(t % gd);
+        t /= gd;
+      }
+    }
+    ++slot;
+    bits &= bits - 1;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Statistics.
 struct TileIdx {  // mixed-radix tile index of an element for one tile shape
@@ -698,9 +881,9 @@ __global__ __launch_bounds__(256) void coo_mark_kernel(const int32_t *__restrict
                                                        TileIdx ti, uint32_t *__restrict__ map,
                                                        int64_t *bad) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= nnz) return;
-  uint64_t t;
-  if (entry_tile(idx, vals, i, ti, bad, &t)) atomicOr(&map[t >> 5], 1u << (t & 31));
+  uint64_t t = 0;
+  const bool keep = i < nnz && entry_tile(idx, vals, i, ti, bad, &t);
+  wave_set_bit(map, t, keep);
 }
 
 __global__ __launch_bounds__(256) void map_count_kernel(const uint32_t *__restrict__ words,
@@ -1240,11 +1423,17 @@ extern "C" int ej_extract_coo_fill(const void *dense, int32_t dtype, int32_t ndi
 }
 
 // ---- COO to tiles --------------------------------------------------------------
-extern "C" int ej_bucket_coo_workspace_size(int64_t nnz, size_t *bytes) {
+extern "C" int ej_bucket_coo_workspace_size(int64_t nnz, int32_t dtype, int32_t ndim,
+                                            const int64_t *shape, const int64_t *tile_shape,
+                                            size_t *bytes) {
   clear_error();
   EJ_CHECK_ARG(bytes, "bytes is null");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
   EJ_CHECK_ARG(nnz >= 0 && nnz <= INT32_MAX, "nnz=%lld outside [0, 2^31)", (long long)nnz);
-  *bytes = carve_coo(nullptr, nnz).bytes;
+  CooGeom g;
+  EJ_TRY(make_coo_geom(ndim, shape, tile_shape, &g));
+  *bytes = coo_map_path(dtype, g) ? carve_coo_map(nullptr, g.n_tiles).bytes
+                                  : carve_coo(nullptr, nnz).bytes;
   return EJ_OK;
 }
 
@@ -1265,13 +1454,45 @@ extern "C" int ej_bucket_coo_count(const int32_t *indices, const void *values, i
     return EJ_OK;
   }
   EJ_CHECK_ARG(indices && values, "null pointer argument");
+  const dim3 grid(grid_for(nnz));
+  if (coo_map_path(dtype, g)) {
+    CooMapWs w = carve_coo_map(workspace, g.n_tiles);
+    EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes,
+                 "workspace too small: %zu < %zu bytes", workspace_bytes, w.bytes);
+    const int64_t words = (g.n_tiles + 31) / 32;
+    hipLaunchKernelGGL(fill_zero_kernel<int64_t>, dim3(1), dim3(64), 0, stream, w.scalars,
+                       int64_t(4));
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(fill_zero_kernel<uint32_t>, dim3(stride_grid(words * 8)), dim3(kBlock),
+                       0, stream, reinterpret_cast<uint32_t *>(w.flags), words * 8);
+    EJ_LAUNCH_CHECK();
+    if (dtype == EJ_F64)
+      hipLaunchKernelGGL(coo_tile_mark_kernel<double>, grid, dim3(kBlock), 0, stream, indices,
+                         static_cast<const double *>(values), nnz, g, w.flags, w.scalars + 1);
+    else
+      hipLaunchKernelGGL(coo_tile_mark_kernel<float>, grid, dim3(kBlock), 0, stream, indices,
+                         static_cast<const float *>(values), nnz, g, w.flags, w.scalars + 1);
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(pack_flags_kernel, dim3(grid_for(words)), dim3(kBlock), 0, stream,
+                       w.flags, words, w.map, w.cnt);
+    EJ_LAUNCH_CHECK();
+    EJ_TRY(scan_exclusive_i64(w.cnt, w.prefix, words, w.scalars, w.scan_ws, stream));
+    int64_t host[2] = {0, 0};
+    EJ_HIP(hipMemcpyAsync(host, w.scalars, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    EJ_HIP(hipStreamSynchronize(stream));
+    if (host[1]) {
+      set_error("a nonzero entry has an index outside the tensor shape");
+      return EJ_E_RANGE;
+    }
+    *n_tiles = host[0];
+    return EJ_OK;
+  }
   CooWs w = carve_coo(workspace, nnz);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
   hipLaunchKernelGGL(fill_zero_kernel<int64_t>, dim3(1), dim3(64), 0, stream, w.scalars,
                      int64_t(4));
   EJ_LAUNCH_CHECK();
-  const dim3 grid(grid_for(nnz));
   // Keys go to the alternate buffers when the sort takes an odd number of
   // passes, so the sorted result lands in keys / order without a copy.
   const bool alt = radix_passes(g.bits) % 2 == 1;
@@ -1304,11 +1525,11 @@ extern "C" int ej_bucket_coo_count(const int32_t *indices, const void *values, i
   return EJ_OK;
 }
 
-extern "C" int ej_bucket_coo_fill(const void *values, int32_t dtype, int64_t nnz, int32_t ndim,
-                                  const int64_t *shape, const int64_t *tile_shape,
-                                  const void *workspace, size_t workspace_bytes, int64_t n_tiles,
-                                  int32_t *coords, void *tiles, int64_t capacity,
-                                  ej_stream_t stream_) {
+extern "C" int ej_bucket_coo_fill(const int32_t *indices, const void *values, int32_t dtype,
+                                  int64_t nnz, int32_t ndim, const int64_t *shape,
+                                  const int64_t *tile_shape, const void *workspace,
+                                  size_t workspace_bytes, int64_t n_tiles, int32_t *coords,
+                                  void *tiles, int64_t capacity, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
   EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
@@ -1322,10 +1543,40 @@ extern "C" int ej_bucket_coo_fill(const void *values, int32_t dtype, int64_t nnz
   }
   if (n_tiles == 0) return EJ_OK;
   EJ_CHECK_ARG(values && coords && tiles, "null pointer argument");
-  CooWs w = carve_coo(const_cast<void *>(workspace), nnz);
-  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
   const int64_t elems = n_tiles * g.tile_elems;
   const dim3 grid(grid_for(nnz));
+  if (coo_map_path(dtype, g)) {
+    EJ_CHECK_ARG(indices, "null pointer argument");
+    CooMapWs w = carve_coo_map(const_cast<void *>(workspace), g.n_tiles);
+    EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
+    const int64_t words = (g.n_tiles + 31) / 32;
+    int32_t *win = static_cast<int32_t *>(tiles);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(stride_grid(elems)), dim3(kBlock), 0, stream, win,
+                       elems, int32_t(-1));
+    EJ_LAUNCH_CHECK();
+    if (dtype == EJ_F64) {
+      hipLaunchKernelGGL(coo_winner_kernel<double>, grid, dim3(kBlock), 0, stream, indices,
+                         static_cast<const double *>(values), nnz, g, w.map, w.prefix, n_tiles,
+                         w.scalars + 1, win);
+      EJ_LAUNCH_CHECK();
+      hipLaunchKernelGGL(coo_resolve_kernel<double>, dim3(stride_grid(elems)), dim3(kBlock), 0,
+                         stream, static_cast<const double *>(values), win, elems);
+    } else {
+      hipLaunchKernelGGL(coo_winner_kernel<float>, grid, dim3(kBlock), 0, stream, indices,
+                         static_cast<const float *>(values), nnz, g, w.map, w.prefix, n_tiles,
+                         w.scalars + 1, win);
+      EJ_LAUNCH_CHECK();
+      hipLaunchKernelGGL(coo_resolve_kernel<float>, dim3(stride_grid(elems)), dim3(kBlock), 0,
+                         stream, static_cast<const float *>(values), win, elems);
+    }
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(coo_map_coords_kernel, dim3(grid_for(words)), dim3(kBlock), 0, stream,
+                       w.map, w.prefix, words, g, n_tiles, coords);
+    EJ_LAUNCH_CHECK();
+    return EJ_OK;
+  }
+  CooWs w = carve_coo(const_cast<void *>(workspace), nnz);
+  EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
   if (dtype == EJ_BF16) {
     hipLaunchKernelGGL(fill_zero_kernel<uint16_t>, dim3(stride_grid(elems)), dim3(kBlock), 0,
                        stream, static_cast<uint16_t *>(tiles), elems);

@@ -71,7 +71,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 5
+#define EJ_ABI_VERSION 6
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -336,16 +336,18 @@ int ej_extract_coo_fill(const void *dense, int32_t dtype, int32_t ndim, const in
  * reference's fancy assignment leaves it.  A nonzero entry whose index lies
  * outside shape gives EJ_E_RANGE; tile_shape must divide shape (EJ_E_INVAL).
  * Tiles are fp32 for EJ_F64 / EJ_F32 values and bf16 for EJ_BF16 values. */
-int ej_bucket_coo_workspace_size(int64_t nnz, size_t *bytes);
+int ej_bucket_coo_workspace_size(int64_t nnz, int32_t dtype, int32_t ndim, const int64_t *shape,
+                                 const int64_t *tile_shape, size_t *bytes);
 int ej_bucket_coo_count(const int32_t *indices, const void *values, int32_t dtype, int64_t nnz,
                         int32_t ndim, const int64_t *shape, const int64_t *tile_shape,
                         void *workspace, size_t workspace_bytes, int64_t *n_tiles,
                         ej_stream_t stream);
-/* coords int32 [n_tiles, ndim]; tiles [n_tiles, *tile_shape]. */
-int ej_bucket_coo_fill(const void *values, int32_t dtype, int64_t nnz, int32_t ndim,
-                       const int64_t *shape, const int64_t *tile_shape, const void *workspace,
-                       size_t workspace_bytes, int64_t n_tiles, int32_t *coords, void *tiles,
-                       int64_t capacity, ej_stream_t stream);
+/* coords int32 [n_tiles, ndim]; tiles [n_tiles, *tile_shape]; indices and
+ * values as given to ej_bucket_coo_count. */
+int ej_bucket_coo_fill(const int32_t *indices, const void *values, int32_t dtype, int64_t nnz,
+                       int32_t ndim, const int64_t *shape, const int64_t *tile_shape,
+                       const void *workspace, size_t workspace_bytes, int64_t n_tiles,
+                       int32_t *coords, void *tiles, int64_t capacity, ej_stream_t stream);
 
 /* ---- statistics (reference: _compute_sparsity_metrics, tensor/sparse.py:124-158) */
 /* For each of n_schemes tile shapes (tile_shapes: HOST int64

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 5
+    assert _lib.load().ej_version() == 6
 
 
 def describe(spec, lt, rt):
@@ -207,10 +207,18 @@ def test_coo_calls_host_paths():
     assert lib.ej_bucket_coo_count(None, None, _lib.EJ_F64, 3, 2, i64_array([4, 4]),
                                    i64_array([3, 2]), None, 0, ctypes.byref(n),
                                    None) == _lib.EJ_E_INVAL
-    assert lib.ej_bucket_coo_workspace_size(1 << 31, ctypes.byref(a)) == _lib.EJ_E_INVAL
-    assert lib.ej_bucket_coo_workspace_size(1000, ctypes.byref(a)) == 0 and a.value > 32000
-    assert lib.ej_bucket_coo_fill(None, _lib.EJ_F32, 10, 2, i64_array([4, 4]), i64_array([2, 2]),
-                                  None, 0, 3, None, None, 2, None) == _lib.EJ_E_CAPACITY
+    sh, ts = i64_array([64, 64]), i64_array([4, 4])
+    assert lib.ej_bucket_coo_workspace_size(1 << 31, _lib.EJ_F64, 2, sh, ts,
+                                            ctypes.byref(a)) == _lib.EJ_E_INVAL
+    # bf16 values: sorted path, workspace grows with the entries
+    assert lib.ej_bucket_coo_workspace_size(1000, _lib.EJ_BF16, 2, sh, ts,
+                                            ctypes.byref(a)) == 0 and a.value > 32000
+    # fp32 tiles: occupancy-map path, workspace follows the 256-tile grid
+    assert lib.ej_bucket_coo_workspace_size(1000, _lib.EJ_F64, 2, sh, ts,
+                                            ctypes.byref(a)) == 0 and a.value < 8192
+    assert lib.ej_bucket_coo_fill(None, None, _lib.EJ_F32, 10, 2, i64_array([4, 4]),
+                                  i64_array([2, 2]), None, 0, 3, None, None, 2,
+                                  None) == _lib.EJ_E_CAPACITY
     assert lib.ej_extract_coo_fill(None, _lib.EJ_F32, 2, i64_array([4, 4]), None, 0, 5, None,
                                    None, 4, None) == _lib.EJ_E_CAPACITY
 
