@@ -18,7 +18,7 @@ GEMM, segment sum; plus tiling), achieved GB/s against HBM for
 join+gather+segment-sum, the roofline of the dominant kernel, and the CPU
 oracle timed on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--all-configs]
+Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--no-cpu-baseline] [--all-configs]
                        [--ingest] [--backward] [--copy-calibration]
 """
 
@@ -314,8 +314,8 @@ def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 5) -
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all-configs", action="store_true",
                     help="also time every workload configuration at full size (adds 'configs')")

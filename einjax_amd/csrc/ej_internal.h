@@ -89,6 +89,11 @@ int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *v
                    int64_t n, int bits, void *ws, hipStream_t stream,
                    bool input_in_alt = false, const int64_t *n_dev = nullptr);
 
+// Zeroes n bytes (a multiple of 4, 4-byte aligned) with a kernel rather than
+// hipMemsetAsync, which misbehaves when a caller records the call into a
+// HIP graph.
+int zero_async(void *p, size_t bytes, hipStream_t stream);
+
 // ---- device helpers --------------------------------------------------------
 __device__ inline uint64_t pack_key(const int32_t *row, const KeySpec &ks, int *bad) {
   uint64_t key = 0;

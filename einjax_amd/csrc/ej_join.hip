@@ -278,7 +278,7 @@ int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
                workspace_bytes, w.bytes);
   *dev_scalars = w.scalars;
 
-  EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
+  EJ_TRY(zero_async(w.scalars, 4 * sizeof(int64_t), stream));
   int *bad = reinterpret_cast<int *>(w.scalars + 1);
   // Sorted sides are packed where an odd number of radix passes leaves them
   // in the primary buffers.
@@ -621,7 +621,7 @@ int segment_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
   *dev_scalars = w.scalars;
-  EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
+  EJ_TRY(zero_async(w.scalars, 4 * sizeof(int64_t), stream));
   const bool alt = n_pairs > 1 && (radix_passes(bits) & 1);
   hipLaunchKernelGGL(pair_keys_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream,
                      lhs_coords, rhs_coords, lhs_idx, rhs_idx, n_pairs, n_pairs_dev, a,
@@ -696,7 +696,7 @@ extern "C" int ej_segment_count_async(const int32_t *lhs_coords, int64_t n_lhs,
   if (empty) {
     SegWs w = carve_seg(workspace, 0);
     EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
-    EJ_HIP(hipMemsetAsync(w.scalars, 0, 4 * sizeof(int64_t), stream));
+    EJ_TRY(zero_async(w.scalars, 4 * sizeof(int64_t), stream));
     scal = w.scalars;
   }
   EJ_HIP(hipMemcpyAsync(counts, scal, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
@@ -717,7 +717,7 @@ extern "C" int ej_segment_fill(int64_t n_pairs, int64_t n_segments, int32_t n_ou
     return EJ_E_CAPACITY;
   }
   if (n_pairs == 0) {
-    if (seg_offsets) EJ_HIP(hipMemsetAsync(seg_offsets, 0, sizeof(int32_t), stream));
+    if (seg_offsets) EJ_TRY(zero_async(seg_offsets, sizeof(int32_t), stream));
     return EJ_OK;
   }
   EJ_CHECK_ARG(seg_offsets && perm && (out_coords || n_out == 0), "null output pointer");

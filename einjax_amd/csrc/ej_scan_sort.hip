@@ -20,6 +20,22 @@ void set_error(const char *fmt, ...) {
 
 void clear_error() { g_error.clear(); }
 
+__global__ void zero_words_kernel(uint32_t *p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+int zero_async(void *p, size_t bytes, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(bytes / 4);
+  if (n <= 0) return EJ_OK;
+  const int64_t g = ceil_div(n, kBlock);
+  hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<unsigned>(g < 1024 ? g : 1024)),
+                     dim3(kBlock), 0, stream, static_cast<uint32_t *>(p), n);
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
 int key_bits(const int64_t *radix, int n, int *bits) {
   // prod(radix) must stay below 2^63 so that packed keys are exact.
   unsigned __int128 prod = 1;
@@ -100,7 +116,7 @@ size_t scan_workspace_bytes(int64_t n) {
 int scan_exclusive_i64(const int64_t *in, int64_t *out, int64_t n, int64_t *total, void *ws,
                        hipStream_t stream, const int64_t *n_dev) {
   if (n <= 0) {
-    if (total) EJ_HIP(hipMemsetAsync(total, 0, sizeof(int64_t), stream));
+    if (total) EJ_TRY(zero_async(total, sizeof(int64_t), stream));
     return EJ_OK;
   }
   if (n <= kFastScanMax) {
