@@ -194,7 +194,7 @@ def measure_config(name: str, reps: int = 5) -> dict:
     e = 2 if bf16 else 4
     out_tile = sd._infer_output_tile_shape(ks, L.tile_shape, Rr.tile_shape)
     B_fused = W.bytes_fused(int(torch.unique(li).numel()), int(torch.unique(ri).numel()),
-                            L.tile_shape, Rr.tile_shape, e, U, out_tile, len(ak))
+                            L.tile_shape, Rr.tile_shape, e, U, out_tile, len(ak), e)
     peak = MFMA_PEAK_TFLOPS["bf16" if bf16 else "fp32"]
     res = {
         "workload": w["name"], "dtype": w["dtype"], "pairs": P, "output_tiles": U,
@@ -286,27 +286,31 @@ def measure_ingest(cpu: bool = True) -> dict:
 
 def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 5) -> dict:
     """Backward of the headline's per-pair einsum (sparse_einsum_raw's
-    gradient): both operand gradients for an fp32 cotangent of every pair,
-    and each alone.  FLOPs: 2·M·N·K per pair per gradient."""
+    gradient): both operand gradients for a cotangent of every pair in the
+    forward output's dtype (bf16: bf16 gradient einsums, fp32 sums), each
+    gradient alone, and both for an fp32 cotangent (operands widened to
+    fp32).  FLOPs: 2·M·N·K per pair per gradient."""
     import torch
 
     from einjax_amd import _device
 
-    g = torch.randn((li.numel(), lhs.tile_shape[0], rhs.tile_shape[1]), device="cuda")
+    g32 = torch.randn((li.numel(), lhs.tile_shape[0], rhs.tile_shape[1]), device="cuda")
+    g = g32.to(lhs.values.dtype)
+    vjp = lambda gg, **k: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri,
+                                                  gg, **k)
     run = {
-        "both": lambda: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri, g),
-        "lhs": lambda: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri, g,
-                                               need_rhs=False),
-        "rhs": lambda: _device.pair_einsum_vjp(kernel_string, lhs.values, rhs.values, li, ri, g,
-                                               need_lhs=False),
+        "both": lambda: vjp(g),
+        "lhs": lambda: vjp(g, need_rhs=False),
+        "rhs": lambda: vjp(g, need_lhs=False),
+        "both_fp32_cotangent": lambda: vjp(g32),
     }
     out = {}
     for k, fn in run.items():
         t = wall_time_ms(fn, reps)
-        flops = 2 * F if k == "both" else F
+        flops = 2 * F if k.startswith("both") else F
         out[f"{k}_ms"] = t
         out[f"{k}_tflops"] = flops / (t * 1e-3) / 1e12
-    del g
+    del g, g32
     torch.cuda.empty_cache()
     return out
 
@@ -411,12 +415,12 @@ def main():
     F = W.flops_gemm(ks, L.tile_shape, Rr.tile_shape, P)
     B_join = W.bytes_join(L.coords.shape[0], Rr.coords.shape[0], P)
     B_gather = W.bytes_gather(P, L.tile_shape, Rr.tile_shape, e)
-    B_segsum = W.bytes_segsum(P, U, (L.tile_shape[0], Rr.tile_shape[1]), 2)
+    B_segsum = W.bytes_segsum(P, U, (L.tile_shape[0], Rr.tile_shape[1]), 2, e)
     B_bucket = W.bytes_bucket(int(np.prod(L.shape)), L.coords.shape[0], L.tile_shape, e, 2)
     n_lhs_used = len(np.unique(li.cpu().numpy()))
     n_rhs_used = len(np.unique(ri.cpu().numpy()))
     B_fused = W.bytes_fused(n_lhs_used, n_rhs_used, L.tile_shape, Rr.tile_shape, e, U,
-                            (L.tile_shape[0], Rr.tile_shape[1]), 2)
+                            (L.tile_shape[0], Rr.tile_shape[1]), 2, e)
     jgs_gbs = (B_join + B_gather + B_segsum) / ((t_join + t_gather + t_segsum) * 1e-3) / 1e9
     fused_tflops = F / (t_fused * 1e-3) / 1e12
     kernel_name = "seg_gemm_kernel<SegOpBf16<128,128>,4,4,2,8,false>"

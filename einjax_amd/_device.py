@@ -172,26 +172,43 @@ def _out_tile(desc: _lib.EinsumDesc) -> tuple:
     return tuple(int(desc.out_ext[i]) for i in range(desc.n_out))
 
 
-def pair_einsum(desc, lhs_values, rhs_values, lhs_idx=None, rhs_idx=None, n_pairs=None):
-    """fp32 [P, *out_tile]: the tile einsum of every matched pair."""
+def _set_out_dtype(desc, values: torch.Tensor, out_dtype) -> torch.dtype:
+    """Output dtype of an einsum on `values`: out_dtype, or by default the
+    operands' own dtype (float32, or bfloat16 for bfloat16 tiles), as the
+    reference's jnp.einsum returns.  Written into the descriptor."""
+    dt = values.dtype if out_dtype is None else out_dtype
+    if dt not in _VALUE_DTYPES:
+        raise TypeError(f"einsum outputs are float32 or bfloat16, got {dt}")
+    desc.out_dtype = _VALUE_DTYPES[dt]
+    return dt
+
+
+def pair_einsum(desc, lhs_values, rhs_values, lhs_idx=None, rhs_idx=None, n_pairs=None,
+                out_dtype=None):
+    """[P, *out_tile]: the tile einsum of every matched pair, summed in fp32,
+    in out_dtype (default: the operands' dtype)."""
     code = value_code(lhs_values)
     if rhs_values.dtype != lhs_values.dtype:
         raise TypeError("both operands must have the same value dtype")
     P = lhs_idx.numel() if lhs_idx is not None else int(n_pairs)
-    out = torch.empty((P, *_out_tile(desc)), dtype=torch.float32, device=lhs_values.device)
+    odt = _set_out_dtype(desc, lhs_values, out_dtype)
+    out = torch.empty((P, *_out_tile(desc)), dtype=odt, device=lhs_values.device)
     check(_lib.load().ej_pair_einsum(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                      lhs_values.shape[0], rhs_values.shape[0], ptr(lhs_idx),
                                      ptr(rhs_idx), P, ptr(out), stream_ptr()), "ej_pair_einsum")
     return out
 
 
-def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_offsets):
-    """fp32 [U, *out_tile]: fused gather + tile einsum + segment sum."""
+def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_offsets,
+                   out_dtype=None):
+    """[U, *out_tile]: fused gather + tile einsum + segment sum, summed in
+    fp32, in out_dtype (default: the operands' dtype)."""
     code = value_code(lhs_values)
     if rhs_values.dtype != lhs_values.dtype:
         raise TypeError("both operands must have the same value dtype")
     U = seg_offsets.numel() - 1
-    out = torch.empty((U, *_out_tile(desc)), dtype=torch.float32, device=lhs_values.device)
+    odt = _set_out_dtype(desc, lhs_values, out_dtype)
+    out = torch.empty((U, *_out_tile(desc)), dtype=odt, device=lhs_values.device)
     check(_lib.load().ej_segment_einsum(ctypes.byref(desc), code, ptr(lhs_values),
                                         ptr(rhs_values), lhs_values.shape[0], rhs_values.shape[0],
                                         ptr(lhs_idx), ptr(rhs_idx), ptr(perm), ptr(seg_offsets),
@@ -218,7 +235,8 @@ def _count_buffer() -> tuple[torch.Tensor, torch.cuda.Event]:
 
 
 def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys,
-                          agg_radices, desc, lhs_values, rhs_values, pair_bound: int):
+                          agg_radices, desc, lhs_values, rhs_values, pair_bound: int,
+                          out_dtype=None):
     """Join, segment plan and fused segment einsum queued back to back on the
     current stream, with the pair count bounded by pair_bound instead of
     read first.  The host waits only for an event recorded after the plan's
@@ -257,7 +275,8 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
     offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
     perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
-    out = torch.empty((cap_u, *_out_tile(desc)), dtype=torch.float32, device=dev)
+    odt = _set_out_dtype(desc, lhs_values, out_dtype)
+    out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
     ldims = i32_array([k[0] for k in join_keys])
     rdims = i32_array([k[1] for k in join_keys])
     jrad = i64_array(join_radices)
@@ -297,11 +316,13 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
 
 
 def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:
-    """fp32 [U, *tile]: per-segment sums in plan order."""
+    """[U, *tile] in the pair values' dtype (float32 or bfloat16): per-segment
+    sums in plan order, formed in fp32."""
+    code = value_code(pair_values)
     U = seg_offsets.numel() - 1
     tile = tuple(pair_values.shape[1:])
-    out = torch.empty((U, *tile), dtype=torch.float32, device=pair_values.device)
-    check(_lib.load().ej_segment_sum(ptr(pair_values), max(prod(tile), 1), ptr(perm),
+    out = torch.empty((U, *tile), dtype=pair_values.dtype, device=pair_values.device)
+    check(_lib.load().ej_segment_sum(ptr(pair_values), code, max(prod(tile), 1), ptr(perm),
                                      ptr(seg_offsets), U, ptr(out), stream_ptr()),
           "ej_segment_sum")
     return out
@@ -479,9 +500,11 @@ def index_plan(idx: torch.Tensor, n_targets: int) -> tuple[torch.Tensor, torch.T
 def pair_einsum_vjp(kernel_string: str, lhs_values: torch.Tensor, rhs_values: torch.Tensor,
                     lhs_idx: torch.Tensor, rhs_idx: torch.Tensor, grad_out: torch.Tensor,
                     need_lhs: bool = True, need_rhs: bool = True):
-    """(grad_lhs, grad_rhs), fp32 with the operands' tile shapes (None when
-    not requested): the gradients of the per-pair tile einsum for the
-    cotangent grad_out [P, *out_tile]."""
+    """(grad_lhs, grad_rhs) with the operands' tile shapes (None when not
+    requested): the gradients of the per-pair tile einsum for the cotangent
+    grad_out [P, *out_tile].  bfloat16 operands with a bfloat16 cotangent give
+    bfloat16 gradients (bf16 einsums, fp32 sums); otherwise the cotangent is
+    taken in float32 and the gradients are float32."""
     lib = _lib.load()
     code = value_code(lhs_values)
     if rhs_values.dtype != lhs_values.dtype:
@@ -491,18 +514,21 @@ def pair_einsum_vjp(kernel_string: str, lhs_values: torch.Tensor, rhs_values: to
     li = lhs_idx.to(dtype=torch.int64).contiguous().reshape(-1)
     ri = rhs_idx.to(dtype=torch.int64).contiguous().reshape(-1)
     P = li.numel()
-    g = grad_out.to(dtype=torch.float32).contiguous()
+    gdt = torch.bfloat16 if (lhs_values.dtype == torch.bfloat16 and
+                             grad_out.dtype == torch.bfloat16) else torch.float32
+    gcode = _VALUE_DTYPES[gdt]
+    g = grad_out.to(dtype=gdt).contiguous()
     dev = lhs_values.device
-    gl = torch.empty((nl, *lt), dtype=torch.float32, device=dev) if need_lhs else None
-    gr = torch.empty((nr, *rt), dtype=torch.float32, device=dev) if need_rhs else None
+    gl = torch.empty((nl, *lt), dtype=gdt, device=dev) if need_lhs else None
+    gr = torch.empty((nr, *rt), dtype=gdt, device=dev) if need_rhs else None
     nbytes = ctypes.c_size_t()
     check(lib.ej_pair_einsum_vjp_workspace_size(P, nl, nr, max(prod(lt), 1), max(prod(rt), 1),
-                                                code, ctypes.byref(nbytes)),
+                                                code, gcode, ctypes.byref(nbytes)),
           "ej_pair_einsum_vjp_workspace_size")
     ws = workspace(nbytes.value, dev)
     check(lib.ej_pair_einsum_vjp(kernel_string.encode(), i64_array(lt), len(lt), i64_array(rt),
                                  len(rt), code, ptr(lhs_values.contiguous()), nl,
-                                 ptr(rhs_values.contiguous()), nr, ptr(li), ptr(ri), P, ptr(g),
-                                 ptr(gl), ptr(gr), ptr(ws), ws.numel(), stream_ptr()),
+                                 ptr(rhs_values.contiguous()), nr, ptr(li), ptr(ri), P, gcode,
+                                 ptr(g), ptr(gl), ptr(gr), ptr(ws), ws.numel(), stream_ptr()),
           "ej_pair_einsum_vjp")
     return gl, gr

@@ -51,6 +51,7 @@ class EinsumDesc(ctypes.Structure):
         ("a_sb", _i64), ("a_sm", _i64), ("a_sk", _i64),
         ("b_sb", _i64), ("b_sk", _i64), ("b_sn", _i64),
         ("c_sb", _i64), ("c_sm", _i64), ("c_sn", _i64),
+        ("out_dtype", _i32), ("reserved", _i32),
     ]
 
 
@@ -84,7 +85,7 @@ SIGNATURES = {
                                  _vp, _vp, _vp, _i64, _vp, _vp]),
     "ej_segment_einsum_async": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64,
                                        _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
-    "ej_segment_sum": (_i32, [_vp, _i64, _vp, _vp, _i64, _vp, _vp]),
+    "ej_segment_sum": (_i32, [_vp, _i32, _i64, _vp, _vp, _i64, _vp, _vp]),
     "ej_bucket_workspace_size": (_i32, [_i32, _P_i64, _P_i64, _P_sz]),
     "ej_bucket_dense_count": (_i32, [_vp, _i32, _i32, _P_i64, _P_i64, _vp, _sz, _P_i64, _vp]),
     "ej_bucket_dense_fill": (_i32, [_vp, _i32, _i32, _P_i64, _P_i64, _vp, _sz, _i64, _vp, _vp,
@@ -107,9 +108,11 @@ SIGNATURES = {
                                    _sz, _P_i64, _P_i64, _vp]),
     "ej_index_plan_workspace_size": (_i32, [_i64, _P_sz]),
     "ej_index_plan": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
-    "ej_pair_einsum_vjp_workspace_size": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32, _P_sz]),
+    "ej_pair_einsum_vjp_workspace_size": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32, _i32,
+                                                 _P_sz]),
     "ej_pair_einsum_vjp": (_i32, [ctypes.c_char_p, _P_i64, _i32, _P_i64, _i32, _i32, _vp, _i64,
-                                  _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+                                  _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _sz,
+                                  _vp]),
 }
 
 _lock = threading.Lock()

@@ -51,7 +51,8 @@ def _torch_pair_einsum():
     import torch
 
     class _PairEinsum(torch.autograd.Function):
-        """out[p] = einsum(kernel_string, lhs[li[p]], rhs[ri[p]]), fp32."""
+        """out[p] = einsum(kernel_string, lhs[li[p]], rhs[ri[p]]) in the values'
+        dtype (float32, or bfloat16 for bfloat16 values)."""
 
         @staticmethod
         def forward(ctx, lhs_values, rhs_values, li, ri, kernel_string):
@@ -79,9 +80,11 @@ def sparse_einsum_raw(lhs_values, rhs_values, lhs_coords, rhs_coords, lhs_indice
     """Per-pair tile einsum [P, *out_tile], differentiable in the tile values
     (reference: custom_vjp.py:204-278).  Coordinates and indices are static.
 
-    GPU torch values give an fp32 GPU tensor that torch.autograd
-    differentiates (gradients in the values' dtypes); host NumPy values give
-    a NumPy result (no gradient tracking; use sparse_einsum_raw_vjp)."""
+    GPU torch values give a GPU tensor of the values' dtype (float32, or
+    bfloat16 for bfloat16 values, as the reference's jnp.einsum returns) that
+    torch.autograd differentiates (gradients in the values' dtypes); host
+    NumPy values give a NumPy result (no gradient tracking; use
+    sparse_einsum_raw_vjp)."""
     global _PAIR_EINSUM
     _add_batch_dim(kernel_string)  # the reference's ValueError for a missing "->"
     if not (_is_torch(lhs_values) and _is_torch(rhs_values)):
@@ -103,8 +106,11 @@ def sparse_einsum_raw_vjp(lhs_values, rhs_values, lhs_indices, rhs_indices, kern
     """(grad_lhs, grad_rhs) of sparse_einsum_raw for the cotangent grad_out
     [P, *out_tile] (reference: the _bwd rule, custom_vjp.py:254-275): per-pair
     gradient einsums with the reversed strings, summed per operand tile in
-    ascending pair order.  Gradients have the values' shapes and dtypes;
-    tiles no pair touches get zeros.  Host inputs give host results."""
+    ascending pair order, in fp32.  Gradients have the values' shapes and
+    dtypes; tiles no pair touches get zeros.  bfloat16 values with a bfloat16
+    cotangent run the gradient einsums on bfloat16 operands (the reference's
+    dtypes); any other cotangent is taken in float32.  Host inputs give host
+    results."""
     import torch
 
     host = not (_is_torch(lhs_values) and lhs_values.is_cuda)
@@ -121,7 +127,8 @@ def sparse_einsum_raw_vjp(lhs_values, rhs_values, lhs_indices, rhs_indices, kern
     else:
         lv, rv = lv.to(torch.float32), rv.to(torch.float32)
     li, ri = to_dev(lhs_indices, torch.int64), to_dev(rhs_indices, torch.int64)
-    g = to_dev(grad_out, torch.float32)
+    bf16 = lv.dtype == torch.bfloat16 and _is_torch(grad_out) and grad_out.dtype == torch.bfloat16
+    g = to_dev(grad_out, None if bf16 else torch.float32)
     P = li.numel()
     out_tile = _infer_output_tile_shape(kernel_string, tuple(lv.shape[1:]), tuple(rv.shape[1:]))
     if tuple(g.shape) != (P, *out_tile):

@@ -264,6 +264,14 @@ __device__ inline bool pair_tiles(const PairSrc &s, int64_t q, int64_t *at, int6
 __device__ inline float to_f32(float x) { return x; }
 __device__ inline float to_f32(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }
 
+// Output element stores: fp32 as is, bf16 rounded to nearest even
+// (v_cvt_pk_bf16_f32).  Sums are always formed in fp32; a bf16 output is
+// rounded once, when the finished tile is written.
+__device__ inline void put_out(float *p, float v) { *p = v; }
+__device__ inline void put_out(uint16_t *p, float v) {
+  *p = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+}
+
 // Spreads consecutive block ids over the 8 XCDs in contiguous chunks, so
 // that neighbouring logical blocks (sharing operand tiles) share an L2.
 __device__ inline int64_t xcd_logical_block() {
@@ -296,6 +304,7 @@ struct GemmGeom {
   int64_t a_sb, a_sm, a_sk, b_sb, b_sk, b_sn, c_sb, c_sm, c_sn;
   int64_t a_elems, b_elems, c_elems;
   int64_t mblocks, nblocks;
+  int32_t out_bf16;  // output tiles in bf16 (else fp32)
 };
 
 // LDS placement of a [rows][BK] operand chunk in 16-byte chunks of VEC
@@ -432,7 +441,7 @@ __device__ inline PairTiles load_pair(const PairSrc &s, int64_t q) {
 template <typename T, int BM, int BN, int BK, bool A_DIRECT, bool B_DIRECT>
 __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
                                                         const T *__restrict__ B,
-                                                        float *__restrict__ C, PairSrc src,
+                                                        void *__restrict__ C, PairSrc src,
                                                         GemmGeom g) {
   using SA = OperandStage<T, BM, BK, A_DIRECT>;
   using SB = OperandStage<T, BN, BK, B_DIRECT>;
@@ -544,17 +553,21 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
     __syncthreads();
   }
 
-  float *cb = C + seg * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+  const int64_t c0 = seg * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+  auto store = [&](auto *cb) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = wm * WM + i * 16 + (lane >> 4) * 4 + r;
-        const int col = wn * WN + j * 16 + (lane & 15);
-        cb[row * g.c_sm + col * g.c_sn] = acc[i][j][r];
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm * WM + i * 16 + (lane >> 4) * 4 + r;
+          const int col = wn * WN + j * 16 + (lane & 15);
+          put_out(cb + row * g.c_sm + col * g.c_sn, acc[i][j][r]);
+        }
+  };
+  if (g.out_bf16) store(static_cast<uint16_t *>(C) + c0);
+  else store(static_cast<float *>(C) + c0);
 }
 
 // ---------------------------------------------------------------------------
@@ -683,7 +696,7 @@ __device__ inline int swz_b(int krow) {
 template <int BM, int BN, int BK, int NS>
 __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__restrict__ A,
                                                             const uint16_t *__restrict__ B,
-                                                            float *__restrict__ C, PairSrc src,
+                                                            void *__restrict__ C, PairSrc src,
                                                             GemmGeom g) {
 #if defined(__HIP_DEVICE_COMPILE__)  // device-only body (LDS address-space casts, gfx950 asm)
   constexpr int A_ROWB = BK * 2;               // bytes per A row of a stage
@@ -818,17 +831,21 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
     }
   }
 
-  float *cb = C + seg * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+  const int64_t c0 = seg * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+  auto store = [&](auto *cb) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = wm * WM + i * 16 + (lane >> 4) * 4 + r;
-        const int col = wn * WN + j * 16 + (lane & 15);
-        cb[row * g.c_sm + col * g.c_sn] = acc[i][j][r];
-      }
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm * WM + i * 16 + (lane >> 4) * 4 + r;
+          const int col = wn * WN + j * 16 + (lane & 15);
+          put_out(cb + row * g.c_sm + col * g.c_sn, acc[i][j][r]);
+        }
+  };
+  if (g.out_bf16) store(static_cast<uint16_t *>(C) + c0);
+  else store(static_cast<float *>(C) + c0);
 #endif
 }
 
@@ -983,7 +1000,7 @@ struct SegOpF32 {
 template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
 __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
                                                            const typename Op::elem *__restrict__ B,
-                                                           float *__restrict__ C, PairSrc src,
+                                                           void *__restrict__ C, PairSrc src,
                                                            GemmGeom g, int64_t n_seg, int spw,
                                                            int mb_loop) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1198,16 +1215,20 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
   // fewer, wider stores after an in-quad transpose.)
   const uint32_t row0 = static_cast<uint32_t>(wm * WM + (lane >> 4) * 4);
   const uint32_t col0 = static_cast<uint32_t>(wcol + (lane & 15));
-  auto block_ptr = [&](int sseg, int64_t mb) -> float * {
-    return C + (seg0 + sseg) * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
+  auto block_off = [&](int sseg, int64_t mb) -> int64_t {  // in elements
+    return (seg0 + sseg) * g.c_elems + bi * g.c_sb + mb * BM * g.c_sm + nb * BN * g.c_sn;
   };
   auto store_zero = [&](int sseg, int64_t mb) {
     if (sseg >= nls) return;
-    float *cb = block_ptr(sseg, mb);
-    for (int i = 0; i < FM; ++i)
-      for (int j = 0; j < FN; ++j)
-        for (int r = 0; r < 4; ++r)
-          cb[(row0 + i * 16 + r) * g.c_sm + (col0 + j * 16) * g.c_sn] = 0.f;
+    auto zero = [&](auto *cb) {
+      for (int i = 0; i < FM; ++i)
+        for (int j = 0; j < FN; ++j)
+          for (int r = 0; r < 4; ++r)
+            put_out(cb + (row0 + i * 16 + r) * g.c_sm + (col0 + j * 16) * g.c_sn, 0.f);
+    };
+    const int64_t c0 = block_off(sseg, mb);
+    if (g.out_bf16) zero(static_cast<uint16_t *>(C) + c0);
+    else zero(static_cast<float *>(C) + c0);
   };
 
 #pragma unroll
@@ -1300,19 +1321,23 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
     if (done) {
       const int sseg = G > 1 ? wseg : static_cast<int>(code & 0xFu);
       if (sseg < nls) {
-        float *cb = block_ptr(sseg, cmb);
         // Strides made opaque here, so that the store offsets are formed at
         // the store and not hoisted out of the stage loop into registers.
         int32_t csm = static_cast<int32_t>(g.c_sm), csn = static_cast<int32_t>(g.c_sn);
         asm volatile("" : "+s"(csm), "+s"(csn));
         const uint32_t o0 = row0 * csm + col0 * csn;
+        auto store = [&](auto *cb) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+          for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              cb[o0 + (i * 16 + r) * csm + j * 16 * csn] = acc[i][j][r];
+              for (int r = 0; r < 4; ++r)
+                put_out(cb + o0 + (i * 16 + r) * csm + j * 16 * csn, acc[i][j][r]);
+        };
+        const int64_t c0 = block_off(sseg, cmb);
+        if (g.out_bf16) store(static_cast<uint16_t *>(C) + c0);
+        else store(static_cast<float *>(C) + c0);
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -1326,17 +1351,21 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
   }
   if constexpr (!MULTI) {
     if (wseg < nls) {
-      float *cb = block_ptr(wseg, mb0);
+      auto store = [&](auto *cb) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+          for (int j = 0; j < FN; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t o = static_cast<uint32_t>((row0 + i * 16 + r) * g.c_sm +
-                                                     (col0 + j * 16) * g.c_sn);
-            cb[o] = acc[i][j][r];
-          }
+            for (int r = 0; r < 4; ++r) {
+              const uint32_t o = static_cast<uint32_t>((row0 + i * 16 + r) * g.c_sm +
+                                                       (col0 + j * 16) * g.c_sn);
+              put_out(cb + o, acc[i][j][r]);
+            }
+      };
+      const int64_t c0 = block_off(wseg, mb0);
+      if (g.out_bf16) store(static_cast<uint16_t *>(C) + c0);
+      else store(static_cast<float *>(C) + c0);
     }
     return;
   }
@@ -1365,12 +1394,13 @@ struct GenDesc {
   int64_t out_ext[EJ_MAX_LABELS], out_a[EJ_MAX_LABELS], out_b[EJ_MAX_LABELS];
   int64_t red_ext[EJ_MAX_LABELS], red_a[EJ_MAX_LABELS], red_b[EJ_MAX_LABELS];
   int64_t red_total, a_elems, b_elems, c_elems, eblocks;
+  int32_t out_bf16;
 };
 
 template <typename T>
 __global__ __launch_bounds__(256) void generic_einsum_kernel(const T *__restrict__ A,
                                                              const T *__restrict__ B,
-                                                             float *__restrict__ C, PairSrc src,
+                                                             void *__restrict__ C, PairSrc src,
                                                              GenDesc d) {
   const int64_t seg = blockIdx.x / d.eblocks;
   const int64_t e = (blockIdx.x % d.eblocks) * 256 + threadIdx.x;
@@ -1408,14 +1438,15 @@ __global__ __launch_bounds__(256) void generic_einsum_kernel(const T *__restrict
     }
     acc += pacc;
   }
-  C[seg * d.c_elems + e] = acc;
+  if (d.out_bf16) put_out(static_cast<uint16_t *>(C) + seg * d.c_elems + e, acc);
+  else put_out(static_cast<float *>(C) + seg * d.c_elems + e, acc);
 }
 
 // ---------------------------------------------------------------------------
 // Dispatch.
 
 template <typename T, int BM, int BN, int BK>
-int launch_gemm_layout(bool a_direct, bool b_direct, const void *A, const void *B, float *C,
+int launch_gemm_layout(bool a_direct, bool b_direct, const void *A, const void *B, void *C,
                        const PairSrc &src, const GemmGeom &g, int64_t nblk, hipStream_t stream) {
   const T *a = static_cast<const T *>(A);
   const T *b = static_cast<const T *>(B);
@@ -1433,7 +1464,7 @@ int launch_gemm_layout(bool a_direct, bool b_direct, const void *A, const void *
 }
 
 template <typename T, int BK>
-int launch_gemm_bk(int bm, int bn, bool ad, bool bd, const void *A, const void *B, float *C,
+int launch_gemm_bk(int bm, int bn, bool ad, bool bd, const void *A, const void *B, void *C,
                    const PairSrc &src, const GemmGeom &g, int64_t nblk, hipStream_t s) {
 #define EJ_GEMM_CASE(M_, N_) \
   if (bm == M_ && bn == N_) return launch_gemm_layout<T, M_, N_, BK>(ad, bd, A, B, C, src, g, nblk, s);
@@ -1462,7 +1493,7 @@ constexpr int64_t kSegMinBlocks = 1024;
 constexpr int kSegMaxRun = 8;  // segments per workgroup when G == 1 (SMAX)
 
 template <class Op, int G, int WGM, int NW>
-int launch_seg_gemm_t(const void *A, const void *B, float *C, const PairSrc &src,
+int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src,
                       const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
   constexpr int NS = seg_ring_depth(Op::A_BYTES + G * Op::B_BYTES, EJ_SEG_NS);
   const int64_t groups = ceil_div(n_seg, G);
@@ -1494,7 +1525,7 @@ int launch_seg_gemm_t(const void *A, const void *B, float *C, const PairSrc &src
 
 // bf16: 128 x 128 tiles, a group of 4 on 8 waves (2 x 4, one segment per wave
 // column) or one segment on 4 waves (2 x 2); 64 x 64 tiles on 4 waves.
-int launch_seg_gemm_bf16(int bm, int grp, const void *A, const void *B, float *C,
+int launch_seg_gemm_bf16(int bm, int grp, const void *A, const void *B, void *C,
                          const PairSrc &src, const GemmGeom &g, int64_t n_seg,
                          hipStream_t stream) {
   if (bm == 128) {
@@ -1507,7 +1538,7 @@ int launch_seg_gemm_bf16(int bm, int grp, const void *A, const void *B, float *C
 
 // fp32 on 4 waves: a group of 4 puts one segment on each wave (WGM = 1);
 // one segment splits the tile into wave tiles of at least 16 x 16.
-int launch_seg_gemm_f32(int bm, int bn, int grp, const void *A, const void *B, float *C,
+int launch_seg_gemm_f32(int bm, int bn, int grp, const void *A, const void *B, void *C,
                         const PairSrc &src, const GemmGeom &g, int64_t n_seg,
                         hipStream_t stream) {
 #define EJ_F32_CASE(M_, N_, WGM1_)                                                             \
@@ -1528,7 +1559,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Chooses the MFMA path when the einsum is GEMM-shaped with tile-friendly
 // extents and 16-byte aligned operand rows; returns false to fall back.
-bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B, float *C,
+bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B, void *C,
               const PairSrc &src, int64_t n_seg, hipStream_t stream, int *status) {
   if (!d->is_gemm) return false;
   const int esz = dtype == EJ_BF16 ? 2 : 4;
@@ -1557,6 +1588,7 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
   g.a_elems = d->a_elems; g.b_elems = d->b_elems; g.c_elems = d->c_elems;
   g.mblocks = d->m / bm;
   g.nblocks = d->n / bn;
+  g.out_bf16 = d->out_dtype == EJ_BF16;
   const int64_t nblk = n_seg * g.batch * g.mblocks * g.nblocks;
   if (nblk >= (int64_t(1) << 32)) return false;
   // bf16, k-contiguous lhs, n-contiguous rhs: the LDS-ring kernels (direct
@@ -1611,7 +1643,7 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
   return true;
 }
 
-int run_generic(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B, float *C,
+int run_generic(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B, void *C,
                 const PairSrc &src, int64_t n_seg, hipStream_t stream) {
   GenDesc g;
   memset(&g, 0, sizeof(g));
@@ -1633,6 +1665,7 @@ int run_generic(const ej_einsum_desc *d, int32_t dtype, const void *A, const voi
   g.b_elems = d->b_elems;
   g.c_elems = d->c_elems;
   g.eblocks = ceil_div(d->c_elems, 256);
+  g.out_bf16 = d->out_dtype == EJ_BF16;
   const int64_t nblk = n_seg * g.eblocks;
   if (nblk >= (int64_t(1) << 32)) {
     set_error("einsum launch too large");
@@ -1684,9 +1717,12 @@ int check_desc(const ej_einsum_desc *d) {
 }
 
 int einsum_common(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B,
-                  const PairSrc &src, int64_t n_seg, float *C, hipStream_t stream) {
+                  const PairSrc &src, int64_t n_seg, void *C, hipStream_t stream) {
   EJ_CHECK_ARG(d, "desc is null");
   EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(d->out_dtype == EJ_F32 || (d->out_dtype == EJ_BF16 && dtype == EJ_BF16),
+               "output dtype %d with operand dtype %d: outputs are fp32, or bf16 for bf16 "
+               "operands", d->out_dtype, dtype);
   EJ_CHECK_ARG(n_seg >= 0, "negative count");
   EJ_CHECK_ARG(d->n_out >= 0 && d->n_out <= EJ_MAX_LABELS && d->n_red >= 0 &&
                    d->n_red <= EJ_MAX_LABELS && d->c_elems >= 1 && d->a_elems >= 1 &&
@@ -1723,19 +1759,53 @@ __global__ __launch_bounds__(256) void segment_sum_vec4_kernel(const float4 *__r
   out[seg * tile_vecs + e] = acc;
 }
 
-__global__ __launch_bounds__(256) void segment_sum_scalar_kernel(const float *__restrict__ vals,
+// bf16 pair values, 8 per thread (one 16-byte load); fp32 sums, rounded
+// to bf16 once.
+__global__ __launch_bounds__(256) void segment_sum_bf16x8_kernel(const uint4 *__restrict__ vals,
+                                                                 int64_t tile_vecs,
+                                                                 const int32_t *perm,
+                                                                 const int32_t *off,
+                                                                 int64_t eblocks,
+                                                                 uint4 *__restrict__ out) {
+  const int64_t seg = blockIdx.x / eblocks;
+  const int64_t e = (blockIdx.x % eblocks) * 256 + threadIdx.x;
+  if (e >= tile_vecs) return;
+  const int32_t q0 = off[seg], q1 = off[seg + 1];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int32_t q = q0; q < q1; ++q) {
+    const uint4 v = vals[static_cast<int64_t>(perm[q]) * tile_vecs + e];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      acc[2 * h] += __uint_as_float(w[h] << 16);
+      acc[2 * h + 1] += __uint_as_float(w[h] & 0xFFFF0000u);
+    }
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    uint16_t lo, hi;
+    put_out(&lo, acc[2 * h]);
+    put_out(&hi, acc[2 * h + 1]);
+    w[h] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+  }
+  out[seg * tile_vecs + e] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void segment_sum_scalar_kernel(const T *__restrict__ vals,
                                                                  int64_t tile_elems,
                                                                  const int32_t *perm,
                                                                  const int32_t *off,
                                                                  int64_t eblocks,
-                                                                 float *__restrict__ out) {
+                                                                 T *__restrict__ out) {
   const int64_t seg = blockIdx.x / eblocks;
   const int64_t e = (blockIdx.x % eblocks) * 256 + threadIdx.x;
   if (e >= tile_elems) return;
   float acc = 0.f;
   for (int32_t q = off[seg]; q < off[seg + 1]; ++q)
-    acc += vals[static_cast<int64_t>(perm[q]) * tile_elems + e];
-  out[seg * tile_elems + e] = acc;
+    acc += to_f32(vals[static_cast<int64_t>(perm[q]) * tile_elems + e]);
+  put_out(out + seg * tile_elems + e, acc);
 }
 
 template <typename V>
@@ -1766,7 +1836,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const V *__restrict__ vals,
 extern "C" int ej_pair_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                               const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                               const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
-                              float *out, ej_stream_t stream) {
+                              void *out, ej_stream_t stream) {
   clear_error();
   PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles, nullptr};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_pairs, out, as_stream(stream));
@@ -1776,7 +1846,7 @@ extern "C" int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, cons
                                  const void *rhs_values, int64_t n_lhs_tiles,
                                  int64_t n_rhs_tiles, const int64_t *lhs_idx,
                                  const int64_t *rhs_idx, const int32_t *perm,
-                                 const int32_t *seg_offsets, int64_t n_segments, float *out,
+                                 const int32_t *seg_offsets, int64_t n_segments, void *out,
                                  ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || n_segments == 0, "seg_offsets is null");
@@ -1791,7 +1861,7 @@ extern "C" int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype
                                        const int64_t *lhs_idx, const int64_t *rhs_idx,
                                        const int32_t *perm, const int32_t *seg_offsets,
                                        int64_t max_segments, const int64_t *n_segments_dev,
-                                       float *out, ej_stream_t stream) {
+                                       void *out, ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || max_segments == 0, "seg_offsets is null");
   EJ_CHECK_ARG(n_segments_dev, "n_segments_dev is null");
@@ -1800,23 +1870,42 @@ extern "C" int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype
                        as_stream(stream));
 }
 
-extern "C" int ej_segment_sum(const float *pair_values, int64_t tile_elems, const int32_t *perm,
-                              const int32_t *seg_offsets, int64_t n_segments, float *out,
-                              ej_stream_t stream_) {
+extern "C" int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t tile_elems,
+                              const int32_t *perm, const int32_t *seg_offsets,
+                              int64_t n_segments, void *out, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
   EJ_CHECK_ARG(tile_elems >= 1 && n_segments >= 0, "bad sizes");
   if (n_segments == 0) return EJ_OK;
   EJ_CHECK_ARG(pair_values && perm && seg_offsets && out, "null pointer argument");
-  if (tile_elems % 4 == 0 && aligned16(pair_values) && aligned16(out)) {
+  if (n_segments * ceil_div(tile_elems, 256) >= (int64_t(1) << 32)) {
+    set_error("segment sum launch too large");
+    return EJ_E_UNSUPPORTED;
+  }
+  const bool vec = aligned16(pair_values) && aligned16(out);
+  if (dtype == EJ_F32 && vec && tile_elems % 4 == 0) {
     const int64_t tv = tile_elems / 4, eb = ceil_div(tv, 256);
     hipLaunchKernelGGL(segment_sum_vec4_kernel, dim3(static_cast<unsigned>(n_segments * eb)),
-                       dim3(256), 0, stream, reinterpret_cast<const float4 *>(pair_values), tv,
-                       perm, seg_offsets, eb, reinterpret_cast<float4 *>(out));
+                       dim3(256), 0, stream, static_cast<const float4 *>(pair_values), tv,
+                       perm, seg_offsets, eb, static_cast<float4 *>(out));
+  } else if (dtype == EJ_BF16 && vec && tile_elems % 8 == 0) {
+    const int64_t tv = tile_elems / 8, eb = ceil_div(tv, 256);
+    hipLaunchKernelGGL(segment_sum_bf16x8_kernel, dim3(static_cast<unsigned>(n_segments * eb)),
+                       dim3(256), 0, stream, static_cast<const uint4 *>(pair_values), tv,
+                       perm, seg_offsets, eb, static_cast<uint4 *>(out));
   } else {
     const int64_t eb = ceil_div(tile_elems, 256);
-    hipLaunchKernelGGL(segment_sum_scalar_kernel, dim3(static_cast<unsigned>(n_segments * eb)),
-                       dim3(256), 0, stream, pair_values, tile_elems, perm, seg_offsets, eb, out);
+    if (dtype == EJ_F32)
+      hipLaunchKernelGGL(segment_sum_scalar_kernel<float>,
+                         dim3(static_cast<unsigned>(n_segments * eb)), dim3(256), 0, stream,
+                         static_cast<const float *>(pair_values), tile_elems, perm, seg_offsets,
+                         eb, static_cast<float *>(out));
+    else
+      hipLaunchKernelGGL(segment_sum_scalar_kernel<uint16_t>,
+                         dim3(static_cast<unsigned>(n_segments * eb)), dim3(256), 0, stream,
+                         static_cast<const uint16_t *>(pair_values), tile_elems, perm,
+                         seg_offsets, eb, static_cast<uint16_t *>(out));
   }
   EJ_LAUNCH_CHECK();
   return EJ_OK;

@@ -55,10 +55,11 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t *__rest
     out[i] = __uint_as_float(static_cast<uint32_t>(in[i]) << 16);
 }
 
-__global__ void zero_f32_kernel(float *p, int64_t n) {
+template <typename T>
+__global__ void zero_kernel(T *p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    p[i] = 0.0f;
+    p[i] = T(0);
 }
 
 unsigned grid_capped(int64_t n) {
@@ -118,6 +119,14 @@ int split_terms(const char *ks, std::string *a, std::string *b, std::string *c) 
   return EJ_OK;
 }
 
+int check_dtypes(int32_t dtype, int32_t grad_dtype) {
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(grad_dtype == EJ_F32 || (grad_dtype == EJ_BF16 && dtype == EJ_BF16),
+               "gradient dtype %d with operand dtype %d: gradients are fp32, or bf16 for bf16 "
+               "operands", grad_dtype, dtype);
+  return EJ_OK;
+}
+
 struct VjpWs {
   int32_t *perm_l, *off_l, *perm_r, *off_r;
   float *lhs32, *rhs32;
@@ -125,15 +134,16 @@ struct VjpWs {
   size_t bytes;
 };
 
+// Widened operands are needed for bf16 operands under an fp32 cotangent.
 VjpWs carve_vjp(void *base, int64_t n_pairs, int64_t n_lhs, int64_t n_rhs, int64_t lhs_elems,
-                int64_t rhs_elems, int32_t dtype) {
+                int64_t rhs_elems, int32_t dtype, int32_t grad_dtype) {
   Carver c(base);
   VjpWs w{};
   w.perm_l = c.take<int32_t>(n_pairs);
   w.off_l = c.take<int32_t>(n_lhs + 1);
   w.perm_r = c.take<int32_t>(n_pairs);
   w.off_r = c.take<int32_t>(n_rhs + 1);
-  if (dtype == EJ_BF16) {
+  if (dtype == EJ_BF16 && grad_dtype == EJ_F32) {
     w.lhs32 = c.take<float>(n_lhs * lhs_elems);
     w.rhs32 = c.take<float>(n_rhs * rhs_elems);
   }
@@ -173,15 +183,16 @@ extern "C" int ej_index_plan(const int64_t *idx, int64_t n, int64_t n_targets, i
 extern "C" int ej_pair_einsum_vjp_workspace_size(int64_t n_pairs, int64_t n_lhs_tiles,
                                                  int64_t n_rhs_tiles, int64_t lhs_elems,
                                                  int64_t rhs_elems, int32_t dtype,
-                                                 size_t *bytes) {
+                                                 int32_t grad_dtype, size_t *bytes) {
   clear_error();
   EJ_CHECK_ARG(bytes, "bytes is null");
-  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_TRY(check_dtypes(dtype, grad_dtype));
   EJ_CHECK_ARG(n_pairs >= 0 && n_pairs <= INT32_MAX, "n_pairs outside [0, 2^31)");
   EJ_CHECK_ARG(n_lhs_tiles >= 0 && n_lhs_tiles < INT32_MAX && n_rhs_tiles >= 0 &&
                    n_rhs_tiles < INT32_MAX && lhs_elems >= 1 && rhs_elems >= 1,
                "bad sizes");
-  *bytes = carve_vjp(nullptr, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype).bytes;
+  *bytes = carve_vjp(nullptr, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype,
+                     grad_dtype).bytes;
   return EJ_OK;
 }
 
@@ -190,12 +201,12 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
                                   int32_t dtype, const void *lhs_values, int64_t n_lhs_tiles,
                                   const void *rhs_values, int64_t n_rhs_tiles,
                                   const int64_t *lhs_idx, const int64_t *rhs_idx,
-                                  int64_t n_pairs, const float *grad_out, float *grad_lhs,
-                                  float *grad_rhs, void *workspace, size_t workspace_bytes,
-                                  ej_stream_t stream_) {
+                                  int64_t n_pairs, int32_t grad_dtype, const void *grad_out,
+                                  void *grad_lhs, void *grad_rhs, void *workspace,
+                                  size_t workspace_bytes, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
-  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_TRY(check_dtypes(dtype, grad_dtype));
   EJ_CHECK_ARG(n_pairs >= 0 && n_pairs <= INT32_MAX, "n_pairs outside [0, 2^31)");
   EJ_CHECK_ARG(n_lhs_tiles >= 0 && n_lhs_tiles < INT32_MAX && n_rhs_tiles >= 0 &&
                    n_rhs_tiles < INT32_MAX,
@@ -231,7 +242,9 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
     }
   }
   if (!grad_lhs && !grad_rhs) return EJ_OK;
-  VjpWs w = carve_vjp(workspace, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype);
+  dl.out_dtype = dr.out_dtype = grad_dtype;
+  VjpWs w = carve_vjp(workspace, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype,
+                      grad_dtype);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
   EJ_CHECK_ARG(n_pairs == 0 || (grad_out && lhs_idx && rhs_idx), "null pointer argument");
@@ -239,9 +252,10 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
                    (!grad_rhs || n_lhs_tiles == 0 || lhs_values),
                "null operand values");
   const void *lhs_v = lhs_values, *rhs_v = rhs_values;
-  if (dtype == EJ_BF16) {
-    // The cotangent is fp32; the operands are widened to fp32 once so the
-    // gradient einsums run in fp32 throughout.
+  if (dtype == EJ_BF16 && grad_dtype == EJ_F32) {
+    // An fp32 cotangent with bf16 operands: the operands are widened to fp32
+    // once so the gradient einsums run in fp32 throughout.  (A bf16
+    // cotangent runs them on bf16 operands with fp32 sums.)
     if (grad_rhs && n_lhs_tiles > 0) {
       hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_capped(n_lhs_tiles * lhs_elems)),
                          dim3(kBlock), 0, stream, static_cast<const uint16_t *>(lhs_values),
@@ -257,25 +271,33 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
       rhs_v = w.rhs32;
     }
   }
+  // Operand dtype of the gradient einsums: the cotangent's.
+  const int32_t edt = grad_dtype;
+  auto zero = [&](void *p, int64_t n) -> int {
+    if (grad_dtype == EJ_BF16)
+      hipLaunchKernelGGL(zero_kernel<uint16_t>, dim3(grid_capped(n)), dim3(kBlock), 0, stream,
+                         static_cast<uint16_t *>(p), n);
+    else
+      hipLaunchKernelGGL(zero_kernel<float>, dim3(grid_capped(n)), dim3(kBlock), 0, stream,
+                         static_cast<float *>(p), n);
+    EJ_LAUNCH_CHECK();
+    return EJ_OK;
+  };
   if (grad_lhs && n_lhs_tiles > 0) {
     if (n_pairs == 0 || n_rhs_tiles == 0) {
-      hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_capped(n_lhs_tiles * lhs_elems)),
-                         dim3(kBlock), 0, stream, grad_lhs, n_lhs_tiles * lhs_elems);
-      EJ_LAUNCH_CHECK();
+      EJ_TRY(zero(grad_lhs, n_lhs_tiles * lhs_elems));
     } else {
       EJ_TRY(index_plan(lhs_idx, n_pairs, n_lhs_tiles, w.perm_l, w.off_l, w.plan, stream));
-      EJ_TRY(ej_segment_einsum(&dl, EJ_F32, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
+      EJ_TRY(ej_segment_einsum(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
                                rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, grad_lhs, stream_));
     }
   }
   if (grad_rhs && n_rhs_tiles > 0) {
     if (n_pairs == 0 || n_lhs_tiles == 0) {
-      hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_capped(n_rhs_tiles * rhs_elems)),
-                         dim3(kBlock), 0, stream, grad_rhs, n_rhs_tiles * rhs_elems);
-      EJ_LAUNCH_CHECK();
+      EJ_TRY(zero(grad_rhs, n_rhs_tiles * rhs_elems));
     } else {
       EJ_TRY(index_plan(rhs_idx, n_pairs, n_rhs_tiles, w.perm_r, w.off_r, w.plan, stream));
-      EJ_TRY(ej_segment_einsum(&dr, EJ_F32, lhs_v, grad_out, n_lhs_tiles, n_pairs, lhs_idx,
+      EJ_TRY(ej_segment_einsum(&dr, edt, lhs_v, grad_out, n_lhs_tiles, n_pairs, lhs_idx,
                                nullptr, w.perm_r, w.off_r, n_rhs_tiles, grad_rhs, stream_));
     }
   }

@@ -226,9 +226,10 @@ def _infer_output_tile_shape(kernel_string: str, lhs_tile_shape, rhs_tile_shape)
 
 
 def kernel_einsum(lhs_values, rhs_values, lhs_indices, rhs_indices, kernel_string: str):
-    """einsum(kernel_string) of every matched tile pair, float32
-    [P, *out_tile] (reference: sparse_dispatch.py:85-126).  No pairs gives
-    zeros of the lhs values' dtype."""
+    """einsum(kernel_string) of every matched tile pair, [P, *out_tile] of the
+    operands' dtype, as the reference's jnp.einsum returns (sparse_dispatch.py:
+    85-126): float32, or bfloat16 for bfloat16 tiles (summed in fp32 and
+    rounded once).  No pairs gives zeros of the lhs values' dtype."""
     host = _on_host(lhs_values, rhs_values, lhs_indices, rhs_indices)
     n = int(lhs_indices.shape[0]) if hasattr(lhs_indices, "shape") else len(lhs_indices)
     lt, rt = tuple(lhs_values.shape[1:]), tuple(rhs_values.shape[1:])
@@ -295,8 +296,9 @@ def _plan_from_coords(oc):
 def segment_sum(values, output_coords):
     """Sums the pair tiles of equal output coordinate (reference:
     sparse_dispatch.py:129-171).  Returns (unique_coords int32 [U, nd] in
-    ascending lexicographic order, aggregated float32 [U, *tile]); tiles are
-    added in pair order, as the reference does."""
+    ascending lexicographic order, aggregated [U, *tile] in the values' dtype,
+    float32 or bfloat16, as the reference keeps it, :165); tiles are added in
+    pair order, as the reference does, in fp32."""
     import torch
 
     host = _on_host(values, output_coords)
@@ -308,7 +310,7 @@ def segment_sum(values, output_coords):
         return (torch.zeros((0, nd), dtype=torch.int32, device=values.device),
                 torch.zeros((0, *tile), dtype=values.dtype, device=values.device))
     oc = _dev_coords(output_coords, output_coords.shape[1] if output_coords.ndim > 1 else 0)
-    vals = _dev(values, torch.float32)
+    vals = _dev_values(values)
     coords, offsets, perm, _ = _plan_from_coords(oc)
     agg = _device.segment_sum(vals, perm, offsets)
     return (_host(coords), _host(agg)) if host else (coords, agg)
@@ -317,7 +319,7 @@ def segment_sum(values, output_coords):
 # ---------------------------------------------------------------------------
 # End to end.
 
-def _empty_result(lhs, n_out, out_tile, output_shape, host):
+def _empty_result(lhs, n_out, out_tile, output_shape, host, out_dtype=None):
     import torch
 
     if host:
@@ -325,14 +327,15 @@ def _empty_result(lhs, n_out, out_tile, output_shape, host):
         return SparseTensorRelation(np.zeros((0, n_out), np.int32),
                                     np.zeros((0, *out_tile), dtype=dt), output_shape, out_tile)
     dev = _device.require_gpu()
+    dt = out_dtype or (lhs.values.dtype if _is_torch(lhs.values) else torch.float32)
     return SparseTensorRelation(torch.zeros((0, n_out), dtype=torch.int32, device=dev),
-                                torch.zeros((0, *out_tile), dtype=lhs.values.dtype, device=dev),
+                                torch.zeros((0, *out_tile), dtype=dt, device=dev),
                                 output_shape, out_tile)
 
 
 def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys,
                    kernel_string: str, agg_keys, output_shape=None, output_tile_shape=None, *,
-                   fused: bool = True) -> SparseTensorRelation:
+                   fused: bool = True, out_dtype=None) -> SparseTensorRelation:
     """Sparse tensor-relational einsum (reference: sparse_dispatch.py:226-297).
 
     join_keys: [(lhs_dim, rhs_dim)] contracted tile dims; kernel_string: the
@@ -342,7 +345,10 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     einsum and the segment sum as one kernel writing every output tile once;
     ``fused=False`` runs the reference's phase split (per-pair results, then
     the segment sum in pair order).  Returns coords int32 [U, nd] sorted and
-    float32 values [U, *output_tile_shape]."""
+    values [U, *output_tile_shape] summed in fp32, of dtype ``out_dtype``: by
+    default the operands' dtype, as in the reference (float32, or bfloat16
+    for bfloat16 tiles, rounded once from the fp32 sum); ``torch.float32``
+    keeps fp32 results for bfloat16 tiles."""
     if output_tile_shape is None:
         output_tile_shape = _infer_output_tile_shape(kernel_string, lhs.tile_shape,
                                                      rhs.tile_shape)
@@ -384,7 +390,7 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
         if bound is not None and bound > 0:
             desc, a, b = operands()
             status, res = _device.queued_segment_einsum(lc, rc, keys, j_rad, agg, radices(None),
-                                                        desc, a, b, bound)
+                                                        desc, a, b, bound, out_dtype)
             if status == "ok":
                 queued = res
                 _pair_hints[hint_key] = res[0]
@@ -393,21 +399,21 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     if queued is not None:
         P, coords, offsets, perm, vals, li, ri = queued
         if P == 0:
-            return _empty_result(lhs, n_out, output_tile_shape, output_shape, host)
+            return _empty_result(lhs, n_out, output_tile_shape, output_shape, host, out_dtype)
     else:
         li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
         if hint_key is not None and _pair_hints.get(hint_key, 0) >= 0:
             _remember_pairs(hint_key, li.numel())
         if li.numel() == 0:
-            return _empty_result(lhs, n_out, output_tile_shape, output_shape, host)
+            return _empty_result(lhs, n_out, output_tile_shape, output_shape, host, out_dtype)
         cols = [((lc if s == 0 else rc), dim) for s, dim in agg]
         coords, offsets, perm, _ = _retry_radices(
             lambda r: _device.segment_plan(lc, rc, li, ri, agg, r), radices, cols)
         desc, a, b = operands()
         if fused:
-            vals = _device.segment_einsum(desc, a, b, li, ri, perm, offsets)
+            vals = _device.segment_einsum(desc, a, b, li, ri, perm, offsets, out_dtype)
         else:
-            pair_vals = _device.pair_einsum(desc, a, b, li, ri)
+            pair_vals = _device.pair_einsum(desc, a, b, li, ri, out_dtype=out_dtype)
             vals = _device.segment_sum(pair_vals, perm, offsets)
     if coords.shape[1] != n_out:
         import torch

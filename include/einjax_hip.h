@@ -57,9 +57,12 @@
  *   - No global mutable state: calls on different streams with different
  *     workspaces may run concurrently.
  *   - Coordinates are int32, row-major [n, ncols].  Pair indices are int64,
- *     as the reference returns them.  Values are EJ_F32 or EJ_BF16; tile
- *     einsum results are always fp32 (the reference computes the per-pair
- *     einsum in float32, sparse_dispatch.py:125).
+ *     as the reference returns them.  Values are EJ_F32 or EJ_BF16.  Tile
+ *     einsums accumulate in fp32 and write fp32, or bf16 when the operands
+ *     are bf16 and the descriptor's out_dtype asks for it: the reference's
+ *     jnp.einsum returns the operands' dtype (sparse_dispatch.py:125) and its
+ *     segment sum keeps it (:165); here a bf16 result is rounded once, from
+ *     the finished fp32 sum.
  */
 #ifndef EINJAX_HIP_H
 #define EINJAX_HIP_H
@@ -71,7 +74,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 6
+#define EJ_ABI_VERSION 7
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -126,6 +129,10 @@ typedef struct ej_einsum_desc {
   int64_t a_sb, a_sm, a_sk;
   int64_t b_sb, b_sk, b_sn;
   int64_t c_sb, c_sm, c_sn;
+  /* Output dtype, set by the caller (ej_einsum_describe writes EJ_F32):
+   * EJ_F32, or EJ_BF16 with bf16 operands (fp32 sums rounded once). */
+  int32_t out_dtype;
+  int32_t reserved;
 } ej_einsum_desc;
 
 /* ---- diagnostics ------------------------------------------------------- */
@@ -255,19 +262,20 @@ int ej_gather_tiles(const void *values, int64_t n_tiles, int64_t tile_bytes, con
  * caller cleared, runs on the generic strided kernel.  A pair whose tile
  * index lies outside [0, n_*_tiles) contributes nothing.
  * Per-pair mode: out[p] = einsum(lhs_values[lhs_idx[p]], rhs_values[rhs_idx[p]])
- * for p < n_pairs, fp32 [n_pairs, c_elems].  lhs_idx / rhs_idx may be NULL,
- * meaning pair p reads tile p (a gathered panel). */
+ * for p < n_pairs, [n_pairs, c_elems] of desc->out_dtype.  lhs_idx / rhs_idx
+ * may be NULL, meaning pair p reads tile p (a gathered panel). */
 int ej_pair_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                    const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
-                   const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs, float *out,
+                   const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs, void *out,
                    ej_stream_t stream);
 /* Fused mode (gather + einsum + segment sum): out[u] = sum over the pairs
- * of segment u, in plan order, of the per-pair einsum; fp32
- * [n_segments, c_elems], each output tile written once, no atomics. */
+ * of segment u, in plan order, of the per-pair einsum, formed in fp32;
+ * [n_segments, c_elems] of desc->out_dtype, each output tile written once,
+ * no atomics. */
 int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                       const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                       const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
-                      const int32_t *seg_offsets, int64_t n_segments, float *out,
+                      const int32_t *seg_offsets, int64_t n_segments, void *out,
                       ej_stream_t stream);
 
 /* ej_segment_einsum with the segment count read on the device from
@@ -280,14 +288,16 @@ int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const voi
                             const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                             const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
                             const int32_t *seg_offsets, int64_t max_segments,
-                            const int64_t *n_segments_dev, float *out, ej_stream_t stream);
+                            const int64_t *n_segments_dev, void *out, ej_stream_t stream);
 
 /* ---- segment sum (reference: segment_sum accumulation, :164-171) -------- */
 /* out[u] = sum_{q in [seg_offsets[u], seg_offsets[u+1])} pair_values[perm[q]],
- * added sequentially in q order in fp32 (the reference's order and dtype). */
-int ej_segment_sum(const float *pair_values, int64_t tile_elems, const int32_t *perm,
-                   const int32_t *seg_offsets, int64_t n_segments, float *out,
-                   ej_stream_t stream);
+ * added sequentially in q order (the reference's order).  pair_values and out
+ * are both of dtype (EJ_F32 or EJ_BF16, the reference keeps the values' dtype,
+ * :165); the sums are formed in fp32 and a bf16 output is rounded once. */
+int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t tile_elems,
+                   const int32_t *perm, const int32_t *seg_offsets, int64_t n_segments,
+                   void *out, ej_stream_t stream);
 
 /* ---- tiling (reference: SparseTensor.to_relation, tensor/sparse.py:160-219) */
 /* Dense row-major input of rank ndim.  A tile is kept iff it holds an element
@@ -389,29 +399,32 @@ int ej_index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *per
                   int32_t *offsets, void *workspace, size_t workspace_bytes, ej_stream_t stream);
 
 /* Gradients of out[p] = einsum(kernel_string, lhs_values[lhs_idx[p]],
- * rhs_values[rhs_idx[p]]) for the fp32 cotangent grad_out [n_pairs,
- * *out_tile]:
+ * rhs_values[rhs_idx[p]]) for the cotangent grad_out [n_pairs, *out_tile]:
  *   grad_lhs[l] = sum_{p: lhs_idx[p] == l} einsum("C,B->A", grad_out[p], rhs_values[rhs_idx[p]])
  *   grad_rhs[r] = sum_{p: rhs_idx[p] == r} einsum("A,C->B", lhs_values[lhs_idx[p]], grad_out[p])
  * for kernel_string "A,B->C" (the reference's reversed strings,
- * custom_vjp.py:31-62).  grad_lhs fp32 [n_lhs_tiles, *lhs_tile] and grad_rhs
- * fp32 [n_rhs_tiles, *rhs_tile] are fully written (zeros where no pair
+ * custom_vjp.py:31-62).  grad_lhs [n_lhs_tiles, *lhs_tile] and grad_rhs
+ * [n_rhs_tiles, *rhs_tile] are fully written (zeros where no pair
  * contributes); either may be NULL to skip it.  Each gradient tile is summed
- * in ascending pair order, without atomics, so results are reproducible.  A
- * pair whose index lies outside its operand's tile count contributes
- * nothing.  A reversed string that is not a valid einsum of its operands (a
- * label of A found in neither C nor B) gives EJ_E_INVAL, as the reference's
- * jnp.einsum raises.  dtype (EJ_F32 / EJ_BF16) is the dtype of the operand
- * values; bf16 operands are widened to fp32 in the workspace. */
+ * in fp32 in ascending pair order, without atomics, so results are
+ * reproducible.  A pair whose index lies outside its operand's tile count
+ * contributes nothing.  A reversed string that is not a valid einsum of its
+ * operands (a label of A found in neither C nor B) gives EJ_E_INVAL, as the
+ * reference's jnp.einsum raises.  dtype (EJ_F32 / EJ_BF16) is the dtype of
+ * the operand values; grad_dtype that of grad_out, grad_lhs and grad_rhs:
+ * EJ_F32 (bf16 operands are then widened to fp32 in the workspace), or
+ * EJ_BF16 with bf16 operands (the reference's dtype for bf16 values: the
+ * einsums run on bf16 operands and each gradient is rounded once). */
 int ej_pair_einsum_vjp_workspace_size(int64_t n_pairs, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                                       int64_t lhs_elems, int64_t rhs_elems, int32_t dtype,
-                                      size_t *bytes);
+                                      int32_t grad_dtype, size_t *bytes);
 int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_tile, int32_t lhs_ndim,
                        const int64_t *rhs_tile, int32_t rhs_ndim, int32_t dtype,
                        const void *lhs_values, int64_t n_lhs_tiles, const void *rhs_values,
                        int64_t n_rhs_tiles, const int64_t *lhs_idx, const int64_t *rhs_idx,
-                       int64_t n_pairs, const float *grad_out, float *grad_lhs, float *grad_rhs,
-                       void *workspace, size_t workspace_bytes, ej_stream_t stream);
+                       int64_t n_pairs, int32_t grad_dtype, const void *grad_out,
+                       void *grad_lhs, void *grad_rhs, void *workspace, size_t workspace_bytes,
+                       ej_stream_t stream);
 
 /* ---- relation to dense (reference: SparseTensorRelation.to_dense, :75-90) */
 /* Writes every tile of the relation into `dense` (row-major `shape`, fp32 or

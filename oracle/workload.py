@@ -39,9 +39,11 @@ def bytes_gather(n_pairs, lhs_tile, rhs_tile, elem_bytes) -> float:
     return 2.0 * n_pairs * (prod(lhs_tile) + prod(rhs_tile)) * elem_bytes
 
 
-def bytes_segsum(n_pairs, n_segments, out_tile, out_ndim) -> float:
+def bytes_segsum(n_pairs, n_segments, out_tile, out_ndim, out_bytes=4) -> float:
+    """Pair tiles read, output tiles and int32 coordinates written; out_bytes
+    per value (4 fp32, 2 bf16: results keep the operands' dtype)."""
     t = prod(out_tile)
-    return 4.0 * n_pairs * t + 4.0 * n_segments * t + 4.0 * n_segments * out_ndim
+    return out_bytes * (float(n_pairs) * t + float(n_segments) * t) + 4.0 * n_segments * out_ndim
 
 
 def bytes_bucket(dense_elems, n_tiles, tile, elem_bytes, ndim) -> float:
@@ -49,6 +51,8 @@ def bytes_bucket(dense_elems, n_tiles, tile, elem_bytes, ndim) -> float:
 
 
 def bytes_fused(n_lhs_used, n_rhs_used, lhs_tile, rhs_tile, elem_bytes, n_segments, out_tile,
-                out_ndim) -> float:
+                out_ndim, out_bytes=4) -> float:
+    """Every used operand tile read once, every output tile written once
+    (out_bytes per value) plus its int32 coordinates."""
     return (float(n_lhs_used) * prod(lhs_tile) + float(n_rhs_used) * prod(rhs_tile)) * elem_bytes \
-        + 4.0 * n_segments * prod(out_tile) + 4.0 * n_segments * out_ndim
+        + float(out_bytes) * n_segments * prod(out_tile) + 4.0 * n_segments * out_ndim

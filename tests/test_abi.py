@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 6
+    assert _lib.load().ej_version() == 7
 
 
 def describe(spec, lt, rt):
@@ -227,18 +227,48 @@ def test_backward_host_validation():
     lib = _lib.load()
     a = ctypes.c_size_t()
     assert lib.ej_index_plan_workspace_size(1000, ctypes.byref(a)) == 0 and a.value > 16000
-    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, _lib.EJ_BF16,
+    F32, BF16 = _lib.EJ_F32, _lib.EJ_BF16
+    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, BF16, F32,
                                                  ctypes.byref(a)) == 0
     bf = a.value
-    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, _lib.EJ_F32,
+    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, F32, F32,
                                                  ctypes.byref(a)) == 0
-    assert bf >= a.value + 4 * 64 * 20  # bf16 operands are widened in the workspace
+    assert bf >= a.value + 4 * 64 * 20  # bf16 operands under an fp32 cotangent are widened
+    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, BF16, BF16,
+                                                 ctypes.byref(a)) == 0
+    assert a.value < bf  # a bf16 cotangent needs no widened operands
+    # bf16 gradients need bf16 operands
+    assert lib.ej_pair_einsum_vjp_workspace_size(100, 10, 10, 64, 64, F32, BF16,
+                                                 ctypes.byref(a)) == _lib.EJ_E_INVAL
     t = i64_array([2, 2])
     fake = ctypes.c_void_p(16)
     # "ij,jk->k": the lhs gradient string "k,jk->ij" names i, found in no operand
-    st = lib.ej_pair_einsum_vjp(b"ij,jk->k", t, 2, t, 2, _lib.EJ_F32, fake, 1, fake, 1, fake,
-                                fake, 1, fake, fake, None, None, 0, None)
+    st = lib.ej_pair_einsum_vjp(b"ij,jk->k", t, 2, t, 2, F32, fake, 1, fake, 1, fake,
+                                fake, 1, F32, fake, fake, None, None, 0, None)
     assert st == _lib.EJ_E_INVAL and b"gradient string" in lib.ej_last_error()
-    st = lib.ej_pair_einsum_vjp(b"ij,jk", t, 2, t, 2, _lib.EJ_F32, fake, 1, fake, 1, fake,
-                                fake, 1, fake, fake, None, None, 0, None)
+    st = lib.ej_pair_einsum_vjp(b"ij,jk", t, 2, t, 2, F32, fake, 1, fake, 1, fake,
+                                fake, 1, F32, fake, fake, None, None, 0, None)
     assert st == _lib.EJ_E_INVAL
+    st = lib.ej_pair_einsum_vjp(b"ij,jk->ik", t, 2, t, 2, F32, fake, 1, fake, 1, fake,
+                                fake, 1, BF16, fake, fake, None, None, 0, None)
+    assert st == _lib.EJ_E_INVAL and b"gradient dtype" in lib.ej_last_error()
+
+
+def test_output_dtype_validation():
+    """Descriptors start with fp32 outputs; bf16 outputs need bf16 operands
+    (checked before any launch, so no GPU is needed)."""
+    lib = _lib.load()
+    st, d = describe("ij,jk->ik", (32, 32), (32, 32))
+    assert st == 0 and d.out_dtype == _lib.EJ_F32
+    d.out_dtype = _lib.EJ_BF16
+    fake = ctypes.c_void_p(16)
+    st = lib.ej_segment_einsum(ctypes.byref(d), _lib.EJ_F32, fake, fake, 1, 1, None, None, None,
+                               fake, 0, fake, None)
+    assert st == _lib.EJ_E_INVAL and b"output dtype" in lib.ej_last_error()
+    assert lib.ej_segment_einsum(ctypes.byref(d), _lib.EJ_BF16, fake, fake, 1, 1, None, None,
+                                 None, fake, 0, fake, None) == _lib.EJ_OK
+    d.out_dtype = 7
+    assert lib.ej_pair_einsum(ctypes.byref(d), _lib.EJ_BF16, fake, fake, 1, 1, None, None, 0,
+                              fake, None) == _lib.EJ_E_INVAL
+    assert lib.ej_segment_sum(fake, 5, 4, fake, fake, 0, fake, None) == _lib.EJ_E_INVAL
+    assert lib.ej_segment_sum(fake, _lib.EJ_BF16, 4, fake, fake, 0, fake, None) == _lib.EJ_OK

@@ -140,10 +140,14 @@ SPECS = [("ij,jk->ik", (32, 64), (64, 32)), ("ij,kj->ik", (16, 32), (48, 32)),
          ("ijk,kl->ijl", (8, 8, 32), (32, 16)), ("ij,jk->ik", (128, 128), (128, 128))]
 
 
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "bf16-bf16"])
 @pytest.mark.parametrize("spec,lt,rt", SPECS)
 def test_vjp_parity(gpu, dtype, spec, lt, rt):
+    """dtype: operand values' dtype; "bf16-bf16" also hands in a bf16
+    cotangent (bf16 gradient einsums), the others an fp32 one."""
     note("vjp", dtype, spec, lt, rt)
+    g_bf16 = dtype == "bf16-bf16"
+    dtype = "bf16" if g_bf16 else dtype
     rng = np.random.default_rng(len(spec) + lt[0])
     nl, nr, P = 13, 9, 60
     L = rng.standard_normal((nl, *lt)).astype(np.float32)
@@ -154,11 +158,15 @@ def test_vjp_parity(gpu, dtype, spec, lt, rt):
     ri = rng.integers(0, nr, P)
     out_shape = R.kernel_einsum(L, Rv, li, ri, spec, precision="fp64").shape
     g = rng.standard_normal(out_shape).astype(np.float32)
+    if g_bf16:
+        g = R.bf16_round(g)
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     lv = torch.from_numpy(L).cuda().to(tdt)
     rv = torch.from_numpy(Rv).cuda().to(tdt)
+    gt = torch.from_numpy(g).cuda()
     gl, gr = ej.sparse_einsum_raw_vjp(lv, rv, torch.from_numpy(li).cuda(),
-                                      torch.from_numpy(ri).cuda(), spec, torch.from_numpy(g).cuda())
+                                      torch.from_numpy(ri).cuda(), spec,
+                                      gt.to(torch.bfloat16) if g_bf16 else gt)
     assert gl.dtype == tdt and gr.dtype == tdt
     wl, wr = R.pair_einsum_vjp(L, Rv, li, ri, spec, g)
     tol = 1e-5 if dtype == "fp32" else 1e-2
@@ -176,9 +184,10 @@ def test_vjp_through_autograd_bf16_and_determinism(gpu):
     lv = torch.from_numpy(L).cuda().to(torch.bfloat16).requires_grad_()
     rv = torch.from_numpy(Rv).cuda().to(torch.bfloat16).requires_grad_()
     out = ej.sparse_einsum_raw(lv, rv, None, None, li, ri, "ij,jk->ik")
-    assert out.dtype == torch.float32
-    W = torch.from_numpy(rng.standard_normal(tuple(out.shape)).astype(np.float32)).cuda()
-    (out * W).sum().backward()
+    assert out.dtype == torch.bfloat16  # the values' dtype, as jnp.einsum returns
+    W = torch.from_numpy(R.bf16_round(rng.standard_normal(tuple(out.shape)).astype(
+        np.float32))).cuda()
+    (out * W.to(torch.bfloat16)).sum().backward()  # cotangent W, in bf16
     assert lv.grad.dtype == torch.bfloat16 and rv.grad.dtype == torch.bfloat16
     wl, wr = R.pair_einsum_vjp(L, Rv, li, ri, "ij,jk->ik", W.cpu().numpy())
     assert rel_l2(lv.grad.float().cpu().numpy(), wl) <= 1e-2
@@ -243,10 +252,11 @@ def test_vjp_blocksparse_16k_adjoint_and_rows(gpu):
     dL = torch.randn(lv.shape, generator=gen, device="cuda").to(torch.bfloat16)
     dR = torch.randn(rv.shape, generator=gen, device="cuda").to(torch.bfloat16)
     desc = D.describe("ij,jk->ik", (128, 128), (128, 128))
-    lhs_side = (g.double() * D.pair_einsum(desc, dL, rv, li, ri).double()).sum().item()
+    f32 = torch.float32
+    lhs_side = (g.double() * D.pair_einsum(desc, dL, rv, li, ri, out_dtype=f32).double()).sum().item()
     rhs_side = (gl32.double() * dL.double()).sum().item()
     assert abs(lhs_side - rhs_side) <= 1e-4 * max(abs(lhs_side), 1.0)
-    lhs_side = (g.double() * D.pair_einsum(desc, lv, dR, li, ri).double()).sum().item()
+    lhs_side = (g.double() * D.pair_einsum(desc, lv, dR, li, ri, out_dtype=f32).double()).sum().item()
     rhs_side = (gr32.double() * dR.double()).sum().item()
     assert abs(lhs_side - rhs_side) <= 1e-4 * max(abs(lhs_side), 1.0)
     # a few tiles against the oracle, from their own pairs
@@ -263,3 +273,11 @@ def test_vjp_blocksparse_16k_adjoint_and_rows(gpu):
         for p in sel:
             want += lv[li_h[p]].double().cpu().numpy().T @ g[p].double().cpu().numpy()
         assert rel_l2(gr32[r].cpu().numpy(), want) <= 1e-5
+    # the bf16 cotangent path (bf16 gradient einsums, fp32 sums, one rounding)
+    # against the fp32 path on the same rounded cotangent
+    g16 = g.to(torch.bfloat16)
+    gl16, gr16 = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g16)
+    assert gl16.dtype == torch.bfloat16 and gr16.dtype == torch.bfloat16
+    gl32b, gr32b = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g16.float())
+    assert rel_l2(gl16.float().cpu().numpy(), gl32b.cpu().numpy()) <= 4e-3
+    assert rel_l2(gr16.float().cpu().numpy(), gr32b.cpu().numpy()) <= 4e-3

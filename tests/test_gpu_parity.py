@@ -40,6 +40,11 @@ def host_rel(r: R.Rel):
     return SparseTensorRelation(r.coords, r.values, r.shape, r.tile_shape)
 
 
+def hv(t: torch.Tensor) -> np.ndarray:
+    """Device values (float32 or bfloat16) as a host float32 array."""
+    return t.float().cpu().numpy()
+
+
 # ---------------------------------------------------------------------------
 # joins
 
@@ -214,9 +219,9 @@ def test_pair_einsum(gpu, spec, lt, rt, dtype):
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     got = ej.kernel_einsum(torch.from_numpy(lv).cuda().to(tdt), torch.from_numpy(rv).cuda().to(tdt),
                            torch.from_numpy(li).cuda(), torch.from_numpy(ri).cuda(), spec)
-    assert got.dtype == torch.float32
+    assert got.dtype == tdt  # the operands' dtype, as jnp.einsum returns
     assert tuple(got.shape) == want.shape
-    err = R.rel_l2(got.cpu().numpy(), want)
+    err = R.rel_l2(hv(got), want)
     assert err <= TOL[dtype], err
 
 
@@ -243,8 +248,76 @@ def test_segment_einsum_matches_pairs_plus_segsum(gpu, spec, lt, rt, dtype):
                                  torch.from_numpy(rv).cuda().to(tdt),
                                  torch.from_numpy(li).cuda(), torch.from_numpy(ri).cuda(),
                                  torch.from_numpy(perm).cuda(), torch.from_numpy(off).cuda())
-    err = R.rel_l2(got.cpu().numpy(), want)
+    err = R.rel_l2(hv(got), want)
     assert err <= TOL[dtype], err
+
+
+def _same_bits(x: torch.Tensor, y: torch.Tensor) -> bool:
+    return x.dtype == y.dtype and x.shape == y.shape and torch.equal(
+        x.view(torch.int16), y.view(torch.int16))
+
+
+@pytest.mark.parametrize("spec,lt,rt", EINSUM_CASES)
+def test_bf16_output_is_rounded_fp32_output(gpu, spec, lt, rt):
+    """bf16 operands: the default bf16 output of every kernel (per pair,
+    fused segment sums, segment sum of bf16 pair values) is the fp32 output
+    of the same kernel rounded to nearest even, bit for bit: the sums are
+    formed in fp32 either way and rounded once."""
+    note("bf16 output", spec, lt, rt)
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(zlib.crc32(repr((spec, lt, rt, "bf16out")).encode()))
+    nl, nr, P = 9, 6, 60
+    c = lambda a: torch.from_numpy(a).cuda()
+    a = c(_rand_tiles(rng, nl, lt, "bf16")).to(torch.bfloat16)
+    b = c(_rand_tiles(rng, nr, rt, "bf16")).to(torch.bfloat16)
+    li, ri = c(rng.integers(0, nl, P)), c(rng.integers(0, nr, P))
+    oc = np.minimum(rng.zipf(1.6, size=(P, 1)) - 1, 11).astype(np.int32)
+    _, perm, off, _ = R.segment_plan(oc)
+    perm, off = c(perm), c(off)
+    desc = _device.describe(spec, lt, rt)
+    p16 = _device.pair_einsum(desc, a, b, li, ri)
+    p32 = _device.pair_einsum(desc, a, b, li, ri, out_dtype=torch.float32)
+    assert p16.dtype == torch.bfloat16 and p32.dtype == torch.float32
+    assert _same_bits(p16, p32.to(torch.bfloat16))
+    s16 = _device.segment_einsum(desc, a, b, li, ri, perm, off)
+    s32 = _device.segment_einsum(desc, a, b, li, ri, perm, off, out_dtype=torch.float32)
+    assert _same_bits(s16, s32.to(torch.bfloat16))
+    q16 = _device.segment_sum(p16, perm, off)
+    q32 = _device.segment_sum(p16.float(), perm, off)
+    assert _same_bits(q16, q32.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("lt,rt,n_seg", [((64, 32), (32, 64), 3000), ((128, 32), (32, 128), 2100)])
+def test_bf16_output_multi_segment_workgroups(gpu, lt, rt, n_seg):
+    """bf16 'ij,jk->ik' with K = 32 and thousands of segments: the ring kernel
+    runs several consecutive segments per workgroup and stores each output
+    block inside its stage loop; bf16 outputs there are the fp32 ones
+    rounded, and empty segments are zero."""
+    note("bf16 output, multi-segment workgroups", lt, rt, n_seg)
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(n_seg)
+    counts = rng.integers(0, 4, n_seg)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    P = int(off[-1])
+    c = lambda x: torch.from_numpy(x).cuda()
+    a = c(_rand_tiles(rng, 40, lt, "bf16")).to(torch.bfloat16)
+    b = c(_rand_tiles(rng, 30, rt, "bf16")).to(torch.bfloat16)
+    li, ri = c(rng.integers(0, 40, P)), c(rng.integers(0, 30, P))
+    perm = c(rng.permutation(P).astype(np.int32))
+    desc = _device.describe("ij,jk->ik", lt, rt)
+    s16 = _device.segment_einsum(desc, a, b, li, ri, perm, c(off))
+    s32 = _device.segment_einsum(desc, a, b, li, ri, perm, c(off), out_dtype=torch.float32)
+    assert _same_bits(s16, s32.to(torch.bfloat16))
+    assert torch.all(s16[c(counts == 0)] == 0)
+    want = np.zeros((n_seg, lt[0], rt[1]))
+    A, B = hv(a).astype(np.float64), hv(b).astype(np.float64)
+    lin, rin, pn = li.cpu().numpy(), ri.cpu().numpy(), perm.cpu().numpy()
+    for u in range(0, n_seg, 7):  # a sample of segments in float64
+        for q in range(off[u], off[u + 1]):
+            want[u] += A[lin[pn[q]]] @ B[rin[pn[q]]]
+    assert R.rel_l2(hv(s32)[::7], want[::7]) <= TOL["fp32"]
 
 
 def test_gemm_index_out_of_range_contributes_nothing(gpu):
@@ -298,8 +371,7 @@ def _segment_einsum_groups(lhs, rhs, groups, li_override=None):
     out = {}
     for gsz in groups:
         desc.seg_group = gsz
-        out[gsz] = _device.segment_einsum(desc, L.values, Rr.values, li, ri, perm,
-                                          offs).cpu().numpy()
+        out[gsz] = hv(_device.segment_einsum(desc, L.values, Rr.values, li, ri, perm, offs))
     return coords.cpu().numpy(), out
 
 
@@ -562,7 +634,8 @@ def test_workload_end_to_end(gpu, name, fused):
                             fused=fused)
     assert got.is_device
     npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
-    err = R.rel_l2(got.values.cpu().numpy(), want.values)
+    assert got.values.dtype == (torch.bfloat16 if w["dtype"] == "bf16" else torch.float32)
+    err = R.rel_l2(hv(got.values), want.values)
     assert err <= TOL[w["dtype"]], err
     # host inputs give host outputs with the same content
     if name == "blocksparse_1k" and fused:
@@ -601,7 +674,7 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
     exact = run()
     assert statuses == [] and len(sd._pair_hints) == 1
     key, P = next(iter(sd._pair_hints.items()))
-    ref_c, ref_v = exact.coords.cpu().numpy(), exact.values.cpu().numpy()
+    ref_c, ref_v = exact.coords.cpu().numpy(), hv(exact.values)
     want = R.execute_sparse(w["lhs"], w["rhs"], w["join_keys"], w["kernel_string"],
                             w["agg_keys"], precision="fp64")
     npt.assert_array_equal(ref_c, want.coords)
@@ -611,7 +684,7 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
         got = run()
         assert statuses[-1] == status, (bound, statuses)
         npt.assert_array_equal(got.coords.cpu().numpy(), ref_c)
-        npt.assert_array_equal(got.values.cpu().numpy(), ref_v)
+        npt.assert_array_equal(hv(got.values), ref_v)
         assert got.values.shape == exact.values.shape
         assert sd._pair_hints[key] == P
 
@@ -640,7 +713,7 @@ def test_queued_step_range_fallback(gpu, monkeypatch):
     for _ in range(3):
         got = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
         npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
-        assert R.rel_l2(got.values.cpu().numpy(), want.values) <= TOL[w["dtype"]]
+        assert R.rel_l2(hv(got.values), want.values) <= TOL[w["dtype"]]
     assert statuses == ["range"]
 
 
@@ -652,21 +725,27 @@ def _device_mod():
 
 def test_headline_workload_full_size(gpu):
     """16384^2 block-sparse (5%, 128^2 bf16 tiles) x dense 16384x4096 at full
-    size: coordinates bit-exact, a checksum of checksums (C @ x against
-    A @ (B @ x) in float64), fused == unfused, and a row-band subset
-    against the oracle's full result."""
+    size: coordinates bit-exact; the default bf16 output is the fp32 output
+    rounded; the fp32 output passes a checksum of checksums (C @ x against
+    A @ (B @ x) in float64), equals the unfused path's, and a row-band
+    subset matches the oracle's full result."""
     note("headline workload full size")
     w = G.workload_blocksparse_16k()
     L, Rr = w["lhs"], w["rhs"]
     lhs, rhs = dev_rel(L, "bf16"), dev_rel(Rr, "bf16")
-    fused = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
-    unfused = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"],
-                                fused=False)
+    args = (lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    fused = ej.execute_sparse(*args, out_dtype=torch.float32)
+    unfused = ej.execute_sparse(*args, fused=False, out_dtype=torch.float32)
+    fused16 = ej.execute_sparse(*args)
     torch.cuda.synchronize()
-    assert fused.num_tuples == 4096
+    assert fused.num_tuples == 4096 and fused16.values.dtype == torch.bfloat16
     npt.assert_array_equal(fused.coords.cpu().numpy(), unfused.coords.cpu().numpy())
-    fv, uv = fused.values.cpu().numpy(), unfused.values.cpu().numpy()
+    assert torch.equal(fused16.coords, fused.coords)
+    assert torch.equal(fused16.values.view(torch.int16),
+                       fused.values.to(torch.bfloat16).view(torch.int16))
+    fv, uv = hv(fused.values), hv(unfused.values)
     assert R.rel_l2(fv, uv) <= 1e-5
+    del unfused
     # checksum: C x == A (B x), float64 on the host
     rng = np.random.default_rng(9)
     x = rng.standard_normal(4096)
@@ -687,8 +766,8 @@ def test_headline_workload_full_size(gpu):
                             precision="fp64")
     rows = fused.coords.cpu().numpy()[:, 0] < 8
     npt.assert_array_equal(fused.coords.cpu().numpy()[rows], want.coords)
-    assert R.rel_l2(fv[rows], want.values) <= TOL["bf16"]
     assert R.rel_l2(fv[rows], want.values) <= 1e-5  # bf16 products are exact in fp32
+    assert R.rel_l2(hv(fused16.values)[rows], want.values) <= TOL["bf16"]
 
 
 def test_fused_is_deterministic(gpu):
