@@ -139,6 +139,154 @@ __global__ __launch_bounds__(kProbeThreads) void probe_scan_small_kernel(
   if (threadIdx.x == 0) *total = tot;
 }
 
+// The whole EJ_ORDER_PROBE count in one workgroup, for a build side (lhs) of
+// at most kJoinSmallBuild rows and a probe side of at most kProbeSmallMax:
+// the lhs keys are packed and stably radix-sorted in LDS (8-bit digits;
+// ranks inside a wave from ballot peer masks, across waves from per-digit
+// counts), the sorted permutation is written to lperm, every rhs row's equal
+// range is found by side-by-side branch-free searches, and the counts are
+// scanned into offs.  scalars[0] = P and scalars[1] = the out-of-range flag
+// are written outright, so nothing needs clearing first.  One launch replaces
+// the clear, pack, sort and probe launches of the general path.
+constexpr int kJoinSmallThreads = 1024;
+constexpr int kJoinSmallBuild = 4096;
+
+__global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
+    const int32_t *__restrict__ lc, int n_build, KeySpec lks, const int32_t *__restrict__ rc,
+    int64_t n_probe, KeySpec rks, int bits, int32_t *__restrict__ lperm,
+    int64_t *__restrict__ lo_out, int64_t *__restrict__ offs, int64_t *__restrict__ scalars) {
+  constexpr int NW = kJoinSmallThreads / 64;
+  __shared__ uint64_t skey[2][kJoinSmallBuild];
+  __shared__ int32_t sidx[2][kJoinSmallBuild];
+  __shared__ int32_t wcnt[NW][256];
+  __shared__ int32_t dbase[256];
+  __shared__ int bad_any;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  if (tid == 0) bad_any = 0;
+  __syncthreads();
+  int bad = 0;
+  for (int i = tid; i < n_build; i += kJoinSmallThreads) {
+    skey[0][i] = pack_key(lc + static_cast<int64_t>(i) * lks.ncols, lks, &bad);
+    sidx[0][i] = i;
+  }
+  if (bad) bad_any = 1;
+  int cur = 0;
+  for (int shift = 0; shift < bits; shift += 8) {
+    if (tid < 256) dbase[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < n_build; i += kJoinSmallThreads)
+      atomicAdd(&dbase[(skey[cur][i] >> shift) & 255], 1);
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the 256 digit counts, 4 per lane
+      int v[4], sum = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[u] = dbase[lane * 4 + u];
+        sum += v[u];
+      }
+      int inc = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+      }
+      int run = inc - sum;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        dbase[lane * 4 + u] = run;
+        run += v[u];
+      }
+    }
+    // Stable scatter, kJoinSmallThreads keys per round in index order.
+    for (int r0 = 0; r0 < n_build; r0 += kJoinSmallThreads) {
+      for (int x = tid; x < NW * 256; x += kJoinSmallThreads) (&wcnt[0][0])[x] = 0;
+      __syncthreads();
+      const int i = r0 + tid;
+      const bool valid = i < n_build;
+      const uint64_t k = valid ? skey[cur][i] : 0;
+      const int d = static_cast<int>((k >> shift) & 255);
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int bit = (d >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      const int rank = __popcll(peers & lt_mask);
+      if (valid && rank == 0) wcnt[wave][d] = __popcll(peers);
+      __syncthreads();
+      int total = 0;
+      if (tid < 256) {  // per digit: exclusive prefix over the waves, in place
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const int c = wcnt[w][tid];
+          wcnt[w][tid] = total;
+          total += c;
+        }
+      }
+      __syncthreads();
+      if (valid) {
+        const int pos = dbase[d] + wcnt[wave][d] + rank;
+        skey[cur ^ 1][pos] = k;
+        sidx[cur ^ 1][pos] = sidx[cur][i];
+      }
+      __syncthreads();
+      if (tid < 256) dbase[tid] += total;
+    }
+    cur ^= 1;
+  }
+  __syncthreads();
+  for (int i = tid; i < n_build; i += kJoinSmallThreads) lperm[i] = sidx[cur][i];
+  const uint64_t *bk = skey[cur];
+  const int64_t c = (n_probe + kJoinSmallThreads - 1) / kJoinSmallThreads;
+  const int64_t lo = min(n_probe, static_cast<int64_t>(tid) * c);
+  const int64_t hi = min(n_probe, lo + c);
+  int64_t s = 0;
+  for (int64_t j0 = lo; j0 < hi; j0 += kProbeBatch) {
+    uint64_t k[kProbeBatch];
+    int lb[kProbeBatch], ub[kProbeBatch];
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      k[u] = j0 + u < hi ? pack_key(rc + (j0 + u) * rks.ncols, rks, &bad) : 0;
+      lb[u] = 0;
+      ub[u] = 0;
+    }
+    // Invariant: the answer lies in [base, base + len]; base + len <= n_build.
+    for (int len = n_build; len > 1;) {
+      const int half = len >> 1;
+#pragma unroll
+      for (int u = 0; u < kProbeBatch; ++u) {
+        lb[u] += bk[lb[u] + half] < k[u] ? half : 0;
+        ub[u] += bk[ub[u] + half] <= k[u] ? half : 0;
+      }
+      len -= half;
+    }
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      lb[u] += bk[lb[u]] < k[u] ? 1 : 0;
+      ub[u] += bk[ub[u]] <= k[u] ? 1 : 0;
+      if (j0 + u < hi) {
+        lo_out[j0 + u] = lb[u];
+        offs[j0 + u] = ub[u] - lb[u];
+        s += ub[u] - lb[u];
+      }
+    }
+  }
+  if (bad) bad_any = 1;
+  int64_t tot;
+  int64_t run = block_exclusive_sum<kJoinSmallThreads>(s, &tot);
+  for (int64_t j = lo; j < hi; ++j) {
+    const int64_t v = offs[j];
+    offs[j] = run;
+    run += v;
+  }
+  if (tid == 0) {
+    scalars[0] = tot;
+    scalars[1] = bad_any;
+  }
+}
+
 // EJ_ORDER_PROBE fill: pair q belongs to rhs row j = owner_of(offs, q).
 __global__ void fill_probe_order_kernel(const int64_t *offs, int64_t n_rhs, const int64_t *lo,
                                         const int32_t *lhs_perm, int64_t n_pairs,
@@ -277,6 +425,13 @@ int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
   *dev_scalars = w.scalars;
+  if (order == EJ_ORDER_PROBE && n_lhs <= kJoinSmallBuild && n_rhs <= kProbeSmallMax) {
+    hipLaunchKernelGGL(join_probe_small_kernel, dim3(1), dim3(kJoinSmallThreads), 0, stream,
+                       lhs_coords, static_cast<int>(n_lhs), lks, rhs_coords, n_rhs, rks, bits,
+                       w.lperm, w.lo, w.offs, w.scalars);
+    EJ_LAUNCH_CHECK();
+    return EJ_OK;
+  }
 
   EJ_TRY(zero_async(w.scalars, 4 * sizeof(int64_t), stream));
   int *bad = reinterpret_cast<int *>(w.scalars + 1);

@@ -165,7 +165,10 @@ int scan_exclusive_i64(const int64_t *in, int64_t *out, int64_t n, int64_t *tota
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kMaxSortItems = 8;
-constexpr int64_t kInlineOffsetBlocks = 128;
+#ifndef EJ_INLINE_OFFSET_BLOCKS
+#define EJ_INLINE_OFFSET_BLOCKS 32
+#endif
+constexpr int64_t kInlineOffsetBlocks = EJ_INLINE_OFFSET_BLOCKS;
 static_assert(kRadix == kBlock, "one thread per digit in the scatter bookkeeping");
 
 template <int ITEMS>

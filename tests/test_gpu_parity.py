@@ -92,9 +92,10 @@ def test_join_and_plan_full_size(gpu, name):
 
 
 # Sizes straddling the sort's tile choices (1, 2, 4, 8 keys per thread; up
-# to 128 blocks with offsets read inline, more with a scanned histogram), the
-# two-launch scan limit (524288) and odd/even radix pass counts.
-PLAN_SIZES = [1, 2, 255, 257, 32768, 32769, 65537, 262145, 600000]
+# to 32 blocks with offsets read inline, more with a scanned histogram), the
+# one-workgroup flag scan (up to 65536 pairs), the two-launch scan limit
+# (524288) and odd/even radix pass counts.
+PLAN_SIZES = [1, 2, 255, 257, 8192, 8193, 16385, 32768, 32769, 65536, 65537, 262145, 600000]
 
 
 @pytest.mark.parametrize("P", PLAN_SIZES)
@@ -141,6 +142,68 @@ def test_join_sizes(gpu, n_lhs, n_rhs):
     sl_o, sr_o = R.coordinate_join_sorted(lc, rc, keys)
     npt.assert_array_equal(sl, sl_o)
     npt.assert_array_equal(sr, sr_o)
+
+
+@pytest.mark.parametrize("n_lhs,n_rhs,ncols", [(4096, 8192, 1), (4097, 8192, 1), (4096, 8193, 1),
+                                               (1000, 3000, 3), (50, 70, 3), (1, 8192, 1)])
+def test_join_probe_small_limits(gpu, n_lhs, n_rhs, ncols):
+    """Probe-order joins around the one-workgroup count (at most 4096 build
+    rows sorted in LDS, 8192 probe rows) with one or three key columns (one to
+    three 8-bit radix passes in LDS), bit-exact against the oracle."""
+    note("join probe small limits", n_lhs, n_rhs, ncols)
+    rng = np.random.default_rng(n_lhs * 3 + n_rhs + ncols)
+    if ncols == 1:
+        lc = rng.integers(0, 3000, (n_lhs, 4), dtype=np.int32)
+        rc = rng.integers(0, 3000, (n_rhs, 4), dtype=np.int32)
+        keys = [(1, 0)]
+    else:  # radix 3000 per column (35-bit keys, five passes), 64 distinct keys
+        vals = np.array([0, 7, 999, 2999], np.int32)
+        lc = rng.choice(vals, (n_lhs, 4))
+        rc = rng.choice(vals, (n_rhs, 4))
+        keys = [(1, 0), (2, 2), (3, 1)]
+    hl, hr = ej.coordinate_join_hash(lc, rc, keys)
+    li_o, ri_o = R.coordinate_join(lc, rc, keys)
+    assert len(li_o) > 0
+    npt.assert_array_equal(hl, li_o)
+    npt.assert_array_equal(hr, ri_o)
+
+
+@pytest.mark.parametrize("n_lhs,n_rhs", [(100, 200), (5000, 200), (100, 9000)])
+@pytest.mark.parametrize("side", ["lhs", "rhs"])
+def test_join_and_plan_range_flag(gpu, n_lhs, n_rhs, side):
+    """A key or output coordinate outside its declared radix is reported
+    (ValueError) by the one-workgroup and by the general count paths."""
+    note("join/plan range flag", n_lhs, n_rhs, side)
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(n_lhs + n_rhs)
+    lc = rng.integers(0, 10, (n_lhs, 2), dtype=np.int32)
+    rc = rng.integers(0, 10, (n_rhs, 2), dtype=np.int32)
+    t = lambda a: torch.from_numpy(a).cuda()
+    # join: a key coordinate of 10 on one side against a radix of 10
+    lb, rb = lc.copy(), rc.copy()
+    if side == "lhs":
+        lb[n_lhs // 2, 1] = 10
+    else:
+        rb[n_rhs // 2, 0] = 10
+    with pytest.raises(ValueError, match="outside"):
+        _device.join(t(lb), t(rb), [(1, 0)], [10])
+    li, ri = _device.join(t(lc), t(rc), [(1, 0)], [10])
+    assert li.numel() > 0
+    # plan: an output coordinate (a non-key column) of 10 against a radix of 10
+    if side == "lhs":
+        lc[int(li[li.numel() // 2]), 0] = 10
+    else:
+        rc[int(ri[ri.numel() // 2]), 1] = 10
+    agg = [(0, 0), (1, 1)]
+    with pytest.raises(ValueError, match="outside"):
+        _device.segment_plan(t(lc), t(rc), li, ri, agg, [10, 10])
+    coords, off, perm, seg = _device.segment_plan(t(lc), t(rc), li, ri, agg, [11, 11])
+    oc_o = R.compute_output_coords(lc, rc, li.cpu().numpy(), ri.cpu().numpy(), agg)
+    uc_o, perm_o, off_o, _ = R.segment_plan(oc_o)
+    npt.assert_array_equal(coords.cpu().numpy(), uc_o)
+    npt.assert_array_equal(off.cpu().numpy(), off_o)
+    npt.assert_array_equal(perm.cpu().numpy(), perm_o)
 
 
 def test_join_edge_cases(gpu):
