@@ -217,8 +217,9 @@ def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_off
 
 
 class _Counts(threading.local):
-    """Per-thread pinned count buffer [P, join range flag, U, plan range
-    flag] and the event that marks when the queued counts have landed."""
+    """Per-thread pinned count buffer (the counts of ej_pair_plan_async: U,
+    plan range flag, pairs planned, -, P, join range flag) and the event that
+    marks when the queued counts have landed."""
 
     buf: torch.Tensor | None = None
     event: torch.cuda.Event | None = None
@@ -229,7 +230,7 @@ _counts = _Counts()
 
 def _count_buffer() -> tuple[torch.Tensor, torch.cuda.Event]:
     if _counts.buf is None:
-        _counts.buf = torch.zeros(4, dtype=torch.int64, pin_memory=True)
+        _counts.buf = torch.zeros(8, dtype=torch.int64, pin_memory=True)
         _counts.event = torch.cuda.Event()
     return _counts.buf, _counts.event
 
@@ -284,16 +285,10 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     dim = i32_array([d for _, d in agg_keys])
     rad = i64_array(agg_radices)
 
-    check(lib.ej_join_count_async(
+    check(lib.ej_pair_plan_async(
         ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
-        ldims, rdims, jrad, order, ptr(jws), jws.numel(), ctypes.c_void_p(base), stream),
-        "ej_join_count_async")
-    check(lib.ej_join_fill(n_l, n_r, nk, order, ptr(jws), jws.numel(), cap_p, ptr(li), ptr(ri),
-                           cap_p, stream), "ej_join_fill")
-    check(lib.ej_segment_count_async(
-        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1],
-        ptr(li), ptr(ri), cap_p, ptr(jws), n_out, src, dim, rad, ptr(sws), sws.numel(),
-        ctypes.c_void_p(base + 16), stream), "ej_segment_count_async")
+        ldims, rdims, jrad, n_out, src, dim, rad, cap_p, ptr(jws), jws.numel(), ptr(sws),
+        sws.numel(), ptr(li), ptr(ri), ctypes.c_void_p(base), stream), "ej_pair_plan_async")
     event.record()
     check(lib.ej_segment_fill_async(cap_p, n_out, rad, ptr(sws), sws.numel(), ptr(coords),
                                     ptr(offsets), ptr(perm), None, cap_u, stream),
@@ -303,7 +298,7 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
                                       ptr(perm), ptr(offsets), cap_u, ptr(sws), ptr(out), stream),
           "ej_segment_einsum_async")
     event.synchronize()
-    P, bad_join, U, bad_plan = (int(x) for x in buf.tolist())
+    U, bad_plan, _, _, P, bad_join = (int(x) for x in buf.tolist()[:6])
     if bad_join:
         return "range", None
     if P > cap_p:

@@ -146,15 +146,17 @@ __global__ __launch_bounds__(kProbeThreads) void probe_scan_small_kernel(
 // counts), the sorted permutation is written to lperm, every rhs row's equal
 // range is found by side-by-side branch-free searches, and the counts are
 // scanned into offs.  scalars[0] = P and scalars[1] = the out-of-range flag
-// are written outright, so nothing needs clearing first.  One launch replaces
-// the clear, pack, sort and probe launches of the general path.
+// are written outright, so nothing needs clearing first; the n_clear int64s
+// at `clear` (another phase's counters) are zeroed on the way.  One launch
+// replaces the clear, pack, sort and probe launches of the general path.
 constexpr int kJoinSmallThreads = 1024;
 constexpr int kJoinSmallBuild = 4096;
 
 __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
     const int32_t *__restrict__ lc, int n_build, KeySpec lks, const int32_t *__restrict__ rc,
     int64_t n_probe, KeySpec rks, int bits, int32_t *__restrict__ lperm,
-    int64_t *__restrict__ lo_out, int64_t *__restrict__ offs, int64_t *__restrict__ scalars) {
+    int64_t *__restrict__ lo_out, int64_t *__restrict__ offs, int64_t *__restrict__ scalars,
+    int64_t *__restrict__ clear, int n_clear) {
   constexpr int NW = kJoinSmallThreads / 64;
   __shared__ uint64_t skey[2][kJoinSmallBuild];
   __shared__ int32_t sidx[2][kJoinSmallBuild];
@@ -164,6 +166,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   if (tid == 0) bad_any = 0;
+  if (tid < n_clear) clear[tid] = 0;
   __syncthreads();
   int bad = 0;
   for (int i = tid; i < n_build; i += kJoinSmallThreads) {
@@ -393,12 +396,16 @@ namespace {
 // Enqueues the join count.  *host_known >= 0 on return: the pair count is
 // known on the host (cross product or an empty side) and nothing was
 // enqueued; otherwise (-1) the count and a range flag land in w.scalars[0..1].
+// clear (optional): kClearScalars int64s of a later phase, zeroed in stream
+// order before the count finishes.
+constexpr int kClearScalars = 8;
+
 int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
                        const int64_t *radices, int32_t order, void *workspace,
                        size_t workspace_bytes, int64_t *host_known, int64_t **dev_scalars,
-                       hipStream_t stream) {
+                       hipStream_t stream, int64_t *clear = nullptr) {
   *host_known = -1;
   EJ_CHECK_ARG(n_lhs >= 0 && n_rhs >= 0, "negative relation size");
   EJ_CHECK_ARG(n_lhs < (int64_t(1) << 31) && n_rhs < (int64_t(1) << 31),
@@ -428,12 +435,13 @@ int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
   if (order == EJ_ORDER_PROBE && n_lhs <= kJoinSmallBuild && n_rhs <= kProbeSmallMax) {
     hipLaunchKernelGGL(join_probe_small_kernel, dim3(1), dim3(kJoinSmallThreads), 0, stream,
                        lhs_coords, static_cast<int>(n_lhs), lks, rhs_coords, n_rhs, rks, bits,
-                       w.lperm, w.lo, w.offs, w.scalars);
+                       w.lperm, w.lo, w.offs, w.scalars, clear, clear ? kClearScalars : 0);
     EJ_LAUNCH_CHECK();
     return EJ_OK;
   }
 
   EJ_TRY(zero_async(w.scalars, 4 * sizeof(int64_t), stream));
+  if (clear) EJ_TRY(zero_async(clear, kClearScalars * sizeof(int64_t), stream));
   int *bad = reinterpret_cast<int *>(w.scalars + 1);
   // Sorted sides are packed where an odd number of radix passes leaves them
   // in the primary buffers.
@@ -644,6 +652,47 @@ __global__ void pair_keys_kernel(const int32_t *lc, const int32_t *rc, const int
   if (b) atomicOr(bad, 1);
 }
 
+// EJ_ORDER_PROBE fill that also forms each pair's output key for the segment
+// sort (what pair_keys_kernel does for caller-supplied pairs): writes li, ri,
+// keys and perm = q for q < n = min(P, cap).  Thread 0 stores n as the plan's
+// live pair count (sscal[2]) and copies P and the join's range flag to
+// sscal[4..5], next to the plan's counts, so that one copy returns them all.
+__global__ void fill_probe_keys_kernel(const int64_t *offs, int64_t n_rhs, const int64_t *lo,
+                                       const int32_t *lhs_perm, int64_t cap,
+                                       const int64_t *jscal, const int32_t *lc,
+                                       const int32_t *rc, AggSpec a, int64_t *lhs_idx,
+                                       int64_t *rhs_idx, uint64_t *keys, int32_t *perm,
+                                       int64_t *sscal) {
+  const int64_t P = jscal[0];
+  const int64_t n = P < cap ? P : cap;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (q == 0) {
+    sscal[2] = n;
+    sscal[4] = P;
+    sscal[5] = jscal[1];
+  }
+  if (q >= n) return;
+  const int64_t j = owner_of(offs, n_rhs, q);
+  const int64_t l = lhs_perm[lo[j] + (q - offs[j])];
+  lhs_idx[q] = l;
+  rhs_idx[q] = j;
+  perm[q] = static_cast<int32_t>(q);
+  const int32_t *lrow = lc + l * a.lncols;
+  const int32_t *rrow = rc + j * a.rncols;
+  uint64_t key = 0;
+  bool b = false;
+  for (int d = 0; d < a.n; ++d) {
+    int64_t c = a.src[d] == 0 ? lrow[a.dim[d]] : rrow[a.dim[d]];
+    if (c < 0 || c >= a.radix[d]) {
+      b = true;
+      c = 0;
+    }
+    key = key * static_cast<uint64_t>(a.radix[d]) + static_cast<uint64_t>(c);
+  }
+  keys[q] = key;
+  if (b) atomicOr(reinterpret_cast<int *>(sscal + 1), 1);
+}
+
 __global__ void seg_flags_kernel(const uint64_t *skeys, int64_t n, const int64_t *n_dev,
                                  int64_t *flags) {
   n = live_count(n, n_dev);
@@ -696,7 +745,7 @@ __global__ void seg_fill_kernel(const uint64_t *skeys, const int32_t *sperm, con
 }
 
 struct SegWs {
-  int64_t *scalars;  // [0] = U, [1] = bad flag
+  int64_t *scalars;  // [0] = U, [1] = bad flag, [2] = live pairs; 8 slots
   uint64_t *keys, *keys_alt;
   int32_t *perm, *perm_alt;
   int64_t *flags, *excl;
@@ -707,7 +756,7 @@ struct SegWs {
 SegWs carve_seg(void *base, int64_t n) {
   Carver c(base);
   SegWs w;
-  w.scalars = c.take<int64_t>(4);
+  w.scalars = c.take<int64_t>(kClearScalars);
   w.keys = c.take<uint64_t>(n);
   w.keys_alt = c.take<uint64_t>(n);
   w.perm = c.take<int32_t>(n);
@@ -750,6 +799,23 @@ extern "C" int ej_segment_workspace_size(int64_t n_pairs, size_t *bytes) {
 namespace ej {
 namespace {
 
+// Segment flags of the sorted keys and their exclusive scan (w.flags, w.excl);
+// U lands in w.scalars[0].
+int segment_scan_enqueue(const SegWs &w, int64_t n_pairs, const int64_t *live,
+                         hipStream_t stream) {
+  if (n_pairs <= kFastScanMax) {
+    launch_fast_scan(SegFlagLoad{w.keys}, StoreFlag{w.flags}, n_pairs, live,
+                     static_cast<int64_t *>(w.scan_ws), w.excl, w.scalars, stream);
+    EJ_LAUNCH_CHECK();
+  } else {
+    hipLaunchKernelGGL(seg_flags_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream, w.keys,
+                       n_pairs, live, w.flags);
+    EJ_LAUNCH_CHECK();
+    EJ_TRY(scan_exclusive_i64(w.flags, w.excl, n_pairs, w.scalars, w.scan_ws, stream, live));
+  }
+  return EJ_OK;
+}
+
 // Enqueues the segment count; *known_empty on return: no pairs, nothing
 // enqueued.  Otherwise U and a range flag land in w.scalars[0..1] and the
 // live pair count in w.scalars[2].
@@ -786,17 +852,7 @@ int segment_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_
   const int64_t *live = n_pairs_dev ? w.scalars + 2 : nullptr;
   EJ_TRY(sort_pairs_u64(w.keys, w.perm, w.keys_alt, w.perm_alt, n_pairs, bits, w.sort_ws, stream,
                         alt, live));
-  if (n_pairs <= kFastScanMax) {
-    launch_fast_scan(SegFlagLoad{w.keys}, StoreFlag{w.flags}, n_pairs, live,
-                     static_cast<int64_t *>(w.scan_ws), w.excl, w.scalars, stream);
-    EJ_LAUNCH_CHECK();
-  } else {
-    hipLaunchKernelGGL(seg_flags_kernel, dim3(grid_for(n_pairs)), dim3(kBlock), 0, stream, w.keys,
-                       n_pairs, live, w.flags);
-    EJ_LAUNCH_CHECK();
-    EJ_TRY(scan_exclusive_i64(w.flags, w.excl, n_pairs, w.scalars, w.scan_ws, stream, live));
-  }
-  return EJ_OK;
+  return segment_scan_enqueue(w, n_pairs, live, stream);
 }
 
 }  // namespace
@@ -908,6 +964,52 @@ extern "C" int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64
                      w.perm, w.flags, w.excl, n_pairs, capacity, w.scalars, a, out_coords,
                      seg_offsets, perm, seg_ids);
   EJ_LAUNCH_CHECK();
+  return EJ_OK;
+}
+
+extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                                  const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                                  int32_t n_keys, const int32_t *lhs_dims,
+                                  const int32_t *rhs_dims, const int64_t *join_radices,
+                                  int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
+                                  const int64_t *agg_radices, int64_t pair_capacity,
+                                  void *join_workspace, size_t join_workspace_bytes,
+                                  void *seg_workspace, size_t seg_workspace_bytes,
+                                  int64_t *lhs_idx, int64_t *rhs_idx, int64_t *counts,
+                                  ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  EJ_CHECK_ARG(counts && lhs_idx && rhs_idx, "null pointer argument");
+  EJ_CHECK_ARG(n_keys >= 1 && n_lhs >= 1 && n_rhs >= 1,
+               "the queued pair plan needs join keys and two non-empty relations");
+  EJ_CHECK_ARG(pair_capacity >= 1 && pair_capacity < (int64_t(1) << 31),
+               "pair_capacity must lie in [1, 2^31)");
+  EJ_CHECK_ARG(agg_radices || n_out == 0, "agg_radices is null");
+  AggSpec a;
+  EJ_TRY(check_agg(n_out, agg_src, agg_dim, n_lhs, lhs_ncols, n_rhs, rhs_ncols, agg_radices, &a));
+  int sbits = 0;
+  EJ_TRY(key_bits(a.radix, n_out, &sbits));
+  SegWs sw = carve_seg(seg_workspace, pair_capacity);
+  EJ_CHECK_ARG(seg_workspace && seg_workspace_bytes >= sw.bytes,
+               "segment workspace too small: %zu < %zu bytes", seg_workspace_bytes, sw.bytes);
+  int64_t known = -1;
+  int64_t *jscal = nullptr;
+  EJ_TRY(join_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
+                            lhs_dims, rhs_dims, join_radices, EJ_ORDER_PROBE, join_workspace,
+                            join_workspace_bytes, &known, &jscal, stream, sw.scalars));
+  EJ_CHECK_ARG(known < 0, "internal: join size known on the host");
+  JoinWs jw = carve_join(join_workspace, n_lhs, n_rhs, EJ_ORDER_PROBE);
+  const bool alt = pair_capacity > 1 && (radix_passes(sbits) & 1);
+  hipLaunchKernelGGL(fill_probe_keys_kernel, dim3(grid_for(pair_capacity)), dim3(kBlock), 0,
+                     stream, jw.offs, n_rhs, jw.lo, jw.lperm, pair_capacity, jw.scalars,
+                     lhs_coords, rhs_coords, a, lhs_idx, rhs_idx, alt ? sw.keys_alt : sw.keys,
+                     alt ? sw.perm_alt : sw.perm, sw.scalars);
+  EJ_LAUNCH_CHECK();
+  const int64_t *live = sw.scalars + 2;
+  EJ_TRY(sort_pairs_u64(sw.keys, sw.perm, sw.keys_alt, sw.perm_alt, pair_capacity, sbits,
+                        sw.sort_ws, stream, alt, live));
+  EJ_TRY(segment_scan_enqueue(sw, pair_capacity, live, stream));
+  EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   return EJ_OK;
 }
 

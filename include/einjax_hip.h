@@ -28,6 +28,7 @@
  *                 (replaces jnp.einsum(_add_batch_dim(kernel_string)),
  *                  execution/sparse_dispatch.py:121-126)
  *   queued step   ej_join_count_async / ej_segment_count_async /
+ *                 ej_pair_plan_async (both counts in one call) /
  *                 ej_segment_fill_async / ej_segment_einsum_async
  *                 (the same phases with the counts kept on the device, so a
  *                  caller can queue a whole execute_sparse,
@@ -74,7 +75,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 7
+#define EJ_ABI_VERSION 8
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -248,6 +249,30 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
                           const void *workspace, size_t workspace_bytes, int32_t *out_coords,
                           int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids,
                           int64_t capacity, ej_stream_t stream);
+
+/* ej_join_count_async (EJ_ORDER_PROBE), ej_join_fill and ej_segment_count_async
+ * in one call, with fewer launches: the pair fill also forms the output keys,
+ * the plan's counters are cleared inside the join count, and one copy returns
+ * every count.  No counterpart in the reference (see ej_join_count_async); it
+ * queues the phases of execute_sparse (sparse_dispatch.py:226-297) up to the
+ * einsum.  Needs n_keys >= 1 and non-empty relations.  join_workspace: sized
+ * by ej_join_workspace_size(n_lhs, n_rhs, EJ_ORDER_PROBE); seg_workspace: by
+ * ej_segment_workspace_size(pair_capacity), afterwards the workspace of
+ * ej_segment_fill_async (n_pairs = pair_capacity) and, through its first
+ * int64 (U), of ej_segment_einsum_async.  lhs_idx / rhs_idx hold
+ * pair_capacity entries; writes are clipped to min(P, pair_capacity).
+ * counts (pinned host memory, 6 int64) receives, in stream order:
+ * counts[0] = U, [1] = plan range flag, [2] = pairs planned
+ * min(P, pair_capacity), [4] = P, [5] = join range flag; P > pair_capacity
+ * means the plan covers only the first pair_capacity pairs. */
+int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                       const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                       int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                       const int64_t *join_radices, int32_t n_out, const int32_t *agg_src,
+                       const int32_t *agg_dim, const int64_t *agg_radices,
+                       int64_t pair_capacity, void *join_workspace, size_t join_workspace_bytes,
+                       void *seg_workspace, size_t seg_workspace_bytes, int64_t *lhs_idx,
+                       int64_t *rhs_idx, int64_t *counts, ej_stream_t stream);
 
 /* ---- gather (reference: values[indices], sparse_dispatch.py:118-119) ---- */
 /* out[i] = values[idx[i]] for whole tiles of tile_bytes each.  Indices

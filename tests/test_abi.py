@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 7
+    assert _lib.load().ej_version() == 8
 
 
 def describe(spec, lt, rt):
@@ -272,3 +272,18 @@ def test_output_dtype_validation():
                               fake, None) == _lib.EJ_E_INVAL
     assert lib.ej_segment_sum(fake, 5, 4, fake, fake, 0, fake, None) == _lib.EJ_E_INVAL
     assert lib.ej_segment_sum(fake, _lib.EJ_BF16, 4, fake, fake, 0, fake, None) == _lib.EJ_OK
+
+
+def test_pair_plan_host_validation():
+    """The queued pair plan rejects what it does not cover before any launch."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(16)
+    d = i32_array([1])
+    r = i64_array([4])
+    counts = (ctypes.c_int64 * 8)()
+    args = lambda nk, cap: (fake, 4, 2, fake, 4, 2, nk, d, i32_array([0]), r, 2, i32_array([0, 1]),
+                            i32_array([0, 1]), i64_array([4, 4]), cap, fake, 1 << 20, fake, 1 << 20,
+                            fake, fake, ctypes.cast(counts, ctypes.c_void_p), None)
+    assert lib.ej_pair_plan_async(*args(0, 10)) == _lib.EJ_E_INVAL  # no join keys
+    assert lib.ej_pair_plan_async(*args(1, 0)) == _lib.EJ_E_INVAL  # no capacity
+    assert b"pair_capacity" in lib.ej_last_error()

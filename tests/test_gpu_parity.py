@@ -780,6 +780,47 @@ def test_queued_step_range_fallback(gpu, monkeypatch):
     assert statuses == ["range"]
 
 
+def test_queued_step_large_join(gpu, monkeypatch):
+    """The queued step with a build side above the one-workgroup join (the
+    full-size Zipf workload, 20,971 lhs tiles, 54,516 pairs): bit-identical to
+    the exact path; with shape metadata that understates the coordinates the
+    range flag sends it to the exact path."""
+    note("queued step, large join")
+    statuses = []
+    real = _device_mod().queued_segment_einsum
+
+    def spy(*a, **k):
+        st, res = real(*a, **k)
+        statuses.append(st)
+        return st, res
+
+    monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    w = G.workload_sparse_sparse_zipf(values=False)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+
+    def rel(r, shape):
+        v = torch.rand((len(r.coords), *r.tile_shape), generator=gen, device="cuda") * 2 - 1
+        return SparseTensorRelation(torch.from_numpy(r.coords).cuda(), v, shape, r.tile_shape)
+
+    lhs, rhs = rel(w["lhs"], w["lhs"].shape), rel(w["rhs"], w["rhs"].shape)
+    assert lhs.num_tuples > 4096
+    run = lambda a, b: ej.execute_sparse(a, b, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    sd._pair_hints.clear()
+    exact = run(lhs, rhs)
+    queued = run(lhs, rhs)
+    assert statuses == ["ok"]
+    assert torch.equal(exact.coords, queued.coords)
+    assert torch.equal(exact.values.view(torch.int32), queued.values.view(torch.int32))
+    oc_lhs = SparseTensorRelation(lhs.coords, lhs.values, lhs.tile_shape, lhs.tile_shape)
+    oc_rhs = SparseTensorRelation(rhs.coords, rhs.values, rhs.tile_shape, rhs.tile_shape)
+    sd._pair_hints.clear()
+    for _ in range(2):
+        got = run(oc_lhs, oc_rhs)
+        assert torch.equal(got.coords, exact.coords)
+        assert torch.equal(got.values.view(torch.int32), exact.values.view(torch.int32))
+    assert statuses == ["ok", "range"]
+
+
 def _device_mod():
     from einjax_amd import _device
 
