@@ -288,11 +288,9 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     check(lib.ej_pair_plan_async(
         ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
         ldims, rdims, jrad, n_out, src, dim, rad, cap_p, ptr(jws), jws.numel(), ptr(sws),
-        sws.numel(), ptr(li), ptr(ri), ctypes.c_void_p(base), stream), "ej_pair_plan_async")
+        sws.numel(), ptr(li), ptr(ri), ptr(coords), ptr(offsets), ptr(perm), cap_u,
+        ctypes.c_void_p(base), stream), "ej_pair_plan_async")
     event.record()
-    check(lib.ej_segment_fill_async(cap_p, n_out, rad, ptr(sws), sws.numel(), ptr(coords),
-                                    ptr(offsets), ptr(perm), None, cap_u, stream),
-          "ej_segment_fill_async")
     check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                       lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
                                       ptr(perm), ptr(offsets), cap_u, ptr(sws), ptr(out), stream),

@@ -85,9 +85,23 @@ int scan_exclusive_i64(const int64_t *in, int64_t *out, int64_t n, int64_t *tota
 size_t sort_workspace_bytes(int64_t n);
 int radix_passes(int bits);
 // n_dev (optional): device-side count clipping n (keys beyond it stay put).
+// first_hist_given: the digit histogram of the first pass (bits 0-7) is
+// already in the workspace (see sort_tiling), so that pass skips its
+// histogram launch.
 int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *vals_alt,
                    int64_t n, int bits, void *ws, hipStream_t stream,
-                   bool input_in_alt = false, const int64_t *n_dev = nullptr);
+                   bool input_in_alt = false, const int64_t *n_dev = nullptr,
+                   bool first_hist_given = false);
+// Tiling of a sort of n keys: tile = keys per block, nblocks blocks; when
+// inline_offsets, the first int64s of the workspace hold the digit histogram
+// block-major (hist[block * 256 + digit]), which a producer of the keys may
+// fill itself (zeroed first, then counts of keys [block * tile, ...) that lie
+// below the live count) and pass first_hist_given.
+struct SortTiling {
+  int64_t tile, nblocks;
+  bool inline_offsets;
+};
+SortTiling sort_tiling(int64_t n);
 
 // Zeroes n bytes (a multiple of 4, 4-byte aligned) with a kernel rather than
 // hipMemsetAsync, which misbehaves when a caller records the call into a
@@ -158,7 +172,8 @@ __device__ inline int64_t block_exclusive_sum(int64_t v, int64_t *block_total) {
 // block adds up the sums of the blocks before it, scans its tile and writes
 // the prefixes).  Values come from a functor load(i) -> int64 so callers can
 // generate them (flags from sorted keys, say) instead of materialising them;
-// emit(i, value) runs once per index in scan_apply.
+// emit(i, value, prefix, n) runs once per index i < n in scan_apply, with the
+// exclusive prefix of i.  out (may be null) receives the prefixes.
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kBlock * kScanItems;
 constexpr int64_t kFastScanBlocks = kBlock;
@@ -212,8 +227,8 @@ __global__ __launch_bounds__(kBlock) void scan_apply_kernel(Load load, Emit emit
 #pragma unroll
   for (int r = 0; r < kScanItems; ++r) {
     if (base + r < n) {
-      out[base + r] = run;
-      emit(base + r, v[r]);
+      if (out) out[base + r] = run;
+      emit(base + r, v[r], run, n);
     }
     run += v[r];
   }
@@ -225,7 +240,7 @@ struct LoadI64 {
 };
 
 struct NoEmit {
-  __device__ void operator()(int64_t, int64_t) const {}
+  __device__ void operator()(int64_t, int64_t, int64_t, int64_t) const {}
 };
 
 // Launches the two kernels for n in [1, kFastScanMax] (n_dev: optional

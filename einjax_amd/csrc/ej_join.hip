@@ -147,8 +147,9 @@ __global__ __launch_bounds__(kProbeThreads) void probe_scan_small_kernel(
 // range is found by side-by-side branch-free searches, and the counts are
 // scanned into offs.  scalars[0] = P and scalars[1] = the out-of-range flag
 // are written outright, so nothing needs clearing first; the n_clear int64s
-// at `clear` (another phase's counters) are zeroed on the way.  One launch
-// replaces the clear, pack, sort and probe launches of the general path.
+// at `clear` and the n_clear2 at `clear2` (a later phase's counters) are
+// zeroed on the way.  One launch replaces the clear, pack, sort and probe
+// launches of the general path.
 constexpr int kJoinSmallThreads = 1024;
 constexpr int kJoinSmallBuild = 4096;
 
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
     const int32_t *__restrict__ lc, int n_build, KeySpec lks, const int32_t *__restrict__ rc,
     int64_t n_probe, KeySpec rks, int bits, int32_t *__restrict__ lperm,
     int64_t *__restrict__ lo_out, int64_t *__restrict__ offs, int64_t *__restrict__ scalars,
-    int64_t *__restrict__ clear, int n_clear) {
+    int64_t *__restrict__ clear, int n_clear, int64_t *__restrict__ clear2, int n_clear2) {
   constexpr int NW = kJoinSmallThreads / 64;
   __shared__ uint64_t skey[2][kJoinSmallBuild];
   __shared__ int32_t sidx[2][kJoinSmallBuild];
@@ -167,6 +168,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   if (tid == 0) bad_any = 0;
   if (tid < n_clear) clear[tid] = 0;
+  for (int i = tid; i < n_clear2; i += kJoinSmallThreads) clear2[i] = 0;
   __syncthreads();
   int bad = 0;
   for (int i = tid; i < n_build; i += kJoinSmallThreads) {
@@ -397,15 +399,21 @@ namespace {
 // known on the host (cross product or an empty side) and nothing was
 // enqueued; otherwise (-1) the count and a range flag land in w.scalars[0..1].
 // clear (optional): kClearScalars int64s of a later phase, zeroed in stream
-// order before the count finishes.
+// order before the count finishes; clear2 (optional, one-workgroup count
+// only): n_clear2 more.
 constexpr int kClearScalars = 8;
+
+bool join_small_ok(int32_t order, int64_t n_lhs, int64_t n_rhs) {
+  return order == EJ_ORDER_PROBE && n_lhs <= kJoinSmallBuild && n_rhs <= kProbeSmallMax;
+}
 
 int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
                        const int64_t *radices, int32_t order, void *workspace,
                        size_t workspace_bytes, int64_t *host_known, int64_t **dev_scalars,
-                       hipStream_t stream, int64_t *clear = nullptr) {
+                       hipStream_t stream, int64_t *clear = nullptr, int64_t *clear2 = nullptr,
+                       int n_clear2 = 0) {
   *host_known = -1;
   EJ_CHECK_ARG(n_lhs >= 0 && n_rhs >= 0, "negative relation size");
   EJ_CHECK_ARG(n_lhs < (int64_t(1) << 31) && n_rhs < (int64_t(1) << 31),
@@ -432,16 +440,18 @@ int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
   *dev_scalars = w.scalars;
-  if (order == EJ_ORDER_PROBE && n_lhs <= kJoinSmallBuild && n_rhs <= kProbeSmallMax) {
+  if (join_small_ok(order, n_lhs, n_rhs)) {
     hipLaunchKernelGGL(join_probe_small_kernel, dim3(1), dim3(kJoinSmallThreads), 0, stream,
                        lhs_coords, static_cast<int>(n_lhs), lks, rhs_coords, n_rhs, rks, bits,
-                       w.lperm, w.lo, w.offs, w.scalars, clear, clear ? kClearScalars : 0);
+                       w.lperm, w.lo, w.offs, w.scalars, clear, clear ? kClearScalars : 0,
+                       clear2, clear2 ? n_clear2 : 0);
     EJ_LAUNCH_CHECK();
     return EJ_OK;
   }
 
   EJ_TRY(zero_async(w.scalars, 4 * sizeof(int64_t), stream));
   if (clear) EJ_TRY(zero_async(clear, kClearScalars * sizeof(int64_t), stream));
+  if (clear2) EJ_TRY(zero_async(clear2, n_clear2 * sizeof(int64_t), stream));
   int *bad = reinterpret_cast<int *>(w.scalars + 1);
   // Sorted sides are packed where an odd number of radix passes leaves them
   // in the primary buffers.
@@ -657,12 +667,16 @@ __global__ void pair_keys_kernel(const int32_t *lc, const int32_t *rc, const int
 // keys and perm = q for q < n = min(P, cap).  Thread 0 stores n as the plan's
 // live pair count (sscal[2]) and copies P and the join's range flag to
 // sscal[4..5], next to the plan's counts, so that one copy returns them all.
-__global__ void fill_probe_keys_kernel(const int64_t *offs, int64_t n_rhs, const int64_t *lo,
-                                       const int32_t *lhs_perm, int64_t cap,
-                                       const int64_t *jscal, const int32_t *lc,
-                                       const int32_t *rc, AggSpec a, int64_t *lhs_idx,
-                                       int64_t *rhs_idx, uint64_t *keys, int32_t *perm,
-                                       int64_t *sscal) {
+// hist (optional, zeroed): the sort's first-pass digit histogram, block-major
+// over sort blocks of `tile` keys (a multiple of the block size, so each
+// block's pairs fall in one sort block), counted here in LDS and added once
+// per digit.
+__global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
+    const int64_t *offs, int64_t n_rhs, const int64_t *lo, const int32_t *lhs_perm, int64_t cap,
+    const int64_t *jscal, const int32_t *lc, const int32_t *rc, AggSpec a, int64_t *lhs_idx,
+    int64_t *rhs_idx, uint64_t *keys, int32_t *perm, int64_t *sscal, int64_t *hist,
+    int64_t tile) {
+  __shared__ int digit_count[256];
   const int64_t P = jscal[0];
   const int64_t n = P < cap ? P : cap;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -671,26 +685,41 @@ __global__ void fill_probe_keys_kernel(const int64_t *offs, int64_t n_rhs, const
     sscal[4] = P;
     sscal[5] = jscal[1];
   }
-  if (q >= n) return;
-  const int64_t j = owner_of(offs, n_rhs, q);
-  const int64_t l = lhs_perm[lo[j] + (q - offs[j])];
-  lhs_idx[q] = l;
-  rhs_idx[q] = j;
-  perm[q] = static_cast<int32_t>(q);
-  const int32_t *lrow = lc + l * a.lncols;
-  const int32_t *rrow = rc + j * a.rncols;
-  uint64_t key = 0;
-  bool b = false;
-  for (int d = 0; d < a.n; ++d) {
-    int64_t c = a.src[d] == 0 ? lrow[a.dim[d]] : rrow[a.dim[d]];
-    if (c < 0 || c >= a.radix[d]) {
-      b = true;
-      c = 0;
-    }
-    key = key * static_cast<uint64_t>(a.radix[d]) + static_cast<uint64_t>(c);
+  if (hist) {
+    digit_count[threadIdx.x] = 0;
+    __syncthreads();
   }
-  keys[q] = key;
-  if (b) atomicOr(reinterpret_cast<int *>(sscal + 1), 1);
+  if (q < n) {
+    const int64_t j = owner_of(offs, n_rhs, q);
+    const int64_t l = lhs_perm[lo[j] + (q - offs[j])];
+    lhs_idx[q] = l;
+    rhs_idx[q] = j;
+    perm[q] = static_cast<int32_t>(q);
+    const int32_t *lrow = lc + l * a.lncols;
+    const int32_t *rrow = rc + j * a.rncols;
+    uint64_t key = 0;
+    bool b = false;
+    for (int d = 0; d < a.n; ++d) {
+      int64_t c = a.src[d] == 0 ? lrow[a.dim[d]] : rrow[a.dim[d]];
+      if (c < 0 || c >= a.radix[d]) {
+        b = true;
+        c = 0;
+      }
+      key = key * static_cast<uint64_t>(a.radix[d]) + static_cast<uint64_t>(c);
+    }
+    keys[q] = key;
+    if (b) atomicOr(reinterpret_cast<int *>(sscal + 1), 1);
+    if (hist) atomicAdd(&digit_count[key & 255], 1);
+  }
+  if (hist) {
+    __syncthreads();
+    const int c = digit_count[threadIdx.x];
+    if (c) {
+      const int64_t sb = static_cast<int64_t>(blockIdx.x) * blockDim.x / tile;
+      atomicAdd(reinterpret_cast<unsigned long long *>(hist + sb * 256 + threadIdx.x),
+                static_cast<unsigned long long>(c));
+    }
+  }
 }
 
 __global__ void seg_flags_kernel(const uint64_t *skeys, int64_t n, const int64_t *n_dev,
@@ -711,7 +740,33 @@ struct SegFlagLoad {
 
 struct StoreFlag {
   int64_t *flags;
-  __device__ void operator()(int64_t q, int64_t f) const { flags[q] = f; }
+  __device__ void operator()(int64_t q, int64_t f, int64_t, int64_t) const { flags[q] = f; }
+};
+
+// The segment fill done inside the flag scan (seg_fill_kernel's writes for
+// sorted position q, whose segment is prefix + flag - 1): perm, the start
+// offset and the coordinates of each segment below the capacity, and the
+// end offset after the last segment.
+struct SegFillEmit {
+  const uint64_t *skeys;
+  const int32_t *sperm;
+  AggSpec a;
+  int64_t cap;
+  int32_t *out_coords, *seg_offsets, *perm;
+  __device__ void operator()(int64_t q, int64_t f, int64_t prefix, int64_t n) const {
+    perm[q] = sperm[q];
+    const int64_t seg = prefix + f - 1;
+    if (f && seg < cap) {
+      seg_offsets[seg] = static_cast<int32_t>(q);
+      uint64_t key = skeys[q];
+      for (int d = a.n - 1; d >= 0; --d) {
+        const uint64_t r = static_cast<uint64_t>(a.radix[d]);
+        out_coords[seg * a.n + d] = static_cast<int32_t>(key % r);
+        key /= r;
+      }
+    }
+    if (q == n - 1 && seg < cap) seg_offsets[seg + 1] = static_cast<int32_t>(n);
+  }
 };
 
 // dev_counts (optional): the workspace scalars; the live pair count is
@@ -975,11 +1030,15 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
                                   const int64_t *agg_radices, int64_t pair_capacity,
                                   void *join_workspace, size_t join_workspace_bytes,
                                   void *seg_workspace, size_t seg_workspace_bytes,
-                                  int64_t *lhs_idx, int64_t *rhs_idx, int64_t *counts,
-                                  ej_stream_t stream_) {
+                                  int64_t *lhs_idx, int64_t *rhs_idx, int32_t *out_coords,
+                                  int32_t *seg_offsets, int32_t *perm, int64_t seg_capacity,
+                                  int64_t *counts, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
-  EJ_CHECK_ARG(counts && lhs_idx && rhs_idx, "null pointer argument");
+  EJ_CHECK_ARG(counts && lhs_idx && rhs_idx && seg_offsets && perm &&
+                   (out_coords || n_out == 0),
+               "null pointer argument");
+  EJ_CHECK_ARG(seg_capacity >= 0, "negative seg_capacity");
   EJ_CHECK_ARG(n_keys >= 1 && n_lhs >= 1 && n_rhs >= 1,
                "the queued pair plan needs join keys and two non-empty relations");
   EJ_CHECK_ARG(pair_capacity >= 1 && pair_capacity < (int64_t(1) << 31),
@@ -992,23 +1051,44 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
   SegWs sw = carve_seg(seg_workspace, pair_capacity);
   EJ_CHECK_ARG(seg_workspace && seg_workspace_bytes >= sw.bytes,
                "segment workspace too small: %zu < %zu bytes", seg_workspace_bytes, sw.bytes);
+  // The fill also counts the sort's first-pass digits when the join count
+  // (one workgroup) can clear that histogram and the sort reads it inline.
+  const SortTiling st = sort_tiling(pair_capacity);
+  const bool fill_hist = pair_capacity > 1 && sbits > 0 && st.inline_offsets &&
+                         join_small_ok(EJ_ORDER_PROBE, n_lhs, n_rhs);
+  int64_t *hist = fill_hist ? static_cast<int64_t *>(sw.sort_ws) : nullptr;
   int64_t known = -1;
   int64_t *jscal = nullptr;
   EJ_TRY(join_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
                             lhs_dims, rhs_dims, join_radices, EJ_ORDER_PROBE, join_workspace,
-                            join_workspace_bytes, &known, &jscal, stream, sw.scalars));
+                            join_workspace_bytes, &known, &jscal, stream, sw.scalars, hist,
+                            static_cast<int>(st.nblocks * 256)));
   EJ_CHECK_ARG(known < 0, "internal: join size known on the host");
   JoinWs jw = carve_join(join_workspace, n_lhs, n_rhs, EJ_ORDER_PROBE);
   const bool alt = pair_capacity > 1 && (radix_passes(sbits) & 1);
   hipLaunchKernelGGL(fill_probe_keys_kernel, dim3(grid_for(pair_capacity)), dim3(kBlock), 0,
                      stream, jw.offs, n_rhs, jw.lo, jw.lperm, pair_capacity, jw.scalars,
                      lhs_coords, rhs_coords, a, lhs_idx, rhs_idx, alt ? sw.keys_alt : sw.keys,
-                     alt ? sw.perm_alt : sw.perm, sw.scalars);
+                     alt ? sw.perm_alt : sw.perm, sw.scalars, hist, st.tile);
   EJ_LAUNCH_CHECK();
   const int64_t *live = sw.scalars + 2;
   EJ_TRY(sort_pairs_u64(sw.keys, sw.perm, sw.keys_alt, sw.perm_alt, pair_capacity, sbits,
-                        sw.sort_ws, stream, alt, live));
-  EJ_TRY(segment_scan_enqueue(sw, pair_capacity, live, stream));
+                        sw.sort_ws, stream, alt, live, fill_hist));
+  // Segment flags, their scan and the segment fill: one pass inside the scan
+  // for up to kFastScanMax pairs.
+  if (pair_capacity <= kFastScanMax) {
+    launch_fast_scan(SegFlagLoad{sw.keys},
+                     SegFillEmit{sw.keys, sw.perm, a, seg_capacity, out_coords, seg_offsets, perm},
+                     pair_capacity, live, static_cast<int64_t *>(sw.scan_ws), nullptr,
+                     sw.scalars, stream);
+    EJ_LAUNCH_CHECK();
+  } else {
+    EJ_TRY(segment_scan_enqueue(sw, pair_capacity, live, stream));
+    hipLaunchKernelGGL(seg_fill_kernel, dim3(grid_for(pair_capacity)), dim3(kBlock), 0, stream,
+                       sw.keys, sw.perm, sw.flags, sw.excl, pair_capacity, seg_capacity,
+                       sw.scalars, a, out_coords, seg_offsets, perm, nullptr);
+    EJ_LAUNCH_CHECK();
+  }
   EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
   return EJ_OK;
 }

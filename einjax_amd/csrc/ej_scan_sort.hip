@@ -298,9 +298,17 @@ size_t sort_workspace_bytes(int64_t n) {
 
 int radix_passes(int bits) { return bits <= 0 ? 0 : (bits + kRadixBits - 1) / kRadixBits; }
 
+SortTiling sort_tiling(int64_t n) {
+  SortTiling t;
+  t.tile = static_cast<int64_t>(kBlock) * sort_items(n);
+  t.nblocks = ceil_div(n, t.tile);
+  t.inline_offsets = t.nblocks <= kInlineOffsetBlocks;
+  return t;
+}
+
 template <int ITEMS>
 int sort_passes(uint64_t *&ks, int32_t *&vs, uint64_t *&kd, int32_t *&vd, int64_t n, int bits,
-                void *ws, hipStream_t stream, const int64_t *n_dev) {
+                void *ws, hipStream_t stream, const int64_t *n_dev, bool first_hist_given) {
   const int64_t nblocks = ceil_div(n, static_cast<int64_t>(kBlock) * ITEMS);
   const int64_t h = nblocks * kRadix;
   char *w = static_cast<char *>(ws);
@@ -309,10 +317,12 @@ int sort_passes(uint64_t *&ks, int32_t *&vs, uint64_t *&kd, int32_t *&vd, int64_
   void *scan_ws = w + align_up(sizeof(int64_t) * h * 2, 256);
   const bool inline_offs = nblocks <= kInlineOffsetBlocks;
   for (int shift = 0; shift < bits; shift += kRadixBits) {
-    hipLaunchKernelGGL(radix_hist_kernel<ITEMS>, dim3(static_cast<unsigned>(nblocks)),
-                       dim3(kBlock), 0, stream, ks, n, n_dev, shift, hist, nblocks,
-                       !inline_offs);
-    EJ_LAUNCH_CHECK();
+    if (shift > 0 || !first_hist_given || !inline_offs) {
+      hipLaunchKernelGGL(radix_hist_kernel<ITEMS>, dim3(static_cast<unsigned>(nblocks)),
+                         dim3(kBlock), 0, stream, ks, n, n_dev, shift, hist, nblocks,
+                         !inline_offs);
+      EJ_LAUNCH_CHECK();
+    }
     if (!inline_offs) EJ_TRY(scan_exclusive_i64(hist, offs, h, nullptr, scan_ws, stream));
     hipLaunchKernelGGL(radix_scatter_kernel<ITEMS>, dim3(static_cast<unsigned>(nblocks)),
                        dim3(kBlock), 0, stream, ks, vs, kd, vd, n, n_dev, shift, hist,
@@ -326,15 +336,23 @@ int sort_passes(uint64_t *&ks, int32_t *&vs, uint64_t *&kd, int32_t *&vd, int64_
 
 int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *vals_alt,
                    int64_t n, int bits, void *ws, hipStream_t stream, bool input_in_alt,
-                   const int64_t *n_dev) {
+                   const int64_t *n_dev, bool first_hist_given) {
   uint64_t *ks = input_in_alt ? keys_alt : keys, *kd = input_in_alt ? keys : keys_alt;
   int32_t *vs = input_in_alt ? vals_alt : vals, *vd = input_in_alt ? vals : vals_alt;
   if (n > 1 && bits > 0) {
     switch (sort_items(n)) {
-      case 1: EJ_TRY(sort_passes<1>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
-      case 2: EJ_TRY(sort_passes<2>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
-      case 4: EJ_TRY(sort_passes<4>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
-      default: EJ_TRY(sort_passes<8>(ks, vs, kd, vd, n, bits, ws, stream, n_dev)); break;
+      case 1:
+        EJ_TRY(sort_passes<1>(ks, vs, kd, vd, n, bits, ws, stream, n_dev, first_hist_given));
+        break;
+      case 2:
+        EJ_TRY(sort_passes<2>(ks, vs, kd, vd, n, bits, ws, stream, n_dev, first_hist_given));
+        break;
+      case 4:
+        EJ_TRY(sort_passes<4>(ks, vs, kd, vd, n, bits, ws, stream, n_dev, first_hist_given));
+        break;
+      default:
+        EJ_TRY(sort_passes<8>(ks, vs, kd, vd, n, bits, ws, stream, n_dev, first_hist_given));
+        break;
     }
   }
   if (ks != keys && n > 0) {

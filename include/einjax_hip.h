@@ -250,21 +250,22 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
                           int32_t *seg_offsets, int32_t *perm, int32_t *seg_ids,
                           int64_t capacity, ej_stream_t stream);
 
-/* ej_join_count_async (EJ_ORDER_PROBE), ej_join_fill and ej_segment_count_async
- * in one call, with fewer launches: the pair fill also forms the output keys,
- * the plan's counters are cleared inside the join count, and one copy returns
+/* ej_join_count_async (EJ_ORDER_PROBE), ej_join_fill, ej_segment_count_async
+ * and ej_segment_fill_async in one call, with fewer launches: the pair fill
+ * also forms the output keys, the plan's counters are cleared inside the join
+ * count, the segment fill runs inside the flag scan, and one copy returns
  * every count.  No counterpart in the reference (see ej_join_count_async); it
  * queues the phases of execute_sparse (sparse_dispatch.py:226-297) up to the
  * einsum.  Needs n_keys >= 1 and non-empty relations.  join_workspace: sized
  * by ej_join_workspace_size(n_lhs, n_rhs, EJ_ORDER_PROBE); seg_workspace: by
- * ej_segment_workspace_size(pair_capacity), afterwards the workspace of
- * ej_segment_fill_async (n_pairs = pair_capacity) and, through its first
- * int64 (U), of ej_segment_einsum_async.  lhs_idx / rhs_idx hold
- * pair_capacity entries; writes are clipped to min(P, pair_capacity).
- * counts (pinned host memory, 6 int64) receives, in stream order:
- * counts[0] = U, [1] = plan range flag, [2] = pairs planned
+ * ej_segment_workspace_size(pair_capacity); its first int64 (U) is then the
+ * n_segments_dev of ej_segment_einsum_async.  lhs_idx / rhs_idx / perm hold
+ * pair_capacity entries, out_coords [seg_capacity, n_out] and seg_offsets
+ * [seg_capacity + 1]; writes are clipped to min(P, pair_capacity) pairs and
+ * seg_capacity segments.  counts (pinned host memory, 6 int64) receives, in
+ * stream order: counts[0] = U, [1] = plan range flag, [2] = pairs planned
  * min(P, pair_capacity), [4] = P, [5] = join range flag; P > pair_capacity
- * means the plan covers only the first pair_capacity pairs. */
+ * or U > seg_capacity means the plan is incomplete. */
 int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
@@ -272,7 +273,9 @@ int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
                        const int32_t *agg_dim, const int64_t *agg_radices,
                        int64_t pair_capacity, void *join_workspace, size_t join_workspace_bytes,
                        void *seg_workspace, size_t seg_workspace_bytes, int64_t *lhs_idx,
-                       int64_t *rhs_idx, int64_t *counts, ej_stream_t stream);
+                       int64_t *rhs_idx, int32_t *out_coords, int32_t *seg_offsets,
+                       int32_t *perm, int64_t seg_capacity, int64_t *counts,
+                       ej_stream_t stream);
 
 /* ---- gather (reference: values[indices], sparse_dispatch.py:118-119) ---- */
 /* out[i] = values[idx[i]] for whole tiles of tile_bytes each.  Indices

@@ -821,6 +821,38 @@ def test_queued_step_large_join(gpu, monkeypatch):
     assert statuses == ["ok", "range"]
 
 
+@pytest.mark.parametrize("n_lhs,n_rhs,grid,slack", [(300, 500, 40, 0), (1000, 3000, 100, 7), (3000, 8000, 64, 5),
+                                                    (4000, 8192, 48, 1000), (6000, 9000, 80, 0)])
+def test_pair_plan_matches_exact_phases(gpu, n_lhs, n_rhs, grid, slack):
+    """ej_pair_plan_async (join count and fill, output keys, sort, flag scan
+    and segment fill in one call) against the separate exact phases: pairs,
+    output coordinates, offsets and permutation bit-exact, for one-workgroup
+    and general joins, sorts whose first histogram comes from the pair fill
+    and sorts above the inline-offset tiling (more than 65536 pairs), with a
+    pair capacity equal to P or above it."""
+    note("pair plan", n_lhs, n_rhs, grid, slack)
+    from einjax_amd import _device
+
+    rng = np.random.default_rng(n_lhs + n_rhs + grid)
+    lc = rng.integers(0, grid, (n_lhs, 2), dtype=np.int32)
+    rc = rng.integers(0, grid, (n_rhs, 2), dtype=np.int32)
+    t = lambda a: torch.from_numpy(a).cuda()
+    keys, agg = [(1, 0)], [(0, 0), (1, 1)]
+    li, ri = _device.join(t(lc), t(rc), keys, [grid])
+    coords, off, perm, _ = _device.segment_plan(t(lc), t(rc), li, ri, agg, [grid, grid])
+    P, U = li.numel(), coords.shape[0]
+    desc = _device.describe("ij,jk->ik", (2, 2), (2, 2))
+    vals = lambda n: torch.ones((n, 2, 2), device="cuda")
+    st, res = _device.queued_segment_einsum(t(lc), t(rc), keys, [grid], agg, [grid, grid], desc,
+                                            vals(n_lhs), vals(n_rhs), P + slack)
+    assert st == "ok", st
+    Pq, cq, oq, pq, _, liq, riq = res
+    assert Pq == P
+    for got, want in ((liq, li), (riq, ri), (cq, coords), (oq, off), (pq, perm)):
+        assert torch.equal(got, want)
+    assert U == cq.shape[0]
+
+
 def _device_mod():
     from einjax_amd import _device
 
