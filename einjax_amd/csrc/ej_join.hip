@@ -670,13 +670,24 @@ __global__ void pair_keys_kernel(const int32_t *lc, const int32_t *rc, const int
 // hist (optional, zeroed): the sort's first-pass digit histogram, block-major
 // over sort blocks of `tile` keys (a multiple of the block size, so each
 // block's pairs fall in one sort block), counted here in LDS and added once
-// per digit.
+// per digit.  WIDE: instead, whist (zeroed, int32) counts every key value
+// (keys below wk = 2^bits <= kOnePassMaxKeys) per block of kOnePassTile
+// pairs, for the one-pass plan, and perm is not written (the plan uses the
+// pair index itself).
+constexpr int kOnePassMaxBits = 12;
+constexpr int kOnePassMaxKeys = 1 << kOnePassMaxBits;
+constexpr int kOnePassThreads = 512;
+constexpr int kOnePassItems = 8;  // rounds of 64 pairs per wave
+constexpr int64_t kOnePassTile = static_cast<int64_t>(kOnePassThreads) * kOnePassItems;
+constexpr int64_t kOnePassMaxBlocks = 8;
+
+template <bool WIDE>
 __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
     const int64_t *offs, int64_t n_rhs, const int64_t *lo, const int32_t *lhs_perm, int64_t cap,
     const int64_t *jscal, const int32_t *lc, const int32_t *rc, AggSpec a, int64_t *lhs_idx,
     int64_t *rhs_idx, uint64_t *keys, int32_t *perm, int64_t *sscal, int64_t *hist,
-    int64_t tile) {
-  __shared__ int digit_count[256];
+    int64_t tile, int32_t *whist, int wk) {
+  __shared__ int digit_count[WIDE ? kOnePassMaxKeys : 256];
   const int64_t P = jscal[0];
   const int64_t n = P < cap ? P : cap;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -685,7 +696,10 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
     sscal[4] = P;
     sscal[5] = jscal[1];
   }
-  if (hist) {
+  if constexpr (WIDE) {
+    for (int d = threadIdx.x; d < wk; d += kBlock) digit_count[d] = 0;
+    __syncthreads();
+  } else if (hist) {
     digit_count[threadIdx.x] = 0;
     __syncthreads();
   }
@@ -694,7 +708,7 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
     const int64_t l = lhs_perm[lo[j] + (q - offs[j])];
     lhs_idx[q] = l;
     rhs_idx[q] = j;
-    perm[q] = static_cast<int32_t>(q);
+    if constexpr (!WIDE) perm[q] = static_cast<int32_t>(q);
     const int32_t *lrow = lc + l * a.lncols;
     const int32_t *rrow = rc + j * a.rncols;
     uint64_t key = 0;
@@ -709,15 +723,154 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
     }
     keys[q] = key;
     if (b) atomicOr(reinterpret_cast<int *>(sscal + 1), 1);
-    if (hist) atomicAdd(&digit_count[key & 255], 1);
+    if constexpr (WIDE) atomicAdd(&digit_count[key], 1);
+    else if (hist) atomicAdd(&digit_count[key & 255], 1);
   }
-  if (hist) {
+  if constexpr (WIDE) {
+    __syncthreads();
+    const int64_t sb = static_cast<int64_t>(blockIdx.x) * kBlock / kOnePassTile;
+    for (int d = threadIdx.x; d < wk; d += kBlock) {
+      const int c = digit_count[d];
+      if (c) atomicAdd(whist + sb * wk + d, c);
+    }
+  } else if (hist) {
     __syncthreads();
     const int c = digit_count[threadIdx.x];
     if (c) {
       const int64_t sb = static_cast<int64_t>(blockIdx.x) * blockDim.x / tile;
       atomicAdd(reinterpret_cast<unsigned long long *>(hist + sb * 256 + threadIdx.x),
                 static_cast<unsigned long long>(c));
+    }
+  }
+}
+
+// One-pass segment plan for output keys of at most kOnePassMaxBits bits and
+// at most kOnePassMaxBlocks * kOnePassTile pairs: the key is a single radix
+// digit, so one stable counting sort orders the pairs, and the key histogram
+// (whist, per block of kOnePassTile pairs, from the pair fill) also gives the
+// segments: segment u is the u-th key value that occurs, starting at that
+// value's first sorted position.  Every block derives the sorted start of
+// each key value for its own pairs: counts of the earlier blocks (all
+// histogram rows read at once, each thread's loads independent) plus an
+// exclusive scan of the totals.  Each wave then ranks its own contiguous
+// eighth of the block's pairs (keys loaded up front) in rounds of 64 with
+// ballot peer masks and a wave-private count per key value in LDS, with no
+// workgroup barrier; the waves' totals give their offsets, and every pair
+// lands at key start + earlier waves' counts + its rank.  The blocks share
+// writing the segments (seg_offsets, out_coords decoded by the radices);
+// block 0 stores U = sscal[0] and the end offset.  perm receives the pair
+// indices in sorted order.
+__global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
+    const uint64_t *__restrict__ keys, const int32_t *__restrict__ whist, int64_t nblocks,
+    int wk, int bits, AggSpec a, int64_t seg_cap, int32_t *__restrict__ perm,
+    int32_t *__restrict__ seg_offsets, int32_t *__restrict__ out_coords,
+    int64_t *__restrict__ sscal) {
+  constexpr int NT = kOnePassThreads, NW = NT / 64;
+  constexpr int DPT = kOnePassMaxKeys / NT;          // key values per thread
+  constexpr int RPW = kOnePassItems;                  // rounds of 64 per wave
+  constexpr int64_t WSPAN = static_cast<int64_t>(RPW) * 64;  // pairs per wave
+  __shared__ int32_t base_off[kOnePassMaxKeys];
+  __shared__ int32_t seg_rank[kOnePassMaxKeys];
+  __shared__ uint16_t wcnt[NW][kOnePassMaxKeys];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t n = sscal[2];
+  const int64_t blk = blockIdx.x;
+  const int64_t wbase = blk * kOnePassTile + wave * WSPAN;
+  uint32_t kk[RPW];  // this lane's keys, loaded before anything waits
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t i = wbase + r * 64 + lane;
+    kk[r] = i < n ? static_cast<uint32_t>(keys[i]) : 0u;
+  }
+  int32_t c[kOnePassMaxBlocks][DPT];
+#pragma unroll
+  for (int b = 0; b < kOnePassMaxBlocks; ++b)
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) {
+      const int d = tid + j * NT;
+      c[b][j] = b < nblocks && d < wk ? whist[b * wk + d] : 0;
+    }
+  for (int x = tid; x < NW * kOnePassMaxKeys / 2; x += NT)
+    reinterpret_cast<uint32_t *>(&wcnt[0][0])[x] = 0u;
+#pragma unroll
+  for (int j = 0; j < DPT; ++j) {
+    int32_t tot = 0, before = 0;
+#pragma unroll
+    for (int b = 0; b < kOnePassMaxBlocks; ++b) {
+      tot += c[b][j];
+      before += b < blk ? c[b][j] : 0;
+    }
+    const int d = tid + j * NT;
+    if (d < wk) {
+      base_off[d] = tot;
+      seg_rank[d] = before;
+    }
+  }
+  __syncthreads();
+  // Exclusive scans over the key values, each thread a contiguous run:
+  // sorted start (from totals) and segment rank (from totals > 0).
+  const int per = (wk + NT - 1) / NT;
+  const int d0 = min(wk, tid * per), d1 = min(wk, d0 + per);
+  int64_t sum_t = 0, sum_f = 0;
+  for (int d = d0; d < d1; ++d) {
+    sum_t += base_off[d];
+    sum_f += base_off[d] > 0 ? 1 : 0;
+  }
+  int64_t all_t, all_f;
+  int64_t run_t = block_exclusive_sum<NT>(sum_t, &all_t);
+  int64_t run_f = block_exclusive_sum<NT>(sum_f, &all_f);
+  for (int d = d0; d < d1; ++d) {
+    const int32_t t = base_off[d], bf = seg_rank[d];
+    if (t > 0 && run_f < seg_cap && (static_cast<int64_t>(d) * nblocks) / wk == blk) {
+      seg_offsets[run_f] = static_cast<int32_t>(run_t);
+      uint32_t key = static_cast<uint32_t>(d);
+      for (int cc = a.n - 1; cc >= 0; --cc) {
+        const uint32_t rad = static_cast<uint32_t>(a.radix[cc]);
+        out_coords[run_f * a.n + cc] = static_cast<int32_t>(key % rad);
+        key /= rad;
+      }
+    }
+    base_off[d] = static_cast<int32_t>(run_t) + bf;
+    run_t += t;
+    run_f += t > 0 ? 1 : 0;
+  }
+  if (blk == 0 && tid == 0) {
+    sscal[0] = all_f;
+    if (all_f <= seg_cap) seg_offsets[all_f] = static_cast<int32_t>(n);
+  }
+  // Wave-local stable ranks: rounds of 64 consecutive pairs; the lanes of a
+  // key value read its running count, then its first lane adds the round's
+  // count.  LDS operations of one wave execute in order; the waits and
+  // compiler barriers keep them in program order.
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint16_t rank[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const bool valid = wbase + r * 64 + lane < n;
+    const int d = static_cast<int>(kk[r]);
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+      const int bit = (d >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    asm volatile("" ::: "memory");
+    const int run = valid ? wcnt[wave][d] : 0;
+    rank[r] = static_cast<uint16_t>(run + __popcll(peers & lt_mask));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (valid && (peers & lt_mask) == 0)
+      wcnt[wave][d] = static_cast<uint16_t>(run + __popcll(peers));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t i = wbase + r * 64 + lane;
+    if (i < n) {
+      const int d = static_cast<int>(kk[r]);
+      int pos = base_off[d] + rank[r];
+      for (int w = 0; w < wave; ++w) pos += wcnt[w][d];
+      if (pos < n) perm[pos] = static_cast<int32_t>(i);
     }
   }
 }
@@ -804,9 +957,12 @@ struct SegWs {
   uint64_t *keys, *keys_alt;
   int32_t *perm, *perm_alt;
   int64_t *flags, *excl;
+  int32_t *whist;  // one-pass plan key histogram (pair counts up to the one-pass limit)
   void *sort_ws, *scan_ws;
   size_t bytes;
 };
+
+int64_t one_pass_blocks(int64_t n) { return ceil_div(n, kOnePassTile); }
 
 SegWs carve_seg(void *base, int64_t n) {
   Carver c(base);
@@ -818,6 +974,8 @@ SegWs carve_seg(void *base, int64_t n) {
   w.perm_alt = c.take<int32_t>(n);
   w.flags = c.take<int64_t>(n);
   w.excl = c.take<int64_t>(n);
+  const int64_t nb = one_pass_blocks(n);
+  w.whist = c.take<int32_t>(nb <= kOnePassMaxBlocks ? nb * kOnePassMaxKeys : 0);
   w.sort_ws = c.take<char>(static_cast<int64_t>(sort_workspace_bytes(n)));
   w.scan_ws = c.take<char>(static_cast<int64_t>(scan_workspace_bytes(n)));
   w.bytes = c.off;
@@ -1051,25 +1209,50 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
   SegWs sw = carve_seg(seg_workspace, pair_capacity);
   EJ_CHECK_ARG(seg_workspace && seg_workspace_bytes >= sw.bytes,
                "segment workspace too small: %zu < %zu bytes", seg_workspace_bytes, sw.bytes);
+  const bool small_join = join_small_ok(EJ_ORDER_PROBE, n_lhs, n_rhs);
+  JoinWs jw = carve_join(join_workspace, n_lhs, n_rhs, EJ_ORDER_PROBE);
+  int64_t known = -1;
+  int64_t *jscal = nullptr;
+  // Output keys of at most kOnePassMaxBits bits: one counting-sort pass that
+  // also yields the segments (the join count clears its histogram).
+  const int64_t nb1 = one_pass_blocks(pair_capacity);
+  if (small_join && sbits >= 1 && sbits <= kOnePassMaxBits && nb1 <= kOnePassMaxBlocks) {
+    const int wk = 1 << sbits;
+    EJ_TRY(join_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
+                              lhs_dims, rhs_dims, join_radices, EJ_ORDER_PROBE, join_workspace,
+                              join_workspace_bytes, &known, &jscal, stream, sw.scalars,
+                              reinterpret_cast<int64_t *>(sw.whist),
+                              static_cast<int>(nb1 * wk / 2)));
+    EJ_CHECK_ARG(known < 0, "internal: join size known on the host");
+    hipLaunchKernelGGL(fill_probe_keys_kernel<true>, dim3(grid_for(pair_capacity)), dim3(kBlock),
+                       0, stream, jw.offs, n_rhs, jw.lo, jw.lperm, pair_capacity, jw.scalars,
+                       lhs_coords, rhs_coords, a, lhs_idx, rhs_idx, sw.keys, nullptr, sw.scalars,
+                       nullptr, int64_t(0), sw.whist, wk);
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(plan_one_pass_kernel, dim3(static_cast<unsigned>(nb1)),
+                       dim3(kOnePassThreads), 0,
+                       stream, sw.keys, sw.whist, nb1, wk, sbits, a, seg_capacity, perm,
+                       seg_offsets, out_coords, sw.scalars);
+    EJ_LAUNCH_CHECK();
+    EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost,
+                          stream));
+    return EJ_OK;
+  }
   // The fill also counts the sort's first-pass digits when the join count
   // (one workgroup) can clear that histogram and the sort reads it inline.
   const SortTiling st = sort_tiling(pair_capacity);
-  const bool fill_hist = pair_capacity > 1 && sbits > 0 && st.inline_offsets &&
-                         join_small_ok(EJ_ORDER_PROBE, n_lhs, n_rhs);
+  const bool fill_hist = pair_capacity > 1 && sbits > 0 && st.inline_offsets && small_join;
   int64_t *hist = fill_hist ? static_cast<int64_t *>(sw.sort_ws) : nullptr;
-  int64_t known = -1;
-  int64_t *jscal = nullptr;
   EJ_TRY(join_count_enqueue(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
                             lhs_dims, rhs_dims, join_radices, EJ_ORDER_PROBE, join_workspace,
                             join_workspace_bytes, &known, &jscal, stream, sw.scalars, hist,
                             static_cast<int>(st.nblocks * 256)));
   EJ_CHECK_ARG(known < 0, "internal: join size known on the host");
-  JoinWs jw = carve_join(join_workspace, n_lhs, n_rhs, EJ_ORDER_PROBE);
   const bool alt = pair_capacity > 1 && (radix_passes(sbits) & 1);
-  hipLaunchKernelGGL(fill_probe_keys_kernel, dim3(grid_for(pair_capacity)), dim3(kBlock), 0,
-                     stream, jw.offs, n_rhs, jw.lo, jw.lperm, pair_capacity, jw.scalars,
+  hipLaunchKernelGGL(fill_probe_keys_kernel<false>, dim3(grid_for(pair_capacity)), dim3(kBlock),
+                     0, stream, jw.offs, n_rhs, jw.lo, jw.lperm, pair_capacity, jw.scalars,
                      lhs_coords, rhs_coords, a, lhs_idx, rhs_idx, alt ? sw.keys_alt : sw.keys,
-                     alt ? sw.perm_alt : sw.perm, sw.scalars, hist, st.tile);
+                     alt ? sw.perm_alt : sw.perm, sw.scalars, hist, st.tile, nullptr, 0);
   EJ_LAUNCH_CHECK();
   const int64_t *live = sw.scalars + 2;
   EJ_TRY(sort_pairs_u64(sw.keys, sw.perm, sw.keys_alt, sw.perm_alt, pair_capacity, sbits,

@@ -821,15 +821,20 @@ def test_queued_step_large_join(gpu, monkeypatch):
     assert statuses == ["ok", "range"]
 
 
-@pytest.mark.parametrize("n_lhs,n_rhs,grid,slack", [(300, 500, 40, 0), (1000, 3000, 100, 7), (3000, 8000, 64, 5),
-                                                    (4000, 8192, 48, 1000), (6000, 9000, 80, 0)])
+@pytest.mark.parametrize("n_lhs,n_rhs,grid,slack", [
+    (300, 500, 40, 0), (50, 60, 2, 3), (700, 1800, 64, 9), (1000, 2100, 64, 0),  # one pass
+    (1000, 2100, 64, 100), (1000, 3000, 90, 0), (1000, 8000, 64, 11), (1000, 3000, 100, 7),
+    (3000, 8000, 64, 5), (4000, 8192, 48, 1000), (6000, 9000, 80, 0)])
 def test_pair_plan_matches_exact_phases(gpu, n_lhs, n_rhs, grid, slack):
     """ej_pair_plan_async (join count and fill, output keys, sort, flag scan
     and segment fill in one call) against the separate exact phases: pairs,
-    output coordinates, offsets and permutation bit-exact, for one-workgroup
-    and general joins, sorts whose first histogram comes from the pair fill
-    and sorts above the inline-offset tiling (more than 65536 pairs), with a
-    pair capacity equal to P or above it."""
+    output coordinates, offsets and permutation bit-exact.  Covered: the
+    one-pass plan (output keys of 2 to 12 bits, up to 32768 pairs: 32,685
+    pairs, and the same with a capacity past the limit, which takes the
+    general plan), one-workgroup and general joins,
+    radix sorts whose first histogram comes from the pair fill and sorts
+    above the inline-offset tiling (more than 65536 pairs), with a pair
+    capacity equal to P or above it."""
     note("pair plan", n_lhs, n_rhs, grid, slack)
     from einjax_amd import _device
 
