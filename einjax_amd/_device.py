@@ -4,8 +4,9 @@ Every function takes and returns torch tensors resident on the current
 GPU; torch supplies the memory and the current stream, all arithmetic runs
 in the library's kernels.  Sizes that depend on the data (pairs, segments,
 tiles) come back through the library's *_count calls, one host
-synchronisation each, or, in queued_segment_einsum, through pinned host
-memory read at an event while the einsum is already queued.
+synchronisation each, or, in queued_segment_einsum, through coherent host
+memory that the plan fills and marks with a ticket while the einsum is
+already queued.
 """
 
 from __future__ import annotations
@@ -217,22 +218,40 @@ def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_off
 
 
 class _Counts(threading.local):
-    """Per-thread pinned count buffer (the counts of ej_pair_plan_async: U,
-    plan range flag, pairs planned, -, P, join range flag) and the event that
-    marks when the queued counts have landed."""
+    """Per-thread count buffer in coherent host memory (ej_host_alloc, kept
+    for the thread's lifetime): the counts of ej_pair_plan_async (U, plan
+    range flag, pairs planned, -, P, join range flag) and, in slot 6, the
+    ticket of the call whose counts they are."""
 
-    buf: torch.Tensor | None = None
-    event: torch.cuda.Event | None = None
+    addr: int = 0
+    view = None
+    ticket: int = 0
 
 
 _counts = _Counts()
 
 
-def _count_buffer() -> tuple[torch.Tensor, torch.cuda.Event]:
-    if _counts.buf is None:
-        _counts.buf = torch.zeros(8, dtype=torch.int64, pin_memory=True)
-        _counts.event = torch.cuda.Event()
-    return _counts.buf, _counts.event
+def _count_buffer():
+    """(host address, int64[8] view, new ticket) of this thread's count buffer."""
+    if not _counts.addr:
+        p = ctypes.c_void_p()
+        check(_lib.load().ej_host_alloc(64, ctypes.byref(p)), "ej_host_alloc")
+        _counts.addr = p.value
+        _counts.view = (ctypes.c_int64 * 8).from_address(p.value)
+    _counts.ticket = _counts.ticket % (1 << 30) + 1
+    return _counts.addr, _counts.view, _counts.ticket
+
+
+def _wait_ticket(view, ticket: int) -> None:
+    """Waits until the GPU has stored `ticket` in view[6] (it stores the
+    counts first).  Spins briefly, then synchronizes the stream and checks
+    once more, so an error that stops the stream cannot leave it spinning."""
+    for _ in range(200000):
+        if view[6] == ticket:
+            return
+    torch.cuda.current_stream().synchronize()
+    if view[6] != ticket:
+        raise RuntimeError("the queued plan did not report its counts")
 
 
 def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys,
@@ -240,8 +259,9 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
                           out_dtype=None):
     """Join, segment plan and fused segment einsum queued back to back on the
     current stream, with the pair count bounded by pair_bound instead of
-    read first.  The host waits only for an event recorded after the plan's
-    count (the einsum is already queued behind it), then checks the counts.
+    read first.  The plan stores its counts in coherent host memory followed
+    by this call's ticket; the host waits only for the ticket (the einsum is
+    already queued behind the plan), then checks the counts.
 
     Returns (status, result).  status "ok": result = (P, coords [U, n_out],
     seg_offsets, perm, values [U, *out_tile], li, ri), views clipped to the
@@ -259,8 +279,7 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     cap_p = max(int(pair_bound), 1)
     cap_u = max(1, min(cap_p, prod(agg_radices)))
     n_out = len(agg_keys)
-    buf, event = _count_buffer()
-    base = buf.data_ptr()
+    base, counts, ticket = _count_buffer()
     stream = stream_ptr()
     order = _lib.EJ_ORDER_PROBE
     # Every buffer first, so that the launches below reach the GPU back to back.
@@ -289,14 +308,13 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
         ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
         ldims, rdims, jrad, n_out, src, dim, rad, cap_p, ptr(jws), jws.numel(), ptr(sws),
         sws.numel(), ptr(li), ptr(ri), ptr(coords), ptr(offsets), ptr(perm), cap_u,
-        ctypes.c_void_p(base), stream), "ej_pair_plan_async")
-    event.record()
+        ctypes.c_void_p(base), ticket, stream), "ej_pair_plan_async")
     check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                       lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
                                       ptr(perm), ptr(offsets), cap_u, ptr(sws), ptr(out), stream),
           "ej_segment_einsum_async")
-    event.synchronize()
-    U, bad_plan, _, _, P, bad_join = (int(x) for x in buf.tolist()[:6])
+    _wait_ticket(counts, ticket)
+    U, bad_plan, _, _, P, bad_join = (int(counts[i]) for i in range(6))
     if bad_join:
         return "range", None
     if P > cap_p:

@@ -108,7 +108,9 @@ SIGNATURES = {
                                    _sz, _P_i64, _P_i64, _vp]),
     "ej_pair_plan_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32, _P_i64,
                                   _i32, _P_i32, _P_i32, _P_i64, _i64, _vp, _sz, _vp, _sz, _vp,
-                                  _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+                                  _vp, _vp, _vp, _vp, _i64, _vp, _i32, _vp]),
+    "ej_host_alloc": (_i32, [_sz, ctypes.POINTER(_vp)]),
+    "ej_host_free": (_i32, [_vp]),
     "ej_index_plan_workspace_size": (_i32, [_i64, _P_sz]),
     "ej_index_plan": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
     "ej_pair_einsum_vjp_workspace_size": (_i32, [_i64, _i64, _i64, _i64, _i64, _i32, _i32,

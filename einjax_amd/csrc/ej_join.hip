@@ -758,13 +758,15 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
 // workgroup barrier; the waves' totals give their offsets, and every pair
 // lands at key start + earlier waves' counts + its rank.  The blocks share
 // writing the segments (seg_offsets, out_coords decoded by the radices);
-// block 0 stores U = sscal[0] and the end offset.  perm receives the pair
-// indices in sorted order.
+// block 0 stores U = sscal[0] and the end offset, and, given host_counts
+// (coherent host memory), the six counts there, then the caller's ticket in
+// host_counts[6], each step fenced at system scope, so that a host that sees
+// the ticket sees the counts.  perm receives the pair indices in sorted order.
 __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ whist, int64_t nblocks,
     int wk, int bits, AggSpec a, int64_t seg_cap, int32_t *__restrict__ perm,
     int32_t *__restrict__ seg_offsets, int32_t *__restrict__ out_coords,
-    int64_t *__restrict__ sscal) {
+    int64_t *__restrict__ sscal, int64_t *__restrict__ host_counts, int64_t ticket) {
   constexpr int NT = kOnePassThreads, NW = NT / 64;
   constexpr int DPT = kOnePassMaxKeys / NT;          // key values per thread
   constexpr int RPW = kOnePassItems;                  // rounds of 64 per wave
@@ -837,6 +839,17 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
   if (blk == 0 && tid == 0) {
     sscal[0] = all_f;
     if (all_f <= seg_cap) seg_offsets[all_f] = static_cast<int32_t>(n);
+    if (host_counts) {
+      host_counts[0] = all_f;
+      host_counts[1] = sscal[1];
+      host_counts[2] = n;
+      host_counts[3] = 0;
+      host_counts[4] = sscal[4];
+      host_counts[5] = sscal[5];
+      __threadfence_system();
+      host_counts[6] = ticket;
+      __threadfence_system();
+    }
   }
   // Wave-local stable ranks: rounds of 64 consecutive pairs; the lanes of a
   // key value read its running count, then its first lane adds the round's
@@ -873,6 +886,13 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
       if (pos < n) perm[pos] = static_cast<int32_t>(i);
     }
   }
+}
+
+// Stores a caller's ticket into coherent host memory, fenced at system scope.
+__global__ void store_ticket_kernel(int64_t *host_slot, int64_t ticket) {
+  __threadfence_system();
+  *host_slot = ticket;
+  __threadfence_system();
 }
 
 __global__ void seg_flags_kernel(const uint64_t *skeys, int64_t n, const int64_t *n_dev,
@@ -1190,7 +1210,7 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
                                   void *seg_workspace, size_t seg_workspace_bytes,
                                   int64_t *lhs_idx, int64_t *rhs_idx, int32_t *out_coords,
                                   int32_t *seg_offsets, int32_t *perm, int64_t seg_capacity,
-                                  int64_t *counts, ej_stream_t stream_) {
+                                  int64_t *counts, int32_t counts_direct, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
   EJ_CHECK_ARG(counts && lhs_idx && rhs_idx && seg_offsets && perm &&
@@ -1211,6 +1231,10 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
                "segment workspace too small: %zu < %zu bytes", seg_workspace_bytes, sw.bytes);
   const bool small_join = join_small_ok(EJ_ORDER_PROBE, n_lhs, n_rhs);
   JoinWs jw = carve_join(join_workspace, n_lhs, n_rhs, EJ_ORDER_PROBE);
+  EJ_CHECK_ARG(counts_direct >= 0, "negative counts_direct");
+  int64_t *direct = nullptr;  // device address of counts when the kernels store them
+  if (counts_direct)
+    EJ_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&direct), counts, 0));
   int64_t known = -1;
   int64_t *jscal = nullptr;
   // Output keys of at most kOnePassMaxBits bits: one counting-sort pass that
@@ -1232,10 +1256,11 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
     hipLaunchKernelGGL(plan_one_pass_kernel, dim3(static_cast<unsigned>(nb1)),
                        dim3(kOnePassThreads), 0,
                        stream, sw.keys, sw.whist, nb1, wk, sbits, a, seg_capacity, perm,
-                       seg_offsets, out_coords, sw.scalars);
+                       seg_offsets, out_coords, sw.scalars, direct, int64_t(counts_direct));
     EJ_LAUNCH_CHECK();
-    EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost,
-                          stream));
+    if (!direct)
+      EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost,
+                            stream));
     return EJ_OK;
   }
   // The fill also counts the sort's first-pass digits when the join count
@@ -1273,6 +1298,11 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
     EJ_LAUNCH_CHECK();
   }
   EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  if (direct) {  // the ticket after the copy, in stream order
+    hipLaunchKernelGGL(store_ticket_kernel, dim3(1), dim3(1), 0, stream, direct + 6,
+                       int64_t(counts_direct));
+    EJ_LAUNCH_CHECK();
+  }
   return EJ_OK;
 }
 

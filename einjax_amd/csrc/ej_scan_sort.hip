@@ -367,4 +367,30 @@ int sort_pairs_u64(uint64_t *keys, int32_t *vals, uint64_t *keys_alt, int32_t *v
 
 extern "C" int ej_version(void) { return EJ_ABI_VERSION; }
 
+extern "C" int ej_host_alloc(size_t bytes, void **host_ptr) {
+  ej::clear_error();
+  if (!host_ptr || bytes == 0) {
+    ej::set_error("ej_host_alloc: null pointer or zero size");
+    return EJ_E_INVAL;
+  }
+  *host_ptr = nullptr;
+  const hipError_t e = hipHostMalloc(host_ptr, bytes, hipHostMallocMapped | hipHostMallocCoherent);
+  if (e != hipSuccess) {
+    ej::set_error("hipHostMalloc failed: %s", hipGetErrorString(e));
+    return EJ_E_HIP;
+  }
+  return EJ_OK;
+}
+
+extern "C" int ej_host_free(void *host_ptr) {
+  ej::clear_error();
+  if (!host_ptr) return EJ_OK;
+  const hipError_t e = hipHostFree(host_ptr);
+  if (e != hipSuccess) {
+    ej::set_error("hipHostFree failed: %s", hipGetErrorString(e));
+    return EJ_E_HIP;
+  }
+  return EJ_OK;
+}
+
 extern "C" const char *ej_last_error(void) { return ej::g_error.c_str(); }

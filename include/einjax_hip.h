@@ -265,7 +265,12 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
  * seg_capacity segments.  counts (pinned host memory, 6 int64) receives, in
  * stream order: counts[0] = U, [1] = plan range flag, [2] = pairs planned
  * min(P, pair_capacity), [4] = P, [5] = join range flag; P > pair_capacity
- * or U > seg_capacity means the plan is incomplete. */
+ * or U > seg_capacity means the plan is incomplete.  counts_direct > 0
+ * declares counts coherent host memory from ej_host_alloc, of 8 int64: a plan
+ * kernel may then store the counts there itself instead of a copy following
+ * it, and counts[6] = counts_direct (a caller's ticket) is stored after them
+ * in stream order, so that a host may wait for the ticket instead of an
+ * event. */
 int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
@@ -275,7 +280,12 @@ int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
                        void *seg_workspace, size_t seg_workspace_bytes, int64_t *lhs_idx,
                        int64_t *rhs_idx, int32_t *out_coords, int32_t *seg_offsets,
                        int32_t *perm, int64_t seg_capacity, int64_t *counts,
-                       ej_stream_t stream);
+                       int32_t counts_direct, ej_stream_t stream);
+
+/* Coherent, device-mapped host memory (hipHostMalloc, mapped | coherent) for
+ * counts that kernels store directly (ej_pair_plan_async, counts_direct). */
+int ej_host_alloc(size_t bytes, void **host_ptr);
+int ej_host_free(void *host_ptr);
 
 /* ---- gather (reference: values[indices], sparse_dispatch.py:118-119) ---- */
 /* out[i] = values[idx[i]] for whole tiles of tile_bytes each.  Indices
