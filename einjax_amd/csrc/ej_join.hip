@@ -166,11 +166,21 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   __shared__ int bad_any;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  // This thread's probe rows [plo, phi), at most PPT, packed first so that
+  // their loads overlap the build side's.
+  constexpr int PPT = static_cast<int>(kProbeSmallMax / kJoinSmallThreads);
+  const int64_t pc = (n_probe + kJoinSmallThreads - 1) / kJoinSmallThreads;
+  const int64_t plo = min(n_probe, static_cast<int64_t>(tid) * pc);
+  const int64_t phi = min(n_probe, plo + pc);
+  int bad = 0;
+  uint64_t pk[PPT];
+#pragma unroll
+  for (int u = 0; u < PPT; ++u)
+    pk[u] = plo + u < phi ? pack_key(rc + (plo + u) * rks.ncols, rks, &bad) : 0;
   if (tid == 0) bad_any = 0;
   if (tid < n_clear) clear[tid] = 0;
   for (int i = tid; i < n_clear2; i += kJoinSmallThreads) clear2[i] = 0;
   __syncthreads();
-  int bad = 0;
   for (int i = tid; i < n_build; i += kJoinSmallThreads) {
     skey[0][i] = pack_key(lc + static_cast<int64_t>(i) * lks.ncols, lks, &bad);
     sidx[0][i] = i;
@@ -244,47 +254,42 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   __syncthreads();
   for (int i = tid; i < n_build; i += kJoinSmallThreads) lperm[i] = sidx[cur][i];
   const uint64_t *bk = skey[cur];
-  const int64_t c = (n_probe + kJoinSmallThreads - 1) / kJoinSmallThreads;
-  const int64_t lo = min(n_probe, static_cast<int64_t>(tid) * c);
-  const int64_t hi = min(n_probe, lo + c);
+  // Equal ranges of the PPT probe keys, searched side by side (branch-free,
+  // fixed trip count); the counts stay in registers for the scan.
+  int lb[PPT], ub[PPT];
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) lb[u] = ub[u] = 0;
+  // Invariant: the answer lies in [base, base + len]; base + len <= n_build.
+  for (int len = n_build; len > 1;) {
+    const int half = len >> 1;
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      if (u < pc) {  // pc is the same for every thread
+        lb[u] += bk[lb[u] + half] < pk[u] ? half : 0;
+        ub[u] += bk[ub[u] + half] <= pk[u] ? half : 0;
+      }
+    }
+    len -= half;
+  }
   int64_t s = 0;
-  for (int64_t j0 = lo; j0 < hi; j0 += kProbeBatch) {
-    uint64_t k[kProbeBatch];
-    int lb[kProbeBatch], ub[kProbeBatch];
 #pragma unroll
-    for (int u = 0; u < kProbeBatch; ++u) {
-      k[u] = j0 + u < hi ? pack_key(rc + (j0 + u) * rks.ncols, rks, &bad) : 0;
-      lb[u] = 0;
-      ub[u] = 0;
-    }
-    // Invariant: the answer lies in [base, base + len]; base + len <= n_build.
-    for (int len = n_build; len > 1;) {
-      const int half = len >> 1;
-#pragma unroll
-      for (int u = 0; u < kProbeBatch; ++u) {
-        lb[u] += bk[lb[u] + half] < k[u] ? half : 0;
-        ub[u] += bk[ub[u] + half] <= k[u] ? half : 0;
-      }
-      len -= half;
-    }
-#pragma unroll
-    for (int u = 0; u < kProbeBatch; ++u) {
-      lb[u] += bk[lb[u]] < k[u] ? 1 : 0;
-      ub[u] += bk[ub[u]] <= k[u] ? 1 : 0;
-      if (j0 + u < hi) {
-        lo_out[j0 + u] = lb[u];
-        offs[j0 + u] = ub[u] - lb[u];
-        s += ub[u] - lb[u];
-      }
+  for (int u = 0; u < PPT; ++u) {
+    lb[u] += bk[lb[u]] < pk[u] ? 1 : 0;
+    ub[u] += bk[ub[u]] <= pk[u] ? 1 : 0;
+    if (plo + u < phi) {
+      lo_out[plo + u] = lb[u];
+      s += ub[u] - lb[u];
     }
   }
   if (bad) bad_any = 1;
   int64_t tot;
   int64_t run = block_exclusive_sum<kJoinSmallThreads>(s, &tot);
-  for (int64_t j = lo; j < hi; ++j) {
-    const int64_t v = offs[j];
-    offs[j] = run;
-    run += v;
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) {
+    if (plo + u < phi) {
+      offs[plo + u] = run;
+      run += ub[u] - lb[u];
+    }
   }
   if (tid == 0) {
     scalars[0] = tot;
@@ -775,6 +780,7 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
   __shared__ int32_t seg_rank[kOnePassMaxKeys];
   __shared__ uint16_t wcnt[NW][kOnePassMaxKeys];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  (void)bits;  // ranks compare all kOnePassMaxBits bits (the keys lie below 2^bits)
   const int64_t n = sscal[2];
   const int64_t blk = blockIdx.x;
   const int64_t wbase = blk * kOnePassTile + wave * WSPAN;
@@ -813,14 +819,13 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
   // sorted start (from totals) and segment rank (from totals > 0).
   const int per = (wk + NT - 1) / NT;
   const int d0 = min(wk, tid * per), d1 = min(wk, d0 + per);
-  int64_t sum_t = 0, sum_f = 0;
-  for (int d = d0; d < d1; ++d) {
-    sum_t += base_off[d];
-    sum_f += base_off[d] > 0 ? 1 : 0;
-  }
-  int64_t all_t, all_f;
-  int64_t run_t = block_exclusive_sum<NT>(sum_t, &all_t);
-  int64_t run_f = block_exclusive_sum<NT>(sum_f, &all_f);
+  // Both prefixes in one scan: pair count (< 2^31) high, segment count low.
+  int64_t sum_tf = 0;
+  for (int d = d0; d < d1; ++d) sum_tf += (int64_t(base_off[d]) << 20) + (base_off[d] > 0 ? 1 : 0);
+  int64_t all_tf;
+  const int64_t run_tf = block_exclusive_sum<NT>(sum_tf, &all_tf);
+  int64_t run_t = run_tf >> 20, run_f = run_tf & ((int64_t(1) << 20) - 1);
+  const int64_t all_f = all_tf & ((int64_t(1) << 20) - 1);
   for (int d = d0; d < d1; ++d) {
     const int32_t t = base_off[d], bf = seg_rank[d];
     if (t > 0 && run_f < seg_cap && (static_cast<int64_t>(d) * nblocks) / wk == blk) {
@@ -862,7 +867,8 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
     const bool valid = wbase + r * 64 + lane < n;
     const int d = static_cast<int>(kk[r]);
     uint64_t peers = __ballot(valid);
-    for (int b = 0; b < bits; ++b) {
+#pragma unroll
+    for (int b = 0; b < kOnePassMaxBits; ++b) {  // keys lie below 2^bits <= 2^kOnePassMaxBits
       const int bit = (d >> b) & 1;
       const uint64_t m = __ballot(bit);
       peers &= bit ? m : ~m;
