@@ -297,6 +297,11 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
     odt = _set_out_dtype(desc, lhs_values, out_dtype)
     out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
+    # Groups of 4 segments per workgroup when the einsum runs grouped (its
+    # seg_group hint): the plan may also write their run order.
+    group = 4 if desc.seg_group > 0 and desc.seg_group % 4 == 0 else 0
+    order = torch.empty((cap_u + 3) // 4 if group else 1, dtype=torch.int32, device=dev)
+    order_written = ctypes.c_int32(0)
     ldims = i32_array([k[0] for k in join_keys])
     rdims = i32_array([k[1] for k in join_keys])
     jrad = i64_array(join_radices)
@@ -307,11 +312,14 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     check(lib.ej_pair_plan_async(
         ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
         ldims, rdims, jrad, n_out, src, dim, rad, cap_p, ptr(jws), jws.numel(), ptr(sws),
-        sws.numel(), ptr(li), ptr(ri), ptr(coords), ptr(offsets), ptr(perm), cap_u,
-        ctypes.c_void_p(base), ticket, stream), "ej_pair_plan_async")
+        sws.numel(), ptr(li), ptr(ri), ptr(coords), ptr(offsets), ptr(perm), cap_u, group,
+        ptr(order) if group else None, ctypes.byref(order_written), ctypes.c_void_p(base), ticket,
+        stream), "ej_pair_plan_async")
     check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                       lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
-                                      ptr(perm), ptr(offsets), cap_u, ptr(sws), ptr(out), stream),
+                                      ptr(perm), ptr(offsets), cap_u, ptr(sws),
+                                      ptr(order) if order_written.value else None, ptr(out),
+                                      stream),
           "ej_segment_einsum_async")
     _wait_ticket(counts, ticket)
     U, bad_plan, _, _, P, bad_join = (int(counts[i]) for i in range(6))

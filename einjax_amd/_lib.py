@@ -84,7 +84,7 @@ SIGNATURES = {
     "ej_segment_einsum": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64, _vp,
                                  _vp, _vp, _vp, _i64, _vp, _vp]),
     "ej_segment_einsum_async": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64,
-                                       _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
+                                       _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "ej_segment_sum": (_i32, [_vp, _i32, _i64, _vp, _vp, _i64, _vp, _vp]),
     "ej_bucket_workspace_size": (_i32, [_i32, _P_i64, _P_i64, _P_sz]),
     "ej_bucket_dense_count": (_i32, [_vp, _i32, _i32, _P_i64, _P_i64, _vp, _sz, _P_i64, _vp]),
@@ -108,7 +108,7 @@ SIGNATURES = {
                                    _sz, _P_i64, _P_i64, _vp]),
     "ej_pair_plan_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32, _P_i64,
                                   _i32, _P_i32, _P_i32, _P_i64, _i64, _vp, _sz, _vp, _sz, _vp,
-                                  _vp, _vp, _vp, _vp, _i64, _vp, _i32, _vp]),
+                                  _vp, _vp, _vp, _vp, _i64, _i32, _vp, _P_i32, _vp, _i32, _vp]),
     "ej_host_alloc": (_i32, [_sz, ctypes.POINTER(_vp)]),
     "ej_host_free": (_i32, [_vp]),
     "ej_index_plan_workspace_size": (_i32, [_i64, _P_sz]),

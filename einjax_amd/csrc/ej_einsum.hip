@@ -236,6 +236,7 @@ struct PairSrc {
   const int32_t *seg_off;      // null: one pair per segment
   int64_t n_a_tiles, n_b_tiles;
   const int64_t *n_live;       // non-null: segments >= *n_live are skipped (grid is a bound)
+  const int32_t *run_order;    // non-null: grouped launches run group run_order[b] as block b
 };
 
 // Whether the workgroup's segment lies beyond the device-side segment count.
@@ -1045,7 +1046,11 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
   }
   const int64_t bi = lb % g.batch;
   const int segs = G > 1 || !MULTI ? G : spw;
-  const int64_t seg0 = (lb / g.batch) * segs;
+  int64_t grp = lb / g.batch;
+  // A run order (heaviest groups first on each XCD) replaces the block's group.
+  if (G == 4 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1)
+    grp = ld_uniform(src.run_order, grp);
+  const int64_t seg0 = grp * segs;
   int64_t nseg = n_seg;
   if (src.n_live) {
     const int64_t live = ld_uniform(src.n_live, 0);
@@ -1838,7 +1843,7 @@ extern "C" int ej_pair_einsum(const ej_einsum_desc *desc, int32_t dtype, const v
                               const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
                               void *out, ej_stream_t stream) {
   clear_error();
-  PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles, nullptr};
+  PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles, nullptr, nullptr};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_pairs, out, as_stream(stream));
 }
 
@@ -1850,7 +1855,7 @@ extern "C" int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, cons
                                  ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || n_segments == 0, "seg_offsets is null");
-  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, nullptr};
+  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, nullptr, nullptr};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_segments, out,
                        as_stream(stream));
 }
@@ -1861,11 +1866,13 @@ extern "C" int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype
                                        const int64_t *lhs_idx, const int64_t *rhs_idx,
                                        const int32_t *perm, const int32_t *seg_offsets,
                                        int64_t max_segments, const int64_t *n_segments_dev,
-                                       void *out, ej_stream_t stream) {
+                                       const int32_t *run_order, void *out,
+                                       ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || max_segments == 0, "seg_offsets is null");
   EJ_CHECK_ARG(n_segments_dev, "n_segments_dev is null");
-  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, n_segments_dev};
+  PairSrc src{lhs_idx, rhs_idx,     perm,           seg_offsets,
+              n_lhs_tiles, n_rhs_tiles, n_segments_dev, run_order};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, max_segments, out,
                        as_stream(stream));
 }

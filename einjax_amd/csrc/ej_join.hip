@@ -767,11 +767,19 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
 // (coherent host memory), the six counts there, then the caller's ticket in
 // host_counts[6], each step fenced at system scope, so that a host that sees
 // the ticket sees the counts.  perm receives the pair indices in sorted order.
+// Given run_order, the blocks also write the order in which a grouped einsum
+// (groups of `group` consecutive segments, ceil(seg_cap / group) workgroups)
+// should run them: the workgroups of each XCD (the contiguous chunks that the
+// einsum's XCD mapping assigns) take their chunk's groups in descending pair
+// count (counts above 255 tie), ties by index, so that the longest groups
+// start first.  Chunk x is ordered by wave x of block x % nblocks: a counting
+// sort over the 256 count classes, ranked in index order with ballots.
 __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ whist, int64_t nblocks,
     int wk, int bits, AggSpec a, int64_t seg_cap, int32_t *__restrict__ perm,
     int32_t *__restrict__ seg_offsets, int32_t *__restrict__ out_coords,
-    int64_t *__restrict__ sscal, int64_t *__restrict__ host_counts, int64_t ticket) {
+    int64_t *__restrict__ sscal, int64_t *__restrict__ host_counts, int64_t ticket,
+    int group, int32_t *__restrict__ run_order) {
   constexpr int NT = kOnePassThreads, NW = NT / 64;
   constexpr int DPT = kOnePassMaxKeys / NT;          // key values per thread
   constexpr int RPW = kOnePassItems;                  // rounds of 64 per wave
@@ -779,6 +787,8 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
   __shared__ int32_t base_off[kOnePassMaxKeys];
   __shared__ int32_t seg_rank[kOnePassMaxKeys];
   __shared__ uint16_t wcnt[NW][kOnePassMaxKeys];
+  __shared__ int32_t seglen[kOnePassMaxKeys];  // pairs of segment u (run order only)
+  __shared__ int32_t cls_base[NW][256];         // per-wave count-class offsets (run order)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   (void)bits;  // ranks compare all kOnePassMaxBits bits (the keys lie below 2^bits)
   const int64_t n = sscal[2];
@@ -826,8 +836,10 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
   const int64_t run_tf = block_exclusive_sum<NT>(sum_tf, &all_tf);
   int64_t run_t = run_tf >> 20, run_f = run_tf & ((int64_t(1) << 20) - 1);
   const int64_t all_f = all_tf & ((int64_t(1) << 20) - 1);
+  const bool order = run_order && group > 0;
   for (int d = d0; d < d1; ++d) {
     const int32_t t = base_off[d], bf = seg_rank[d];
+    if (order && t > 0) seglen[run_f] = t;
     if (t > 0 && run_f < seg_cap && (static_cast<int64_t>(d) * nblocks) / wk == blk) {
       seg_offsets[run_f] = static_cast<int32_t>(run_t);
       uint32_t key = static_cast<uint32_t>(d);
@@ -854,6 +866,71 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
       __threadfence_system();
       host_counts[6] = ticket;
       __threadfence_system();
+    }
+  }
+  if (order) {
+    // Group pair counts (segments beyond U count 0), then per XCD chunk a
+    // stable counting sort of its groups by descending count class.
+    __syncthreads();
+    const int64_t ngroups = (seg_cap + group - 1) / group;  // <= kOnePassMaxKeys
+    int32_t *glen = seg_rank;  // reused: no longer read
+    for (int64_t g = tid; g < ngroups; g += NT) {
+      int32_t sum = 0;
+      for (int u = 0; u < group; ++u) {
+        const int64_t seg = g * group + u;
+        sum += seg < all_f ? seglen[seg] : 0;
+      }
+      glen[g] = sum;
+    }
+    for (int x = lane; x < 256; x += 64) cls_base[wave][x] = 0;
+    __syncthreads();
+    const int64_t x = wave;
+    if (x % nblocks == blk) {
+      const int64_t per = ngroups / 8, rem = ngroups % 8;
+      const int64_t start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+      const int64_t cnt = per + (x < rem ? 1 : 0);
+      auto cls = [&](int64_t i) { return 255 - min(glen[start + i], 255); };
+      for (int64_t i = lane; i < cnt; i += 64) atomicAdd(&cls_base[wave][cls(i)], 1);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // exclusive prefix over the 256 classes, 4 per lane
+      int v[4], sum = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[u] = cls_base[wave][lane * 4 + u];
+        sum += v[u];
+      }
+      int inc = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+      }
+      int run = inc - sum;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        cls_base[wave][lane * 4 + u] = run;
+        run += v[u];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      for (int64_t i0 = 0; i0 < cnt; i0 += 64) {
+        const int64_t i = i0 + lane;
+        const bool valid = i < cnt;
+        const int c = valid ? cls(i) : 0;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const int bit = (c >> b) & 1;
+          const uint64_t m = __ballot(bit);
+          peers &= bit ? m : ~m;
+        }
+        asm volatile("" ::: "memory");
+        const int base = valid ? cls_base[wave][c] : 0;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (valid) run_order[start + base + __popcll(peers & lt)] = static_cast<int32_t>(start + i);
+        if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
     }
   }
   // Wave-local stable ranks: rounds of 64 consecutive pairs; the lanes of a
@@ -1216,6 +1293,7 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
                                   void *seg_workspace, size_t seg_workspace_bytes,
                                   int64_t *lhs_idx, int64_t *rhs_idx, int32_t *out_coords,
                                   int32_t *seg_offsets, int32_t *perm, int64_t seg_capacity,
+                                  int32_t group, int32_t *run_order, int32_t *run_order_written,
                                   int64_t *counts, int32_t counts_direct, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
@@ -1223,6 +1301,8 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
                    (out_coords || n_out == 0),
                "null pointer argument");
   EJ_CHECK_ARG(seg_capacity >= 0, "negative seg_capacity");
+  EJ_CHECK_ARG(group >= 0, "negative group");
+  if (run_order_written) *run_order_written = 0;
   EJ_CHECK_ARG(n_keys >= 1 && n_lhs >= 1 && n_rhs >= 1,
                "the queued pair plan needs join keys and two non-empty relations");
   EJ_CHECK_ARG(pair_capacity >= 1 && pair_capacity < (int64_t(1) << 31),
@@ -1259,11 +1339,15 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
                        lhs_coords, rhs_coords, a, lhs_idx, rhs_idx, sw.keys, nullptr, sw.scalars,
                        nullptr, int64_t(0), sw.whist, wk);
     EJ_LAUNCH_CHECK();
+    // Run order for grouped einsums: groups of up to kOnePassMaxKeys segments.
+    const bool order = run_order && group > 0 && seg_capacity <= kOnePassMaxKeys;
     hipLaunchKernelGGL(plan_one_pass_kernel, dim3(static_cast<unsigned>(nb1)),
                        dim3(kOnePassThreads), 0,
                        stream, sw.keys, sw.whist, nb1, wk, sbits, a, seg_capacity, perm,
-                       seg_offsets, out_coords, sw.scalars, direct, int64_t(counts_direct));
+                       seg_offsets, out_coords, sw.scalars, direct, int64_t(counts_direct),
+                       order ? group : 0, order ? run_order : nullptr);
     EJ_LAUNCH_CHECK();
+    if (order && run_order_written) *run_order_written = 1;
     if (!direct)
       EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost,
                             stream));

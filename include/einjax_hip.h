@@ -75,7 +75,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 8
+#define EJ_ABI_VERSION 9
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -270,7 +270,14 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
  * kernel may then store the counts there itself instead of a copy following
  * it, and counts[6] = counts_direct (a caller's ticket) is stored after them
  * in stream order, so that a host may wait for the ticket instead of an
- * event. */
+ * event.  run_order (may be NULL, ceil(seg_capacity / group) int32): for an
+ * einsum that will run groups of `group` consecutive segments per workgroup
+ * (ej_segment_einsum_async with a seg_group hint of 4: group = 4), the plan
+ * may write the order in which the workgroups should take the groups
+ * (heaviest first within each XCD's share of the grid); *run_order_written
+ * (host, set before the call returns) says whether it will, and only then
+ * should the order be passed to the einsum.  Scheduling only: any order gives
+ * the same results. */
 int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
@@ -279,8 +286,9 @@ int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
                        int64_t pair_capacity, void *join_workspace, size_t join_workspace_bytes,
                        void *seg_workspace, size_t seg_workspace_bytes, int64_t *lhs_idx,
                        int64_t *rhs_idx, int32_t *out_coords, int32_t *seg_offsets,
-                       int32_t *perm, int64_t seg_capacity, int64_t *counts,
-                       int32_t counts_direct, ej_stream_t stream);
+                       int32_t *perm, int64_t seg_capacity, int32_t group, int32_t *run_order,
+                       int32_t *run_order_written, int64_t *counts, int32_t counts_direct,
+                       ej_stream_t stream);
 
 /* Coherent, device-mapped host memory (hipHostMalloc, mapped | coherent) for
  * counts that kernels store directly (ej_pair_plan_async, counts_direct). */
@@ -320,13 +328,15 @@ int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs
  * *n_segments_dev (e.g. the first int64 of a segment workspace after
  * ej_segment_count_async): the grid covers max_segments, seg_offsets holds
  * at least min(U, max_segments) + 1 entries and out max_segments tiles, of
- * which the first U are written.  No counterpart in the reference (see
- * ej_join_count_async). */
+ * which the first U are written.  run_order (may be NULL): a run order from
+ * ej_pair_plan_async for groups of 4 segments, used when the einsum runs
+ * grouped.  No counterpart in the reference (see ej_join_count_async). */
 int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                             const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                             const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
                             const int32_t *seg_offsets, int64_t max_segments,
-                            const int64_t *n_segments_dev, void *out, ej_stream_t stream);
+                            const int64_t *n_segments_dev, const int32_t *run_order, void *out,
+                            ej_stream_t stream);
 
 /* ---- segment sum (reference: segment_sum accumulation, :164-171) -------- */
 /* out[u] = sum_{q in [seg_offsets[u], seg_offsets[u+1])} pair_values[perm[q]],

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 8
+    assert _lib.load().ej_version() == 9
 
 
 def describe(spec, lt, rt):
@@ -283,8 +283,8 @@ def test_pair_plan_host_validation():
     counts = (ctypes.c_int64 * 8)()
     args = lambda nk, cap: (fake, 4, 2, fake, 4, 2, nk, d, i32_array([0]), r, 2, i32_array([0, 1]),
                             i32_array([0, 1]), i64_array([4, 4]), cap, fake, 1 << 20, fake, 1 << 20,
-                            fake, fake, fake, fake, fake, 16, ctypes.cast(counts, ctypes.c_void_p),
-                            0, None)
+                            fake, fake, fake, fake, fake, 16, 0, None, None,
+                            ctypes.cast(counts, ctypes.c_void_p), 0, None)
     assert lib.ej_pair_plan_async(*args(0, 10)) == _lib.EJ_E_INVAL  # no join keys
     assert lib.ej_pair_plan_async(*args(1, 0)) == _lib.EJ_E_INVAL  # no capacity
     assert b"pair_capacity" in lib.ej_last_error()
