@@ -44,6 +44,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, reps: int):
+    """Average duration of the fused einsum as the step launches it (the
+    queued form: after the device-side join and plan, with the plan's run
+    order), from HIP events recorded on the launch stream around each
+    launch; None when the step does not take the queued form."""
+    import torch
+
+    evs = []
+    for _ in range(reps):
+        execute_sparse(lhs, rhs, jk, ks, ak, _einsum_events=evs)
+    torch.cuda.synchronize()
+    if len(evs) < reps:
+        return None
+    return sum(s.elapsed_time(e) for s, e in evs) / len(evs)
+
+
 def event_time_ms(fn, reps: int) -> float:
     """Average duration of fn() over reps, with HIP events on the current stream."""
     import torch
@@ -185,7 +201,9 @@ def measure_config(name: str, reps: int = 5) -> dict:
     run = sd._segment_run(rhs, jk, ak)
     desc.seg_group = run
     fused = lambda: _device.segment_einsum(desc, lhs.values, rhs.values, li, ri, perm, offs)
-    t_fused = event_time_ms(fused, reps)
+    t_fused = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, reps)
+    if t_fused is None:
+        t_fused = event_time_ms(fused, reps)
     t_fused_single = None
     if run:
         desc.seg_group = 0
@@ -396,8 +414,11 @@ def main():
     reps = 10
     t_join = wall_time_ms(lambda: sd._join_dev(lhs, rhs, jk, lc, rc), reps)
     t_plan = wall_time_ms(lambda: _device.segment_plan(lc, rc, li, ri, ak, radices), reps)
-    t_fused = event_time_ms(
+    # The fused einsum as the step launches it, and as the exact path does
+    # (its own segment plan, no run order).
+    t_fused_exact = event_time_ms(
         lambda: _device.segment_einsum(desc, lhs.values, rhs.values, li, ri, perm, offs), reps)
+    t_fused = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, 20) or t_fused_exact
     ga = _device.gather_tiles(lhs.values, li)
     gb = _device.gather_tiles(rhs.values, ri)
     t_gather = event_time_ms(lambda: (_device.gather_tiles(lhs.values, li),
@@ -455,6 +476,7 @@ def main():
         },
         "stages_ms": {
             "join": t_join, "segment_plan": t_plan, "fused_gemm_segsum": t_fused,
+            "fused_gemm_segsum_exact_path": t_fused_exact,
             "gather": t_gather, "pair_gemm": t_pair, "segment_sum": t_segsum,
             "bucket_dense_A": t_bucket,
         },

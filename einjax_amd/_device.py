@@ -256,7 +256,7 @@ def _wait_ticket(view, ticket: int) -> None:
 
 def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys,
                           agg_radices, desc, lhs_values, rhs_values, pair_bound: int,
-                          out_dtype=None):
+                          out_dtype=None, einsum_events=None):
     """Join, segment plan and fused segment einsum queued back to back on the
     current stream, with the pair count bounded by pair_bound instead of
     read first.  The plan stores its counts in coherent host memory followed
@@ -268,7 +268,10 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     counts.  "bound": P exceeded pair_bound (result[0] = P); "range": a
     coordinate fell outside its radix.  Either way the caller runs the exact
     path; every kernel clips its work to the device-side counts, so an
-    exceeded bound costs a rerun, never a stray access."""
+    exceeded bound costs a rerun, never a stray access.  einsum_events: an
+    optional list; when given, a (start, end) pair of timing events recorded
+    around the einsum launch is appended to it (for measurement; the records
+    add a little to the step)."""
     lib = _lib.load()
     dev = lhs_coords.device
     code = value_code(lhs_values)
@@ -315,12 +318,18 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
         sws.numel(), ptr(li), ptr(ri), ptr(coords), ptr(offsets), ptr(perm), cap_u, group,
         ptr(order) if group else None, ctypes.byref(order_written), ctypes.c_void_p(base), ticket,
         stream), "ej_pair_plan_async")
+    if einsum_events is not None:
+        einsum_events.append((torch.cuda.Event(enable_timing=True),
+                              torch.cuda.Event(enable_timing=True)))
+        einsum_events[-1][0].record()
     check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                       lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
                                       ptr(perm), ptr(offsets), cap_u, ptr(sws),
                                       ptr(order) if order_written.value else None, ptr(out),
                                       stream),
           "ej_segment_einsum_async")
+    if einsum_events is not None:
+        einsum_events[-1][1].record()
     _wait_ticket(counts, ticket)
     U, bad_plan, _, _, P, bad_join = (int(counts[i]) for i in range(6))
     if bad_join:

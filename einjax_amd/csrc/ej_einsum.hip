@@ -273,14 +273,35 @@ __device__ inline void put_out(uint16_t *p, float v) {
   *p = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
 }
 
-// Spreads consecutive block ids over the 8 XCDs in contiguous chunks, so
-// that neighbouring logical blocks (sharing operand tiles) share an L2.
-__device__ inline int64_t xcd_logical_block() {
-  const int64_t bid = blockIdx.x, total = gridDim.x;
-  const int64_t per = total / 8, rem = total % 8;
+// Reads a workgroup-uniform element of a read-only index array through the
+// scalar cache, so the load does not occupy the vector memory counter that
+// paces the LDS ring.
+template <typename T>
+__device__ inline T ld_uniform(const T *p, int64_t i) {
+  return ((const __attribute__((address_space(4))) T *)(p))[i];
+}
+
+// Spreads the first `live` block ids over the 8 XCDs (block id b runs on XCD
+// b % 8) in contiguous chunks of logical blocks, so that neighbouring logical
+// blocks (sharing operand tiles) share an L2.  Block ids from `live` on keep
+// their id: they lie beyond the work of a grid sized for a bound.
+__device__ inline int64_t xcd_logical_block(int64_t live) {
+  const int64_t bid = blockIdx.x;
+  if (bid >= live) return bid;
+  const int64_t per = live / 8, rem = live % 8;
   const int64_t xcd = bid % 8, local = bid / 8;
   const int64_t start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
   return start + local;
+}
+
+// Blocks that carry work when each segment takes blocks_per_seg of them: the
+// whole grid, or, given a device-side segment count, that many segments' blocks
+// (so that a grid sized for a bound still spreads its live work over every XCD).
+__device__ inline int64_t live_blocks(const PairSrc &s, int64_t blocks_per_seg) {
+  const int64_t total = gridDim.x;
+  if (!s.n_live) return total;
+  const int64_t live = ld_uniform(s.n_live, 0) * blocks_per_seg;
+  return live < total ? live : total;
 }
 
 // ---------------------------------------------------------------------------
@@ -457,7 +478,7 @@ __global__ __launch_bounds__(256) void tile_gemm_kernel(const T *__restrict__ A,
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  int64_t lb = xcd_logical_block();
+  int64_t lb = xcd_logical_block(live_blocks(src, g.nblocks * g.mblocks * g.batch));
   const int64_t nb = lb % g.nblocks;
   lb /= g.nblocks;
   const int64_t mb = lb % g.mblocks;
@@ -638,14 +659,6 @@ __device__ inline void lgkm_wait_all(i32x4_t (&v)[N]) {
 #define EJ_USE_DMA_GEMM 1
 #endif
 
-// Reads a workgroup-uniform element of a read-only index array through the
-// scalar cache, so the load does not occupy the vector memory counter that
-// paces the LDS ring.
-template <typename T>
-__device__ inline T ld_uniform(const T *p, int64_t i) {
-  return ((const __attribute__((address_space(4))) T *)(p))[i];
-}
-
 __device__ inline PairTiles load_pair_uniform(const PairSrc &s, int64_t q) {
   const int32_t qq = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(q));
   const int32_t p = s.perm ? ld_uniform(s.perm, qq) : qq;
@@ -721,7 +734,7 @@ __global__ __launch_bounds__(256) void tile_gemm_dma_kernel(const uint16_t *__re
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  int64_t lb = xcd_logical_block();
+  int64_t lb = xcd_logical_block(live_blocks(src, g.nblocks * g.mblocks * g.batch));
   const int64_t nb = lb % g.nblocks;
   lb /= g.nblocks;
   const int64_t mb = lb % g.mblocks;
@@ -1035,7 +1048,17 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
   const int wcol = (wn * WN) % BN;  // its first column inside that segment's tile
   // Work of this workgroup: m-blocks [mb0, mb0 + nmb) of segments
   // [seg0, seg0 + nls) for one n-block and one batch index.
-  int64_t lb = xcd_logical_block();
+  const int segs = G > 1 || !MULTI ? G : spw;
+  int64_t nseg = n_seg;
+  int64_t live = gridDim.x;  // blocks with work
+  if (src.n_live) {
+    const int64_t nl = ld_uniform(src.n_live, 0);
+    nseg = nl < nseg ? nl : nseg;
+    const int64_t per_grp = g.nblocks * (MULTI && mb_loop ? 1 : g.mblocks) * g.batch;
+    const int64_t lg = (nseg + segs - 1) / segs * per_grp;
+    live = lg < live ? lg : live;
+  }
+  int64_t lb = xcd_logical_block(live);
   const int64_t nb = lb % g.nblocks;
   lb /= g.nblocks;
   int64_t mb0 = 0, nmb = g.mblocks;
@@ -1045,17 +1068,13 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
     nmb = 1;
   }
   const int64_t bi = lb % g.batch;
-  const int segs = G > 1 || !MULTI ? G : spw;
   int64_t grp = lb / g.batch;
-  // A run order (heaviest groups first on each XCD) replaces the block's group.
+  if (grp * segs >= nseg) return;
+  // A run order (heaviest groups first on each XCD) replaces the block's
+  // group; it permutes the live groups, ceil(nseg / 4) of them.
   if (G == 4 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1)
     grp = ld_uniform(src.run_order, grp);
   const int64_t seg0 = grp * segs;
-  int64_t nseg = n_seg;
-  if (src.n_live) {
-    const int64_t live = ld_uniform(src.n_live, 0);
-    nseg = live < nseg ? live : nseg;
-  }
   if (seg0 >= nseg) return;
   const int nls = nseg - seg0 < segs ? static_cast<int>(nseg - seg0) : segs;  // live segments
   int32_t off[SMAX + 1];  // off[s] = off[nls] for s > nls

@@ -768,11 +768,11 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
 // host_counts[6], each step fenced at system scope, so that a host that sees
 // the ticket sees the counts.  perm receives the pair indices in sorted order.
 // Given run_order, the blocks also write the order in which a grouped einsum
-// (groups of `group` consecutive segments, ceil(seg_cap / group) workgroups)
-// should run them: the workgroups of each XCD (the contiguous chunks that the
-// einsum's XCD mapping assigns) take their chunk's groups in descending pair
-// count (counts above 255 tie), ties by index, so that the longest groups
-// start first.  Chunk x is ordered by wave x of block x % nblocks: a counting
+// (groups of `group` consecutive segments, one workgroup each) should run
+// the ceil(min(U, seg_cap) / group) live groups: the workgroups of each XCD
+// (the contiguous chunks that the einsum's XCD mapping assigns to the live
+// workgroups) take their chunk's groups in descending pair count (counts
+// above 255 tie), ties by index, so that the longest groups start first.  Chunk x is ordered by wave x of block x % nblocks: a counting
 // sort over the 256 count classes, ranked in index order with ballots.
 __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
     const uint64_t *__restrict__ keys, const int32_t *__restrict__ whist, int64_t nblocks,
@@ -872,7 +872,8 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
     // Group pair counts (segments beyond U count 0), then per XCD chunk a
     // stable counting sort of its groups by descending count class.
     __syncthreads();
-    const int64_t ngroups = (seg_cap + group - 1) / group;  // <= kOnePassMaxKeys
+    const int64_t live_segs = all_f < seg_cap ? all_f : seg_cap;
+    const int64_t ngroups = (live_segs + group - 1) / group;  // <= kOnePassMaxKeys
     int32_t *glen = seg_rank;  // reused: no longer read
     for (int64_t g = tid; g < ngroups; g += NT) {
       int32_t sum = 0;

@@ -335,7 +335,8 @@ def _empty_result(lhs, n_out, out_tile, output_shape, host, out_dtype=None):
 
 def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys,
                    kernel_string: str, agg_keys, output_shape=None, output_tile_shape=None, *,
-                   fused: bool = True, out_dtype=None) -> SparseTensorRelation:
+                   fused: bool = True, out_dtype=None,
+                   _einsum_events=None) -> SparseTensorRelation:
     """Sparse tensor-relational einsum (reference: sparse_dispatch.py:226-297).
 
     join_keys: [(lhs_dim, rhs_dim)] contracted tile dims; kernel_string: the
@@ -348,7 +349,9 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     values [U, *output_tile_shape] summed in fp32, of dtype ``out_dtype``: by
     default the operands' dtype, as in the reference (float32, or bfloat16
     for bfloat16 tiles, rounded once from the fp32 sum); ``torch.float32``
-    keeps fp32 results for bfloat16 tiles."""
+    keeps fp32 results for bfloat16 tiles.  ``_einsum_events`` (measurement
+    only): a list that collects timing events recorded around the fused
+    einsum of a queued call."""
     if output_tile_shape is None:
         output_tile_shape = _infer_output_tile_shape(kernel_string, lhs.tile_shape,
                                                      rhs.tile_shape)
@@ -390,7 +393,8 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
         if bound is not None and bound > 0:
             desc, a, b = operands()
             status, res = _device.queued_segment_einsum(lc, rc, keys, j_rad, agg, radices(None),
-                                                        desc, a, b, bound, out_dtype)
+                                                        desc, a, b, bound, out_dtype,
+                                                        _einsum_events)
             if status == "ok":
                 queued = res
                 _pair_hints[hint_key] = res[0]

@@ -273,8 +273,9 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
  * event.  run_order (may be NULL, ceil(seg_capacity / group) int32): for an
  * einsum that will run groups of `group` consecutive segments per workgroup
  * (ej_segment_einsum_async with a seg_group hint of 4: group = 4), the plan
- * may write the order in which the workgroups should take the groups
- * (heaviest first within each XCD's share of the grid); *run_order_written
+ * may write the order in which the workgroups should take the
+ * ceil(min(U, seg_capacity) / group) live groups (heaviest first within
+ * each XCD's share of the live workgroups); *run_order_written
  * (host, set before the call returns) says whether it will, and only then
  * should the order be passed to the einsum.  Scheduling only: any order gives
  * the same results. */
@@ -328,7 +329,8 @@ int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs
  * *n_segments_dev (e.g. the first int64 of a segment workspace after
  * ej_segment_count_async): the grid covers max_segments, seg_offsets holds
  * at least min(U, max_segments) + 1 entries and out max_segments tiles, of
- * which the first U are written.  run_order (may be NULL): a run order from
+ * which the first U are written; the workgroups of the first U segments are
+ * the ones spread over the XCDs.  run_order (may be NULL): a run order from
  * ej_pair_plan_async for groups of 4 segments, used when the einsum runs
  * grouped.  No counterpart in the reference (see ej_join_count_async). */
 int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,

@@ -750,6 +750,13 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
         npt.assert_array_equal(hv(got.values), ref_v)
         assert got.values.shape == exact.values.shape
         assert sd._pair_hints[key] == P
+    # Timing events around the queued einsum launch leave the result as it is.
+    evs = []
+    got = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                            _einsum_events=evs)
+    assert statuses[-1] == "ok" and len(evs) == 1
+    npt.assert_array_equal(hv(got.values), ref_v)
+    assert evs[0][0].elapsed_time(evs[0][1]) > 0
 
 
 def test_queued_step_range_fallback(gpu, monkeypatch):
