@@ -300,10 +300,14 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
     odt = _set_out_dtype(desc, lhs_values, out_dtype)
     out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
-    # Groups of 4 segments per workgroup when the einsum runs grouped (its
-    # seg_group hint): the plan may also write their run order.
-    group = 4 if desc.seg_group > 0 and desc.seg_group % 4 == 0 else 0
-    order = torch.empty((cap_u + 3) // 4 if group else 1, dtype=torch.int32, device=dev)
+    # The einsum's segments per workgroup when it runs grouped (its seg_group
+    # hint): the plan may also write the run order of those groups.
+    gq = ctypes.c_int32(1)
+    check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
+          "ej_segment_einsum_group")
+    group = gq.value if gq.value > 1 else 0
+    order = torch.empty((cap_u + group - 1) // group if group else 1, dtype=torch.int32,
+                        device=dev)
     order_written = ctypes.c_int32(0)
     ldims = i32_array([k[0] for k in join_keys])
     rdims = i32_array([k[1] for k in join_keys])
@@ -325,8 +329,8 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
                                       lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
                                       ptr(perm), ptr(offsets), cap_u, ptr(sws),
-                                      ptr(order) if order_written.value else None, ptr(out),
-                                      stream),
+                                      ptr(order) if order_written.value else None, group,
+                                      ptr(out), stream),
           "ej_segment_einsum_async")
     if einsum_events is not None:
         einsum_events[-1][1].record()

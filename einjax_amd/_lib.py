@@ -84,7 +84,8 @@ SIGNATURES = {
     "ej_segment_einsum": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64, _vp,
                                  _vp, _vp, _vp, _i64, _vp, _vp]),
     "ej_segment_einsum_async": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _vp, _vp, _i64, _i64,
-                                       _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+                                       _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp]),
+    "ej_segment_einsum_group": (_i32, [ctypes.POINTER(EinsumDesc), _i32, _P_i32]),
     "ej_segment_sum": (_i32, [_vp, _i32, _i64, _vp, _vp, _i64, _vp, _vp]),
     "ej_bucket_workspace_size": (_i32, [_i32, _P_i64, _P_i64, _P_sz]),
     "ej_bucket_dense_count": (_i32, [_vp, _i32, _i32, _P_i64, _P_i64, _vp, _sz, _P_i64, _vp]),

@@ -237,6 +237,7 @@ struct PairSrc {
   int64_t n_a_tiles, n_b_tiles;
   const int64_t *n_live;       // non-null: segments >= *n_live are skipped (grid is a bound)
   const int32_t *run_order;    // non-null: grouped launches run group run_order[b] as block b
+  int32_t order_group;         // segments per group that run_order was made for
 };
 
 // Whether the workgroup's segment lies beyond the device-side segment count.
@@ -1012,7 +1013,7 @@ struct SegOpF32 {
 };
 
 template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
-__global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
+__global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
                                                            const typename Op::elem *__restrict__ B,
                                                            void *__restrict__ C, PairSrc src,
                                                            GemmGeom g, int64_t n_seg, int spw,
@@ -1071,8 +1072,9 @@ __global__ __launch_bounds__(NW * 64) void seg_gemm_kernel(const typename Op::el
   int64_t grp = lb / g.batch;
   if (grp * segs >= nseg) return;
   // A run order (heaviest groups first on each XCD) replaces the block's
-  // group; it permutes the live groups, ceil(nseg / 4) of them.
-  if (G == 4 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1)
+  // group; it permutes the live groups, ceil(nseg / G) of them (the launcher
+  // passes only an order made for groups of G).
+  if (G > 1 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1)
     grp = ld_uniform(src.run_order, grp);
   const int64_t seg0 = grp * segs;
   if (seg0 >= nseg) return;
@@ -1516,10 +1518,12 @@ constexpr int seg_ring_depth(int slot_bytes, int want) {
 constexpr int64_t kSegMinBlocks = 1024;
 constexpr int kSegMaxRun = 8;  // segments per workgroup when G == 1 (SMAX)
 
-template <class Op, int G, int WGM, int NW>
-int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src,
+template <class Op, int G, int WGM, int NW, int NSW = EJ_SEG_NS>
+int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src_in,
                       const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
-  constexpr int NS = seg_ring_depth(Op::A_BYTES + G * Op::B_BYTES, EJ_SEG_NS);
+  constexpr int NS = seg_ring_depth(Op::A_BYTES + G * Op::B_BYTES, NSW);
+  PairSrc src = src_in;
+  if (src.order_group != G) src.run_order = nullptr;  // an order for other groups
   const int64_t groups = ceil_div(n_seg, G);
   int64_t per_group = g.batch * g.nblocks;  // workgroups per group, m-blocks looped inside
   const int mb_loop = g.mblocks > 1 && groups * per_group >= kSegMinBlocks ? 1 : 0;
@@ -1547,13 +1551,15 @@ int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src,
   return EJ_OK;
 }
 
-// bf16: 128 x 128 tiles, a group of 4 on 8 waves (2 x 4, one segment per wave
-// column) or one segment on 4 waves (2 x 2); 64 x 64 tiles on 4 waves.
+// bf16: 128 x 128 tiles, a group of 2 on 4 waves (2 x 2, one segment per wave
+// column) with a 3-stage ring (72 KB of LDS, so two workgroups share a CU and
+// one's prologue and epilogue overlap the other's stream), or one segment on
+// 4 waves (2 x 2); 64 x 64 tiles on 4 waves.
 int launch_seg_gemm_bf16(int bm, int grp, const void *A, const void *B, void *C,
                          const PairSrc &src, const GemmGeom &g, int64_t n_seg,
                          hipStream_t stream) {
   if (bm == 128) {
-    if (grp == 4) return launch_seg_gemm_t<SegOpBf16<128, 128>, 4, 2, 8>(A, B, C, src, g, n_seg, stream);
+    if (grp == 4) return launch_seg_gemm_t<SegOpBf16<128, 128>, 2, 2, 4, 3>(A, B, C, src, g, n_seg, stream);
     return launch_seg_gemm_t<SegOpBf16<128, 128>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
   }
   if (grp == 4) return launch_seg_gemm_t<SegOpBf16<64, 64>, 4, 1, 4>(A, B, C, src, g, n_seg, stream);
@@ -1578,6 +1584,22 @@ int launch_seg_gemm_f32(int bm, int bn, int grp, const void *A, const void *B, v
 }
 
 int pick_block(int64_t x) { return x % 128 == 0 ? 128 : x % 64 == 0 ? 64 : x % 32 == 0 ? 32 : 0; }
+
+// Segments per workgroup of the fused kernel that try_gemm picks for a
+// descriptor with the seg_group hint, given 16-byte aligned operands: the
+// group size a run order must be made for (1: the einsum does not run
+// grouped).  The launcher checks the order's group size again, so an order
+// made for another size is ignored, never misapplied.
+int fused_group(const ej_einsum_desc *d, int32_t dtype) {
+  if (!d->is_gemm || d->seg_group <= 0 || d->seg_group % 4 != 0) return 1;
+  const int vec = dtype == EJ_BF16 ? 8 : 4;
+  const int bm = pick_block(d->m), bn = pick_block(d->n);
+  if (!bm || !bn || d->a_sk != 1 || d->a_sm % vec != 0 || d->b_sn != 1 || d->b_sk % vec != 0 ||
+      d->k % 32 != 0)
+    return 1;
+  if (dtype == EJ_BF16) return bm == bn && bm == 128 ? 2 : bm == bn && bm == 64 ? 4 : 1;
+  return (bm == 32 || bm == 64 || bm == 128) && d->n % 32 == 0 ? 4 : 1;
+}
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -1862,7 +1884,7 @@ extern "C" int ej_pair_einsum(const ej_einsum_desc *desc, int32_t dtype, const v
                               const int64_t *lhs_idx, const int64_t *rhs_idx, int64_t n_pairs,
                               void *out, ej_stream_t stream) {
   clear_error();
-  PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles, nullptr, nullptr};
+  PairSrc src{lhs_idx, rhs_idx, nullptr, nullptr, n_lhs_tiles, n_rhs_tiles, nullptr, nullptr, 0};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_pairs, out, as_stream(stream));
 }
 
@@ -1874,7 +1896,7 @@ extern "C" int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, cons
                                  ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || n_segments == 0, "seg_offsets is null");
-  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, nullptr, nullptr};
+  PairSrc src{lhs_idx, rhs_idx, perm, seg_offsets, n_lhs_tiles, n_rhs_tiles, nullptr, nullptr, 0};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, n_segments, out,
                        as_stream(stream));
 }
@@ -1885,15 +1907,25 @@ extern "C" int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype
                                        const int64_t *lhs_idx, const int64_t *rhs_idx,
                                        const int32_t *perm, const int32_t *seg_offsets,
                                        int64_t max_segments, const int64_t *n_segments_dev,
-                                       const int32_t *run_order, void *out,
-                                       ej_stream_t stream) {
+                                       const int32_t *run_order, int32_t run_order_group,
+                                       void *out, ej_stream_t stream) {
   clear_error();
   EJ_CHECK_ARG(seg_offsets || max_segments == 0, "seg_offsets is null");
   EJ_CHECK_ARG(n_segments_dev, "n_segments_dev is null");
-  PairSrc src{lhs_idx, rhs_idx,     perm,           seg_offsets,
-              n_lhs_tiles, n_rhs_tiles, n_segments_dev, run_order};
+  PairSrc src{lhs_idx,     rhs_idx,     perm,           seg_offsets,
+              n_lhs_tiles, n_rhs_tiles, n_segments_dev, run_order,
+              run_order_group};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, max_segments, out,
                        as_stream(stream));
+}
+
+extern "C" int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype,
+                                       int32_t *group) {
+  clear_error();
+  EJ_CHECK_ARG(desc && group, "null pointer argument");
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  *group = fused_group(desc, dtype);
+  return EJ_OK;
 }
 
 extern "C" int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t tile_elems,

@@ -75,7 +75,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 9
+#define EJ_ABI_VERSION 10
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -272,7 +272,7 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
  * in stream order, so that a host may wait for the ticket instead of an
  * event.  run_order (may be NULL, ceil(seg_capacity / group) int32): for an
  * einsum that will run groups of `group` consecutive segments per workgroup
- * (ej_segment_einsum_async with a seg_group hint of 4: group = 4), the plan
+ * (group from ej_segment_einsum_group for the einsum's descriptor), the plan
  * may write the order in which the workgroups should take the
  * ceil(min(U, seg_capacity) / group) live groups (heaviest first within
  * each XCD's share of the live workgroups); *run_order_written
@@ -331,14 +331,22 @@ int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs
  * at least min(U, max_segments) + 1 entries and out max_segments tiles, of
  * which the first U are written; the workgroups of the first U segments are
  * the ones spread over the XCDs.  run_order (may be NULL): a run order from
- * ej_pair_plan_async for groups of 4 segments, used when the einsum runs
- * grouped.  No counterpart in the reference (see ej_join_count_async). */
+ * ej_pair_plan_async made for groups of run_order_group segments; the einsum
+ * uses it when it runs groups of that size and ignores it otherwise (any
+ * order gives the same results).  No counterpart in the reference (see
+ * ej_join_count_async). */
 int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                             const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                             const int64_t *lhs_idx, const int64_t *rhs_idx, const int32_t *perm,
                             const int32_t *seg_offsets, int64_t max_segments,
-                            const int64_t *n_segments_dev, const int32_t *run_order, void *out,
-                            ej_stream_t stream);
+                            const int64_t *n_segments_dev, const int32_t *run_order,
+                            int32_t run_order_group, void *out, ej_stream_t stream);
+
+/* Segments per workgroup of the fused einsum for this descriptor and dtype
+ * (grouped by the seg_group hint; 16-byte aligned operands assumed): the
+ * group size to pass to ej_pair_plan_async for a run order.  1 means the
+ * einsum does not run grouped.  No counterpart in the reference. */
+int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype, int32_t *group);
 
 /* ---- segment sum (reference: segment_sum accumulation, :164-171) -------- */
 /* out[u] = sum_{q in [seg_offsets[u], seg_offsets[u+1])} pair_values[perm[q]],

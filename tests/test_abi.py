@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 9
+    assert _lib.load().ej_version() == 10
 
 
 def describe(spec, lt, rt):
@@ -288,3 +288,28 @@ def test_pair_plan_host_validation():
     assert lib.ej_pair_plan_async(*args(0, 10)) == _lib.EJ_E_INVAL  # no join keys
     assert lib.ej_pair_plan_async(*args(1, 0)) == _lib.EJ_E_INVAL  # no capacity
     assert b"pair_capacity" in lib.ej_last_error()
+
+
+def test_segment_einsum_group():
+    """The group size a run order is made for: two 128 x 128 bf16 output
+    tiles per workgroup, four 64 x 64 bf16 or fp32 ones, 1 without the
+    seg_group hint or for shapes the grouped kernels do not take."""
+    lib = _lib.load()
+
+    def group(spec, lt, rt, dtype, hint=4):
+        st, d = describe(spec, lt, rt)
+        assert st == _lib.EJ_OK
+        d.seg_group = hint
+        g = ctypes.c_int32(-1)
+        assert lib.ej_segment_einsum_group(ctypes.byref(d), dtype, ctypes.byref(g)) == _lib.EJ_OK
+        return g.value
+
+    assert group("ij,jk->ik", (128, 128), (128, 128), _lib.EJ_BF16) == 2
+    assert group("ij,jk->ik", (64, 64), (64, 64), _lib.EJ_BF16) == 4
+    assert group("ij,jk->ik", (64, 64), (64, 64), _lib.EJ_F32) == 4
+    assert group("ij,jk->ik", (128, 128), (128, 128), _lib.EJ_BF16, hint=0) == 1
+    assert group("ij,kj->ik", (128, 128), (128, 128), _lib.EJ_BF16) == 1  # rhs k-contiguous
+    st, d = describe("ij,jk->ik", (32, 32), (32, 32))
+    g = ctypes.c_int32(-1)
+    assert lib.ej_segment_einsum_group(ctypes.byref(d), 7, ctypes.byref(g)) == _lib.EJ_E_INVAL
+    assert lib.ej_segment_einsum_group(ctypes.byref(d), _lib.EJ_F32, None) == _lib.EJ_E_INVAL

@@ -865,6 +865,37 @@ def test_pair_plan_matches_exact_phases(gpu, n_lhs, n_rhs, grid, slack):
     assert U == cq.shape[0]
 
 
+@pytest.mark.parametrize("m,n,density", [(2048, 512, 0.2), (4096, 1024, 0.05), (2048, 1536, 0.06),
+                                         (4096, 512, 0.02)])
+def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
+    """Block-sparse x dense with 128^2 bf16 tiles: the queued step runs the
+    grouped einsum (two output tiles per workgroup) in the plan's run order
+    (groups of 2, heaviest first per XCD); its output must be bit-identical
+    to the exact path's (own plan, no order), with 4 to 12 output tiles per
+    row and 30 to 112 groups (66 and 30: not a multiple of the 8 XCDs)."""
+    note("queued run order bf16", m, n, density)
+    w = G.workload_blocksparse_16k(seed=3, m=m, n=n, density=density)
+    lhs, rhs = dev_rel(w["lhs"], "bf16"), dev_rel(w["rhs"], "bf16")
+    args = (lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    written = []
+    lib = _device_mod()._lib.load()
+    real = lib.ej_pair_plan_async
+
+    def spy(*a):
+        rc = real(*a)
+        written.append((a[25], a[27]._obj.value if hasattr(a[27], "_obj") else None))
+        return rc
+
+    sd._pair_hints.clear()
+    exact = ej.execute_sparse(*args)
+    monkeypatch.setattr(lib, "ej_pair_plan_async", spy)
+    for _ in range(2):
+        got = ej.execute_sparse(*args)
+        assert torch.equal(got.coords, exact.coords)
+        assert torch.equal(got.values.view(torch.int16), exact.values.view(torch.int16))
+    assert written and all(g == 2 and wr == 1 for g, wr in written), written
+
+
 def _device_mod():
     from einjax_amd import _device
 
