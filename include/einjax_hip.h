@@ -30,6 +30,7 @@
  *   queued step   ej_join_count_async / ej_segment_count_async /
  *                 ej_pair_plan_async (both counts in one call) /
  *                 ej_segment_fill_async / ej_segment_einsum_async
+ *                 (+ ej_segment_einsum_group for the plan's run order)
  *                 (the same phases with the counts kept on the device, so a
  *                  caller can queue a whole execute_sparse,
  *                  execution/sparse_dispatch.py:226-297, without waiting)
