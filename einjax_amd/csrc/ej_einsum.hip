@@ -1074,8 +1074,12 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
   // A run order (heaviest groups first on each XCD) replaces the block's
   // group; it permutes the live groups, ceil(nseg / G) of them (the launcher
   // passes only an order made for groups of G).
-  if (G > 1 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1)
-    grp = ld_uniform(src.run_order, grp);
+  // An entry outside the live groups (an order made for another capacity)
+  // is not followed: the block keeps its own group, so no access strays.
+  if (G > 1 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1) {
+    const int64_t o = ld_uniform(src.run_order, grp);
+    if (o >= 0 && o * segs < nseg) grp = o;
+  }
   const int64_t seg0 = grp * segs;
   if (seg0 >= nseg) return;
   const int nls = nseg - seg0 < segs ? static_cast<int>(nseg - seg0) : segs;  // live segments

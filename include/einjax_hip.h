@@ -334,7 +334,8 @@ int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs
  * the ones spread over the XCDs.  run_order (may be NULL): a run order from
  * ej_pair_plan_async made for groups of run_order_group segments; the einsum
  * uses it when it runs groups of that size and ignores it otherwise (any
- * order gives the same results).  No counterpart in the reference (see
+ * order gives the same results; the plan's seg_capacity must equal
+ * max_segments, and an entry outside the live groups is not followed).  No counterpart in the reference (see
  * ej_join_count_async). */
 int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                             const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
