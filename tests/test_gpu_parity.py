@@ -709,7 +709,7 @@ def test_workload_end_to_end(gpu, name, fused):
         npt.assert_array_equal(h.values, got.values.cpu().numpy())
 
 
-@pytest.mark.parametrize("name", ["blocksparse_1k", "order3_small", "zipf_small"])
+@pytest.mark.parametrize("name", ["blocksparse_1k", "order3_small", "zipf_small", "zipf_small_bf16"])
 def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
     """A repeated execute_sparse on the same relations queues its whole step
     on the pair count remembered from the previous call.  Its output must be
@@ -720,6 +720,8 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
         w = G.workload_blocksparse_1k()
     elif name == "order3_small":
         w = G.workload_order3(n=512, l=128, density=0.02)
+    elif name == "zipf_small_bf16":  # one segment per workgroup on the bf16 DMA kernel
+        w = dict(G.workload_sparse_sparse_zipf(n=4096), dtype="bf16")
     else:
         w = G.workload_sparse_sparse_zipf(n=4096)
     statuses = []
