@@ -267,24 +267,7 @@ class SparseTensor:
         per-scheme statistics (sparse.py:124-158), computed on the GPU for
         every tile shape at once on first access."""
         if self._schemes is None:
-            schemes = {ts: TilingScheme(self, self.shape, ts) for ts in self.tile_shapes}
-            if self.ndim == 0:
-                n = 1 if self.nnz else 0
-                for sch in schemes.values():
-                    sch.num_tuples, sch.value_count = n, ()
-            else:
-                from .._device import scheme_stats
-
-                form = self._gpu_form()
-                if form[0] == "coo":
-                    nt, vc = scheme_stats(self.tile_shapes, self.shape, indices=form[1],
-                                          values=form[2])
-                else:
-                    nt, vc = scheme_stats(self.tile_shapes, self.shape, dense=form[1])
-                for ts, n, v in zip(self.tile_shapes, nt, vc):
-                    schemes[ts].num_tuples = n
-                    schemes[ts].value_count = v
-            self._schemes = schemes
+            self._schemes = _measured_schemes(self, self._gpu_form)
         return self._schemes
 
     def to_relation(self, tile_shape: tuple) -> SparseTensorRelation:
@@ -336,6 +319,33 @@ class SparseTensor:
                 out[tuple(idx[:, d] for d in range(self.ndim))] = vals
             return out
         return np.array(self.data, dtype=np.float64)
+
+
+def _measured_schemes(tensor, gpu_form) -> dict:
+    """tile_shape -> TilingScheme of `tensor` (shape, tile_shapes, ndim),
+    with num_tuples and value_count counted on the GPU over the elements
+    != 0 of gpu_form() for every tile shape in one call (the reference's
+    _compute_sparsity_metrics, sparse.py:124-158 and dense.py:44-66)."""
+    schemes = {ts: TilingScheme(tensor, tensor.shape, ts) for ts in tensor.tile_shapes}
+    form = gpu_form()
+    if tensor.ndim == 0:
+        if form[0] == "coo":
+            n = 1 if int(form[2].numel()) else 0
+        else:
+            n = 1 if bool((form[1] != 0).any()) else 0
+        for sch in schemes.values():
+            sch.num_tuples, sch.value_count = n, ()
+        return schemes
+    from .._device import scheme_stats
+
+    if form[0] == "coo":
+        nt, vc = scheme_stats(tensor.tile_shapes, tensor.shape, indices=form[1], values=form[2])
+    else:
+        nt, vc = scheme_stats(tensor.tile_shapes, tensor.shape, dense=form[1])
+    for ts, n, v in zip(tensor.tile_shapes, nt, vc):
+        schemes[ts].num_tuples = n
+        schemes[ts].value_count = v
+    return schemes
 
 
 def _is_scipy(x) -> bool:
