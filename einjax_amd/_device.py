@@ -306,7 +306,7 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
           "ej_segment_einsum_group")
     group = gq.value if gq.value > 1 else 0
-    order = torch.empty((cap_u + group - 1) // group if group else 1, dtype=torch.int32,
+    order = torch.empty(1 + (cap_u + group - 1) // group if group else 1, dtype=torch.int32,
                         device=dev)
     order_written = ctypes.c_int32(0)
     ldims = i32_array([k[0] for k in join_keys])
@@ -363,11 +363,10 @@ def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:
 def bucket_dense(dense: torch.Tensor, tile_shape) -> tuple[torch.Tensor, torch.Tensor]:
     """Dense tensor -> (coords int32 [T, nd], values [T, *tile_shape]).
 
-    float32 / bfloat16 tiles keep the input dtype; float64 input decides
-    occupancy in float64 and yields float32 tiles."""
+    The tiles keep the input dtype: float64, float32 or bfloat16."""
     lib = _lib.load()
-    code = _lib.EJ_F64 if dense.dtype == torch.float64 else value_code(dense)
-    out_dtype = torch.float32 if dense.dtype == torch.float64 else dense.dtype
+    code = _elem_code(dense)
+    out_dtype = dense.dtype
     dense = dense.contiguous()
     nd = dense.dim()
     shape = i64_array(dense.shape)
@@ -389,7 +388,7 @@ def bucket_dense(dense: torch.Tensor, tile_shape) -> tuple[torch.Tensor, torch.T
 
 
 def relation_to_dense(coords, values, shape, tile_shape) -> torch.Tensor:
-    code = value_code(values)
+    code = _elem_code(values)
     dense = torch.empty(tuple(shape), dtype=values.dtype, device=values.device)
     check(_lib.load().ej_relation_to_dense(ptr(coords), ptr(values), coords.shape[0], code,
                                            len(shape), i64_array(shape), i64_array(tile_shape),
@@ -445,15 +444,15 @@ def bucket_coo(indices: torch.Tensor, values: torch.Tensor, shape,
                tile_shape) -> tuple[torch.Tensor, torch.Tensor]:
     """COO entries -> (coords int32 [T, nd], values [T, *tile_shape]).
 
-    float64 / float32 values give float32 tiles, bfloat16 values bfloat16
-    tiles.  Entries equal to zero are dropped; an element listed twice keeps
-    its last nonzero entry."""
+    The tiles have the values' dtype (float64, float32 or bfloat16).
+    Entries equal to zero are dropped; an element listed twice keeps its last
+    nonzero entry."""
     lib = _lib.load()
     nd = len(shape)
     indices = indices.to(dtype=torch.int32).reshape(-1, nd).contiguous()
     values = values.contiguous().reshape(-1)
     code = _elem_code(values)
-    out_dtype = torch.bfloat16 if values.dtype == torch.bfloat16 else torch.float32
+    out_dtype = values.dtype
     n = values.numel()
     sh, ts = i64_array(shape), i64_array(tile_shape)
     nbytes = ctypes.c_size_t()

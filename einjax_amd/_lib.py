@@ -147,11 +147,18 @@ class CapacityError(RuntimeError):
     """An output buffer was smaller than the size the library counted."""
 
 
+class RangeError(ValueError):
+    """A coordinate lies outside the radix (grid extent) it was declared
+    with (status EJ_E_RANGE)."""
+
+
 def check(status: int, what: str) -> None:
     if status == EJ_OK:
         return
     msg = f"{what}: {load().ej_last_error().decode(errors='replace')}"
-    if status in (EJ_E_INVAL, EJ_E_RANGE):
+    if status == EJ_E_RANGE:
+        raise RangeError(msg)
+    if status == EJ_E_INVAL:
         raise ValueError(msg)
     if status == EJ_E_UNSUPPORTED:
         raise NotImplementedError(msg)

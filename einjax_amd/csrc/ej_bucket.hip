@@ -80,11 +80,8 @@ __device__ inline bool nonzero(double x) { return x != 0.0; }  // NaN != 0 holds
 __device__ inline bool nonzero(float x) { return x != 0.0f; }
 __device__ inline bool nonzero(uint16_t x) { return (x & 0x7fffu) != 0; }  // bf16: +-0 are zero
 // Tile element as stored: zeros become +0.0 (the reference scatters the
-// nonzero values into np.zeros tiles); float64 input is rounded to fp32.
-__device__ inline float stored(double x) {
-  float f = static_cast<float>(x);
-  return f == 0.0f ? 0.0f : f;
-}
+// nonzero values into np.zeros tiles); every dtype keeps its precision.
+__device__ inline double stored(double x) { return x == 0.0 ? 0.0 : x; }
 __device__ inline float stored(float x) { return x == 0.0f ? 0.0f : x; }
 __device__ inline uint16_t stored(uint16_t x) { return (x & 0x7fffu) ? x : 0; }
 
@@ -174,7 +171,6 @@ __global__ __launch_bounds__(256) void tile_copy_vec_kernel(const unsigned char 
                                                             int32_t *coords,
                                                             unsigned char *__restrict__ values) {
   constexpr int ESZ = MODE == 0 ? 2 : MODE == 1 ? 4 : 8;
-  constexpr int OSZ = MODE == 2 ? 4 : ESZ;  // stored element size
   const int64_t slot = blockIdx.x;
   if (slot >= *counted) return;
   const int64_t t = tile_of_slot[slot];
@@ -186,27 +182,25 @@ __global__ __launch_bounds__(256) void tile_copy_vec_kernel(const unsigned char 
     }
   }
   const unsigned char *base = dense + tile_origin(g, t) * ESZ;
-  unsigned char *dst = values + slot * g.tile_elems * OSZ;
+  unsigned char *dst = values + slot * g.tile_elems * ESZ;
   const int c = threadIdx.x & (vpr - 1);
   const int rstep = 256 / vpr;
   const int per_vec = 16 / ESZ;  // input elements per vector
   for (int64_t r = threadIdx.x / vpr; r < g.rows; r += rstep) {
     const int64_t roff = ND2 ? r * row_pitch : row_offset(g, r) * ESZ;
     const uint4 x = *reinterpret_cast<const uint4 *>(base + roff + c * 16);
-    unsigned char *o = dst + (r * g.inner + static_cast<int64_t>(c) * per_vec) * OSZ;
+    unsigned char *o = dst + (r * g.inner + static_cast<int64_t>(c) * per_vec) * ESZ;
     if constexpr (MODE == 0) {
       *reinterpret_cast<uint4 *>(o) = make_uint4(zero_norm_bf16x2(x.x), zero_norm_bf16x2(x.y),
                                                  zero_norm_bf16x2(x.z), zero_norm_bf16x2(x.w));
     } else if constexpr (MODE == 1) {
       *reinterpret_cast<uint4 *>(o) = make_uint4(zero_norm_f32(x.x), zero_norm_f32(x.y),
                                                  zero_norm_f32(x.z), zero_norm_f32(x.w));
-    } else {
-      const double d0 = __longlong_as_double(static_cast<long long>(x.x | (static_cast<uint64_t>(x.y) << 32)));
-      const double d1 = __longlong_as_double(static_cast<long long>(x.z | (static_cast<uint64_t>(x.w) << 32)));
-      float f0 = static_cast<float>(d0), f1 = static_cast<float>(d1);
-      if (f0 == 0.0f) f0 = 0.0f;
-      if (f1 == 0.0f) f1 = 0.0f;
-      *reinterpret_cast<float2 *>(o) = make_float2(f0, f1);
+    } else {  // float64: a word pair is zero when both halves are, ignoring the sign bit
+      const bool z0 = (x.x | (x.y & 0x7fffffffu)) == 0u;
+      const bool z1 = (x.z | (x.w & 0x7fffffffu)) == 0u;
+      *reinterpret_cast<uint4 *>(o) = make_uint4(z0 ? 0u : x.x, z0 ? 0u : x.y, z1 ? 0u : x.z,
+                                                 z1 ? 0u : x.w);
     }
   }
 }
@@ -401,9 +395,9 @@ extern "C" int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t nd
     }
 #undef EJ_COPY
   } else if (dtype == EJ_F64)
-    hipLaunchKernelGGL((tile_copy_kernel<double, float>), grid, dim3(256), 0, stream,
+    hipLaunchKernelGGL((tile_copy_kernel<double, double>), grid, dim3(256), 0, stream,
                        static_cast<const double *>(dense), g, w.tile_of_slot, w.scalars, coords,
-                       static_cast<float *>(values));
+                       static_cast<double *>(values));
   else if (dtype == EJ_F32)
     hipLaunchKernelGGL((tile_copy_kernel<float, float>), grid, dim3(256), 0, stream,
                        static_cast<const float *>(dense), g, w.tile_of_slot, w.scalars, coords,
@@ -422,7 +416,7 @@ extern "C" int ej_relation_to_dense(const int32_t *coords, const void *values, i
                                     ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
-  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64, "unknown dtype %d", dtype);
   BucketGeom g;
   EJ_TRY(make_geom(ndim, shape, tile_shape, &g));
   EJ_CHECK_ARG(n_tiles >= 0 && n_tiles < (int64_t(1) << 32), "n_tiles out of range");
@@ -431,7 +425,10 @@ extern "C" int ej_relation_to_dense(const int32_t *coords, const void *values, i
   if (total == 0) return EJ_OK;
   EJ_CHECK_ARG(dense, "dense is null");
   const unsigned zb = static_cast<unsigned>(ceil_div(total, 256) < 65536 ? ceil_div(total, 256) : 65536);
-  if (dtype == EJ_F32)
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL(fill_zero_kernel<double>, dim3(zb), dim3(256), 0, stream,
+                       static_cast<double *>(dense), total);
+  else if (dtype == EJ_F32)
     hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(zb), dim3(256), 0, stream,
                        static_cast<float *>(dense), total);
   else
@@ -440,7 +437,11 @@ extern "C" int ej_relation_to_dense(const int32_t *coords, const void *values, i
   EJ_LAUNCH_CHECK();
   if (n_tiles == 0) return EJ_OK;
   EJ_CHECK_ARG(coords && values, "null pointer argument");
-  if (dtype == EJ_F32)
+  if (dtype == EJ_F64)
+    hipLaunchKernelGGL(scatter_tiles_kernel<double>, dim3(static_cast<unsigned>(n_tiles)),
+                       dim3(256), 0, stream, coords, static_cast<const double *>(values), g,
+                       static_cast<double *>(dense));
+  else if (dtype == EJ_F32)
     hipLaunchKernelGGL(scatter_tiles_kernel<float>, dim3(static_cast<unsigned>(n_tiles)), dim3(256),
                        0, stream, coords, static_cast<const float *>(values), g,
                        static_cast<float *>(dense));

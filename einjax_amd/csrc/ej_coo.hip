@@ -57,12 +57,8 @@ __device__ inline double as_f64(float x) { return static_cast<double>(x); }
 __device__ inline double as_f64(uint16_t x) {
   return static_cast<double>(__uint_as_float(static_cast<uint32_t>(x) << 16));
 }
-// Tile element written for a nonzero entry: float64 rounds to fp32 (a value
-// that underflows is written as +0.0), fp32 and bf16 are kept.
-__device__ inline float tile_val(double x) {
-  const float f = static_cast<float>(x);
-  return f == 0.0f ? 0.0f : f;
-}
+// Tile element written for a nonzero entry: every dtype is kept.
+__device__ inline double tile_val(double x) { return x; }
 __device__ inline float tile_val(float x) { return x; }
 __device__ inline uint16_t tile_val(uint16_t x) { return x; }
 
@@ -430,7 +426,7 @@ CooWs carve_coo(void *base, int64_t nnz) {
   return w;
 }
 
-// COO to tiles without sorting, for fp32 tiles on grids of at most 2^30
+// COO to tiles without sorting, for fp32 or float64 tiles on grids of at most 2^30
 // tiles: every entry marks its tile in a byte-per-tile flag array with a
 // plain store (concurrent stores write the same value, and no two tiles
 // share a byte, so no atomics); the flags are packed into a bit map whose
@@ -535,34 +531,42 @@ __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
     p[i] = v;
 }
 
-template <typename T>
+__global__ void fill_i64_kernel(long long *p, int64_t n, long long v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = v;
+}
+
+// W: the winner's integer type, as wide as the tile element (int32 for fp32
+// tiles, long long for float64 tiles), so the winners live in the output.
+template <typename T, typename W>
 __global__ __launch_bounds__(256) void coo_winner_kernel(const int32_t *__restrict__ idx,
                                                          const T *__restrict__ vals, int64_t nnz,
                                                          CooGeom g,
                                                          const uint32_t *__restrict__ map,
                                                          const int64_t *__restrict__ prefix,
                                                          int64_t n_slots, int64_t *bad,
-                                                         int32_t *__restrict__ win) {
+                                                         W *__restrict__ win) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= nnz) return;
   uint64_t t, w;
   if (!coo_entry(idx, vals, i, g, bad, &t, &w)) return;
   const uint32_t word = map[t >> 5];
   const int64_t slot = prefix[t >> 5] + __popc(word & ((1u << (t & 31)) - 1u));
-  if (slot < n_slots) atomicMax(&win[slot * g.tile_elems + static_cast<int64_t>(w)], int32_t(i));
+  if (slot < n_slots) atomicMax(&win[slot * g.tile_elems + static_cast<int64_t>(w)], W(i));
 }
 
 // In place: the entry index each element holds becomes that entry's value
-// (fp32), or +0.0 where no entry names the element.
-template <typename T>
+// (T, fp32 or float64), or +0.0 where no entry names the element.
+template <typename T, typename W>
 __global__ __launch_bounds__(256) void coo_resolve_kernel(const T *__restrict__ vals,
-                                                          int32_t *__restrict__ tiles,
-                                                          int64_t elems) {
+                                                          W *__restrict__ tiles, int64_t elems) {
+  static_assert(sizeof(T) == sizeof(W), "winners are held in the output elements");
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < elems;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int32_t wi = tiles[e];
-    const float f = wi >= 0 ? tile_val(vals[wi]) : 0.0f;
-    tiles[e] = __float_as_int(f);
+    const W wi = tiles[e];
+    const T f = wi >= 0 ? tile_val(vals[wi]) : T(0);
+    tiles[e] = __builtin_bit_cast(W, f);
   }
 }
 
@@ -1550,24 +1554,29 @@ extern "C" int ej_bucket_coo_fill(const int32_t *indices, const void *values, in
     CooMapWs w = carve_coo_map(const_cast<void *>(workspace), g.n_tiles);
     EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small");
     const int64_t words = (g.n_tiles + 31) / 32;
-    int32_t *win = static_cast<int32_t *>(tiles);
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(stride_grid(elems)), dim3(kBlock), 0, stream, win,
-                       elems, int32_t(-1));
-    EJ_LAUNCH_CHECK();
     if (dtype == EJ_F64) {
-      hipLaunchKernelGGL(coo_winner_kernel<double>, grid, dim3(kBlock), 0, stream, indices,
-                         static_cast<const double *>(values), nnz, g, w.map, w.prefix, n_tiles,
-                         w.scalars + 1, win);
+      long long *win = static_cast<long long *>(tiles);
+      hipLaunchKernelGGL(fill_i64_kernel, dim3(stride_grid(elems)), dim3(kBlock), 0, stream, win,
+                         elems, -1ll);
       EJ_LAUNCH_CHECK();
-      hipLaunchKernelGGL(coo_resolve_kernel<double>, dim3(stride_grid(elems)), dim3(kBlock), 0,
-                         stream, static_cast<const double *>(values), win, elems);
+      hipLaunchKernelGGL((coo_winner_kernel<double, long long>), grid, dim3(kBlock), 0, stream,
+                         indices, static_cast<const double *>(values), nnz, g, w.map, w.prefix,
+                         n_tiles, w.scalars + 1, win);
+      EJ_LAUNCH_CHECK();
+      hipLaunchKernelGGL((coo_resolve_kernel<double, long long>), dim3(stride_grid(elems)),
+                         dim3(kBlock), 0, stream, static_cast<const double *>(values), win,
+                         elems);
     } else {
-      hipLaunchKernelGGL(coo_winner_kernel<float>, grid, dim3(kBlock), 0, stream, indices,
-                         static_cast<const float *>(values), nnz, g, w.map, w.prefix, n_tiles,
-                         w.scalars + 1, win);
+      int32_t *win = static_cast<int32_t *>(tiles);
+      hipLaunchKernelGGL(fill_i32_kernel, dim3(stride_grid(elems)), dim3(kBlock), 0, stream, win,
+                         elems, int32_t(-1));
       EJ_LAUNCH_CHECK();
-      hipLaunchKernelGGL(coo_resolve_kernel<float>, dim3(stride_grid(elems)), dim3(kBlock), 0,
-                         stream, static_cast<const float *>(values), win, elems);
+      hipLaunchKernelGGL((coo_winner_kernel<float, int32_t>), grid, dim3(kBlock), 0, stream,
+                         indices, static_cast<const float *>(values), nnz, g, w.map, w.prefix,
+                         n_tiles, w.scalars + 1, win);
+      EJ_LAUNCH_CHECK();
+      hipLaunchKernelGGL((coo_resolve_kernel<float, int32_t>), dim3(stride_grid(elems)),
+                         dim3(kBlock), 0, stream, static_cast<const float *>(values), win, elems);
     }
     EJ_LAUNCH_CHECK();
     hipLaunchKernelGGL(coo_map_coords_kernel, dim3(grid_for(words)), dim3(kBlock), 0, stream,
@@ -1584,18 +1593,20 @@ extern "C" int ej_bucket_coo_fill(const int32_t *indices, const void *values, in
     hipLaunchKernelGGL((coo_scatter_kernel<uint16_t, uint16_t>), grid, dim3(kBlock), 0, stream,
                        w.keys, w.order, w.flags, w.excl, static_cast<const uint16_t *>(values),
                        nnz, g, n_tiles, coords, static_cast<uint16_t *>(tiles));
+  } else if (dtype == EJ_F64) {
+    hipLaunchKernelGGL(fill_zero_kernel<double>, dim3(stride_grid(elems)), dim3(kBlock), 0,
+                       stream, static_cast<double *>(tiles), elems);
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL((coo_scatter_kernel<double, double>), grid, dim3(kBlock), 0, stream,
+                       w.keys, w.order, w.flags, w.excl, static_cast<const double *>(values),
+                       nnz, g, n_tiles, coords, static_cast<double *>(tiles));
   } else {
     hipLaunchKernelGGL(fill_zero_kernel<float>, dim3(stride_grid(elems)), dim3(kBlock), 0,
                        stream, static_cast<float *>(tiles), elems);
     EJ_LAUNCH_CHECK();
-    if (dtype == EJ_F64)
-      hipLaunchKernelGGL((coo_scatter_kernel<double, float>), grid, dim3(kBlock), 0, stream,
-                         w.keys, w.order, w.flags, w.excl, static_cast<const double *>(values),
-                         nnz, g, n_tiles, coords, static_cast<float *>(tiles));
-    else
-      hipLaunchKernelGGL((coo_scatter_kernel<float, float>), grid, dim3(kBlock), 0, stream,
-                         w.keys, w.order, w.flags, w.excl, static_cast<const float *>(values),
-                         nnz, g, n_tiles, coords, static_cast<float *>(tiles));
+    hipLaunchKernelGGL((coo_scatter_kernel<float, float>), grid, dim3(kBlock), 0, stream,
+                       w.keys, w.order, w.flags, w.excl, static_cast<const float *>(values),
+                       nnz, g, n_tiles, coords, static_cast<float *>(tiles));
   }
   EJ_LAUNCH_CHECK();
   return EJ_OK;

@@ -461,8 +461,10 @@ __device__ inline PairTiles load_pair(const PairSrc &s, int64_t q) {
   return t;
 }
 
+// Three workgroups per CU for bf16 (40 KB of LDS each with the padded rows);
+// fp32 tiles need more registers and keep two.
 template <typename T, int BM, int BN, int BK, bool A_DIRECT, bool B_DIRECT>
-__global__ __launch_bounds__(256, 3) void tile_gemm_kernel(const T *__restrict__ A,
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 3 : 2) void tile_gemm_kernel(const T *__restrict__ A,
                                                         const T *__restrict__ B,
                                                         void *__restrict__ C, PairSrc src,
                                                         GemmGeom g) {
@@ -1072,13 +1074,17 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
   int64_t grp = lb / g.batch;
   if (grp * segs >= nseg) return;
   // A run order (heaviest groups first on each XCD) replaces the block's
-  // group; it permutes the live groups, ceil(nseg / G) of them (the launcher
-  // passes only an order made for groups of G).
-  // An entry outside the live groups (an order made for another capacity)
-  // is not followed: the block keeps its own group, so no access strays.
+  // group.  Its header, run_order[0], is the number of live groups it
+  // permutes (the launcher passes only an order made for groups of G): only
+  // an order made for exactly ceil(nseg / G) live groups is followed, by
+  // every block alike, so each live group runs once; any other order is
+  // ignored as a whole.
   if (G > 1 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1) {
-    const int64_t o = ld_uniform(src.run_order, grp);
-    if (o >= 0 && o * segs < nseg) grp = o;
+    const int64_t ngroups = (nseg + segs - 1) / segs;
+    if (ld_uniform(src.run_order, 0) == ngroups) {
+      const int64_t o = ld_uniform(src.run_order, grp + 1);
+      if (o >= 0 && o < ngroups) grp = o;
+    }
   }
   const int64_t seg0 = grp * segs;
   if (seg0 >= nseg) return;

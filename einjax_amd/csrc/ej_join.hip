@@ -769,7 +769,8 @@ __global__ __launch_bounds__(kBlock) void fill_probe_keys_kernel(
 // the ticket sees the counts.  perm receives the pair indices in sorted order.
 // Given run_order, the blocks also write the order in which a grouped einsum
 // (groups of `group` consecutive segments, one workgroup each) should run
-// the ceil(min(U, seg_cap) / group) live groups: the workgroups of each XCD
+// the ngroups = ceil(min(U, seg_cap) / group) live groups, into
+// run_order[1 .. ngroups], with ngroups in run_order[0]: the workgroups of each XCD
 // (the contiguous chunks that the einsum's XCD mapping assigns to the live
 // workgroups) take their chunk's groups in descending pair count (counts
 // above 255 tie), ties by index, so that the longest groups start first.  Chunk x is ordered by wave x of block x % nblocks: a counting
@@ -884,6 +885,7 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
       glen[g] = sum;
     }
     for (int x = lane; x < 256; x += 64) cls_base[wave][x] = 0;
+    if (blk == 0 && tid == 0) run_order[0] = static_cast<int32_t>(ngroups);  // the header
     __syncthreads();
     const int64_t x = wave;
     if (x % nblocks == blk) {
@@ -928,7 +930,8 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
         asm volatile("" ::: "memory");
         const int base = valid ? cls_base[wave][c] : 0;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (valid) run_order[start + base + __popcll(peers & lt)] = static_cast<int32_t>(start + i);
+        if (valid)
+          run_order[1 + start + base + __popcll(peers & lt)] = static_cast<int32_t>(start + i);
         if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }

@@ -15,6 +15,9 @@ reference) or GPU torch tensors (results stay on the GPU).
 
 from __future__ import annotations
 
+import threading
+import weakref
+
 import numpy as np
 
 from .. import _device, _lib
@@ -53,9 +56,18 @@ def _dev(x, dtype=None):
 
 
 def _dev_values(v):
-    """Tile values on the GPU as float32, or bfloat16 when already bfloat16."""
+    """Tile values on the GPU as float32, or bfloat16 when already bfloat16.
+    float64 and float16 become float32, as the reference's jnp.array turns
+    float64 relation values into float32 before its einsum
+    (sparse_dispatch.py:125).  Integer and boolean values raise TypeError:
+    the tile einsums and segment sums compute in floating point only, where
+    the reference would keep an integer dtype (:164-169)."""
     import torch
 
+    dt = v.dtype if _is_torch(v) else torch.from_numpy(np.zeros(0, dtype=v.dtype)).dtype
+    if not dt.is_floating_point:
+        raise TypeError(f"tile values must be floating point, got {dt}: the GPU path "
+                        "computes in float32 / bfloat16")
     t = _dev(v)
     if t.dtype not in (torch.float32, torch.bfloat16):
         t = t.to(torch.float32)
@@ -103,12 +115,12 @@ def _host_col_max(coords, d) -> int:
 
 def _retry_radices(fn, make_radices, cols):
     """Runs fn(radices) with radices from grid metadata; if a coordinate
-    falls outside them, sizes the radices from the data and runs again."""
+    falls outside them (the library's EJ_E_RANGE status), sizes the radices
+    from the data and runs again."""
     try:
         return fn(make_radices(None))
-    except ValueError as e:
-        if "outside [0, radix)" not in str(e):
-            raise
+    except _lib.RangeError:
+        pass
     maxima = []
     for coords, d in cols:
         lo, hi = _device.coords_range(coords)
@@ -165,19 +177,47 @@ def _segment_run(rhs: SparseTensorRelation, join_keys, agg_keys) -> int:
     return _grid(rhs, d)
 
 
-# Pair counts of recent joins, keyed by the coordinate buffers, their shapes,
-# the keys and the radices: a bound for the next execute_sparse on the same
-# relations, which can then queue its whole step without waiting for the
-# count (a wrong bound is detected and costs one rerun).  -1: the queued
-# path found a coordinate outside the metadata radices; do not retry it.
+# Pair counts of recent joins: a bound for the next execute_sparse on the
+# same relations, which can then queue its whole step without waiting for
+# the count (a wrong bound is detected and costs one rerun, never a wrong
+# result).  -1: the queued path found a coordinate outside the metadata
+# radices; do not retry it.  A hint belongs to the pair of coordinate arrays
+# the caller passed (host arrays or device tensors, never the per-call
+# device copies of host arrays): it is keyed by their ids and holds weak
+# references to them, so a hint whose arrays were freed, or whose id now
+# names another array, is never used.
 _pair_hints: dict = {}
 _PAIR_HINTS_MAX = 256
+_pair_hints_lock = threading.Lock()
 
 
-def _remember_pairs(key, n_pairs: int):
-    if key not in _pair_hints and len(_pair_hints) >= _PAIR_HINTS_MAX:
-        _pair_hints.pop(next(iter(_pair_hints)))
-    _pair_hints[key] = int(n_pairs)
+def _hint_key(lhs: SparseTensorRelation, rhs: SparseTensorRelation, rest: tuple):
+    return (id(lhs.coords), id(rhs.coords), *rest)
+
+
+def _hint_get(key, lhs: SparseTensorRelation, rhs: SparseTensorRelation):
+    with _pair_hints_lock:
+        ent = _pair_hints.get(key)
+    if ent is None:
+        return None
+    wl, wr, bound = ent
+    if wl() is not lhs.coords or wr() is not rhs.coords:
+        with _pair_hints_lock:
+            if _pair_hints.get(key) is ent:
+                del _pair_hints[key]
+        return None
+    return bound
+
+
+def _hint_set(key, lhs: SparseTensorRelation, rhs: SparseTensorRelation, bound: int):
+    try:
+        ent = (weakref.ref(lhs.coords), weakref.ref(rhs.coords), int(bound))
+    except TypeError:  # coordinates that cannot be weakly referenced get no hint
+        return
+    with _pair_hints_lock:
+        if key not in _pair_hints and len(_pair_hints) >= _PAIR_HINTS_MAX:
+            _pair_hints.pop(next(iter(_pair_hints)))
+        _pair_hints[key] = ent
 
 
 def coordinate_join(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys):
@@ -384,12 +424,13 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
 
     keys = [tuple(k) for k in join_keys]
     hint_key = None
+    bound = None
     queued = None
     if fused and keys and lc.shape[0] and rc.shape[0]:
         j_rad = _join_radices(lhs, rhs, keys, None)
-        hint_key = (lc.data_ptr(), rc.data_ptr(), tuple(lc.shape), tuple(rc.shape), tuple(keys),
-                    tuple(j_rad), tuple(agg))
-        bound = _pair_hints.get(hint_key)
+        hint_key = _hint_key(lhs, rhs, (tuple(lc.shape), tuple(rc.shape), tuple(keys),
+                                        tuple(j_rad), tuple(agg)))
+        bound = _hint_get(hint_key, lhs, rhs)
         if bound is not None and bound > 0:
             desc, a, b = operands()
             status, res = _device.queued_segment_einsum(lc, rc, keys, j_rad, agg, radices(None),
@@ -397,17 +438,18 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
                                                         _einsum_events)
             if status == "ok":
                 queued = res
-                _pair_hints[hint_key] = res[0]
+                _hint_set(hint_key, lhs, rhs, res[0])
             else:
-                _pair_hints[hint_key] = res[0] if status == "bound" else -1
+                bound = res[0] if status == "bound" else -1
+                _hint_set(hint_key, lhs, rhs, bound)
     if queued is not None:
         P, coords, offsets, perm, vals, li, ri = queued
         if P == 0:
             return _empty_result(lhs, n_out, output_tile_shape, output_shape, host, out_dtype)
     else:
         li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
-        if hint_key is not None and _pair_hints.get(hint_key, 0) >= 0:
-            _remember_pairs(hint_key, li.numel())
+        if hint_key is not None and (bound is None or bound >= 0):
+            _hint_set(hint_key, lhs, rhs, li.numel())
         if li.numel() == 0:
             return _empty_result(lhs, n_out, output_tile_shape, output_shape, host, out_dtype)
         cols = [((lc if s == 0 else rc), dim) for s, dim in agg]

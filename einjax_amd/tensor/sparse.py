@@ -275,9 +275,9 @@ class SparseTensor:
 
         Tiles holding any element != 0 are kept, in lexicographic coordinate
         order, with the other elements of a kept tile set to +0.0.  Host data
-        gives a host relation (int32 coords, float32 tiles: occupancy is
-        decided on the float64 values, tiles hold them rounded to float32);
-        GPU float32 / bfloat16 data gives a device relation of that dtype.
+        gives a host relation with int32 coords and float64 tiles, as the
+        reference's (sparse.py:191, :210); GPU float64 / float32 / bfloat16
+        data gives a device relation of that dtype.
         scipy data is bucketed from its COO entries (a repeated entry keeps
         its last nonzero value) without forming the dense matrix.
         Raises ValueError when a tile extent does not divide the shape."""
@@ -298,7 +298,8 @@ class SparseTensor:
         dev = form[1].device
         if prod(self.shape) == 0:
             coords = torch.zeros((0, self.ndim), dtype=torch.int32, device=dev)
-            vals = torch.zeros((0, *tile_shape), dtype=torch.float32, device=dev)
+            vals = torch.zeros((0, *tile_shape), dtype=form[-1].dtype if form[0] == "coo"
+                               else form[1].dtype, device=dev)
         elif form[0] == "coo":
             coords, vals = bucket_coo(form[1], form[2], self.shape, tile_shape)
         else:

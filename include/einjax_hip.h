@@ -76,7 +76,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 10
+#define EJ_ABI_VERSION 11
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -87,7 +87,7 @@ extern "C" {
 
 #define EJ_F32 0
 #define EJ_BF16 1
-#define EJ_F64 2 /* dense input of the bucketing calls only; tiles come out fp32 */
+#define EJ_F64 2 /* tiling, COO ingest and to_dense only (the einsums take EJ_F32 / EJ_BF16) */
 
 /* Pair orders of the join.  With n_keys == 0 both give the cross product in
  * lhs-major order (sparse_dispatch.py:53-59, pallas_gather.py:50-54). */
@@ -271,15 +271,16 @@ int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64_t *radices
  * kernel may then store the counts there itself instead of a copy following
  * it, and counts[6] = counts_direct (a caller's ticket) is stored after them
  * in stream order, so that a host may wait for the ticket instead of an
- * event.  run_order (may be NULL, ceil(seg_capacity / group) int32): for an
- * einsum that will run groups of `group` consecutive segments per workgroup
- * (group from ej_segment_einsum_group for the einsum's descriptor), the plan
- * may write the order in which the workgroups should take the
- * ceil(min(U, seg_capacity) / group) live groups (heaviest first within
- * each XCD's share of the live workgroups); *run_order_written
- * (host, set before the call returns) says whether it will, and only then
- * should the order be passed to the einsum.  Scheduling only: any order gives
- * the same results. */
+ * event.  run_order (may be NULL, 1 + ceil(seg_capacity / group) int32): for
+ * an einsum that will run groups of `group` consecutive segments per
+ * workgroup (group from ej_segment_einsum_group for the einsum's descriptor),
+ * the plan may write the order in which the workgroups should take the
+ * ngroups = ceil(min(U, seg_capacity) / group) live groups (heaviest first
+ * within each XCD's share of the live workgroups): run_order[0] = ngroups,
+ * run_order[1 .. ngroups] a permutation of 0 .. ngroups - 1;
+ * *run_order_written (host, set before the call returns) says whether it
+ * will, and only then should the order be passed to the einsum.  Scheduling
+ * only: the results do not depend on it. */
 int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
@@ -333,9 +334,10 @@ int ej_segment_einsum(const ej_einsum_desc *desc, int32_t dtype, const void *lhs
  * which the first U are written; the workgroups of the first U segments are
  * the ones spread over the XCDs.  run_order (may be NULL): a run order from
  * ej_pair_plan_async made for groups of run_order_group segments; the einsum
- * uses it when it runs groups of that size and ignores it otherwise (any
- * order gives the same results; the plan's seg_capacity must equal
- * max_segments, and an entry outside the live groups is not followed).  No counterpart in the reference (see
+ * follows it only when it runs groups of that size and the order's header
+ * (run_order[0]) equals its number of live groups, ceil(min(U,
+ * max_segments) / group); otherwise it ignores the whole order.  The
+ * results do not depend on the order.  No counterpart in the reference (see
  * ej_join_count_async). */
 int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype, const void *lhs_values,
                             const void *rhs_values, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
@@ -366,16 +368,14 @@ int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t tile_elems,
  * lexicographic coordinate order; inside a kept tile every element that
  * compares == 0 is written as +0.0.  tile_shape must divide shape
  * (EJ_E_INVAL otherwise, as the reference raises ValueError).
- * dtype EJ_F32 or EJ_BF16 keeps the dtype in the tiles.  dtype EJ_F64 decides
- * occupancy on the float64 values (the reference's dtype, sparse.py:260) and
- * writes fp32 tiles (the precision its einsum computes in). */
+ * The tiles keep the input's dtype: EJ_F64 (the reference's dtype for
+ * relation values, sparse.py:191, :210), EJ_F32 or EJ_BF16. */
 int ej_bucket_workspace_size(int32_t ndim, const int64_t *shape, const int64_t *tile_shape,
                              size_t *bytes);
 int ej_bucket_dense_count(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
                           const int64_t *tile_shape, void *workspace, size_t workspace_bytes,
                           int64_t *n_tiles, ej_stream_t stream);
-/* coords int32 [n_tiles, ndim]; values [n_tiles, *tile_shape] of `dtype`
- * (fp32 for EJ_F64 input). */
+/* coords int32 [n_tiles, ndim]; values [n_tiles, *tile_shape] of `dtype`. */
 int ej_bucket_dense_fill(const void *dense, int32_t dtype, int32_t ndim, const int64_t *shape,
                          const int64_t *tile_shape, const void *workspace,
                          size_t workspace_bytes, int64_t n_tiles, int32_t *coords, void *values,
@@ -405,7 +405,8 @@ int ej_extract_coo_fill(const void *dense, int32_t dtype, int32_t ndim, const in
  * more than once takes the value of its last nonzero entry, as the
  * reference's fancy assignment leaves it.  A nonzero entry whose index lies
  * outside shape gives EJ_E_RANGE; tile_shape must divide shape (EJ_E_INVAL).
- * Tiles are fp32 for EJ_F64 / EJ_F32 values and bf16 for EJ_BF16 values. */
+ * Tiles have the values' dtype (float64 for EJ_F64, as the reference's
+ * float64 tiles, sparse.py:210). */
 int ej_bucket_coo_workspace_size(int64_t nnz, int32_t dtype, int32_t ndim, const int64_t *shape,
                                  const int64_t *tile_shape, size_t *bytes);
 int ej_bucket_coo_count(const int32_t *indices, const void *values, int32_t dtype, int64_t nnz,
@@ -487,8 +488,9 @@ int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_tile, int32
                        ej_stream_t stream);
 
 /* ---- relation to dense (reference: SparseTensorRelation.to_dense, :75-90) */
-/* Writes every tile of the relation into `dense` (row-major `shape`, fp32 or
- * bf16 like `values`).  Elements not covered by a tile are set to zero. */
+/* Writes every tile of the relation into `dense` (row-major `shape`, of the
+ * values' dtype: EJ_F32, EJ_BF16 or EJ_F64).  Elements not covered by a tile
+ * are set to zero. */
 int ej_relation_to_dense(const int32_t *coords, const void *values, int64_t n_tiles,
                          int32_t dtype, int32_t ndim, const int64_t *shape,
                          const int64_t *tile_shape, void *dense, ej_stream_t stream);

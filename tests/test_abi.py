@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 10
+    assert _lib.load().ej_version() == 11
 
 
 def describe(spec, lt, rt):

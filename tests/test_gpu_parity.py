@@ -738,20 +738,21 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
     run = lambda: ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
     exact = run()
     assert statuses == [] and len(sd._pair_hints) == 1
-    key, P = next(iter(sd._pair_hints.items()))
+    key = next(iter(sd._pair_hints))
+    P = sd._hint_get(key, lhs, rhs)
     ref_c, ref_v = exact.coords.cpu().numpy(), hv(exact.values)
     want = R.execute_sparse(w["lhs"], w["rhs"], w["join_keys"], w["kernel_string"],
                             w["agg_keys"], precision="fp64")
     npt.assert_array_equal(ref_c, want.coords)
     assert R.rel_l2(ref_v, want.values) <= TOL[w["dtype"]]
     for bound, status in [(P, "ok"), (max(P - 1, 1), "bound"), (3 * P + 7, "ok")]:
-        sd._pair_hints[key] = bound
+        sd._hint_set(key, lhs, rhs, bound)
         got = run()
         assert statuses[-1] == status, (bound, statuses)
         npt.assert_array_equal(got.coords.cpu().numpy(), ref_c)
         npt.assert_array_equal(hv(got.values), ref_v)
         assert got.values.shape == exact.values.shape
-        assert sd._pair_hints[key] == P
+        assert sd._hint_get(key, lhs, rhs) == P
     # Timing events around the queued einsum launch leave the result as it is.
     evs = []
     got = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"],
@@ -898,6 +899,56 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
     assert written and all(g == 2 and wr == 1 for g, wr in written), written
 
 
+def test_run_order_header_must_match_live_groups(gpu):
+    """ej_segment_einsum_async follows a run order only when its header
+    (run_order[0]) equals the number of live groups; an order made for
+    another group count is ignored as a whole, so every output tile is still
+    written once.  A valid permutation gives the same output as no order."""
+    note("run order header")
+    import ctypes
+
+    from einjax_amd import _device, _lib
+
+    w = G.workload_blocksparse_16k(seed=5, m=2048, n=768, density=0.2)
+    lhs, rhs = dev_rel(w["lhs"], "bf16"), dev_rel(w["rhs"], "bf16")
+    li, ri = sd._join_dev(lhs, rhs, w["join_keys"], lhs.coords, rhs.coords)
+    coords, off, perm, _ = _device.segment_plan(lhs.coords, rhs.coords, li, ri, w["agg_keys"],
+                                                [16, 6])
+    U = coords.shape[0]
+    desc = _device.describe("ij,jk->ik", (128, 128), (128, 128))
+    desc.seg_group = 6
+    desc.out_dtype = _lib.EJ_BF16
+    gq = ctypes.c_int32(1)
+    lib = _lib.load()
+    _lib.check(lib.ej_segment_einsum_group(ctypes.byref(desc), _lib.EJ_BF16, ctypes.byref(gq)),
+               "ej_segment_einsum_group")
+    group = gq.value
+    assert group == 2 and U == 96
+    ngroups = (U + group - 1) // group
+    n_dev = torch.tensor([U], dtype=torch.int64, device="cuda")
+
+    def run(order):
+        out = torch.full((U, 128, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+        o = None if order is None else torch.tensor(order, dtype=torch.int32, device="cuda")
+        _lib.check(lib.ej_segment_einsum_async(
+            ctypes.byref(desc), _lib.EJ_BF16, _device.ptr(lhs.values), _device.ptr(rhs.values),
+            lhs.values.shape[0], rhs.values.shape[0], _device.ptr(li), _device.ptr(ri),
+            _device.ptr(perm), _device.ptr(off), U, _device.ptr(n_dev), _device.ptr(o), group,
+            _device.ptr(out), _device.stream_ptr()), "ej_segment_einsum_async")
+        torch.cuda.synchronize()
+        return out
+
+    ref = run(None)
+    assert not torch.isnan(ref.float()).any()
+    same = lambda x: torch.equal(x.view(torch.int16), ref.view(torch.int16))
+    assert same(run([ngroups] + list(range(ngroups))[::-1]))
+    rng = np.random.default_rng(1)
+    assert same(run([ngroups] + rng.permutation(ngroups).tolist()))
+    # made for one group more / fewer: ignored, every tile written once
+    assert same(run([ngroups + 1, 1] + list(range(ngroups))))
+    assert same(run([ngroups - 1] + [1, 0] + list(range(2, ngroups - 1)) + [0]))
+
+
 def _device_mod():
     from einjax_amd import _device
 
@@ -964,8 +1015,10 @@ def test_fused_is_deterministic(gpu):
 # ---------------------------------------------------------------------------
 # tiling
 
-@pytest.mark.parametrize("dtype", ["f64host", "f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f64host", "f64dev", "f32", "bf16"])
 def test_to_relation_parity(gpu, dtype):
+    """Tiles keep the input's dtype: float64 host data gives float64 tiles,
+    as the reference's (tensor/sparse.py:191, :210), so 1e-300 survives."""
     note("to_relation", dtype)
     rng = np.random.default_rng(4)
     d = rng.standard_normal((64, 96)) * np.kron(rng.random((8, 6)) < 0.3, np.ones((8, 16)))
@@ -973,8 +1026,8 @@ def test_to_relation_parity(gpu, dtype):
     d[60, 0] = -0.0  # -0.0 is zero
     d[9, 17] = 1e-300  # nonzero in float64 only
     tile = (8, 16)
-    if dtype == "f64host":
-        src = d
+    if dtype in ("f64host", "f64dev"):
+        src = d if dtype == "f64host" else torch.from_numpy(d).cuda()
         want = R.dense_to_relation(d, tile)
     else:
         f = d.astype(np.float32)
@@ -985,10 +1038,23 @@ def test_to_relation_parity(gpu, dtype):
         src = t.to(torch.bfloat16) if dtype == "bf16" else t
     got = SparseTensor("x", src).to_relation(tile)
     gc = got.coords.cpu().numpy() if dtype != "f64host" else got.coords
-    gv = (got.values.float().cpu().numpy() if dtype != "f64host" else got.values)
+    if dtype == "f64host":
+        gv = got.values
+        assert isinstance(gv, np.ndarray) and gv.dtype == np.float64
+    elif dtype == "f64dev":
+        assert got.values.dtype == torch.float64 and got.is_device
+        gv = got.values.cpu().numpy()
+    else:
+        gv = got.values.float().cpu().numpy()
     npt.assert_array_equal(gc, want.coords)
-    npt.assert_array_equal(gv, want.values.astype(np.float32))  # NaN == NaN, +0.0 for zeros
+    exact = want.values if dtype.startswith("f64") else want.values.astype(np.float32)
+    npt.assert_array_equal(gv, exact)  # NaN == NaN, +0.0 for zeros
     assert not np.any(np.signbit(gv[gv == 0]))
+    if dtype.startswith("f64"):
+        assert (gv == 1e-300).sum() == 1
+        # the device relation's to_dense gives back the float64 values
+        dev = got if dtype == "f64dev" else got.to_device(torch.float64)
+        npt.assert_array_equal(dev.to_dense().cpu().numpy(), R.relation_to_dense(want))
 
 
 def test_to_relation_edge_cases(gpu):

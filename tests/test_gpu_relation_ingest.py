@@ -111,6 +111,7 @@ def test_bucket_coo_parity(gpu, dtype, shape, tile, n):
     idx[n // 2:n // 2 + k] = idx[:k]          # repeated elements: the last nonzero wins
     vals[3] = np.nan
     vals[5] = -0.0
+    vals[7] = 1e-300                          # kept by float64 tiles only
     if dtype == "f64":
         v64 = vals
         tv = torch.from_numpy(vals).cuda()
@@ -125,10 +126,15 @@ def test_bucket_coo_parity(gpu, dtype, shape, tile, n):
     coords, tiles = D.bucket_coo(torch.from_numpy(idx).cuda(), tv, shape, tile)
     want = R.to_relation(idx, v64, shape, tile)
     npt.assert_array_equal(coords.cpu().numpy(), want.coords)
-    got = tiles.float().cpu().numpy()
-    npt.assert_array_equal(got, want.values.astype(np.float32))
+    if dtype == "f64":  # float64 tiles, bit-exact: the reference's dtype
+        got = tiles.cpu().numpy()
+        npt.assert_array_equal(got, want.values)
+    else:
+        got = tiles.float().cpu().numpy()
+        npt.assert_array_equal(got, want.values.astype(np.float32))
     assert not np.any(np.signbit(got[got == 0]))
-    assert tiles.dtype == (torch.bfloat16 if dtype == "bf16" else torch.float32)
+    assert tiles.dtype == {"f64": torch.float64, "f32": torch.float32,
+                           "bf16": torch.bfloat16}[dtype]
 
 
 def test_bucket_coo_sorted_input_and_errors(gpu):
@@ -165,7 +171,8 @@ def test_scipy_to_relation_without_densifying(gpu):
         want = R.to_relation(want_idx, want_vals, shape, rel.tile_shape)
         assert isinstance(rel.coords, np.ndarray)
         npt.assert_array_equal(rel.coords, want.coords)
-        npt.assert_array_equal(rel.values, want.values.astype(np.float32))
+        assert rel.values.dtype == np.float64
+        npt.assert_array_equal(rel.values, want.values)
         npt.assert_array_equal(t.to_dense_array(), R.relation_to_dense(want))
 
 
