@@ -909,21 +909,21 @@ def test_run_order_header_must_match_live_groups(gpu):
 
     from einjax_amd import _device, _lib
 
-    w = G.workload_blocksparse_16k(seed=5, m=2048, n=768, density=0.2)
+    w = G.workload_blocksparse_16k(seed=5, m=2048, n=1024, density=0.2)
     lhs, rhs = dev_rel(w["lhs"], "bf16"), dev_rel(w["rhs"], "bf16")
     li, ri = sd._join_dev(lhs, rhs, w["join_keys"], lhs.coords, rhs.coords)
     coords, off, perm, _ = _device.segment_plan(lhs.coords, rhs.coords, li, ri, w["agg_keys"],
-                                                [16, 6])
+                                                [16, 8])
     U = coords.shape[0]
     desc = _device.describe("ij,jk->ik", (128, 128), (128, 128))
-    desc.seg_group = 6
+    desc.seg_group = 8
     desc.out_dtype = _lib.EJ_BF16
     gq = ctypes.c_int32(1)
     lib = _lib.load()
     _lib.check(lib.ej_segment_einsum_group(ctypes.byref(desc), _lib.EJ_BF16, ctypes.byref(gq)),
                "ej_segment_einsum_group")
     group = gq.value
-    assert group == 2 and U == 96
+    assert group == 2 and U == 128
     ngroups = (U + group - 1) // group
     n_dev = torch.tensor([U], dtype=torch.int64, device="cuda")
 
