@@ -110,6 +110,10 @@ SIGNATURES = {
     "ej_pair_plan_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32, _P_i64,
                                   _i32, _P_i32, _P_i32, _P_i64, _i64, _vp, _sz, _vp, _sz, _vp,
                                   _vp, _vp, _vp, _vp, _i64, _i32, _vp, _P_i32, _vp, _i32, _vp]),
+    "ej_pair_plan_async_noalloc": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32,
+                                          _P_i64, _i32, _P_i32, _P_i32, _P_i64, _i64, _vp, _vp,
+                                          _vp, _vp, _vp, _i64, _i32, _vp, _P_i32, _vp, _i32,
+                                          _vp]),
     "ej_host_alloc": (_i32, [_sz, ctypes.POINTER(_vp)]),
     "ej_host_free": (_i32, [_vp]),
     "ej_index_plan_workspace_size": (_i32, [_i64, _P_sz]),

@@ -13,6 +13,7 @@
 //      pair.  Probe order EJ_ORDER_PROBE: probe side = rhs in index order,
 //      giving the hash join's order.  EJ_ORDER_SORTED: both sides sorted,
 //      probe side = lhs in sorted order, giving the sort-merge order.
+#include <mutex>
 #include "ej_internal.h"
 
 namespace ej {
@@ -1287,26 +1288,26 @@ extern "C" int ej_segment_fill_async(int64_t n_pairs, int32_t n_out, const int64
   return EJ_OK;
 }
 
-extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
-                                  const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
-                                  int32_t n_keys, const int32_t *lhs_dims,
-                                  const int32_t *rhs_dims, const int64_t *join_radices,
-                                  int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
-                                  const int64_t *agg_radices, int64_t pair_capacity,
-                                  void *join_workspace, size_t join_workspace_bytes,
-                                  void *seg_workspace, size_t seg_workspace_bytes,
-                                  int64_t *lhs_idx, int64_t *rhs_idx, int32_t *out_coords,
-                                  int32_t *seg_offsets, int32_t *perm, int64_t seg_capacity,
-                                  int32_t group, int32_t *run_order, int32_t *run_order_written,
-                                  int64_t *counts, int32_t counts_direct, ej_stream_t stream_) {
-  clear_error();
-  hipStream_t stream = as_stream(stream_);
+namespace ej {
+namespace {
+
+// The queued pair plan on caller-supplied workspaces (ej_pair_plan_async) or
+// on the library's static scratch (ej_pair_plan_async_noalloc).
+int pair_plan_impl(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                   const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols, int32_t n_keys,
+                   const int32_t *lhs_dims, const int32_t *rhs_dims, const int64_t *join_radices,
+                   int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
+                   const int64_t *agg_radices, int64_t pair_capacity, void *join_workspace,
+                   size_t join_workspace_bytes, void *seg_workspace, size_t seg_workspace_bytes,
+                   int64_t *lhs_idx, int64_t *rhs_idx, int32_t *out_coords,
+                   int32_t *seg_offsets, int32_t *perm, int64_t seg_capacity, int32_t group,
+                   int32_t *run_order, int32_t *run_order_written, int64_t *counts,
+                   int32_t counts_direct, hipStream_t stream) {
   EJ_CHECK_ARG(counts && lhs_idx && rhs_idx && seg_offsets && perm &&
                    (out_coords || n_out == 0),
                "null pointer argument");
   EJ_CHECK_ARG(seg_capacity >= 0, "negative seg_capacity");
   EJ_CHECK_ARG(group >= 0, "negative group");
-  if (run_order_written) *run_order_written = 0;
   EJ_CHECK_ARG(n_keys >= 1 && n_lhs >= 1 && n_rhs >= 1,
                "the queued pair plan needs join keys and two non-empty relations");
   EJ_CHECK_ARG(pair_capacity >= 1 && pair_capacity < (int64_t(1) << 31),
@@ -1398,6 +1399,99 @@ extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int3
     EJ_LAUNCH_CHECK();
   }
   return EJ_OK;
+}
+
+// Static scratch of the allocation-free plan: the join workspace and the
+// segment workspace of one call, carved from one device array that every
+// GPU holds (its own copy) from the library's load to the end of the
+// process.  The array's name is a host-side stand-in: kernels receive its
+// device address, looked up once per device with hipGetSymbolAddress.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kNoAllocMaxDevices];  // device address of scratch, per device
+
+int scratch_base(void **base) {
+  int dev = -1;
+  EJ_HIP(hipGetDevice(&dev));
+  EJ_CHECK_ARG(dev >= 0 && dev < kNoAllocMaxDevices, "device %d beyond the %d supported", dev,
+               kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return EJ_E_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *base = g_scratch_ptr[dev];
+  return EJ_OK;
+}
+
+}  // namespace
+}  // namespace ej
+
+extern "C" int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                                  const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                                  int32_t n_keys, const int32_t *lhs_dims,
+                                  const int32_t *rhs_dims, const int64_t *join_radices,
+                                  int32_t n_out, const int32_t *agg_src, const int32_t *agg_dim,
+                                  const int64_t *agg_radices, int64_t pair_capacity,
+                                  void *join_workspace, size_t join_workspace_bytes,
+                                  void *seg_workspace, size_t seg_workspace_bytes,
+                                  int64_t *lhs_idx, int64_t *rhs_idx, int32_t *out_coords,
+                                  int32_t *seg_offsets, int32_t *perm, int64_t seg_capacity,
+                                  int32_t group, int32_t *run_order, int32_t *run_order_written,
+                                  int64_t *counts, int32_t counts_direct, ej_stream_t stream_) {
+  clear_error();
+  if (run_order_written) *run_order_written = 0;
+  return pair_plan_impl(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
+                        lhs_dims, rhs_dims, join_radices, n_out, agg_src, agg_dim, agg_radices,
+                        pair_capacity, join_workspace, join_workspace_bytes, seg_workspace,
+                        seg_workspace_bytes, lhs_idx, rhs_idx, out_coords, seg_offsets, perm,
+                        seg_capacity, group, run_order, run_order_written, counts,
+                        counts_direct, as_stream(stream_));
+}
+
+extern "C" int ej_pair_plan_async_noalloc(
+    const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols, const int32_t *rhs_coords,
+    int64_t n_rhs, int32_t rhs_ncols, int32_t n_keys, const int32_t *lhs_dims,
+    const int32_t *rhs_dims, const int64_t *join_radices, int32_t n_out, const int32_t *agg_src,
+    const int32_t *agg_dim, const int64_t *agg_radices, int64_t pair_capacity, int64_t *lhs_idx,
+    int64_t *rhs_idx, int32_t *out_coords, int32_t *seg_offsets, int32_t *perm,
+    int64_t seg_capacity, int32_t group, int32_t *run_order, int32_t *run_order_written,
+    int64_t *counts, int32_t counts_direct, ej_stream_t stream_) {
+  clear_error();
+  if (run_order_written) *run_order_written = 0;
+  EJ_CHECK_ARG(n_lhs >= 1 && n_rhs >= 1 && n_lhs < (int64_t(1) << 31) &&
+                   n_rhs < (int64_t(1) << 31),
+               "the queued pair plan needs two non-empty relations below 2^31 tiles");
+  EJ_CHECK_ARG(pair_capacity >= 1 && pair_capacity < (int64_t(1) << 31),
+               "pair_capacity must lie in [1, 2^31)");
+  const size_t jb = carve_join(nullptr, n_lhs, n_rhs, EJ_ORDER_PROBE).bytes;
+  const size_t sb = carve_seg(nullptr, pair_capacity).bytes;
+  const size_t joff = 0, soff = (jb + 255) & ~size_t(255);
+  if (soff + sb > kNoAllocScratchBytes) {
+    set_error("the allocation-free plan needs %zu bytes of scratch for %lld x %lld tiles and "
+              "%lld pairs; its static scratch holds %zu (use ej_pair_plan_async with "
+              "caller workspaces)",
+              soff + sb, (long long)n_lhs, (long long)n_rhs, (long long)pair_capacity,
+              kNoAllocScratchBytes);
+    return EJ_E_CAPACITY;
+  }
+  void *base = nullptr;
+  EJ_TRY(scratch_base(&base));
+  unsigned char *b = static_cast<unsigned char *>(base);
+  return pair_plan_impl(lhs_coords, n_lhs, lhs_ncols, rhs_coords, n_rhs, rhs_ncols, n_keys,
+                        lhs_dims, rhs_dims, join_radices, n_out, agg_src, agg_dim, agg_radices,
+                        pair_capacity, b + joff, jb, b + soff, sb, lhs_idx, rhs_idx, out_coords,
+                        seg_offsets, perm, seg_capacity, group, run_order, run_order_written,
+                        counts, counts_direct, as_stream(stream_));
 }
 
 // ---------------------------------------------------------------------------

@@ -293,6 +293,32 @@ int ej_pair_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
                        int32_t *run_order_written, int64_t *counts, int32_t counts_direct,
                        ej_stream_t stream);
 
+/* ej_pair_plan_async without workspace arguments: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * join and segment workspaces come from a static device scratch of 64 MiB
+ * that the library holds on every GPU it runs on until the process ends (it
+ * fits, e.g., 15,488 x 131,072 tiles with 991,232 pairs); a call that needs
+ * more returns EJ_E_CAPACITY.  The call allocates nothing (no hipMalloc, no
+ * hipFree) and clears what must start at zero itself.  Every call on one GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (other streams or
+ * threads, before the previous call's kernels finished reading the scratch
+ * through its einsum) race.  Arguments and results as ej_pair_plan_async,
+ * except that the device-side segment count stays in the scratch: U is
+ * returned in counts[0] (with counts_direct, the device address of counts,
+ * from hipHostGetDevicePointer, can serve as the n_segments_dev of
+ * ej_segment_einsum_async). */
+int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                               const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                               int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                               const int64_t *join_radices, int32_t n_out, const int32_t *agg_src,
+                               const int32_t *agg_dim, const int64_t *agg_radices,
+                               int64_t pair_capacity, int64_t *lhs_idx, int64_t *rhs_idx,
+                               int32_t *out_coords, int32_t *seg_offsets, int32_t *perm,
+                               int64_t seg_capacity, int32_t group, int32_t *run_order,
+                               int32_t *run_order_written, int64_t *counts, int32_t counts_direct,
+                               ej_stream_t stream);
+
 /* Coherent, device-mapped host memory (hipHostMalloc, mapped | coherent) for
  * counts that kernels store directly (ej_pair_plan_async, counts_direct). */
 int ej_host_alloc(size_t bytes, void **host_ptr);

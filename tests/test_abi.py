@@ -290,6 +290,25 @@ def test_pair_plan_host_validation():
     assert b"pair_capacity" in lib.ej_last_error()
 
 
+def test_pair_plan_noalloc_host_validation():
+    """The allocation-free plan checks its arguments and its scratch limit
+    (64 MiB) on the host, before it looks up the scratch or launches
+    anything: a request beyond the limit gets EJ_E_CAPACITY here, where no
+    GPU is visible."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(16)
+    d = i32_array([1])
+    counts = (ctypes.c_int64 * 8)()
+    args = lambda nl, cap: (fake, nl, 2, fake, 4, 2, 1, d, i32_array([0]), i64_array([4]), 2,
+                            i32_array([0, 1]), i32_array([0, 1]), i64_array([4, 4]), cap, fake,
+                            fake, fake, fake, fake, 16, 0, None, None,
+                            ctypes.cast(counts, ctypes.c_void_p), 0, None)
+    assert lib.ej_pair_plan_async_noalloc(*args(4, 2_000_000)) == _lib.EJ_E_CAPACITY
+    assert b"static scratch" in lib.ej_last_error()
+    assert lib.ej_pair_plan_async_noalloc(*args(4, 0)) == _lib.EJ_E_INVAL
+    assert lib.ej_pair_plan_async_noalloc(*args(0, 10)) == _lib.EJ_E_INVAL
+
+
 def test_segment_einsum_group():
     """The group size a run order is made for: two 128 x 128 bf16 output
     tiles per workgroup, four 64 x 64 bf16 or fp32 ones, 1 without the
