@@ -102,48 +102,107 @@ def load_traffic(kernel: str):
         return None
 
 
-def cpu_baseline(w, band_tiles: int, min_seconds: float = 10.0):
-    """The oracle (NumPy restatement of the reference path, fp32 math) over
-    bands of `band_tiles` A row tiles, cycling through the whole workload
-    until at least min_seconds of CPU work have been timed.  Each band is a
-    complete execute_sparse (join, gather, fp32 tile einsum, segment sum)."""
-    from oracle import reference_path as R
-    from oracle import workload as W
-
+def _cpu_info() -> dict:
+    """The host the CPU baseline ran on: model, logical CPUs, the CPUs this
+    process may use, and the BLAS / OpenMP thread settings."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    blas = []
     try:
         from threadpoolctl import threadpool_info
 
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+        blas = [{"api": i.get("internal_api"), "num_threads": i.get("num_threads")}
+                for i in threadpool_info()]
     except Exception:
-        cores = os.cpu_count() or 1
+        pass
+    env = {k: os.environ[k] for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS",
+                                      "MKL_NUM_THREADS", "XLA_FLAGS") if k in os.environ}
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "sched_getaffinity": len(os.sched_getaffinity(0)), "blas_threadpools": blas,
+            "thread_env": env}
+
+
+def cpu_baseline(w, band_tiles: int, min_seconds: float = 10.0):
+    """The oracle (NumPy restatement of the reference path, fp32 math) over
+    bands of `band_tiles` A row tiles, cycling through the whole workload
+    until at least min_seconds of CPU work have been timed.  Each band runs
+    the reference's phases one after another, each timed on its own
+    (reference: sparse_dispatch.py:29-171 and tensor/sparse.py:160-219):
+    bucketing of the band's dense rows into tiles, the dict hash join, the
+    gather of the matched tiles, the batched fp32 tile einsum, the output
+    coordinates and the sequential segment sum.  value counts the phases of
+    execute_sparse (join to segment sum); bucketing is reported beside it."""
+    from oracle import reference_path as R
+    from oracle import workload as W
+
+    info = _cpu_info()
+    cores = max([b["num_threads"] or 1 for b in info["blas_threadpools"]] or [1])
     L, Rr = w["lhs"], w["rhs"]
-    n_bands = -(-(L.shape[0] // L.tile_shape[0]) // band_tiles)
+    tm, tk = L.tile_shape
+    n_bands = -(-(L.shape[0] // tm) // band_tiles)
     bands = []
     for b in range(n_bands):
         sel = (L.coords[:, 0] >= b * band_tiles) & (L.coords[:, 0] < (b + 1) * band_tiles)
-        sub = R.Rel(L.coords[sel], L.values[sel], L.shape, L.tile_shape)
-        li, _ = R.coordinate_join(sub.coords, Rr.coords, w["join_keys"])
-        bands.append((sub, len(li)))
+        bands.append(R.Rel(L.coords[sel], L.values[sel], L.shape, L.tile_shape))
+    phases = dict.fromkeys(["bucketing", "join", "gather", "einsum", "output_coords",
+                            "segment_sum"], 0.0)
     flops = 0.0
     n_runs = 0
     t = 0.0
+    rv32 = Rr.values.astype(np.float32)
+    # Bucketing (np.nonzero + np.unique over the band's nonzeros) is slow in
+    # NumPy: it is timed on the first band only and scaled to the workload.
+    sub = bands[0]
+    dense = np.zeros((band_tiles * tm, L.shape[1]))
+    for (i, j), v in zip(sub.coords, sub.values):
+        dense[i * tm:(i + 1) * tm, j * tk:(j + 1) * tk] = v
+    t0 = time.perf_counter()
+    R.dense_to_relation(dense, L.tile_shape)
+    t_bucket_band = time.perf_counter() - t0
+    del dense
     while t < min_seconds:
-        sub, n_pairs = bands[n_runs % n_bands]
-        t0 = time.perf_counter()
-        R.execute_sparse(sub, Rr, w["join_keys"], w["kernel_string"], w["agg_keys"],
-                         precision="fp32")
-        t += time.perf_counter() - t0
-        flops += W.flops_gemm(w["kernel_string"], L.tile_shape, Rr.tile_shape, n_pairs)
+        sub = bands[n_runs % n_bands]
+        t1 = time.perf_counter()
+        li, ri = R.coordinate_join(sub.coords, Rr.coords, w["join_keys"])
+        t2 = time.perf_counter()
+        ga = sub.values.astype(np.float32)[li]
+        gb = rv32[ri]
+        t3 = time.perf_counter()
+        tiles = R.batched_einsum(R.add_batch_dim(w["kernel_string"]), ga, gb)
+        t4 = time.perf_counter()
+        oc = R.compute_output_coords(sub.coords, Rr.coords, li, ri, w["agg_keys"])
+        t5 = time.perf_counter()
+        R.segment_sum(tiles, oc)
+        t6 = time.perf_counter()
+        for k, dt in zip(list(phases)[1:], (t2 - t1, t3 - t2, t4 - t3, t5 - t4, t6 - t5)):
+            phases[k] += dt
+        t += t6 - t1
+        flops += W.flops_gemm(w["kernel_string"], L.tile_shape, Rr.tile_shape, len(li))
         n_runs += 1
+        del ga, gb, tiles
+    phases["bucketing"] = t_bucket_band * n_runs
     return {
         "value": flops / t / 1e12,
         "unit": "TFLOP/s",
         "cores": int(cores),
         "kind": "port",
-        "sample": (f"{n_runs} execute_sparse runs of the oracle, each on a band of {band_tiles} "
+        "sample": (f"{n_runs} runs of the oracle's phases, each on a band of {band_tiles} "
                    f"A row tiles x full B, cycling over the {n_bands} bands "
-                   f"({n_runs / n_bands:.2f} x the whole workload, {flops / 1e9:.0f} GFLOP) in "
-                   f"{t:.1f} s"),
+                   f"({n_runs / n_bands:.2f} x the whole workload, {flops / 1e9:.0f} GFLOP); "
+                   f"join to segment sum {t:.1f} s; bucketing, beside it, timed on one band "
+                   f"({t_bucket_band:.1f} s) and counted once per run"),
+        "phases_s": phases,
+        "phase_frac": {k: v / t for k, v in phases.items() if k != "bucketing"},
+        "einsum_tflops": flops / phases["einsum"] / 1e12,
+        "host": info,
+        "excluded": "per-tile-shape statistics (_compute_sparsity_metrics), construction "
+                    "metadata, as the reference computes them before execute_sparse",
     }
 
 
@@ -392,17 +451,12 @@ def main():
     def step():
         return execute_sparse(lhs, rhs, jk, ks, ak)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    gc.collect()
-    gc.disable()  # no collector pause inside the timed steps
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = step()
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    gc.enable()
+    # The CPU baseline and the stage timings run before the timed steps, so
+    # that the GPU is at its working clocks when the warm-up steps start.
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on a sample ...")
+        cpu = cpu_baseline(w, band_tiles=16)
 
     # ---- stages ----------------------------------------------------------
     lc, rc = lhs.coords, rhs.coords
@@ -416,35 +470,62 @@ def main():
     reps = 10
     t_join = wall_time_ms(lambda: sd._join_dev(lhs, rhs, jk, lc, rc), reps)
     t_plan = wall_time_ms(lambda: _device.segment_plan(lc, rc, li, ri, ak, radices), reps)
-    # The fused einsum as the step launches it, and as the exact path does
-    # (its own segment plan, no run order).
+    # The fused einsum as the exact path launches it (its own segment plan,
+    # no run order); the step's launch is timed after the steps.
     t_fused_exact = event_time_ms(
         lambda: _device.segment_einsum(desc, lhs.values, rhs.values, li, ri, perm, offs), reps)
-    t_fused = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, 20) or t_fused_exact
     ga = _device.gather_tiles(lhs.values, li)
     gb = _device.gather_tiles(rhs.values, ri)
     t_gather = event_time_ms(lambda: (_device.gather_tiles(lhs.values, li),
                                       _device.gather_tiles(rhs.values, ri)), reps)
     t_pair = event_time_ms(lambda: _device.pair_einsum(desc, ga, gb, n_pairs=P), reps)
     pv = _device.pair_einsum(desc, ga, gb, n_pairs=P)
+    t_segsum16 = event_time_ms(lambda: _device.segment_sum(pv, perm, offs), reps)
+    del pv
+    pv = _device.pair_einsum(desc, ga, gb, n_pairs=P, out_dtype=torch.float32)
     t_segsum = event_time_ms(lambda: _device.segment_sum(pv, perm, offs), reps)
     del ga, gb, pv
     dense_a = lhs.to_dense()
     t_bucket = wall_time_ms(lambda: _device.bucket_dense(dense_a, L.tile_shape), 5)
     del dense_a
+    # The step with fp32 output tiles (out_dtype=float32): twice the bytes written.
+    step32 = lambda: execute_sparse(lhs, rhs, jk, ks, ak, out_dtype=torch.float32)
+    t_step32 = wall_time_ms(step32, 20)
+    t_fused32 = fused_in_step_ms(
+        lambda *a, **k: execute_sparse(*a, out_dtype=torch.float32, **k), lhs, rhs, jk, ks, ak,
+        20)
     torch.cuda.synchronize()
+
+    # ---- the timed steps -------------------------------------------------
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()  # no collector pause inside the timed steps
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    gc.enable()
+    # The fused einsum as the step launches it (after the device-side join
+    # and plan, in the plan's run order): HIP events on the launch stream.
+    t_fused = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, 20) or t_fused_exact
 
     e = 2
     F = W.flops_gemm(ks, L.tile_shape, Rr.tile_shape, P)
+    out_tile = (L.tile_shape[0], Rr.tile_shape[1])
     B_join = W.bytes_join(L.coords.shape[0], Rr.coords.shape[0], P)
     B_gather = W.bytes_gather(P, L.tile_shape, Rr.tile_shape, e)
-    B_segsum = W.bytes_segsum(P, U, (L.tile_shape[0], Rr.tile_shape[1]), 2, e)
+    B_segsum = W.bytes_segsum(P, U, out_tile, 2, 4)  # fp32 pair values and sums
+    B_segsum16 = W.bytes_segsum(P, U, out_tile, 2, e)  # bf16 pair values and sums
     B_bucket = W.bytes_bucket(int(np.prod(L.shape)), L.coords.shape[0], L.tile_shape, e, 2)
     n_lhs_used = len(np.unique(li.cpu().numpy()))
     n_rhs_used = len(np.unique(ri.cpu().numpy()))
     B_fused = W.bytes_fused(n_lhs_used, n_rhs_used, L.tile_shape, Rr.tile_shape, e, U,
-                            (L.tile_shape[0], Rr.tile_shape[1]), 2, e)
+                            out_tile, 2, e)
     jgs_gbs = (B_join + B_gather + B_segsum) / ((t_join + t_gather + t_segsum) * 1e-3) / 1e9
+    jgs16_gbs = (B_join + B_gather + B_segsum16) / ((t_join + t_gather + t_segsum16) * 1e-3) / 1e9
     fused_tflops = F / (t_fused * 1e-3) / 1e12
     kernel_name = "seg_gemm_kernel<SegOpBf16<128,128>,3,2,2,4,false>"
     traffic = load_traffic(kernel_name)
@@ -465,7 +546,7 @@ def main():
         "config": {
             "workload": "block-sparse x dense 'ij,jk->ik': A 16384x16384 bf16, 128x128 tiles, "
                         "5% tile density uniform; B dense 16384x4096 bf16 N(0,1/128); fp32 "
-                        "accumulate",
+                        "accumulate, bf16 output tiles",
             "pairs": P, "output_tiles": U, "lhs_tiles": int(L.coords.shape[0]),
             "rhs_tiles": int(Rr.coords.shape[0]), "gflop": F / 1e9,
         },
@@ -476,28 +557,32 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes": B_fused,
         },
+        "fp32_output": {
+            "ms_per_step": t_step32, "tflops": F / (t_step32 * 1e-3) / 1e12,
+            "fused_ms": t_fused32,
+            "fused_mfma_frac": None if t_fused32 is None else
+            F / (t_fused32 * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"],
+        },
         "stages_ms": {
             "join": t_join, "segment_plan": t_plan, "fused_gemm_segsum": t_fused,
             "fused_gemm_segsum_exact_path": t_fused_exact,
             "gather": t_gather, "pair_gemm": t_pair, "segment_sum": t_segsum,
-            "bucket_dense_A": t_bucket,
+            "segment_sum_bf16_values": t_segsum16, "bucket_dense_A": t_bucket,
         },
         "stages_gbs": {
             "join": B_join / (t_join * 1e-3) / 1e9,
             "gather": B_gather / (t_gather * 1e-3) / 1e9,
             "segment_sum": B_segsum / (t_segsum * 1e-3) / 1e9,
+            "segment_sum_bf16_values": B_segsum16 / (t_segsum16 * 1e-3) / 1e9,
             "bucket_dense_A": B_bucket / (t_bucket * 1e-3) / 1e9,
             "join_gather_segsum": jgs_gbs,
             "join_gather_segsum_hbm_frac": jgs_gbs / HBM_PEAK_GBS,
+            "join_gather_segsum_bf16_values_hbm_frac": jgs16_gbs / HBM_PEAK_GBS,
         },
         "unfused_tflops": F / ((t_join + t_plan + t_gather + t_pair + t_segsum) * 1e-3) / 1e12,
         "pair_gemm_tflops": F / (t_pair * 1e-3) / 1e12,
+        "cpu_baseline": cpu,
     }
-    if not args.no_cpu_baseline:
-        log("timing the CPU oracle on a sample ...")
-        res["cpu_baseline"] = cpu_baseline(w, band_tiles=16)
-    else:
-        res["cpu_baseline"] = None
     if args.backward:
         log("backward ...")
         res["backward"] = measure_backward(lhs, rhs, li, ri, ks, F)

@@ -347,6 +347,96 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     return "ok", (P, coords[:U], offsets[:U + 1], perm[:P], out[:U], li[:P], ri[:P])
 
 
+def dense_plan_applies(n_lhs: int, lhs_ncols: int, rhs_ncols: int, join_keys, agg_keys) -> bool:
+    """Whether the structure of a join suits ej_dense_plan_async (the device
+    then checks the data): rhs join dims 0 .. nk-1 with increasing lhs dims,
+    output = a prefix of the lhs dims then the rhs dims after the join dims,
+    every other lhs dim joined, 1 .. 32768 lhs tiles."""
+    nk = len(join_keys)
+    if nk < 1 or nk > rhs_ncols or not 1 <= n_lhs <= 32768:
+        return False
+    by_r = sorted((b, a) for a, b in join_keys)
+    if [b for b, _ in by_r] != list(range(nk)):
+        return False
+    ld = [a for _, a in by_r]
+    if any(x >= y for x, y in zip(ld, ld[1:])):
+        return False
+    nlo = 0
+    while nlo < len(agg_keys) and tuple(agg_keys[nlo]) == (0, nlo):
+        nlo += 1
+    rest = [tuple(k) for k in agg_keys[nlo:]]
+    if nlo < 1 or rest != [(1, d) for d in range(nk, rhs_ncols)]:
+        return False
+    return all(d in ld for d in range(nlo, lhs_ncols))
+
+
+def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
+                         lhs_values, rhs_values, out_dtype=None, einsum_events=None):
+    """Join, segment plan (ej_dense_plan_async: one launch, for a dense rhs
+    and increasing lhs coordinates) and the fused segment einsum, queued back
+    to back on the current stream; the host waits only for the plan's ticket.
+
+    Returns (status, result): "ok" with result = (P, coords [U, n_out],
+    seg_offsets, None, values [U, *out_tile], li, ri); "miss" when the data
+    does not have the dense structure (the queued einsum did no work);
+    "unsupported" when the join's structure does not suit the dense plan."""
+    lib = _lib.load()
+    dev = lhs_coords.device
+    code = value_code(lhs_values)
+    if rhs_values.dtype != lhs_values.dtype:
+        raise TypeError("both operands must have the same value dtype")
+    n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
+    nk = len(join_keys)
+    NK = prod(int(rhs_grid[d]) for d in range(nk, len(rhs_grid)))
+    nlo = len(agg_keys) - (len(rhs_grid) - nk)
+    cap_p = n_l * NK
+    cap_u = max(1, min(n_l, prod(int(lhs_grid[d]) for d in range(nlo))) * NK)
+    n_out = len(agg_keys)
+    base, counts, ticket = _count_buffer()
+    stream = stream_ptr()
+    li = torch.empty(cap_p, dtype=torch.int64, device=dev)
+    ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
+    coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
+    offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
+    dcounts = torch.empty(8, dtype=torch.int64, device=dev)
+    odt = _set_out_dtype(desc, lhs_values, out_dtype)
+    out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
+    gq = ctypes.c_int32(1)
+    check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
+          "ej_segment_einsum_group")
+    group = gq.value if gq.value > 1 else 0
+    order = torch.empty(1 + (cap_u + group - 1) // group if group else 1, dtype=torch.int32,
+                        device=dev)
+    order_written = ctypes.c_int32(0)
+    st = lib.ej_dense_plan_async(
+        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1],
+        nk, i32_array([k[0] for k in join_keys]), i32_array([k[1] for k in join_keys]),
+        i64_array(lhs_grid), i64_array(rhs_grid), n_out, i32_array([a for a, _ in agg_keys]),
+        i32_array([b for _, b in agg_keys]), ptr(li), ptr(ri), cap_p, ptr(coords), ptr(offsets),
+        cap_u, group, ptr(order) if group else None, ctypes.byref(order_written), ptr(dcounts),
+        ctypes.c_void_p(base), ticket, stream)
+    if st == _lib.EJ_E_UNSUPPORTED:
+        return "unsupported", None
+    check(st, "ej_dense_plan_async")
+    if einsum_events is not None:
+        einsum_events.append((torch.cuda.Event(enable_timing=True),
+                              torch.cuda.Event(enable_timing=True)))
+        einsum_events[-1][0].record()
+    check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
+                                      lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
+                                      None, ptr(offsets), cap_u, ptr(dcounts),
+                                      ptr(order) if order_written.value else None, group,
+                                      ptr(out), stream),
+          "ej_segment_einsum_async")
+    if einsum_events is not None:
+        einsum_events[-1][1].record()
+    _wait_ticket(counts, ticket)
+    U, miss, P = int(counts[0]), int(counts[1]), int(counts[4])
+    if miss:
+        return "miss", None
+    return "ok", (P, coords[:U], offsets[:U + 1], None, out[:U], li[:P], ri[:P])
+
+
 def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:
     """[U, *tile] in the pair values' dtype (float32 or bfloat16): per-segment
     sums in plan order, formed in fp32."""

@@ -1,0 +1,402 @@
+// Join and segment plan of a sparse einsum whose rhs holds every tile of its
+// grid, in one launch and without sorting.
+//
+// The reference joins with a dict and groups the pairs by output coordinate
+// with a second dict and a sort (execution/sparse_dispatch.py:29-82,
+// :129-171).  When the rhs relation is the full tile grid in lexicographic
+// order (a dense operand), its join dimensions lead, and the lhs coordinates
+// are strictly increasing, both results have a closed form: every lhs tile
+// meets exactly one rhs tile per combination of the rhs's free dimensions,
+// and the lhs tiles that share their leading (output) coordinates form a
+// contiguous run.  Output segment (run r, free index k) sums the pairs
+// (lhs tile t, rhs tile jrow(t) * NK + k) for t in run r, in lhs order; the
+// reference accumulates them in the same order (ascending rhs index, which
+// within a run is ascending lhs index).  Segments come in run order, then k:
+// the reference's sorted output coordinates.
+//
+// The kernel checks those properties on the device; where they fail it
+// reports it (counts[1] = 1) and leaves the segment count at 0, so that an
+// einsum queued behind it does no work and the caller takes the general
+// join and plan.
+#include "ej_internal.h"
+
+namespace ej {
+namespace {
+
+constexpr int kDenseThreads = 1024;
+constexpr int kDenseTilesPerThread = 32;  // lhs tiles each thread scans
+constexpr int64_t kDenseMaxLhs = int64_t(kDenseThreads) * kDenseTilesPerThread;
+constexpr int kDenseMaxRuns = 8192;  // run starts held in LDS
+constexpr int kDensePairsPerThread = 8;
+constexpr int64_t kDensePairsPerBlock = int64_t(kDenseThreads) * kDensePairsPerThread;
+
+struct DenseSpec {
+  int32_t lncols, rncols;
+  int32_t nk;    // join keys; rhs dims 0 .. nk-1 are the join dims
+  int32_t nlo;   // lhs dims 0 .. nlo-1 are the output dims taken from the lhs
+  int32_t n_out; // nlo + (rncols - nk)
+  int32_t ldim[EJ_MAX_KEYS];   // lhs dim joined with rhs dim i
+  int64_t lgrid[EJ_MAX_DIMS];  // lhs tile grid
+  int64_t rgrid[EJ_MAX_DIMS];  // rhs tile grid
+  int64_t NK;                  // rhs tiles per join value: prod rgrid[nk .. rncols)
+  int64_t n_lhs, n_rhs, P;     // P = n_lhs * NK
+};
+
+__device__ inline void load_row(const int32_t *__restrict__ c, int64_t t, int ncols,
+                                int32_t (&v)[EJ_MAX_DIMS]) {
+#pragma unroll
+  for (int d = 0; d < EJ_MAX_DIMS; ++d) v[d] = d < ncols ? c[t * ncols + d] : 0;
+}
+
+// Linear index, over the rhs join grid, of lhs tile t's join coordinates.
+__device__ inline int64_t join_row(const int32_t *__restrict__ lc, int64_t t, const DenseSpec &s) {
+  int64_t j = 0;
+#pragma unroll
+  for (int i = 0; i < EJ_MAX_KEYS; ++i)
+    if (i < s.nk) j = j * s.rgrid[i] + lc[t * s.lncols + s.ldim[i]];
+  return j;
+}
+
+// Blocks of kDenseThreads threads.  Every block scans the lhs coordinates
+// (run starts, order and range checks) and keeps the run starts in LDS; block
+// b then writes pairs [b * kDensePairsPerBlock, ...), its share of the
+// segments, its share of the rhs check and (run_order) the order of the XCD
+// chunks assigned to it.  The last block to finish publishes the counts:
+// scal[0] = U (0 when a check failed), scal[1] = not-applicable flag, scal[2]
+// = scal[4] = P, and host_counts as ej_pair_plan_async does, then the ticket.
+// scal[1] and scal[3] (finished blocks) must be zero at launch.
+__global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
+    const int32_t *__restrict__ lc, const int32_t *__restrict__ rc, DenseSpec s,
+    int64_t *__restrict__ lidx, int64_t *__restrict__ ridx, int64_t pair_cap,
+    int32_t *__restrict__ out_coords, int32_t *__restrict__ seg_offsets, int64_t seg_cap,
+    int group, int32_t *__restrict__ run_order, int64_t *__restrict__ scal,
+    int64_t *__restrict__ host_counts, int64_t ticket) {
+  constexpr int NW = kDenseThreads / 64;
+  __shared__ int32_t run_start[kDenseMaxRuns + 1];
+  __shared__ int32_t cls_base[NW][256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t blk = blockIdx.x, nblk = gridDim.x;
+
+  // ---- lhs scan: this thread's tiles [t0, t1), contiguous --------------------
+  const int64_t per = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;
+  const int64_t t0 = min(s.n_lhs, tid * per), t1 = min(s.n_lhs, t0 + per);
+  int bad = 0;
+  uint32_t newmask = 0;  // bit i: tile t0 + i starts a run
+  int64_t nnew = 0;
+  int32_t pv[EJ_MAX_DIMS];
+  if (t0 > 0 && t0 < t1) load_row(lc, t0 - 1, s.lncols, pv);
+  for (int64_t t = t0; t < t1; ++t) {
+    int32_t cv[EJ_MAX_DIMS];
+    load_row(lc, t, s.lncols, cv);
+#pragma unroll
+    for (int d = 0; d < EJ_MAX_DIMS; ++d)
+      if (d < s.lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
+#pragma unroll
+    for (int i = 0; i < EJ_MAX_KEYS; ++i)
+      if (i < s.nk && cv[s.ldim[i]] >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
+    bool newrun = t == 0;
+    if (t > 0) {
+      int cmp = 0, first = EJ_MAX_DIMS;
+#pragma unroll
+      for (int d = 0; d < EJ_MAX_DIMS; ++d)
+        if (d < s.lncols && cmp == 0 && cv[d] != pv[d]) {
+          cmp = cv[d] < pv[d] ? -1 : 1;
+          first = d;
+        }
+      if (cmp <= 0) bad = 1;  // coordinates must be strictly increasing
+      newrun = first < s.nlo;
+    }
+    if (newrun) {
+      newmask |= 1u << (t - t0);
+      ++nnew;
+    }
+#pragma unroll
+    for (int d = 0; d < EJ_MAX_DIMS; ++d) pv[d] = cv[d];
+  }
+  int64_t nruns = 0;
+  const int64_t rbase = block_exclusive_sum<kDenseThreads>(nnew, &nruns);
+  const bool fits = nruns <= kDenseMaxRuns;
+  if (fits) {
+    int64_t r = rbase;
+    for (int64_t t = t0; t < t1; ++t)
+      if (newmask >> (t - t0) & 1u) run_start[r++] = static_cast<int32_t>(t);
+    if (tid == 0) run_start[nruns] = static_cast<int32_t>(s.n_lhs);
+  } else {
+    bad = 1;
+  }
+  __syncthreads();
+  const int64_t U = fits ? nruns * s.NK : 0;
+  const int64_t live_u = U < seg_cap ? U : seg_cap;
+  if (U > seg_cap) bad = 1;
+
+  // Run of pair q (segment order): the last r with run_start[r] * NK <= q.
+  auto run_of = [&](int64_t q) -> int64_t {
+    int64_t lo = 0, len = nruns;
+    while (len > 1) {
+      const int64_t half = len >> 1;
+      lo += static_cast<int64_t>(run_start[lo + half]) * s.NK <= q ? half : 0;
+      len -= half;
+    }
+    return lo;
+  };
+
+  // ---- pairs [q0, q1) in segment order -------------------------------------
+  if (fits) {
+    const int64_t q0 = blk * kDensePairsPerBlock;
+    const int64_t q1 = min(min(s.P, pair_cap), q0 + kDensePairsPerBlock);
+    for (int64_t q = q0 + tid; q < q1; q += kDenseThreads) {
+      const int64_t r = run_of(q);
+      const int64_t rs = run_start[r], len = run_start[r + 1] - rs;
+      const int64_t w = q - rs * s.NK;
+      const int64_t kk = w / len;
+      const int64_t t = rs + (w - kk * len);
+      lidx[q] = t;
+      ridx[q] = join_row(lc, t, s) * s.NK + kk;
+    }
+    // ---- segments: this block's share of [0, live_u) ----------------------
+    const int64_t upb = (live_u + nblk - 1) / nblk;
+    const int64_t u0 = blk * upb, u1 = min(live_u, u0 + upb);
+    for (int64_t u = u0 + tid; u < u1; u += kDenseThreads) {
+      const int64_t r = u / s.NK, kk = u - r * s.NK;
+      const int64_t rs = run_start[r], len = run_start[r + 1] - rs;
+      seg_offsets[u] = static_cast<int32_t>(rs * s.NK + kk * len);
+      int32_t *oc = out_coords + u * s.n_out;
+#pragma unroll
+      for (int d = 0; d < EJ_MAX_DIMS; ++d)
+        if (d < s.nlo) oc[d] = lc[rs * s.lncols + d];
+      int64_t rem = kk;
+#pragma unroll
+      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d)
+        if (d >= s.nk && d < s.rncols) {
+          oc[s.nlo + (d - s.nk)] = static_cast<int32_t>(rem % s.rgrid[d]);
+          rem /= s.rgrid[d];
+        }
+    }
+    if (blk == 0 && tid == 0 && U <= seg_cap) seg_offsets[U] = static_cast<int32_t>(s.P);
+  }
+
+  // ---- rhs check: row r holds the coordinates of grid position r ----------
+  {
+    const int64_t rpb = (s.n_rhs + nblk - 1) / nblk;
+    const int64_t r0 = blk * rpb, r1 = min(s.n_rhs, r0 + rpb);
+    for (int64_t r = r0 + tid; r < r1; r += kDenseThreads) {
+      int64_t rem = r;
+#pragma unroll
+      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d)
+        if (d < s.rncols) {
+          if (rc[r * s.rncols + d] != static_cast<int32_t>(rem % s.rgrid[d])) bad = 1;
+          rem /= s.rgrid[d];
+        }
+    }
+  }
+
+  // ---- run order: per XCD chunk of the live groups, longest first ---------
+  // Chunk x (the workgroups the einsum's XCD mapping gives XCD x) is ordered
+  // by wave x / nblk of block x % nblk: a stable counting sort over 256
+  // pair-count classes (counts above 255 tie), ranked with ballots.
+  if (fits && group > 0 && run_order) {
+    const int64_t ngroups = (live_u + group - 1) / group;
+    if (blk == 0 && tid == 0) run_order[0] = static_cast<int32_t>(ngroups);
+    for (int x = lane; x < 256; x += 64) cls_base[wave][x] = 0;
+    const int64_t x = static_cast<int64_t>(wave) * nblk + blk;  // the chunk of this wave
+    if (x < 8) {
+      const int64_t pc = ngroups / 8, rem = ngroups % 8;
+      const int64_t start = x < rem ? x * (pc + 1) : rem * (pc + 1) + (x - rem) * pc;
+      const int64_t cnt = pc + (x < rem ? 1 : 0);
+      auto cls = [&](int64_t i) {
+        int64_t wsum = 0;
+        for (int v = 0; v < group; ++v) {
+          const int64_t u = (start + i) * group + v;
+          if (u < live_u) {
+            const int64_t r = u / s.NK;
+            wsum += run_start[r + 1] - run_start[r];
+          }
+        }
+        return static_cast<int>(255 - (wsum < 255 ? wsum : 255));
+      };
+      for (int64_t i = lane; i < cnt; i += 64) atomicAdd(&cls_base[wave][cls(i)], 1);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      int v[4], sum = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = cls_base[wave][lane * 4 + k];
+        sum += v[k];
+      }
+      int inc = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int tt = __shfl_up(inc, o);
+        if (lane >= o) inc += tt;
+      }
+      int run = inc - sum;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        cls_base[wave][lane * 4 + k] = run;
+        run += v[k];
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+      for (int64_t i0 = 0; i0 < cnt; i0 += 64) {
+        const int64_t i = i0 + lane;
+        const bool valid = i < cnt;
+        const int c = valid ? cls(i) : 0;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const int bit = (c >> b) & 1;
+          const uint64_t m = __ballot(bit);
+          peers &= bit ? m : ~m;
+        }
+        asm volatile("" ::: "memory");
+        const int base = valid ? cls_base[wave][c] : 0;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (valid)
+          run_order[1 + start + base + __popcll(peers & lt)] = static_cast<int32_t>(start + i);
+        if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+  }
+
+  // ---- publish: the last block to finish writes the counts ----------------
+  const int blk_bad = __syncthreads_or(bad);
+  if (tid == 0) {
+    unsigned long long *flag = reinterpret_cast<unsigned long long *>(scal + 1);
+    unsigned long long *done = reinterpret_cast<unsigned long long *>(scal + 3);
+    if (blk_bad) atomicOr(flag, 1ull);
+    __threadfence();
+    const unsigned long long prev = atomicAdd(done, 1ull);
+    if (prev == static_cast<unsigned long long>(nblk - 1)) {
+      __threadfence();
+      const int64_t any_bad = static_cast<int64_t>(atomicOr(flag, 0ull));
+      const int64_t u_out = any_bad ? 0 : U;
+      scal[0] = u_out;
+      scal[2] = s.P;
+      scal[4] = s.P;
+      scal[5] = 0;
+      if (host_counts) {
+        host_counts[0] = u_out;
+        host_counts[1] = any_bad;
+        host_counts[2] = s.P;
+        host_counts[3] = 0;
+        host_counts[4] = s.P;
+        host_counts[5] = 0;
+        __threadfence_system();
+        host_counts[6] = ticket;
+        __threadfence_system();
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace ej
+
+using namespace ej;
+
+extern "C" int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                                   const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                                   int32_t n_keys, const int32_t *lhs_dims,
+                                   const int32_t *rhs_dims, const int64_t *lhs_grid,
+                                   const int64_t *rhs_grid, int32_t n_out,
+                                   const int32_t *agg_src, const int32_t *agg_dim,
+                                   int64_t *lhs_idx, int64_t *rhs_idx, int64_t pair_capacity,
+                                   int32_t *out_coords, int32_t *seg_offsets,
+                                   int64_t seg_capacity, int32_t group, int32_t *run_order,
+                                   int32_t *run_order_written, int64_t *dev_counts,
+                                   int64_t *counts, int32_t counts_direct,
+                                   ej_stream_t stream_) {
+  clear_error();
+  hipStream_t stream = as_stream(stream_);
+  if (run_order_written) *run_order_written = 0;
+  EJ_CHECK_ARG(lhs_coords && rhs_coords && lhs_idx && rhs_idx && out_coords && seg_offsets &&
+                   dev_counts && counts && lhs_grid && rhs_grid,
+               "null pointer argument");
+  EJ_CHECK_ARG(group >= 0 && counts_direct >= 0, "negative group or counts_direct");
+  EJ_CHECK_ARG(lhs_ncols >= 1 && lhs_ncols <= EJ_MAX_DIMS && rhs_ncols >= 1 &&
+                   rhs_ncols <= EJ_MAX_DIMS,
+               "coordinate rank outside [1, %d]", EJ_MAX_DIMS);
+  EJ_CHECK_ARG(n_keys >= 1 && n_keys <= rhs_ncols && n_keys <= EJ_MAX_KEYS,
+               "the dense plan needs 1 .. rhs rank join keys");
+  EJ_CHECK_ARG(lhs_dims && rhs_dims && (agg_src || n_out == 0) && (agg_dim || n_out == 0),
+               "null key arrays");
+  DenseSpec s{};
+  s.lncols = lhs_ncols;
+  s.rncols = rhs_ncols;
+  s.nk = n_keys;
+  s.n_lhs = n_lhs;
+  s.n_rhs = n_rhs;
+  // Join dims: rhs dims 0 .. nk-1, each once, their lhs dims increasing in
+  // rhs-dim order (so that lhs order within a run is rhs order).
+  for (int i = 0; i < n_keys; ++i) s.ldim[i] = -1;
+  for (int k = 0; k < n_keys; ++k) {
+    const int r = rhs_dims[k], l = lhs_dims[k];
+    if (r < 0 || r >= n_keys || s.ldim[r] >= 0 || l < 0 || l >= lhs_ncols) {
+      set_error("the dense plan needs the join to cover rhs dims 0 .. %d once each", n_keys - 1);
+      return EJ_E_UNSUPPORTED;
+    }
+    s.ldim[r] = l;
+  }
+  for (int i = 1; i < n_keys; ++i)
+    if (s.ldim[i] <= s.ldim[i - 1]) {
+      set_error("the dense plan needs the join's lhs dims in the rhs dims' order");
+      return EJ_E_UNSUPPORTED;
+    }
+  // Output: lhs dims 0 .. nlo-1, then every rhs dim from nk on, in order.
+  int nlo = 0;
+  while (nlo < n_out && agg_src[nlo] == 0 && agg_dim[nlo] == nlo) ++nlo;
+  bool agg_ok = nlo >= 1 && n_out == nlo + (rhs_ncols - n_keys);
+  for (int d = nlo; agg_ok && d < n_out; ++d)
+    agg_ok = agg_src[d] == 1 && agg_dim[d] == n_keys + (d - nlo);
+  // Every lhs dim from nlo on is a join dim (it varies within a run).
+  for (int d = nlo; agg_ok && d < lhs_ncols; ++d) {
+    bool joined = false;
+    for (int i = 0; i < n_keys; ++i) joined = joined || s.ldim[i] == d;
+    agg_ok = joined;
+  }
+  if (!agg_ok) {
+    set_error("the dense plan needs output dims = a prefix of the lhs dims, then the rhs "
+              "dims after its join dims");
+    return EJ_E_UNSUPPORTED;
+  }
+  s.nlo = nlo;
+  s.n_out = n_out;
+  int64_t grid_r = 1;
+  for (int d = 0; d < rhs_ncols; ++d) {
+    EJ_CHECK_ARG(rhs_grid[d] >= 1 && rhs_grid[d] < (int64_t(1) << 31), "bad rhs grid");
+    s.rgrid[d] = rhs_grid[d];
+    grid_r *= rhs_grid[d];
+  }
+  for (int d = 0; d < lhs_ncols; ++d) {
+    EJ_CHECK_ARG(lhs_grid[d] >= 1 && lhs_grid[d] < (int64_t(1) << 31), "bad lhs grid");
+    s.lgrid[d] = lhs_grid[d];
+  }
+  s.NK = 1;
+  for (int d = n_keys; d < rhs_ncols; ++d) s.NK *= rhs_grid[d];
+  if (n_rhs != grid_r || n_lhs < 1 || n_lhs > kDenseMaxLhs) {
+    set_error("the dense plan needs a full rhs grid and 1 .. %lld lhs tiles",
+              (long long)kDenseMaxLhs);
+    return EJ_E_UNSUPPORTED;
+  }
+  s.P = n_lhs * s.NK;
+  EJ_CHECK_ARG(s.P < (int64_t(1) << 31), "pair count beyond 2^31");
+  if (pair_capacity < s.P) {
+    set_error("pair capacity %lld < %lld pairs", (long long)pair_capacity, (long long)s.P);
+    return EJ_E_CAPACITY;
+  }
+  EJ_CHECK_ARG(seg_capacity >= 1, "seg_capacity must be positive");
+  EJ_TRY(zero_async(dev_counts, 8 * sizeof(int64_t), stream));
+  int64_t *direct = nullptr;
+  if (counts_direct) EJ_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&direct), counts, 0));
+  const int64_t nblk = ceil_div(s.P, kDensePairsPerBlock);
+  const bool order = run_order && group > 0;
+  hipLaunchKernelGGL(dense_plan_kernel, dim3(static_cast<unsigned>(nblk)), dim3(kDenseThreads), 0,
+                     stream, lhs_coords, rhs_coords, s, lhs_idx, rhs_idx, pair_capacity,
+                     out_coords, seg_offsets, seg_capacity, order ? group : 0,
+                     order ? run_order : nullptr, dev_counts, direct, int64_t(counts_direct));
+  EJ_LAUNCH_CHECK();
+  if (order && run_order_written) *run_order_written = 1;
+  if (!direct)
+    EJ_HIP(hipMemcpyAsync(counts, dev_counts, 6 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+  return EJ_OK;
+}

@@ -220,6 +220,35 @@ def _hint_set(key, lhs: SparseTensorRelation, rhs: SparseTensorRelation, bound: 
         _pair_hints[key] = ent
 
 
+def _dense_step(lhs, rhs, keys, agg, lc, rc, operands, out_dtype, events):
+    """The whole step on the dense-rhs plan (one plan launch, then the fused
+    einsum) when the join's structure suits it and the rhs holds every tile
+    of its grid; None otherwise.  A device-side miss (coordinates that break
+    the dense structure) is remembered for these coordinate arrays, so later
+    calls go straight to the general plan."""
+    nl, nr = lc.shape[1], rc.shape[1]
+    if nl != lhs.ndim or nr != rhs.ndim:
+        return None
+    rgrid = [_grid(rhs, d) for d in range(nr)]
+    n_full = 1
+    for g in rgrid:
+        n_full *= g
+    if rc.shape[0] != n_full or not _device.dense_plan_applies(lc.shape[0], nl, nr, keys, agg):
+        return None
+    key = _hint_key(lhs, rhs, ("dense", tuple(lc.shape), tuple(rc.shape), tuple(keys),
+                                tuple(agg)))
+    if _hint_get(key, lhs, rhs) == -1:
+        return None
+    lgrid = [_grid(lhs, d) for d in range(nl)]
+    desc, a, b = operands()
+    status, res = _device.dense_segment_einsum(lc, rc, keys, agg, lgrid, rgrid, desc, a, b,
+                                               out_dtype, events)
+    if status == "ok":
+        return res
+    _hint_set(key, lhs, rhs, -1)
+    return None
+
+
 def coordinate_join(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys):
     """Matched tile pairs on join_keys = [(lhs_dim, rhs_dim), ...]
     (reference: sparse_dispatch.py:29-82).
@@ -427,6 +456,8 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     bound = None
     queued = None
     if fused and keys and lc.shape[0] and rc.shape[0]:
+        queued = _dense_step(lhs, rhs, keys, agg, lc, rc, operands, out_dtype, _einsum_events)
+    if queued is None and fused and keys and lc.shape[0] and rc.shape[0]:
         j_rad = _join_radices(lhs, rhs, keys, None)
         hint_key = _hint_key(lhs, rhs, (tuple(lc.shape), tuple(rc.shape), tuple(keys),
                                         tuple(j_rad), tuple(agg)))

@@ -76,7 +76,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 11
+#define EJ_ABI_VERSION 12
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -318,6 +318,42 @@ int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t
                                int64_t seg_capacity, int32_t group, int32_t *run_order,
                                int32_t *run_order_written, int64_t *counts, int32_t counts_direct,
                                ej_stream_t stream);
+
+/* Join and segment plan in one launch for a join against a dense rhs (no
+ * counterpart in the reference, whose join and grouping run on the host,
+ * sparse_dispatch.py:29-82, :129-171; the results are the same).  Applies
+ * when the rhs holds every tile of its grid rhs_grid in lexicographic order,
+ * its join dims are rhs dims 0 .. n_keys-1 (each joined once, their lhs dims
+ * increasing in that order), the output dims are lhs dims 0 .. nlo-1 followed
+ * by rhs dims n_keys .. rhs_ncols-1, every other lhs dim is a join dim, and
+ * the lhs coordinates are strictly increasing in lexicographic order and
+ * inside lhs_grid; 1 <= n_lhs <= 32768.  Then every lhs tile meets one rhs
+ * tile per value of the rhs dims after the join dims (NK of them), P = n_lhs
+ * * NK, and the lhs tiles sharing their first nlo coordinates form a run: the
+ * plan writes the pairs in segment order (perm = identity: pass perm = NULL
+ * to the einsum), segment u = (run u / NK, k = u % NK) holding the run's
+ * tiles in lhs order (the reference's accumulation order),
+ * seg_offsets[0 .. U], out_coords [U, n_out] (ascending, as the reference
+ * sorts them) and, given run_order and group, a run order as
+ * ej_pair_plan_async does.  Structure that does not match gives
+ * EJ_E_UNSUPPORTED (take the general plan).  Properties that fail on the
+ * device (rhs not the full grid in order, lhs not increasing or outside its
+ * grid, more than 8192 runs, U > seg_capacity) give counts[1] = 1 and a
+ * segment count of 0 on the device, so that an einsum queued behind does no
+ * work; the caller then takes the general plan.  Capacities: pair_capacity
+ * >= n_lhs * NK; seg_capacity bounds U.  dev_counts: device int64[8], its
+ * first entry U afterwards (the n_segments_dev of ej_segment_einsum_async).
+ * counts / counts_direct as ej_pair_plan_async (counts[0] = U, [1] = the
+ * not-applicable flag, [2] = [4] = P).  Asynchronous. */
+int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                        const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                        int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                        const int64_t *lhs_grid, const int64_t *rhs_grid, int32_t n_out,
+                        const int32_t *agg_src, const int32_t *agg_dim, int64_t *lhs_idx,
+                        int64_t *rhs_idx, int64_t pair_capacity, int32_t *out_coords,
+                        int32_t *seg_offsets, int64_t seg_capacity, int32_t group,
+                        int32_t *run_order, int32_t *run_order_written, int64_t *dev_counts,
+                        int64_t *counts, int32_t counts_direct, ej_stream_t stream);
 
 /* Coherent, device-mapped host memory (hipHostMalloc, mapped | coherent) for
  * counts that kernels store directly (ej_pair_plan_async, counts_direct). */

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 11
+    assert _lib.load().ej_version() == 12
 
 
 def describe(spec, lt, rt):
@@ -307,6 +307,48 @@ def test_pair_plan_noalloc_host_validation():
     assert b"static scratch" in lib.ej_last_error()
     assert lib.ej_pair_plan_async_noalloc(*args(4, 0)) == _lib.EJ_E_INVAL
     assert lib.ej_pair_plan_async_noalloc(*args(0, 10)) == _lib.EJ_E_INVAL
+
+
+def test_dense_plan_host_validation():
+    """The dense-rhs plan decides from the join's structure, on the host,
+    whether it applies (EJ_E_UNSUPPORTED otherwise) and checks capacities
+    before anything is launched."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(16)
+    counts = (ctypes.c_int64 * 8)()
+
+    def call(keys, agg, lncols=2, rncols=2, n_lhs=4, n_rhs=16, lgrid=(4, 4), rgrid=(4, 4),
+             cap=10 ** 6):
+        return lib.ej_dense_plan_async(
+            fake, n_lhs, lncols, fake, n_rhs, rncols, len(keys),
+            i32_array([a for a, _ in keys]), i32_array([b for _, b in keys]), i64_array(lgrid),
+            i64_array(rgrid), len(agg), i32_array([a for a, _ in agg]),
+            i32_array([b for _, b in agg]), fake, fake, cap, fake, fake, cap, 0, None, None, fake,
+            ctypes.cast(counts, ctypes.c_void_p), 0, None)
+
+    mm = ([(1, 0)], [(0, 0), (1, 1)])
+    assert call([(1, 1)], mm[1]) == _lib.EJ_E_UNSUPPORTED      # join on rhs dim 1
+    assert call(mm[0], [(1, 1), (0, 0)]) == _lib.EJ_E_UNSUPPORTED  # output not lhs-first
+    assert call(mm[0], [(0, 0)]) == _lib.EJ_E_UNSUPPORTED      # rhs free dim dropped
+    assert call(mm[0], mm[1], n_rhs=15) == _lib.EJ_E_UNSUPPORTED  # rhs not the full grid
+    assert call(mm[0], mm[1], n_lhs=40000) == _lib.EJ_E_UNSUPPORTED  # beyond 32768 lhs tiles
+    assert call([(0, 0)], [(0, 0), (1, 1)]) == _lib.EJ_E_UNSUPPORTED  # lhs dim 1 not joined
+    assert call(mm[0], mm[1], cap=15) == _lib.EJ_E_CAPACITY     # 4 x 4 pairs
+    # two join keys whose lhs dims run against the rhs order
+    assert call([(2, 0), (1, 1)], [(0, 0), (1, 2)], lncols=3, rncols=3, lgrid=(2, 2, 2),
+                rgrid=(2, 2, 2), n_rhs=8) == _lib.EJ_E_UNSUPPORTED
+
+
+def test_dense_plan_applies_mirrors_the_library():
+    from einjax_amd import _device as D
+
+    assert D.dense_plan_applies(819, 2, 2, [(1, 0)], [(0, 0), (1, 1)])
+    assert D.dense_plan_applies(15488, 3, 3, [(0, 0), (2, 1)], [(0, 0), (0, 1), (1, 2)])
+    assert D.dense_plan_applies(1311, 3, 2, [(2, 0)], [(0, 0), (0, 1), (1, 1)])
+    assert not D.dense_plan_applies(819, 2, 2, [(1, 1)], [(0, 0), (1, 1)])
+    assert not D.dense_plan_applies(40000, 2, 2, [(1, 0)], [(0, 0), (1, 1)])
+    assert not D.dense_plan_applies(10, 2, 2, [(0, 0)], [(0, 0), (1, 1)])
+    assert not D.dense_plan_applies(10, 3, 3, [(2, 0), (1, 1)], [(0, 0), (1, 2)])
 
 
 def test_segment_einsum_group():

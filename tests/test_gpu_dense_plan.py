@@ -1,0 +1,250 @@
+"""The one-launch plan for a join against a dense rhs (ej_dense_plan_async).
+
+The plan's pairs, grouped by segment, must equal the oracle's join and
+segment plan (reference: execution/sparse_dispatch.py:29-82, :129-171)
+pair for pair, in the reference's accumulation order; execute_sparse on it
+must give results bitwise identical to the general plan's; and data that
+breaks the dense structure must be detected on the device and answered by
+the general plan, with the oracle's results.
+"""
+
+import ctypes
+
+import numpy as np
+import numpy.testing as npt
+import pytest
+import torch
+
+from oracle import generators as G
+from oracle import reference_path as R
+
+import einjax_amd as ej
+from einjax_amd import SparseTensorRelation, _device, _lib
+from einjax_amd.execution import sparse_dispatch as sd
+
+pytestmark = pytest.mark.gpu
+
+
+def note(*a):
+    print("[case]", *a, flush=True)
+
+
+def dev_rel(r: R.Rel, dtype="fp32", shape=None):
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    vals = torch.from_numpy(np.ascontiguousarray(r.values, dtype=np.float32)).cuda().to(tdt)
+    return SparseTensorRelation(torch.from_numpy(np.ascontiguousarray(r.coords)).cuda(), vals,
+                                shape or r.shape, r.tile_shape)
+
+
+def grid(r: R.Rel, shape=None):
+    shape = shape or r.shape
+    return [s // t for s, t in zip(shape, r.tile_shape)]
+
+
+def run_plan(L, Rr, keys, agg, group=0, lshape=None):
+    """ej_dense_plan_async through the C ABI; host results clipped to the counts."""
+    lib = _lib.load()
+    lc, rc = torch.from_numpy(L.coords).cuda(), torch.from_numpy(Rr.coords).cuda()
+    lg, rg = grid(L, lshape), grid(Rr)
+    nk = len(keys)
+    NK = int(np.prod(rg[nk:])) if len(rg) > nk else 1
+    cap_p = len(L.coords) * NK
+    cap_u = cap_p
+    li = torch.full((cap_p,), -7, dtype=torch.int64, device="cuda")
+    ri = torch.full((cap_p,), -7, dtype=torch.int64, device="cuda")
+    coords = torch.full((cap_u, len(agg)), -7, dtype=torch.int32, device="cuda")
+    off = torch.full((cap_u + 1,), -7, dtype=torch.int32, device="cuda")
+    order = torch.full((1 + cap_u,), -7, dtype=torch.int32, device="cuda")
+    dcounts = torch.empty(8, dtype=torch.int64, device="cuda")
+    counts = torch.full((8,), -7, dtype=torch.int64).pin_memory()
+    written = ctypes.c_int32(-1)
+    st = lib.ej_dense_plan_async(
+        _device.ptr(lc), lc.shape[0], lc.shape[1], _device.ptr(rc), rc.shape[0], rc.shape[1], nk,
+        _lib.i32_array([k[0] for k in keys]), _lib.i32_array([k[1] for k in keys]),
+        _lib.i64_array(lg), _lib.i64_array(rg), len(agg), _lib.i32_array([a for a, _ in agg]),
+        _lib.i32_array([b for _, b in agg]), _device.ptr(li), _device.ptr(ri), cap_p,
+        _device.ptr(coords), _device.ptr(off), cap_u, group,
+        _device.ptr(order) if group else None, ctypes.byref(written), _device.ptr(dcounts),
+        ctypes.c_void_p(counts.data_ptr()), 0, _device.stream_ptr())
+    if st != _lib.EJ_OK:
+        return st, None
+    torch.cuda.synchronize()
+    c = counts.tolist()
+    U, P = c[0], c[4]
+    res = dict(counts=c[:6], dev_u=int(dcounts[0]), li=li[:P].cpu().numpy(),
+               ri=ri[:P].cpu().numpy(), coords=coords[:U].cpu().numpy(),
+               off=off[:U + 1].cpu().numpy(), written=written.value)
+    if group:
+        res["order"] = order[:1 + (U + group - 1) // group].cpu().numpy()
+    return st, res
+
+
+def oracle_segments(L, Rr, keys, agg):
+    li, ri = R.coordinate_join(L.coords, Rr.coords, keys)
+    oc = R.compute_output_coords(L.coords, Rr.coords, li, ri, agg)
+    uc, perm, off, _ = R.segment_plan(oc)
+    return li, uc, [(li[perm[off[u]:off[u + 1]]], ri[perm[off[u]:off[u + 1]]])
+                    for u in range(len(uc))]
+
+
+def workloads():
+    w3 = G.workload_order3(n=256, l=64, density=0.05)
+    yield "blocksparse_1k", G.workload_blocksparse_1k()
+    yield "blocksparse_128", G.workload_blocksparse_16k(seed=2, m=2048, n=1024, density=0.1)
+    yield "banded", G.workload_batched_banded(b=2, n=1024)
+    yield "order3", w3
+    # a lhs whose join dims are its last two, against a 3-D dense rhs
+    rng = np.random.default_rng(3)
+    lc = np.array(sorted({(int(a), int(b), int(c)) for a, b, c in
+                          rng.integers(0, (6, 5, 4), size=(60, 3))}), np.int32)
+    L = R.Rel(lc, rng.standard_normal((len(lc), 2, 3, 4)).astype(np.float32), (12, 15, 16),
+              (2, 3, 4))
+    rc = np.stack(np.unravel_index(np.arange(5 * 4 * 3), (5, 4, 3)), 1).astype(np.int32)
+    Rr = R.Rel(rc, rng.standard_normal((len(rc), 3, 4, 2)).astype(np.float32), (15, 16, 6),
+               (3, 4, 2))
+    yield "two_key", dict(lhs=L, rhs=Rr, join_keys=[(1, 0), (2, 1)], agg_keys=[(0, 0), (1, 2)],
+                          kernel_string="ajk,jkb->ab", dtype="fp32")
+
+
+@pytest.mark.parametrize("idx", range(5))
+def test_dense_plan_matches_oracle_segments(gpu, idx):
+    """Output coordinates and, segment by segment, the pairs in the
+    reference's accumulation order, bit-exact; with a run order, a
+    permutation of the live groups behind its header."""
+    name, w = list(workloads())[idx]
+    note("dense plan vs oracle", name)
+    L, Rr, keys, agg = w["lhs"], w["rhs"], w["join_keys"], w["agg_keys"]
+    li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
+    for group in (0, 2, 4):
+        st, res = run_plan(L, Rr, keys, agg, group=group)
+        assert st == _lib.EJ_OK and res["counts"][1] == 0, (name, st)
+        assert res["counts"][4] == len(li_o) and res["counts"][0] == len(uc) == res["dev_u"]
+        npt.assert_array_equal(res["coords"], uc)
+        assert res["off"][-1] == len(li_o)
+        for u, (sl, sr) in enumerate(segs):
+            a, b = res["off"][u], res["off"][u + 1]
+            npt.assert_array_equal(res["li"][a:b], sl, err_msg=f"{name} segment {u}")
+            npt.assert_array_equal(res["ri"][a:b], sr, err_msg=f"{name} segment {u}")
+        if group:
+            ng = (len(uc) + group - 1) // group
+            assert res["written"] == 1 and res["order"][0] == ng
+            npt.assert_array_equal(np.sort(res["order"][1:]), np.arange(ng))
+
+
+@pytest.mark.parametrize("idx", range(5))
+def test_dense_step_bitwise_equals_general_plan(gpu, idx, monkeypatch):
+    """execute_sparse on the dense plan against the general plan: the same
+    coordinates and bitwise the same values (same pairs, same order, same
+    kernel), default and fp32 output; both within tolerance of the oracle."""
+    name, w = list(workloads())[idx]
+    note("dense step vs general", name)
+    statuses = []
+    real = _device.dense_segment_einsum
+
+    def spy(*a, **k):
+        st, res = real(*a, **k)
+        statuses.append(st)
+        return st, res
+
+    monkeypatch.setattr(_device, "dense_segment_einsum", spy)
+    lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
+    args = (lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    want = R.execute_sparse(w["lhs"], w["rhs"], w["join_keys"], w["kernel_string"],
+                            w["agg_keys"], precision="fp64")
+    for out_dtype in (None, torch.float32):
+        sd._pair_hints.clear()
+        dense = [ej.execute_sparse(*args, out_dtype=out_dtype) for _ in range(2)]
+        assert statuses[-2:] == ["ok", "ok"]
+        with monkeypatch.context() as m:
+            m.setattr(sd, "_dense_step", lambda *a, **k: None)
+            general = ej.execute_sparse(*args, out_dtype=out_dtype)
+        for d in dense:
+            assert torch.equal(d.coords, general.coords)
+            bits = torch.int16 if d.values.dtype == torch.bfloat16 else torch.int32
+            assert torch.equal(d.values.view(bits), general.values.view(bits))
+        npt.assert_array_equal(dense[0].coords.cpu().numpy(), want.coords)
+        tol = 1e-2 if w["dtype"] == "bf16" and out_dtype is None else 1e-5
+        assert R.rel_l2(dense[0].values.float().cpu().numpy(), want.values) <= tol
+
+
+def _shuffled(r: R.Rel, seed: int) -> R.Rel:
+    p = np.random.default_rng(seed).permutation(len(r.coords))
+    return R.Rel(r.coords[p], r.values[p], r.shape, r.tile_shape)
+
+
+def _cases():
+    w = G.workload_blocksparse_1k(n=512, tile=32, density=0.2)
+    L, Rr = w["lhs"], w["rhs"]
+    yield "lhs unsorted", w, _shuffled(L, 1), Rr, None
+    yield "rhs out of grid order", w, L, _shuffled(Rr, 2), None
+    dup = R.Rel(np.concatenate([L.coords[:5], L.coords[4:]]),
+                np.concatenate([L.values[:5], L.values[4:]]), L.shape, L.tile_shape)
+    yield "lhs duplicate coordinates", w, dup, Rr, None
+    yield "lhs shape understates rows", w, L, Rr, (256, 512)
+    # a join value beyond the rhs grid: those lhs tiles meet no rhs tile
+    wide = R.Rel(np.concatenate([L.coords, [[15, 17]]]).astype(np.int32),
+                 np.concatenate([L.values, L.values[:1]]), (512, 576), L.tile_shape)
+    yield "lhs join value beyond the rhs grid", w, wide, Rr, None
+    # more runs (9000) than the plan keeps
+    n = 9000
+    lr = R.Rel(np.stack([np.arange(n), np.zeros(n, int)], 1).astype(np.int32),
+               np.ones((n, 1, 1), np.float32), (n, 1), (1, 1))
+    rr = R.Rel(np.array([[0, 0], [0, 1]], np.int32), np.full((2, 1, 1), 2.0, np.float32),
+               (1, 2), (1, 1))
+    yield "9000 runs", dict(w, lhs=lr, rhs=rr), lr, rr, None
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_dense_plan_misses_fall_back(gpu, case, monkeypatch):
+    """Data that breaks the dense structure: the plan reports the miss
+    (counts[1] = 1, no segments on the device), execute_sparse answers with
+    the general plan (the oracle's results), and later calls on the same
+    coordinates skip the dense plan."""
+    name, w, L, Rr, lshape = list(_cases())[case]
+    note("dense miss", name)
+    st, res = run_plan(L, Rr, w["join_keys"], w["agg_keys"], lshape=lshape)
+    assert st == _lib.EJ_OK and res["counts"][1] == 1 and res["dev_u"] == 0, name
+    statuses = []
+    real = _device.dense_segment_einsum
+
+    def spy(*a, **k):
+        st, r = real(*a, **k)
+        statuses.append(st)
+        return st, r
+
+    monkeypatch.setattr(_device, "dense_segment_einsum", spy)
+    sd._pair_hints.clear()
+    lhs = dev_rel(L, shape=lshape)
+    rhs = dev_rel(Rr)
+    want = R.execute_sparse(L, Rr, w["join_keys"], w["kernel_string"], w["agg_keys"],
+                            output_shape=None if lshape is None else
+                            (lshape[0], Rr.shape[1]), precision="fp64")
+    for _ in range(2):
+        got = ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+        npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+        assert R.rel_l2(got.values.float().cpu().numpy(), want.values) <= 1e-5
+    assert statuses == ["miss"]
+
+
+def test_dense_plan_at_its_lhs_limit(gpu):
+    """32768 lhs tiles (every tile of a 128 x 256 grid of 1 x 1 tiles)
+    against a dense 256 x 4 rhs: 131,072 pairs over 16 plan blocks, 512 runs."""
+    note("dense plan at 32768 lhs tiles")
+    rng = np.random.default_rng(8)
+    lc = np.stack(np.unravel_index(np.arange(128 * 256), (128, 256)), 1).astype(np.int32)
+    rc = np.stack(np.unravel_index(np.arange(256 * 4), (256, 4)), 1).astype(np.int32)
+    L = R.Rel(lc, rng.standard_normal((len(lc), 1, 1)).astype(np.float32), (128, 256), (1, 1))
+    Rr = R.Rel(rc, rng.standard_normal((len(rc), 1, 1)).astype(np.float32), (256, 4), (1, 1))
+    keys, agg = [(1, 0)], [(0, 0), (1, 1)]
+    li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
+    st, res = run_plan(L, Rr, keys, agg, group=4)
+    assert st == _lib.EJ_OK and res["counts"][1] == 0 and res["counts"][4] == 131072
+    npt.assert_array_equal(res["coords"], uc)
+    for u in range(0, len(uc), 37):
+        a, b = res["off"][u], res["off"][u + 1]
+        npt.assert_array_equal(res["li"][a:b], segs[u][0])
+        npt.assert_array_equal(res["ri"][a:b], segs[u][1])
+    got = ej.execute_sparse(dev_rel(L), dev_rel(Rr), keys, "ij,jk->ik", agg)
+    want = R.execute_sparse(L, Rr, keys, "ij,jk->ik", agg, precision="fp64")
+    npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+    assert R.rel_l2(got.values.cpu().numpy(), want.values) <= 1e-5

@@ -733,6 +733,7 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
         return st, res
 
     monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
     sd._pair_hints.clear()
     lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
     run = lambda: ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
@@ -889,6 +890,7 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
         written.append((a[25], a[27]._obj.value if hasattr(a[27], "_obj") else None))
         return rc
 
+    monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
     sd._pair_hints.clear()
     exact = ej.execute_sparse(*args)
     monkeypatch.setattr(lib, "ej_pair_plan_async", spy)
