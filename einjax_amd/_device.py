@@ -347,13 +347,34 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
     return "ok", (P, coords[:U], offsets[:U + 1], perm[:P], out[:U], li[:P], ri[:P])
 
 
+class _DenseCounts(threading.local):
+    """Per-thread device counters of the dense plan, one buffer per device:
+    zeroed once, left zero by every plan (its first entry is the segment
+    count the einsum behind it reads)."""
+
+    bufs: dict = {}
+
+    def __init__(self):
+        self.bufs = {}
+
+
+_dense_state = _DenseCounts()
+
+
+def _dense_counts(dev) -> torch.Tensor:
+    buf = _dense_state.bufs.get(dev)
+    if buf is None:
+        buf = _dense_state.bufs[dev] = torch.zeros(8, dtype=torch.int64, device=dev)
+    return buf
+
+
 def dense_plan_applies(n_lhs: int, lhs_ncols: int, rhs_ncols: int, join_keys, agg_keys) -> bool:
     """Whether the structure of a join suits ej_dense_plan_async (the device
     then checks the data): rhs join dims 0 .. nk-1 with increasing lhs dims,
     output = a prefix of the lhs dims then the rhs dims after the join dims,
-    every other lhs dim joined, 1 .. 32768 lhs tiles."""
+    every other lhs dim joined, 1 .. 16384 lhs tiles."""
     nk = len(join_keys)
-    if nk < 1 or nk > rhs_ncols or not 1 <= n_lhs <= 32768:
+    if nk < 1 or nk > rhs_ncols or not 1 <= n_lhs <= 16384:
         return False
     by_r = sorted((b, a) for a, b in join_keys)
     if [b for b, _ in by_r] != list(range(nk)):
@@ -398,7 +419,7 @@ def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, 
     ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
     coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
     offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
-    dcounts = torch.empty(8, dtype=torch.int64, device=dev)
+    dcounts = _dense_counts(dev)
     odt = _set_out_dtype(desc, lhs_values, out_dtype)
     out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
     gq = ctypes.c_int32(1)

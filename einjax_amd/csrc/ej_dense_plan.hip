@@ -24,8 +24,8 @@ namespace ej {
 namespace {
 
 constexpr int kDenseThreads = 1024;
-constexpr int kDenseTilesPerThread = 32;  // lhs tiles each thread scans
-constexpr int64_t kDenseMaxLhs = int64_t(kDenseThreads) * kDenseTilesPerThread;
+constexpr int kDenseTilesPerThread = 16;  // lhs tiles each thread scans
+constexpr int64_t kDenseMaxLhs = int64_t(kDenseThreads) * kDenseTilesPerThread;  // jrow in LDS
 constexpr int kDenseMaxRuns = 8192;  // run starts held in LDS
 constexpr int kDensePairsPerThread = 8;
 constexpr int64_t kDensePairsPerBlock = int64_t(kDenseThreads) * kDensePairsPerThread;
@@ -48,23 +48,31 @@ __device__ inline void load_row(const int32_t *__restrict__ c, int64_t t, int nc
   for (int d = 0; d < EJ_MAX_DIMS; ++d) v[d] = d < ncols ? c[t * ncols + d] : 0;
 }
 
-// Linear index, over the rhs join grid, of lhs tile t's join coordinates.
-__device__ inline int64_t join_row(const int32_t *__restrict__ lc, int64_t t, const DenseSpec &s) {
+// Linear index, over the rhs join grid, of a lhs tile's join coordinates.
+__device__ inline int64_t join_row(const int32_t (&v)[EJ_MAX_DIMS], const DenseSpec &s) {
   int64_t j = 0;
 #pragma unroll
   for (int i = 0; i < EJ_MAX_KEYS; ++i)
-    if (i < s.nk) j = j * s.rgrid[i] + lc[t * s.lncols + s.ldim[i]];
+    if (i < s.nk) {
+      int32_t c = 0;
+#pragma unroll
+      for (int d = 0; d < EJ_MAX_DIMS; ++d) c = d == s.ldim[i] ? v[d] : c;
+      j = j * s.rgrid[i] + c;
+    }
   return j;
 }
 
 // Blocks of kDenseThreads threads.  Every block scans the lhs coordinates
-// (run starts, order and range checks) and keeps the run starts in LDS; block
-// b then writes pairs [b * kDensePairsPerBlock, ...), its share of the
-// segments, its share of the rhs check and (run_order) the order of the XCD
-// chunks assigned to it.  The last block to finish publishes the counts:
-// scal[0] = U (0 when a check failed), scal[1] = not-applicable flag, scal[2]
-// = scal[4] = P, and host_counts as ej_pair_plan_async does, then the ticket.
-// scal[1] and scal[3] (finished blocks) must be zero at launch.
+// (run starts, order and range checks) and keeps the run starts and each
+// tile's rhs join row in LDS; block b then writes pairs
+// [b * kDensePairsPerBlock, ...), its share of the segments, its share of the
+// rhs check (loaded first, so that its latency overlaps the lhs scan) and
+// (run_order) the order of the XCD chunks assigned to it.  The last block to
+// finish publishes the counts: scal[0] = U (0 when a check failed), scal[1] =
+// not-applicable flag, scal[2] = scal[4] = P, scal[3] = scal[5] = 0, and
+// host_counts as ej_pair_plan_async does, then the ticket.  scal[6] (the
+// blocks' flags) and scal[7] (finished blocks) must be zero at launch; the
+// last block returns them to zero.
 __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     const int32_t *__restrict__ lc, const int32_t *__restrict__ rc, DenseSpec s,
     int64_t *__restrict__ lidx, int64_t *__restrict__ ridx, int64_t pair_cap,
@@ -73,14 +81,32 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     int64_t *__restrict__ host_counts, int64_t ticket) {
   constexpr int NW = kDenseThreads / 64;
   __shared__ int32_t run_start[kDenseMaxRuns + 1];
+  __shared__ int32_t jrow[kDenseMaxLhs];
   __shared__ int32_t cls_base[NW][256];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t blk = blockIdx.x, nblk = gridDim.x;
+  int bad = 0;
+
+  // ---- rhs check: row r holds the coordinates of grid position r ----------
+  {
+    const int64_t rpb = (s.n_rhs + nblk - 1) / nblk;
+    const int64_t r0 = blk * rpb, r1 = min(s.n_rhs, r0 + rpb);
+    for (int64_t r = r0 + tid; r < r1; r += kDenseThreads) {
+      int32_t cv[EJ_MAX_DIMS];
+      load_row(rc, r, s.rncols, cv);
+      int64_t rem = r;
+#pragma unroll
+      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d)
+        if (d < s.rncols) {
+          if (cv[d] != static_cast<int32_t>(rem % s.rgrid[d])) bad = 1;
+          rem /= s.rgrid[d];
+        }
+    }
+  }
 
   // ---- lhs scan: this thread's tiles [t0, t1), contiguous --------------------
   const int64_t per = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;
   const int64_t t0 = min(s.n_lhs, tid * per), t1 = min(s.n_lhs, t0 + per);
-  int bad = 0;
   uint32_t newmask = 0;  // bit i: tile t0 + i starts a run
   int64_t nnew = 0;
   int32_t pv[EJ_MAX_DIMS];
@@ -110,6 +136,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       newmask |= 1u << (t - t0);
       ++nnew;
     }
+    jrow[t] = static_cast<int32_t>(join_row(cv, s));
 #pragma unroll
     for (int d = 0; d < EJ_MAX_DIMS; ++d) pv[d] = cv[d];
   }
@@ -151,7 +178,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       const int64_t kk = w / len;
       const int64_t t = rs + (w - kk * len);
       lidx[q] = t;
-      ridx[q] = join_row(lc, t, s) * s.NK + kk;
+      ridx[q] = static_cast<int64_t>(jrow[t]) * s.NK + kk;
     }
     // ---- segments: this block's share of [0, live_u) ----------------------
     const int64_t upb = (live_u + nblk - 1) / nblk;
@@ -173,21 +200,6 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
         }
     }
     if (blk == 0 && tid == 0 && U <= seg_cap) seg_offsets[U] = static_cast<int32_t>(s.P);
-  }
-
-  // ---- rhs check: row r holds the coordinates of grid position r ----------
-  {
-    const int64_t rpb = (s.n_rhs + nblk - 1) / nblk;
-    const int64_t r0 = blk * rpb, r1 = min(s.n_rhs, r0 + rpb);
-    for (int64_t r = r0 + tid; r < r1; r += kDenseThreads) {
-      int64_t rem = r;
-#pragma unroll
-      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d)
-        if (d < s.rncols) {
-          if (rc[r * s.rncols + d] != static_cast<int32_t>(rem % s.rgrid[d])) bad = 1;
-          rem /= s.rgrid[d];
-        }
-    }
   }
 
   // ---- run order: per XCD chunk of the live groups, longest first ---------
@@ -261,8 +273,8 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   // ---- publish: the last block to finish writes the counts ----------------
   const int blk_bad = __syncthreads_or(bad);
   if (tid == 0) {
-    unsigned long long *flag = reinterpret_cast<unsigned long long *>(scal + 1);
-    unsigned long long *done = reinterpret_cast<unsigned long long *>(scal + 3);
+    unsigned long long *flag = reinterpret_cast<unsigned long long *>(scal + 6);
+    unsigned long long *done = reinterpret_cast<unsigned long long *>(scal + 7);
     if (blk_bad) atomicOr(flag, 1ull);
     __threadfence();
     const unsigned long long prev = atomicAdd(done, 1ull);
@@ -271,9 +283,13 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       const int64_t any_bad = static_cast<int64_t>(atomicOr(flag, 0ull));
       const int64_t u_out = any_bad ? 0 : U;
       scal[0] = u_out;
+      scal[1] = any_bad;
       scal[2] = s.P;
+      scal[3] = 0;
       scal[4] = s.P;
       scal[5] = 0;
+      scal[6] = 0;  // ready for the next call
+      scal[7] = 0;
       if (host_counts) {
         host_counts[0] = u_out;
         host_counts[1] = any_bad;
@@ -385,7 +401,6 @@ extern "C" int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int
     return EJ_E_CAPACITY;
   }
   EJ_CHECK_ARG(seg_capacity >= 1, "seg_capacity must be positive");
-  EJ_TRY(zero_async(dev_counts, 8 * sizeof(int64_t), stream));
   int64_t *direct = nullptr;
   if (counts_direct) EJ_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&direct), counts, 0));
   const int64_t nblk = ceil_div(s.P, kDensePairsPerBlock);

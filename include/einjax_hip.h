@@ -327,7 +327,7 @@ int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t
  * increasing in that order), the output dims are lhs dims 0 .. nlo-1 followed
  * by rhs dims n_keys .. rhs_ncols-1, every other lhs dim is a join dim, and
  * the lhs coordinates are strictly increasing in lexicographic order and
- * inside lhs_grid; 1 <= n_lhs <= 32768.  Then every lhs tile meets one rhs
+ * inside lhs_grid; 1 <= n_lhs <= 16384.  Then every lhs tile meets one rhs
  * tile per value of the rhs dims after the join dims (NK of them), P = n_lhs
  * * NK, and the lhs tiles sharing their first nlo coordinates form a run: the
  * plan writes the pairs in segment order (perm = identity: pass perm = NULL
@@ -341,8 +341,11 @@ int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t
  * grid, more than 8192 runs, U > seg_capacity) give counts[1] = 1 and a
  * segment count of 0 on the device, so that an einsum queued behind does no
  * work; the caller then takes the general plan.  Capacities: pair_capacity
- * >= n_lhs * NK; seg_capacity bounds U.  dev_counts: device int64[8], its
- * first entry U afterwards (the n_segments_dev of ej_segment_einsum_async).
+ * >= n_lhs * NK; seg_capacity bounds U.  dev_counts: device int64[8] whose
+ * entries [6] and [7] are zero at the call (the plan returns them to zero, so
+ * a caller zeroes the buffer once and reuses it on its stream); afterwards
+ * dev_counts[0 .. 5] hold the six counts, dev_counts[0] = U being the
+ * n_segments_dev of ej_segment_einsum_async.
  * counts / counts_direct as ej_pair_plan_async (counts[0] = U, [1] = the
  * not-applicable flag, [2] = [4] = P).  Asynchronous. */
 int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,

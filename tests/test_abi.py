@@ -331,7 +331,7 @@ def test_dense_plan_host_validation():
     assert call(mm[0], [(1, 1), (0, 0)]) == _lib.EJ_E_UNSUPPORTED  # output not lhs-first
     assert call(mm[0], [(0, 0)]) == _lib.EJ_E_UNSUPPORTED      # rhs free dim dropped
     assert call(mm[0], mm[1], n_rhs=15) == _lib.EJ_E_UNSUPPORTED  # rhs not the full grid
-    assert call(mm[0], mm[1], n_lhs=40000) == _lib.EJ_E_UNSUPPORTED  # beyond 32768 lhs tiles
+    assert call(mm[0], mm[1], n_lhs=16385) == _lib.EJ_E_UNSUPPORTED  # beyond 16384 lhs tiles
     assert call([(0, 0)], [(0, 0), (1, 1)]) == _lib.EJ_E_UNSUPPORTED  # lhs dim 1 not joined
     assert call(mm[0], mm[1], cap=15) == _lib.EJ_E_CAPACITY     # 4 x 4 pairs
     # two join keys whose lhs dims run against the rhs order
@@ -346,7 +346,7 @@ def test_dense_plan_applies_mirrors_the_library():
     assert D.dense_plan_applies(15488, 3, 3, [(0, 0), (2, 1)], [(0, 0), (0, 1), (1, 2)])
     assert D.dense_plan_applies(1311, 3, 2, [(2, 0)], [(0, 0), (0, 1), (1, 1)])
     assert not D.dense_plan_applies(819, 2, 2, [(1, 1)], [(0, 0), (1, 1)])
-    assert not D.dense_plan_applies(40000, 2, 2, [(1, 0)], [(0, 0), (1, 1)])
+    assert not D.dense_plan_applies(16385, 2, 2, [(1, 0)], [(0, 0), (1, 1)])
     assert not D.dense_plan_applies(10, 2, 2, [(0, 0)], [(0, 0), (1, 1)])
     assert not D.dense_plan_applies(10, 3, 3, [(2, 0), (1, 1)], [(0, 0), (1, 2)])
 

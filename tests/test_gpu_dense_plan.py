@@ -55,7 +55,7 @@ def run_plan(L, Rr, keys, agg, group=0, lshape=None):
     coords = torch.full((cap_u, len(agg)), -7, dtype=torch.int32, device="cuda")
     off = torch.full((cap_u + 1,), -7, dtype=torch.int32, device="cuda")
     order = torch.full((1 + cap_u,), -7, dtype=torch.int32, device="cuda")
-    dcounts = torch.empty(8, dtype=torch.int64, device="cuda")
+    dcounts = torch.zeros(8, dtype=torch.int64, device="cuda")
     counts = torch.full((8,), -7, dtype=torch.int64).pin_memory()
     written = ctypes.c_int32(-1)
     st = lib.ej_dense_plan_async(
@@ -71,6 +71,8 @@ def run_plan(L, Rr, keys, agg, group=0, lshape=None):
     torch.cuda.synchronize()
     c = counts.tolist()
     U, P = c[0], c[4]
+    assert int(dcounts[6]) == 0 and int(dcounts[7]) == 0  # left ready for the next call
+    assert dcounts[:6].tolist() == c[:6]
     res = dict(counts=c[:6], dev_u=int(dcounts[0]), li=li[:P].cpu().numpy(),
                ri=ri[:P].cpu().numpy(), coords=coords[:U].cpu().numpy(),
                off=off[:U + 1].cpu().numpy(), written=written.value)
@@ -227,18 +229,23 @@ def test_dense_plan_misses_fall_back(gpu, case, monkeypatch):
 
 
 def test_dense_plan_at_its_lhs_limit(gpu):
-    """32768 lhs tiles (every tile of a 128 x 256 grid of 1 x 1 tiles)
-    against a dense 256 x 4 rhs: 131,072 pairs over 16 plan blocks, 512 runs."""
-    note("dense plan at 32768 lhs tiles")
+    """16384 lhs tiles (every tile of a 64 x 256 grid of 1 x 1 tiles)
+    against a dense 256 x 8 rhs: 131,072 pairs over 16 plan blocks, 512
+    segments; one tile more is refused on the host."""
+    note("dense plan at 16384 lhs tiles")
     rng = np.random.default_rng(8)
-    lc = np.stack(np.unravel_index(np.arange(128 * 256), (128, 256)), 1).astype(np.int32)
-    rc = np.stack(np.unravel_index(np.arange(256 * 4), (256, 4)), 1).astype(np.int32)
-    L = R.Rel(lc, rng.standard_normal((len(lc), 1, 1)).astype(np.float32), (128, 256), (1, 1))
-    Rr = R.Rel(rc, rng.standard_normal((len(rc), 1, 1)).astype(np.float32), (256, 4), (1, 1))
+    lc = np.stack(np.unravel_index(np.arange(64 * 256), (64, 256)), 1).astype(np.int32)
+    rc = np.stack(np.unravel_index(np.arange(256 * 8), (256, 8)), 1).astype(np.int32)
+    L = R.Rel(lc, rng.standard_normal((len(lc), 1, 1)).astype(np.float32), (64, 256), (1, 1))
+    Rr = R.Rel(rc, rng.standard_normal((len(rc), 1, 1)).astype(np.float32), (256, 8), (1, 1))
     keys, agg = [(1, 0)], [(0, 0), (1, 1)]
     li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
     st, res = run_plan(L, Rr, keys, agg, group=4)
     assert st == _lib.EJ_OK and res["counts"][1] == 0 and res["counts"][4] == 131072
+    big = R.Rel(np.stack(np.unravel_index(np.arange(16385), (16385, 1)), 1).astype(np.int32),
+                np.ones((16385, 1, 1), np.float32), (16385, 1), (1, 1))
+    one = R.Rel(np.array([[0, 0]], np.int32), np.ones((1, 1, 1), np.float32), (1, 1), (1, 1))
+    assert run_plan(big, one, keys, agg)[0] == _lib.EJ_E_UNSUPPORTED
     npt.assert_array_equal(res["coords"], uc)
     for u in range(0, len(uc), 37):
         a, b = res["off"][u], res["off"][u + 1]
