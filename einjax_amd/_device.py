@@ -451,11 +451,25 @@ def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, 
           "ej_segment_einsum_async")
     if einsum_events is not None:
         einsum_events[-1][1].record()
-    _wait_ticket(counts, ticket)
-    U, miss, P = int(counts[0]), int(counts[1]), int(counts[4])
+    word = _wait_packed_ticket(counts, ticket)
+    U, miss, P = word & 0xFFFFFFFF, (word >> 32) & 1, cap_p
     if miss:
         return "miss", None
     return "ok", (P, coords[:U], offsets[:U + 1], None, out[:U], li[:P], ri[:P])
+
+
+def _wait_packed_ticket(view, ticket: int) -> int:
+    """Waits until the GPU has stored the word ticket << 33 | flag << 32 | U
+    in view[6] and returns it (as _wait_ticket, bounded by a stream sync)."""
+    for _ in range(200000):
+        w = view[6]
+        if w >> 33 == ticket:
+            return w
+    torch.cuda.current_stream().synchronize()
+    w = view[6]
+    if w >> 33 != ticket:
+        raise RuntimeError("the dense plan did not report its counts")
+    return w
 
 
 def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:

@@ -69,10 +69,14 @@ __device__ inline int64_t join_row(const int32_t (&v)[EJ_MAX_DIMS], const DenseS
 // rhs check (loaded first, so that its latency overlaps the lhs scan) and
 // (run_order) the order of the XCD chunks assigned to it.  The last block to
 // finish publishes the counts: scal[0] = U (0 when a check failed), scal[1] =
-// not-applicable flag, scal[2] = scal[4] = P, scal[3] = scal[5] = 0, and
-// host_counts as ej_pair_plan_async does, then the ticket.  scal[6] (the
-// blocks' flags) and scal[7] (finished blocks) must be zero at launch; the
-// last block returns them to zero.
+// not-applicable flag, scal[2] = scal[4] = P, scal[3] = scal[5] = 0, and,
+// given host_counts, the single word host_counts[6] = ticket << 33 | flag <<
+// 32 | U.  Blocks meet through one atomic word, scal[7]: each adds 1 plus its
+// check failure in the upper half, so the block that sees nblk - 1 finished
+// blocks before it also sees every failure; no fence is needed (a fence here
+// would write back the L2, which the einsum before this kernel left full of
+// output tiles).  scal[7] must be zero at launch; the last block returns it
+// to zero.
 __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     const int32_t *__restrict__ lc, const int32_t *__restrict__ rc, DenseSpec s,
     int64_t *__restrict__ lidx, int64_t *__restrict__ ridx, int64_t pair_cap,
@@ -273,14 +277,11 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   // ---- publish: the last block to finish writes the counts ----------------
   const int blk_bad = __syncthreads_or(bad);
   if (tid == 0) {
-    unsigned long long *flag = reinterpret_cast<unsigned long long *>(scal + 6);
-    unsigned long long *done = reinterpret_cast<unsigned long long *>(scal + 7);
-    if (blk_bad) atomicOr(flag, 1ull);
-    __threadfence();
-    const unsigned long long prev = atomicAdd(done, 1ull);
-    if (prev == static_cast<unsigned long long>(nblk - 1)) {
-      __threadfence();
-      const int64_t any_bad = static_cast<int64_t>(atomicOr(flag, 0ull));
+    unsigned long long *meet = reinterpret_cast<unsigned long long *>(scal + 7);
+    const unsigned long long prev =
+        atomicAdd(meet, 1ull + (blk_bad ? (1ull << 32) : 0ull));
+    if ((prev & 0xffffffffull) == static_cast<unsigned long long>(nblk - 1)) {
+      const int64_t any_bad = (prev >> 32) != 0 || blk_bad ? 1 : 0;
       const int64_t u_out = any_bad ? 0 : U;
       scal[0] = u_out;
       scal[1] = any_bad;
@@ -288,19 +289,14 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       scal[3] = 0;
       scal[4] = s.P;
       scal[5] = 0;
-      scal[6] = 0;  // ready for the next call
-      scal[7] = 0;
-      if (host_counts) {
-        host_counts[0] = u_out;
-        host_counts[1] = any_bad;
-        host_counts[2] = s.P;
-        host_counts[3] = 0;
-        host_counts[4] = s.P;
-        host_counts[5] = 0;
-        __threadfence_system();
-        host_counts[6] = ticket;
-        __threadfence_system();
-      }
+      scal[6] = 0;
+      scal[7] = 0;  // ready for the next call
+      if (host_counts)
+        __hip_atomic_store(reinterpret_cast<unsigned long long *>(host_counts + 6),
+                           (static_cast<unsigned long long>(ticket) << 33) |
+                               (static_cast<unsigned long long>(any_bad) << 32) |
+                               static_cast<unsigned long long>(u_out),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
   }
 }
@@ -401,6 +397,7 @@ extern "C" int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int
     return EJ_E_CAPACITY;
   }
   EJ_CHECK_ARG(seg_capacity >= 1, "seg_capacity must be positive");
+  EJ_CHECK_ARG(counts_direct < (int64_t(1) << 30), "counts_direct (the ticket) beyond 2^30");
   int64_t *direct = nullptr;
   if (counts_direct) EJ_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&direct), counts, 0));
   const int64_t nblk = ceil_div(s.P, kDensePairsPerBlock);

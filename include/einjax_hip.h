@@ -342,12 +342,17 @@ int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t
  * segment count of 0 on the device, so that an einsum queued behind does no
  * work; the caller then takes the general plan.  Capacities: pair_capacity
  * >= n_lhs * NK; seg_capacity bounds U.  dev_counts: device int64[8] whose
- * entries [6] and [7] are zero at the call (the plan returns them to zero, so
- * a caller zeroes the buffer once and reuses it on its stream); afterwards
- * dev_counts[0 .. 5] hold the six counts, dev_counts[0] = U being the
- * n_segments_dev of ej_segment_einsum_async.
- * counts / counts_direct as ej_pair_plan_async (counts[0] = U, [1] = the
- * not-applicable flag, [2] = [4] = P).  Asynchronous. */
+ * entry [7] is zero at the call (the plan returns it to zero, so a caller
+ * zeroes the buffer once and reuses it on its stream); afterwards
+ * dev_counts[0 .. 5] hold the six counts (U, the not-applicable flag, P, 0,
+ * P, 0), dev_counts[0] = U being the n_segments_dev of
+ * ej_segment_einsum_async.  counts (pinned host memory): with counts_direct
+ * == 0 the six counts are copied there in stream order; counts_direct > 0
+ * (a ticket below 2^30) declares counts coherent host memory from
+ * ej_host_alloc, and the plan stores the single word counts[6] = ticket << 33
+ * | flag << 32 | U instead (P = n_lhs * NK is known to the caller), so that a
+ * host waiting for the ticket reads every count from one store, without the
+ * plan having to order several.  Asynchronous. */
 int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                         const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
                         int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,

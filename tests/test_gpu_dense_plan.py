@@ -242,6 +242,18 @@ def test_dense_plan_at_its_lhs_limit(gpu):
     li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
     st, res = run_plan(L, Rr, keys, agg, group=4)
     assert st == _lib.EJ_OK and res["counts"][1] == 0 and res["counts"][4] == 131072
+    # a wrong rhs row near the end (checked by the last of the 16 plan blocks)
+    # and, separately, two lhs rows out of order: each is reported as a miss
+    bad_r = R.Rel(Rr.coords.copy(), Rr.values, Rr.shape, Rr.tile_shape)
+    bad_r.coords[2000] = bad_r.coords[2001]
+    st, miss = run_plan(L, bad_r, keys, agg, group=4)
+    assert st == _lib.EJ_OK and miss["counts"][1] == 1 and miss["dev_u"] == 0
+    bad_l = R.Rel(L.coords.copy(), L.values, L.shape, L.tile_shape)
+    bad_l.coords[[9000, 9001]] = bad_l.coords[[9001, 9000]]
+    st, miss = run_plan(bad_l, Rr, keys, agg)
+    assert st == _lib.EJ_OK and miss["counts"][1] == 1 and miss["dev_u"] == 0
+    st, again = run_plan(L, Rr, keys, agg, group=4)  # the counters were left ready
+    assert st == _lib.EJ_OK and again["counts"] == res["counts"]
     big = R.Rel(np.stack(np.unravel_index(np.arange(16385), (16385, 1)), 1).astype(np.int32),
                 np.ones((16385, 1, 1), np.float32), (16385, 1), (1, 1))
     one = R.Rel(np.array([[0, 0]], np.int32), np.ones((1, 1, 1), np.float32), (1, 1), (1, 1))
