@@ -411,6 +411,8 @@ def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, 
     NK = prod(int(rhs_grid[d]) for d in range(nk, len(rhs_grid)))
     nlo = len(agg_keys) - (len(rhs_grid) - nk)
     cap_p = n_l * NK
+    if cap_p >= 1 << 30 or prod(int(g) for g in rhs_grid) >= 1 << 31:
+        return "unsupported", None  # beyond the plan's 32-bit indices
     cap_u = max(1, min(n_l, prod(int(lhs_grid[d]) for d in range(nlo))) * NK)
     n_out = len(agg_keys)
     base, counts, ticket = _count_buffer()

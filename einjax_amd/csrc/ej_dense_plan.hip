@@ -18,6 +18,8 @@
 // reports it (counts[1] = 1) and leaves the segment count at 0, so that an
 // einsum queued behind it does no work and the caller takes the general
 // join and plan.
+#include <algorithm>
+
 #include "ej_internal.h"
 
 namespace ej {
@@ -25,111 +27,119 @@ namespace {
 
 constexpr int kDenseThreads = 1024;
 constexpr int kDenseTilesPerThread = 16;  // lhs tiles each thread scans
-constexpr int64_t kDenseMaxLhs = int64_t(kDenseThreads) * kDenseTilesPerThread;  // jrow in LDS
-constexpr int kDenseMaxRuns = 8192;  // run starts held in LDS
-constexpr int kDensePairsPerThread = 8;
-constexpr int64_t kDensePairsPerBlock = int64_t(kDenseThreads) * kDensePairsPerThread;
+constexpr int kDenseMaxLhs = kDenseThreads * kDenseTilesPerThread;  // jrow in LDS
+constexpr int kDenseMaxRuns = 8192;       // run starts held in LDS (run_of is 16-bit)
+constexpr int kDenseMinPairsPerBlock = 2 * kDenseThreads;
+constexpr int kDenseMaxBlocks = 1024;     // every block rescans the lhs coordinates
 
+// Every count and grid extent is below 2^31 (checked on the host), so the
+// kernel's index arithmetic and divisions are 32-bit.
 struct DenseSpec {
   int32_t lncols, rncols;
-  int32_t nk;    // join keys; rhs dims 0 .. nk-1 are the join dims
-  int32_t nlo;   // lhs dims 0 .. nlo-1 are the output dims taken from the lhs
-  int32_t n_out; // nlo + (rncols - nk)
+  int32_t nk;     // join keys; rhs dims 0 .. nk-1 are the join dims
+  int32_t nlo;    // lhs dims 0 .. nlo-1 are the output dims taken from the lhs
+  int32_t n_out;  // nlo + (rncols - nk)
   int32_t ldim[EJ_MAX_KEYS];   // lhs dim joined with rhs dim i
-  int64_t lgrid[EJ_MAX_DIMS];  // lhs tile grid
-  int64_t rgrid[EJ_MAX_DIMS];  // rhs tile grid
-  int64_t NK;                  // rhs tiles per join value: prod rgrid[nk .. rncols)
-  int64_t n_lhs, n_rhs, P;     // P = n_lhs * NK
+  int32_t lgrid[EJ_MAX_DIMS];  // lhs tile grid
+  int32_t rgrid[EJ_MAX_DIMS];  // rhs tile grid
+  int32_t NK;                  // rhs tiles per join value: prod rgrid[nk .. rncols)
+  int32_t n_lhs, n_rhs, P;     // P = n_lhs * NK
+  int32_t ppb;                 // pairs per block
 };
 
-__device__ inline void load_row(const int32_t *__restrict__ c, int64_t t, int ncols,
-                                int32_t (&v)[EJ_MAX_DIMS]) {
-#pragma unroll
-  for (int d = 0; d < EJ_MAX_DIMS; ++d) v[d] = d < ncols ? c[t * ncols + d] : 0;
-}
-
-// Linear index, over the rhs join grid, of a lhs tile's join coordinates.
-__device__ inline int64_t join_row(const int32_t (&v)[EJ_MAX_DIMS], const DenseSpec &s) {
-  int64_t j = 0;
-#pragma unroll
-  for (int i = 0; i < EJ_MAX_KEYS; ++i)
-    if (i < s.nk) {
-      int32_t c = 0;
-#pragma unroll
-      for (int d = 0; d < EJ_MAX_DIMS; ++d) c = d == s.ldim[i] ? v[d] : c;
-      j = j * s.rgrid[i] + c;
-    }
-  return j;
-}
-
-// Blocks of kDenseThreads threads.  Every block scans the lhs coordinates
-// (run starts, order and range checks) and keeps the run starts and each
-// tile's rhs join row in LDS; block b then writes pairs
-// [b * kDensePairsPerBlock, ...), its share of the segments, its share of the
-// rhs check (loaded first, so that its latency overlaps the lhs scan) and
-// (run_order) the order of the XCD chunks assigned to it.  The last block to
-// finish publishes the counts: scal[0] = U (0 when a check failed), scal[1] =
-// not-applicable flag, scal[2] = scal[4] = P, scal[3] = scal[5] = 0, and,
-// given host_counts, the single word host_counts[6] = ticket << 33 | flag <<
-// 32 | U.  Blocks meet through one atomic word, scal[7]: each adds 1 plus its
-// check failure in the upper half, so the block that sees nblk - 1 finished
-// blocks before it also sees every failure; no fence is needed (a fence here
-// would write back the L2, which the einsum before this kernel left full of
-// output tiles).  scal[7] must be zero at launch; the last block returns it
-// to zero.
+// Blocks of kDenseThreads threads; LN and RN are the lhs and rhs coordinate
+// ranks (0: read from the spec, up to EJ_MAX_DIMS).  Every block scans the
+// lhs coordinates (run starts, order and range checks) and keeps in LDS the
+// run starts and, per lhs tile, its run and its rhs join row.  Block b then
+// writes its share of the segments, the pairs of the lhs-major pair indices
+// [b * ppb, (b + 1) * ppb) (pair index i is lhs tile i / NK meeting free
+// index i % NK; its place in segment order follows from the tile's run), its
+// share of the rhs check (the first row loaded before the lhs scan, so that
+// the two latencies overlap) and (run_order) the order of the XCD chunks
+// assigned to it.  The last block to finish publishes the counts: scal[0] =
+// U (0 when a check failed), scal[1] = not-applicable flag, scal[2] = scal[4]
+// = P, scal[3] = scal[5] = 0, and, given host_counts, the single word
+// host_counts[6] = ticket << 33 | flag << 32 | U.  Blocks meet through one
+// atomic word, scal[7]: each adds 1 plus its check failure in the upper
+// half, so the block that sees nblk - 1 finished blocks before it also sees
+// every failure; no fence is needed (a fence here would write back the L2,
+// which the einsum before this kernel left full of output tiles).  scal[7]
+// must be zero at launch; the last block returns it to zero.
+template <int LN, int RN>
 __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     const int32_t *__restrict__ lc, const int32_t *__restrict__ rc, DenseSpec s,
-    int64_t *__restrict__ lidx, int64_t *__restrict__ ridx, int64_t pair_cap,
-    int32_t *__restrict__ out_coords, int32_t *__restrict__ seg_offsets, int64_t seg_cap,
-    int group, int32_t *__restrict__ run_order, int64_t *__restrict__ scal,
+    int64_t *__restrict__ lidx, int64_t *__restrict__ ridx, int32_t *__restrict__ out_coords,
+    int32_t *__restrict__ seg_offsets, int64_t seg_cap, int group,
+    int32_t *__restrict__ run_order, int64_t *__restrict__ scal,
     int64_t *__restrict__ host_counts, int64_t ticket) {
+  constexpr int LD = LN ? LN : EJ_MAX_DIMS, RD = RN ? RN : EJ_MAX_DIMS;
   constexpr int NW = kDenseThreads / 64;
   __shared__ int32_t run_start[kDenseMaxRuns + 1];
   __shared__ int32_t jrow[kDenseMaxLhs];
+  __shared__ uint16_t run_of[kDenseMaxLhs];
   __shared__ int32_t cls_base[NW][256];
+  const int lncols = LN ? LN : s.lncols, rncols = RN ? RN : s.rncols;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t blk = blockIdx.x, nblk = gridDim.x;
+  const int blk = blockIdx.x, nblk = gridDim.x;
+  const uint32_t nk32 = static_cast<uint32_t>(s.NK);
   int bad = 0;
 
-  // ---- rhs check: row r holds the coordinates of grid position r ----------
-  {
-    const int64_t rpb = (s.n_rhs + nblk - 1) / nblk;
-    const int64_t r0 = blk * rpb, r1 = min(s.n_rhs, r0 + rpb);
-    for (int64_t r = r0 + tid; r < r1; r += kDenseThreads) {
-      int32_t cv[EJ_MAX_DIMS];
-      load_row(rc, r, s.rncols, cv);
-      int64_t rem = r;
+  // ---- rhs check, first row: issued before the lhs loads -------------------
+  const int64_t rpb = (static_cast<uint32_t>(s.n_rhs) - 1u) / static_cast<uint32_t>(nblk) + 1u;
+  const int64_t r0 = blk * rpb, r1 = min(static_cast<int64_t>(s.n_rhs), r0 + rpb);
+  const int64_t rfirst = r0 + tid;
+  int32_t rv[RD];
+  auto load_r = [&](int64_t r) {
 #pragma unroll
-      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d)
-        if (d < s.rncols) {
-          if (cv[d] != static_cast<int32_t>(rem % s.rgrid[d])) bad = 1;
-          rem /= s.rgrid[d];
-        }
-    }
-  }
+    for (int d = 0; d < RD; ++d) rv[d] = d < rncols ? rc[r * rncols + d] : 0;
+  };
+  auto rhs_ok = [&](int64_t r) {  // row r holds the coordinates of grid position r
+    uint32_t rem = static_cast<uint32_t>(r);
+    bool ok = true;
+#pragma unroll
+    for (int d = RD - 1; d >= 0; --d)
+      if (d < rncols) {
+        const uint32_t g = static_cast<uint32_t>(s.rgrid[d]), q = rem / g;
+        ok = ok && rv[d] == static_cast<int32_t>(rem - q * g);
+        rem = q;
+      }
+    return ok;
+  };
+  if (rfirst < r1) load_r(rfirst);
 
   // ---- lhs scan: this thread's tiles [t0, t1), contiguous --------------------
-  const int64_t per = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;
-  const int64_t t0 = min(s.n_lhs, tid * per), t1 = min(s.n_lhs, t0 + per);
+  const int per = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;
+  const int t0 = min(s.n_lhs, tid * per), t1 = min(s.n_lhs, t0 + per);
   uint32_t newmask = 0;  // bit i: tile t0 + i starts a run
-  int64_t nnew = 0;
-  int32_t pv[EJ_MAX_DIMS];
-  if (t0 > 0 && t0 < t1) load_row(lc, t0 - 1, s.lncols, pv);
-  for (int64_t t = t0; t < t1; ++t) {
-    int32_t cv[EJ_MAX_DIMS];
-    load_row(lc, t, s.lncols, cv);
+  int nnew = 0;
+  int32_t pv[LD];
+  if (t0 > 0 && t0 < t1) {
 #pragma unroll
-    for (int d = 0; d < EJ_MAX_DIMS; ++d)
-      if (d < s.lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
+    for (int d = 0; d < LD; ++d) pv[d] = d < lncols ? lc[(t0 - 1) * lncols + d] : 0;
+  }
+  for (int t = t0; t < t1; ++t) {
+    int32_t cv[LD];
 #pragma unroll
-    for (int i = 0; i < EJ_MAX_KEYS; ++i)
-      if (i < s.nk && cv[s.ldim[i]] >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
+    for (int d = 0; d < LD; ++d) cv[d] = d < lncols ? lc[t * lncols + d] : 0;
+#pragma unroll
+    for (int d = 0; d < LD; ++d)
+      if (d < lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
+    uint32_t j = 0;  // the rhs join row: its join coordinates over the join grid
+#pragma unroll
+    for (int i = 0; i < RD; ++i)
+      if (i < s.nk) {
+        int32_t c = 0;
+#pragma unroll
+        for (int d = 0; d < LD; ++d) c = d == s.ldim[i] ? cv[d] : c;
+        if (c >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
+        j = j * static_cast<uint32_t>(s.rgrid[i]) + static_cast<uint32_t>(c);
+      }
     bool newrun = t == 0;
     if (t > 0) {
-      int cmp = 0, first = EJ_MAX_DIMS;
+      int cmp = 0, first = LD;
 #pragma unroll
-      for (int d = 0; d < EJ_MAX_DIMS; ++d)
-        if (d < s.lncols && cmp == 0 && cv[d] != pv[d]) {
+      for (int d = 0; d < LD; ++d)
+        if (d < lncols && cmp == 0 && cv[d] != pv[d]) {
           cmp = cv[d] < pv[d] ? -1 : 1;
           first = d;
         }
@@ -140,70 +150,74 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       newmask |= 1u << (t - t0);
       ++nnew;
     }
-    jrow[t] = static_cast<int32_t>(join_row(cv, s));
+    jrow[t] = static_cast<int32_t>(j);
 #pragma unroll
-    for (int d = 0; d < EJ_MAX_DIMS; ++d) pv[d] = cv[d];
+    for (int d = 0; d < LD; ++d) pv[d] = cv[d];
   }
-  int64_t nruns = 0;
-  const int64_t rbase = block_exclusive_sum<kDenseThreads>(nnew, &nruns);
+  if (rfirst < r1 && !rhs_ok(rfirst)) bad = 1;
+
+  int64_t nruns64 = 0;
+  const int rbase = static_cast<int>(block_exclusive_sum<kDenseThreads>(nnew, &nruns64));
+  const int nruns = static_cast<int>(nruns64);
   const bool fits = nruns <= kDenseMaxRuns;
   if (fits) {
-    int64_t r = rbase;
-    for (int64_t t = t0; t < t1; ++t)
-      if (newmask >> (t - t0) & 1u) run_start[r++] = static_cast<int32_t>(t);
-    if (tid == 0) run_start[nruns] = static_cast<int32_t>(s.n_lhs);
+    int r = rbase - 1;  // the run of tile t0 - 1 (tile 0 always starts one)
+    for (int t = t0; t < t1; ++t) {
+      if (newmask >> (t - t0) & 1u) run_start[++r] = t;
+      run_of[t] = static_cast<uint16_t>(r);
+    }
+    if (tid == 0) run_start[nruns] = s.n_lhs;
   } else {
     bad = 1;
   }
   __syncthreads();
-  const int64_t U = fits ? nruns * s.NK : 0;
-  const int64_t live_u = U < seg_cap ? U : seg_cap;
+  const int64_t U = fits ? static_cast<int64_t>(nruns) * s.NK : 0;
+  const int live_u = static_cast<int>(U < seg_cap ? U : seg_cap);
   if (U > seg_cap) bad = 1;
 
-  // Run of pair q (segment order): the last r with run_start[r] * NK <= q.
-  auto run_of = [&](int64_t q) -> int64_t {
-    int64_t lo = 0, len = nruns;
-    while (len > 1) {
-      const int64_t half = len >> 1;
-      lo += static_cast<int64_t>(run_start[lo + half]) * s.NK <= q ? half : 0;
-      len -= half;
-    }
-    return lo;
-  };
-
-  // ---- pairs [q0, q1) in segment order -------------------------------------
   if (fits) {
-    const int64_t q0 = blk * kDensePairsPerBlock;
-    const int64_t q1 = min(min(s.P, pair_cap), q0 + kDensePairsPerBlock);
-    for (int64_t q = q0 + tid; q < q1; q += kDenseThreads) {
-      const int64_t r = run_of(q);
-      const int64_t rs = run_start[r], len = run_start[r + 1] - rs;
-      const int64_t w = q - rs * s.NK;
-      const int64_t kk = w / len;
-      const int64_t t = rs + (w - kk * len);
+    // ---- segments: this block's share of [0, live_u) ----------------------
+    // Run r (tiles rs .. rs + len - 1) owns pairs [rs * NK, (rs + len) * NK):
+    // segment (r, k) is pairs rs * NK + k * len + (t - rs), t ascending.
+    const int64_t upb = live_u ? (static_cast<uint32_t>(live_u) - 1u) / nblk + 1u : 0;
+    const int64_t u0 = blk * upb, u1 = min(static_cast<int64_t>(live_u), u0 + upb);
+    for (int64_t u = u0 + tid; u < u1; u += kDenseThreads) {
+      const uint32_t uu = static_cast<uint32_t>(u);
+      const uint32_t r = uu / nk32, kk = uu - r * nk32;
+      const int rs = run_start[r], len = run_start[r + 1] - rs;
+      seg_offsets[u] = rs * s.NK + static_cast<int>(kk) * len;
+      int32_t *oc = out_coords + u * s.n_out;
+#pragma unroll
+      for (int d = 0; d < LD; ++d)
+        if (d < s.nlo) oc[d] = lc[rs * lncols + d];
+      uint32_t rem = kk;
+#pragma unroll
+      for (int d = RD - 1; d >= 0; --d)
+        if (d >= s.nk && d < rncols) {
+          const uint32_t g = static_cast<uint32_t>(s.rgrid[d]), qd = rem / g;
+          oc[s.nlo + (d - s.nk)] = static_cast<int32_t>(rem - qd * g);
+          rem = qd;
+        }
+    }
+    if (blk == 0 && tid == 0 && U <= seg_cap) seg_offsets[U] = s.P;
+    // ---- pairs: lhs-major indices [i0, i1), placed in segment order -------
+    const int64_t i0 = static_cast<int64_t>(blk) * s.ppb;
+    const int64_t i1 = min(static_cast<int64_t>(s.P), i0 + s.ppb);
+    for (int64_t i = i0 + tid; i < i1; i += kDenseThreads) {
+      const uint32_t ui = static_cast<uint32_t>(i);
+      const uint32_t t = ui / nk32, kk = ui - t * nk32;
+      const int r = run_of[t];
+      const int rs = run_start[r], len = run_start[r + 1] - rs;
+      const int q = rs * s.NK + static_cast<int>(kk) * len + (static_cast<int>(t) - rs);
       lidx[q] = t;
       ridx[q] = static_cast<int64_t>(jrow[t]) * s.NK + kk;
     }
-    // ---- segments: this block's share of [0, live_u) ----------------------
-    const int64_t upb = (live_u + nblk - 1) / nblk;
-    const int64_t u0 = blk * upb, u1 = min(live_u, u0 + upb);
-    for (int64_t u = u0 + tid; u < u1; u += kDenseThreads) {
-      const int64_t r = u / s.NK, kk = u - r * s.NK;
-      const int64_t rs = run_start[r], len = run_start[r + 1] - rs;
-      seg_offsets[u] = static_cast<int32_t>(rs * s.NK + kk * len);
-      int32_t *oc = out_coords + u * s.n_out;
-#pragma unroll
-      for (int d = 0; d < EJ_MAX_DIMS; ++d)
-        if (d < s.nlo) oc[d] = lc[rs * s.lncols + d];
-      int64_t rem = kk;
-#pragma unroll
-      for (int d = EJ_MAX_DIMS - 1; d >= 0; --d)
-        if (d >= s.nk && d < s.rncols) {
-          oc[s.nlo + (d - s.nk)] = static_cast<int32_t>(rem % s.rgrid[d]);
-          rem /= s.rgrid[d];
-        }
-    }
-    if (blk == 0 && tid == 0 && U <= seg_cap) seg_offsets[U] = static_cast<int32_t>(s.P);
+  }
+
+  // ---- rhs check, remaining rows ------------------------------------------
+  for (int64_t r = rfirst + kDenseThreads; r < r1; r += kDenseThreads) {
+    load_r(r);
+    if (!rhs_ok(r)) bad = 1;
   }
 
   // ---- run order: per XCD chunk of the live groups, longest first ---------
@@ -211,26 +225,33 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   // by wave x / nblk of block x % nblk: a stable counting sort over 256
   // pair-count classes (counts above 255 tie), ranked with ballots.
   if (fits && group > 0 && run_order) {
-    const int64_t ngroups = (live_u + group - 1) / group;
-    if (blk == 0 && tid == 0) run_order[0] = static_cast<int32_t>(ngroups);
-    for (int x = lane; x < 256; x += 64) cls_base[wave][x] = 0;
-    const int64_t x = static_cast<int64_t>(wave) * nblk + blk;  // the chunk of this wave
+    const int ngroups = (live_u + group - 1) / group;
+    if (blk == 0 && tid == 0) run_order[0] = ngroups;
+    const int x = wave * nblk + blk;  // the chunk of this wave
     if (x < 8) {
-      const int64_t pc = ngroups / 8, rem = ngroups % 8;
-      const int64_t start = x < rem ? x * (pc + 1) : rem * (pc + 1) + (x - rem) * pc;
-      const int64_t cnt = pc + (x < rem ? 1 : 0);
-      auto cls = [&](int64_t i) {
-        int64_t wsum = 0;
-        for (int v = 0; v < group; ++v) {
-          const int64_t u = (start + i) * group + v;
-          if (u < live_u) {
-            const int64_t r = u / s.NK;
-            wsum += run_start[r + 1] - run_start[r];
+      for (int c = lane; c < 256; c += 64) cls_base[wave][c] = 0;
+      const int pc = ngroups / 8, rem = ngroups % 8;
+      const int start = x < rem ? x * (pc + 1) : rem * (pc + 1) + (x - rem) * pc;
+      const int cnt = pc + (x < rem ? 1 : 0);
+      // Pairs of group start + i: the runs of its segments, walked from one
+      // division.
+      auto cls = [&](int i) {
+        const int ufirst = (start + i) * group;
+        const int ulast = min(live_u, ufirst + group);
+        uint32_t r = static_cast<uint32_t>(ufirst) / nk32;
+        uint32_t kk = static_cast<uint32_t>(ufirst) - r * nk32;
+        int wsum = 0;
+        for (int u = ufirst; u < ulast; ++u) {
+          wsum += run_start[r + 1] - run_start[r];
+          if (++kk == nk32) {
+            kk = 0;
+            ++r;
           }
         }
-        return static_cast<int>(255 - (wsum < 255 ? wsum : 255));
+        return 255 - (wsum < 255 ? wsum : 255);
       };
-      for (int64_t i = lane; i < cnt; i += 64) atomicAdd(&cls_base[wave][cls(i)], 1);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      for (int i = lane; i < cnt; i += 64) atomicAdd(&cls_base[wave][cls(i)], 1);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       int v[4], sum = 0;
 #pragma unroll
@@ -252,8 +273,8 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-      for (int64_t i0 = 0; i0 < cnt; i0 += 64) {
-        const int64_t i = i0 + lane;
+      for (int ib = 0; ib < cnt; ib += 64) {
+        const int i = ib + lane;
         const bool valid = i < cnt;
         const int c = valid ? cls(i) : 0;
         uint64_t peers = __ballot(valid);
@@ -266,8 +287,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
         asm volatile("" ::: "memory");
         const int base = valid ? cls_base[wave][c] : 0;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (valid)
-          run_order[1 + start + base + __popcll(peers & lt)] = static_cast<int32_t>(start + i);
+        if (valid) run_order[1 + start + base + __popcll(peers & lt)] = start + i;
         if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
@@ -298,6 +318,33 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
                                static_cast<unsigned long long>(u_out),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
+  }
+}
+
+using DenseKernel = void (*)(const int32_t *, const int32_t *, DenseSpec, int64_t *, int64_t *,
+                             int32_t *, int32_t *, int64_t, int, int32_t *, int64_t *,
+                             int64_t *, int64_t);
+
+template <int LN>
+DenseKernel dense_kernel_for_rhs(int rn) {
+  switch (rn) {
+    case 1: return dense_plan_kernel<LN, 1>;
+    case 2: return dense_plan_kernel<LN, 2>;
+    case 3: return dense_plan_kernel<LN, 3>;
+    case 4: return dense_plan_kernel<LN, 4>;
+    default: return dense_plan_kernel<0, 0>;
+  }
+}
+
+// The kernel specialised for the coordinate ranks (both up to 4), else the
+// general one.
+DenseKernel dense_kernel_for(int ln, int rn) {
+  switch (ln) {
+    case 1: return dense_kernel_for_rhs<1>(rn);
+    case 2: return dense_kernel_for_rhs<2>(rn);
+    case 3: return dense_kernel_for_rhs<3>(rn);
+    case 4: return dense_kernel_for_rhs<4>(rn);
+    default: return dense_plan_kernel<0, 0>;
   }
 }
 
@@ -336,8 +383,6 @@ extern "C" int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int
   s.lncols = lhs_ncols;
   s.rncols = rhs_ncols;
   s.nk = n_keys;
-  s.n_lhs = n_lhs;
-  s.n_rhs = n_rhs;
   // Join dims: rhs dims 0 .. nk-1, each once, their lhs dims increasing in
   // rhs-dim order (so that lhs order within a run is rhs order).
   for (int i = 0; i < n_keys; ++i) s.ldim[i] = -1;
@@ -373,38 +418,47 @@ extern "C" int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int
   }
   s.nlo = nlo;
   s.n_out = n_out;
-  int64_t grid_r = 1;
+  // The grid product stops growing past 2^31 (no overflow); such a grid is
+  // beyond the kernel's 32-bit indices.
+  int64_t grid_r = 1, NK = 1;
   for (int d = 0; d < rhs_ncols; ++d) {
     EJ_CHECK_ARG(rhs_grid[d] >= 1 && rhs_grid[d] < (int64_t(1) << 31), "bad rhs grid");
-    s.rgrid[d] = rhs_grid[d];
-    grid_r *= rhs_grid[d];
+    s.rgrid[d] = static_cast<int32_t>(rhs_grid[d]);
+    grid_r = std::min(grid_r * rhs_grid[d], int64_t(1) << 31);
+    if (d >= n_keys) NK = std::min(NK * rhs_grid[d], int64_t(1) << 31);
   }
   for (int d = 0; d < lhs_ncols; ++d) {
     EJ_CHECK_ARG(lhs_grid[d] >= 1 && lhs_grid[d] < (int64_t(1) << 31), "bad lhs grid");
-    s.lgrid[d] = lhs_grid[d];
+    s.lgrid[d] = static_cast<int32_t>(lhs_grid[d]);
   }
-  s.NK = 1;
-  for (int d = n_keys; d < rhs_ncols; ++d) s.NK *= rhs_grid[d];
-  if (n_rhs != grid_r || n_lhs < 1 || n_lhs > kDenseMaxLhs) {
-    set_error("the dense plan needs a full rhs grid and 1 .. %lld lhs tiles",
-              (long long)kDenseMaxLhs);
+  if (grid_r >= (int64_t(1) << 31) || n_rhs != grid_r || n_lhs < 1 || n_lhs > kDenseMaxLhs) {
+    set_error("the dense plan needs a full rhs grid of under 2^31 tiles and 1 .. %d lhs tiles",
+              kDenseMaxLhs);
     return EJ_E_UNSUPPORTED;
   }
-  s.P = n_lhs * s.NK;
-  EJ_CHECK_ARG(s.P < (int64_t(1) << 31), "pair count beyond 2^31");
-  if (pair_capacity < s.P) {
-    set_error("pair capacity %lld < %lld pairs", (long long)pair_capacity, (long long)s.P);
+  const int64_t P = n_lhs * NK;
+  if (P >= (int64_t(1) << 30)) {
+    set_error("the dense plan needs under 2^30 pairs (%lld)", (long long)P);
+    return EJ_E_UNSUPPORTED;
+  }
+  if (pair_capacity < P) {
+    set_error("pair capacity %lld < %lld pairs", (long long)pair_capacity, (long long)P);
     return EJ_E_CAPACITY;
   }
+  s.n_lhs = static_cast<int32_t>(n_lhs);
+  s.n_rhs = static_cast<int32_t>(n_rhs);
+  s.NK = static_cast<int32_t>(NK);
+  s.P = static_cast<int32_t>(P);
   EJ_CHECK_ARG(seg_capacity >= 1, "seg_capacity must be positive");
   EJ_CHECK_ARG(counts_direct < (int64_t(1) << 30), "counts_direct (the ticket) beyond 2^30");
   int64_t *direct = nullptr;
   if (counts_direct) EJ_HIP(hipHostGetDevicePointer(reinterpret_cast<void **>(&direct), counts, 0));
-  const int64_t nblk = ceil_div(s.P, kDensePairsPerBlock);
+  s.ppb = static_cast<int32_t>(std::max<int64_t>(kDenseMinPairsPerBlock, ceil_div(P, kDenseMaxBlocks)));
+  const int64_t nblk = ceil_div(P, s.ppb);
   const bool order = run_order && group > 0;
-  hipLaunchKernelGGL(dense_plan_kernel, dim3(static_cast<unsigned>(nblk)), dim3(kDenseThreads), 0,
-                     stream, lhs_coords, rhs_coords, s, lhs_idx, rhs_idx, pair_capacity,
-                     out_coords, seg_offsets, seg_capacity, order ? group : 0,
+  hipLaunchKernelGGL(dense_kernel_for(lhs_ncols, rhs_ncols), dim3(static_cast<unsigned>(nblk)), dim3(kDenseThreads), 0,
+                     stream, lhs_coords, rhs_coords, s, lhs_idx, rhs_idx, out_coords,
+                     seg_offsets, seg_capacity, order ? group : 0,
                      order ? run_order : nullptr, dev_counts, direct, int64_t(counts_direct));
   EJ_LAUNCH_CHECK();
   if (order && run_order_written) *run_order_written = 1;

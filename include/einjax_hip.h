@@ -327,7 +327,8 @@ int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t
  * increasing in that order), the output dims are lhs dims 0 .. nlo-1 followed
  * by rhs dims n_keys .. rhs_ncols-1, every other lhs dim is a join dim, and
  * the lhs coordinates are strictly increasing in lexicographic order and
- * inside lhs_grid; 1 <= n_lhs <= 16384.  Then every lhs tile meets one rhs
+ * inside lhs_grid; 1 <= n_lhs <= 16384, the rhs grid under 2^31 tiles and
+ * n_lhs * NK under 2^30 pairs.  Then every lhs tile meets one rhs
  * tile per value of the rhs dims after the join dims (NK of them), P = n_lhs
  * * NK, and the lhs tiles sharing their first nlo coordinates form a run: the
  * plan writes the pairs in segment order (perm = identity: pass perm = NULL

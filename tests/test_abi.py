@@ -334,6 +334,10 @@ def test_dense_plan_host_validation():
     assert call(mm[0], mm[1], n_lhs=16385) == _lib.EJ_E_UNSUPPORTED  # beyond 16384 lhs tiles
     assert call([(0, 0)], [(0, 0), (1, 1)]) == _lib.EJ_E_UNSUPPORTED  # lhs dim 1 not joined
     assert call(mm[0], mm[1], cap=15) == _lib.EJ_E_CAPACITY     # 4 x 4 pairs
+    # a rhs grid of 2^32 tiles, and 2^31 pairs: beyond the plan's 32-bit indices
+    assert call(mm[0], mm[1], n_rhs=1 << 32, rgrid=(1 << 16, 1 << 16)) == _lib.EJ_E_UNSUPPORTED
+    assert call(mm[0], mm[1], n_lhs=16384, lgrid=(4096, 4), n_rhs=4 << 17,
+                rgrid=(4, 1 << 17)) == _lib.EJ_E_UNSUPPORTED
     # two join keys whose lhs dims run against the rhs order
     assert call([(2, 0), (1, 1)], [(0, 0), (1, 2)], lncols=3, rncols=3, lgrid=(2, 2, 2),
                 rgrid=(2, 2, 2), n_rhs=8) == _lib.EJ_E_UNSUPPORTED

@@ -230,7 +230,7 @@ def test_dense_plan_misses_fall_back(gpu, case, monkeypatch):
 
 def test_dense_plan_at_its_lhs_limit(gpu):
     """16384 lhs tiles (every tile of a 64 x 256 grid of 1 x 1 tiles)
-    against a dense 256 x 8 rhs: 131,072 pairs over 16 plan blocks, 512
+    against a dense 256 x 8 rhs: 131,072 pairs over 64 plan blocks, 512
     segments; one tile more is refused on the host."""
     note("dense plan at 16384 lhs tiles")
     rng = np.random.default_rng(8)
@@ -242,7 +242,7 @@ def test_dense_plan_at_its_lhs_limit(gpu):
     li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
     st, res = run_plan(L, Rr, keys, agg, group=4)
     assert st == _lib.EJ_OK and res["counts"][1] == 0 and res["counts"][4] == 131072
-    # a wrong rhs row near the end (checked by the last of the 16 plan blocks)
+    # a wrong rhs row near the end (checked by one of the last plan blocks)
     # and, separately, two lhs rows out of order: each is reported as a miss
     bad_r = R.Rel(Rr.coords.copy(), Rr.values, Rr.shape, Rr.tile_shape)
     bad_r.coords[2000] = bad_r.coords[2001]
@@ -267,3 +267,29 @@ def test_dense_plan_at_its_lhs_limit(gpu):
     want = R.execute_sparse(L, Rr, keys, "ij,jk->ik", agg, precision="fp64")
     npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
     assert R.rel_l2(got.values.cpu().numpy(), want.values) <= 1e-5
+
+
+def test_dense_plan_tall_rhs(gpu):
+    """Three lhs tiles against a dense 4096 x 2 rhs: one plan block checks
+    all 8192 rhs rows (eight per thread); a wrong row at either end is a
+    miss, and the plan matches the oracle's."""
+    note("dense plan, tall rhs")
+    rng = np.random.default_rng(9)
+    lc = np.array([[0, 5], [0, 4000], [2, 17]], np.int32)
+    rc = np.stack(np.unravel_index(np.arange(4096 * 2), (4096, 2)), 1).astype(np.int32)
+    L = R.Rel(lc, rng.standard_normal((3, 2, 2)).astype(np.float32), (6, 8192), (2, 2))
+    Rr = R.Rel(rc, rng.standard_normal((len(rc), 2, 2)).astype(np.float32), (8192, 4), (2, 2))
+    keys, agg = [(1, 0)], [(0, 0), (1, 1)]
+    li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
+    st, res = run_plan(L, Rr, keys, agg, group=2)
+    assert st == _lib.EJ_OK and res["counts"][1] == 0 and res["counts"][4] == 6
+    npt.assert_array_equal(res["coords"], uc)
+    for u in range(len(uc)):
+        a, b = res["off"][u], res["off"][u + 1]
+        npt.assert_array_equal(res["li"][a:b], segs[u][0])
+        npt.assert_array_equal(res["ri"][a:b], segs[u][1])
+    for row in (0, 8191):
+        bad_r = R.Rel(Rr.coords.copy(), Rr.values, Rr.shape, Rr.tile_shape)
+        bad_r.coords[row, 1] ^= 1
+        st, miss = run_plan(L, bad_r, keys, agg, group=2)
+        assert st == _lib.EJ_OK and miss["counts"][1] == 1 and miss["dev_u"] == 0
