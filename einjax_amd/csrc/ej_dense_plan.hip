@@ -220,11 +220,96 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     if (!rhs_ok(r)) bad = 1;
   }
 
-  // ---- run order: per XCD chunk of the live groups, longest first ---------
+  // ---- run order, whole runs: balanced over the XCDs, longest first --------
+  // When every run holds gpr = NK / group whole groups (which share the
+  // run's lhs tiles), the runs are ranked longest first (a stable counting
+  // sort over 256 pair-count classes, counts above 255 tying) and dealt to
+  // the eight XCDs in snake order (ranks 0-7 to XCDs 0-7, ranks 8-15 to XCDs
+  // 7-0, ...), which evens out the XCDs' pair totals while keeping each run's
+  // groups on one XCD.  The order lists XCD 0's runs, then XCD 1's, ..., each
+  // XCD's longest first and each run's groups in order; the einsum's XCD
+  // mapping cuts it into the XCDs' equal shares of groups.
+  const bool whole_runs = s.NK % (group > 0 ? group : 1) == 0;
+  if (fits && group > 0 && run_order && U <= seg_cap && whole_runs) {
+    const int ngroups = live_u / group;
+    if (blk == 0 && tid == 0) run_order[0] = ngroups;
+    __syncthreads();  // the pairs loop is done with run_of
+    uint16_t *const rank_of = run_of;  // rank of run r (reuses the LDS)
+    const int rpw = ((nruns + NW - 1) / NW + 63) & ~63;  // runs per wave, whole 64-run steps
+    const int w0 = min(nruns, wave * rpw), w1 = min(nruns, w0 + rpw);
+    auto run_cls = [&](int r) {
+      const int len = run_start[r + 1] - run_start[r];
+      return 255 - (len < 255 ? len : 255);
+    };
+    for (int c = lane; c < 256; c += 64) cls_base[wave][c] = 0;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int r = w0 + lane; r < w1; r += 64) atomicAdd(&cls_base[wave][run_cls(r)], 1);
+    __syncthreads();
+    // Exclusive scan of the class counts in (class, wave) order: thread tid
+    // holds entries 4 tid .. 4 tid + 3 of the 256 x NW.
+    int hv[4], hs = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = 4 * tid + k;
+      hv[k] = cls_base[e % NW][e / NW];
+      hs += hv[k];
+    }
+    int64_t htot = 0;
+    int hrun = static_cast<int>(block_exclusive_sum<kDenseThreads>(hs, &htot));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = 4 * tid + k;
+      cls_base[e % NW][e / NW] = hrun;
+      hrun += hv[k];
+    }
+    __syncthreads();
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    for (int rb = w0; rb < w1; rb += 64) {
+      const int r = rb + lane;
+      const bool valid = r < w1;
+      const int c = valid ? run_cls(r) : 0;
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int bit = (c >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      asm volatile("" ::: "memory");
+      const int base = valid ? cls_base[wave][c] : 0;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (valid) rank_of[r] = static_cast<uint16_t>(base + __popcll(peers & lt));
+      if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    // Rank p goes to XCD snake(p) as its (p / 8)-th run; XCD x holds n(x)
+    // runs: one per full round of eight and one more if the last round
+    // reaches it.
+    const int gpr = s.NK / group;
+    const int rounds = (nruns + 7) / 8, last = nruns - 8 * (rounds - 1);
+    const bool last_fwd = ((rounds - 1) & 1) == 0;
+    auto n_of = [&](int x) {
+      return rounds - 1 + ((last_fwd ? x < last : x >= 8 - last) ? 1 : 0);
+    };
+    const int gpb = (ngroups + nblk - 1) / nblk;
+    const int g0 = min(ngroups, blk * gpb), g1 = min(ngroups, g0 + gpb);
+    for (int gi = g0 + tid; gi < g1; gi += kDenseThreads) {
+      const int r = gi / gpr, kg = gi - r * gpr;
+      const int p = rank_of[r];
+      const int q = p & 7, x = (p >> 3) & 1 ? 7 - q : q;
+      int before = 0;  // runs of the XCDs before x
+#pragma unroll
+      for (int y = 0; y < 7; ++y) before += y < x ? n_of(y) : 0;
+      run_order[1 + (before + (p >> 3)) * gpr + kg] = gi;
+    }
+  }
+
+  // ---- run order, otherwise: per XCD chunk of the live groups -------------
   // Chunk x (the workgroups the einsum's XCD mapping gives XCD x) is ordered
-  // by wave x / nblk of block x % nblk: a stable counting sort over 256
-  // pair-count classes (counts above 255 tie), ranked with ballots.
-  if (fits && group > 0 && run_order) {
+  // longest first by wave x / nblk of block x % nblk: a stable counting sort
+  // over 256 pair-count classes (counts above 255 tie), ranked with ballots.
+  if (fits && group > 0 && run_order && !(U <= seg_cap && whole_runs)) {
     const int ngroups = (live_u + group - 1) / group;
     if (blk == 0 && tid == 0) run_order[0] = ngroups;
     const int x = wave * nblk + blk;  // the chunk of this wave

@@ -89,6 +89,50 @@ def oracle_segments(L, Rr, keys, agg):
                     for u in range(len(uc))]
 
 
+def xcd_chunks(ng):
+    """The einsum's split of ng groups over the eight XCDs: XCD x runs
+    positions [start_x, start_x + cnt_x) of the run order."""
+    per, rem = divmod(ng, 8)
+    out, st = [], 0
+    for x in range(8):
+        c = per + (1 if x < rem else 0)
+        out.append((st, st + c))
+        st += c
+    return out
+
+
+def snake_order(lens, gpr):
+    """Runs ranked longest first (counts above 255 tie, ties by run index),
+    dealt to XCDs 0-7, 7-0, 0-7, ...; XCD 0's runs first, each XCD's in rank
+    order, each run's gpr groups in order."""
+    nr = len(lens)
+    ranked = sorted(range(nr), key=lambda r: (-min(lens[r], 255), r))
+    xcd_runs = [[] for _ in range(8)]
+    for p, r in enumerate(ranked):
+        q = p % 8
+        xcd_runs[7 - q if (p // 8) % 2 else q].append(r)
+    return [r * gpr + k for x in range(8) for r in xcd_runs[x] for k in range(gpr)]
+
+
+def check_balanced_order(order, segs, NK, group):
+    """A run order for whole runs: the snake deal, each XCD's groups longest
+    first, and XCD pair totals within one run's weight of each other."""
+    gpr = NK // group
+    lens = [len(segs[r * NK][0]) for r in range(len(segs) // NK)]
+    npt.assert_array_equal(order, snake_order(lens, gpr))
+    if len(lens) % 8:
+        return
+    # whole runs on every XCD: each XCD's share falls in non-increasing run
+    # weights, and the shares' totals differ by at most one run's weight
+    weight = [group * lens[g // gpr] for g in order]
+    loads = []
+    for a, b in xcd_chunks(len(order)):
+        w = weight[a:b]
+        assert all(x >= y for x, y in zip(w, w[1:]))
+        loads.append(sum(w))
+    assert max(loads) - min(loads) <= NK * max(lens)
+
+
 def workloads():
     w3 = G.workload_order3(n=256, l=64, density=0.05)
     yield "blocksparse_1k", G.workload_blocksparse_1k()
@@ -131,6 +175,9 @@ def test_dense_plan_matches_oracle_segments(gpu, idx):
             ng = (len(uc) + group - 1) // group
             assert res["written"] == 1 and res["order"][0] == ng
             npt.assert_array_equal(np.sort(res["order"][1:]), np.arange(ng))
+            NK = int(np.prod(grid(Rr)[len(keys):]))
+            if NK % group == 0:
+                check_balanced_order(res["order"][1:], segs, NK, group)
 
 
 @pytest.mark.parametrize("idx", range(5))
@@ -293,3 +340,27 @@ def test_dense_plan_tall_rhs(gpu):
         bad_r.coords[row, 1] ^= 1
         st, miss = run_plan(L, bad_r, keys, agg, group=2)
         assert st == _lib.EJ_OK and miss["counts"][1] == 1 and miss["dev_u"] == 0
+
+
+def test_dense_run_order_balances_xcds(gpu):
+    """The headline's 128 runs of Binomial(128, 0.05) lhs tiles against 32
+    free rhs tiles, groups of 2: the snake deal leaves the XCDs' pair totals
+    within 3% of their mean (16 whole runs each), where equal shares of
+    consecutive runs differ by 13%."""
+    note("dense run order balance")
+    w = G.workload_blocksparse_16k(values=False)
+    L = R.Rel(w["lhs"].coords, np.zeros((len(w["lhs"].coords), 1, 1), np.float32),
+              (128, 128), (1, 1))
+    rc = np.stack(np.unravel_index(np.arange(128 * 32), (128, 32)), 1).astype(np.int32)
+    Rr = R.Rel(rc, np.zeros((len(rc), 1, 1), np.float32), (128, 32), (1, 1))
+    keys, agg = [(1, 0)], [(0, 0), (1, 1)]
+    li_o, uc, segs = oracle_segments(L, Rr, keys, agg)
+    st, res = run_plan(L, Rr, keys, agg, group=2)
+    assert st == _lib.EJ_OK and res["counts"][0] == 4096
+    order = res["order"][1:]
+    check_balanced_order(order, segs, 32, 2)
+    lens = np.bincount(L.coords[:, 0], minlength=128)
+    loads = [sum(2 * lens[g // 16] for g in order[a:b]) for a, b in xcd_chunks(2048)]
+    assert max(loads) / np.mean(loads) < 1.03
+    naive = [2 * 16 * lens[16 * x:16 * x + 16].sum() for x in range(8)]
+    assert max(naive) / np.mean(naive) > 1.10
