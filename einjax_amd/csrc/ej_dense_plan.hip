@@ -222,15 +222,66 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
 
   // ---- run order, whole runs: balanced over the XCDs, longest first --------
   // When every run holds gpr = NK / group whole groups (which share the
-  // run's lhs tiles), the runs are ranked longest first (a stable counting
-  // sort over 256 pair-count classes, counts above 255 tying) and dealt to
-  // the eight XCDs in snake order (ranks 0-7 to XCDs 0-7, ranks 8-15 to XCDs
-  // 7-0, ...), which evens out the XCDs' pair totals while keeping each run's
-  // groups on one XCD.  The order lists XCD 0's runs, then XCD 1's, ..., each
-  // XCD's longest first and each run's groups in order; the einsum's XCD
-  // mapping cuts it into the XCDs' equal shares of groups.
+  // run's lhs tiles) and the einsum's equal shares of consecutive groups
+  // would leave one XCD more than 5% above the mean pair total, the runs are
+  // ranked longest first (a stable counting sort over 256 pair-count
+  // classes, counts above 255 tying) and dealt to the eight XCDs in snake
+  // order (ranks 0-7 to XCDs 0-7, ranks 8-15 to XCDs 7-0, ...), which evens
+  // out the XCDs' pair totals while keeping each run's groups on one XCD.
+  // The order lists XCD 0's runs, then XCD 1's, ..., each XCD's longest
+  // first and each run's groups in order; the einsum's XCD mapping cuts it
+  // into the XCDs' equal shares of groups.  Balanced consecutive shares are
+  // left in plan order instead (below): neighbouring runs often read the
+  // same rhs tiles (a banded lhs), which their XCD's L2 then serves.
   const bool whole_runs = s.NK % (group > 0 ? group : 1) == 0;
+  bool snake = false;
   if (fits && group > 0 && run_order && U <= seg_cap && whole_runs) {
+    __shared__ unsigned long long share_load[8];
+    const int ngroups = live_u / group, gpr = s.NK / group;
+    const int sper = ngroups / 8, srem = ngroups % 8;
+    auto share_end = [&](int x) {  // end of XCD x's share of the groups
+      return x < srem ? (x + 1) * (sper + 1) : srem * (sper + 1) + (x + 1 - srem) * sper;
+    };
+    if (tid < 8) share_load[tid] = 0;
+    __syncthreads();
+    // pair totals of the consecutive shares: thread tid walks runs [ra, rb)
+    const int rpt = (nruns + kDenseThreads - 1) / kDenseThreads;
+    const int ra = min(nruns, tid * rpt), rb = min(nruns, ra + rpt);
+    if (ra < rb) {
+      int g = ra * gpr;
+      int x = g < srem * (sper + 1) ? g / (sper + 1)
+                                    : srem + (sper ? (g - srem * (sper + 1)) / sper : 0);
+      x = min(x, 7);
+      int end = share_end(x);
+      unsigned long long acc = 0;
+      for (int r = ra; r < rb; ++r) {
+        const unsigned long long w = static_cast<unsigned long long>(group) *
+                                     static_cast<unsigned>(run_start[r + 1] - run_start[r]);
+        int left = gpr;
+        while (left > 0) {
+          while (g >= end && x < 7) {
+            atomicAdd(&share_load[x], acc);
+            acc = 0;
+            end = share_end(++x);
+          }
+          const int take = x < 7 ? min(left, end - g) : left;
+          acc += w * static_cast<unsigned>(take);
+          g += take;
+          left -= take;
+        }
+      }
+      atomicAdd(&share_load[x], acc);
+    }
+    __syncthreads();
+    unsigned long long mx = 0, tot = 0;
+#pragma unroll
+    for (int y = 0; y < 8; ++y) {
+      mx = share_load[y] > mx ? share_load[y] : mx;
+      tot += share_load[y];
+    }
+    snake = mx * 8 * 100 > tot * 105;
+  }
+  if (snake) {
     const int ngroups = live_u / group;
     if (blk == 0 && tid == 0) run_order[0] = ngroups;
     __syncthreads();  // the pairs loop is done with run_of
@@ -305,79 +356,12 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     }
   }
 
-  // ---- run order, otherwise: per XCD chunk of the live groups -------------
-  // Chunk x (the workgroups the einsum's XCD mapping gives XCD x) is ordered
-  // longest first by wave x / nblk of block x % nblk: a stable counting sort
-  // over 256 pair-count classes (counts above 255 tie), ranked with ballots.
-  if (fits && group > 0 && run_order && !(U <= seg_cap && whole_runs)) {
-    const int ngroups = (live_u + group - 1) / group;
-    if (blk == 0 && tid == 0) run_order[0] = ngroups;
-    const int x = wave * nblk + blk;  // the chunk of this wave
-    if (x < 8) {
-      for (int c = lane; c < 256; c += 64) cls_base[wave][c] = 0;
-      const int pc = ngroups / 8, rem = ngroups % 8;
-      const int start = x < rem ? x * (pc + 1) : rem * (pc + 1) + (x - rem) * pc;
-      const int cnt = pc + (x < rem ? 1 : 0);
-      // Pairs of group start + i: the runs of its segments, walked from one
-      // division.
-      auto cls = [&](int i) {
-        const int ufirst = (start + i) * group;
-        const int ulast = min(live_u, ufirst + group);
-        uint32_t r = static_cast<uint32_t>(ufirst) / nk32;
-        uint32_t kk = static_cast<uint32_t>(ufirst) - r * nk32;
-        int wsum = 0;
-        for (int u = ufirst; u < ulast; ++u) {
-          wsum += run_start[r + 1] - run_start[r];
-          if (++kk == nk32) {
-            kk = 0;
-            ++r;
-          }
-        }
-        return 255 - (wsum < 255 ? wsum : 255);
-      };
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      for (int i = lane; i < cnt; i += 64) atomicAdd(&cls_base[wave][cls(i)], 1);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      int v[4], sum = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[k] = cls_base[wave][lane * 4 + k];
-        sum += v[k];
-      }
-      int inc = sum;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int tt = __shfl_up(inc, o);
-        if (lane >= o) inc += tt;
-      }
-      int run = inc - sum;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        cls_base[wave][lane * 4 + k] = run;
-        run += v[k];
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-      for (int ib = 0; ib < cnt; ib += 64) {
-        const int i = ib + lane;
-        const bool valid = i < cnt;
-        const int c = valid ? cls(i) : 0;
-        uint64_t peers = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-          const int bit = (c >> b) & 1;
-          const uint64_t m = __ballot(bit);
-          peers &= bit ? m : ~m;
-        }
-        asm volatile("" ::: "memory");
-        const int base = valid ? cls_base[wave][c] : 0;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (valid) run_order[1 + start + base + __popcll(peers & lt)] = start + i;
-        if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      }
-    }
-  }
+  // ---- run order, otherwise: none ------------------------------------------
+  // A header of 0 matches no launch, so the einsum takes its groups in plan
+  // order (consecutive runs on each XCD).  Measured on a banded lhs, that
+  // beats both the same order read through the table and each share sorted
+  // longest first.
+  if (fits && group > 0 && run_order && !snake && blk == 0 && tid == 0) run_order[0] = 0;
 
   // ---- publish: the last block to finish writes the counts ----------------
   const int blk_bad = __syncthreads_or(bad);

@@ -335,8 +335,13 @@ int ej_pair_plan_async_noalloc(const int32_t *lhs_coords, int64_t n_lhs, int32_t
  * to the einsum), segment u = (run u / NK, k = u % NK) holding the run's
  * tiles in lhs order (the reference's accumulation order),
  * seg_offsets[0 .. U], out_coords [U, n_out] (ascending, as the reference
- * sorts them) and, given run_order and group, a run order as
- * ej_pair_plan_async does.  Structure that does not match gives
+ * sorts them) and, given run_order and group, a run order in the layout of
+ * ej_pair_plan_async's: when NK is a multiple of group and the einsum's
+ * eight equal shares of consecutive groups would leave one share's pair
+ * total more than 5% above the mean, the runs ranked longest first and
+ * dealt to the XCDs in snake order (0-7, 7-0, ...), each run's groups kept
+ * together; otherwise a header of 0, which the einsum ignores (groups in
+ * plan order).  Structure that does not match gives
  * EJ_E_UNSUPPORTED (take the general plan).  Properties that fail on the
  * device (rhs not the full grid in order, lhs not increasing or outside its
  * grid, more than 8192 runs, U > seg_capacity) give counts[1] = 1 and a
