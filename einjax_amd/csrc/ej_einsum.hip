@@ -698,6 +698,24 @@ __device__ inline void wait_stage(int later) {
   wait_vmcnt<0>();
 }
 
+// The same when the stages issued after the one about to be consumed may
+// number up to NS - 1 (the next stage is issued before the wait).
+template <int NS, int LPS>
+__device__ inline void wait_stage_in(int later) {
+  static_assert(NS >= 2 && NS <= 5, "ring depth");
+  if constexpr (NS >= 5) {
+    if (later >= 4) { wait_vmcnt<4 * LPS>(); return; }
+  }
+  if constexpr (NS >= 4) {
+    if (later >= 3) { wait_vmcnt<3 * LPS>(); return; }
+  }
+  if constexpr (NS >= 3) {
+    if (later >= 2) { wait_vmcnt<2 * LPS>(); return; }
+  }
+  if (later >= 1) { wait_vmcnt<LPS>(); return; }
+  wait_vmcnt<0>();
+}
+
 // XOR swizzles of 16-byte chunks (see the kernel comment).
 template <int CHA>
 __device__ inline int swz_a(int row) {
@@ -905,54 +923,94 @@ __device__ inline int32_t lane_value(int32_t v, int lane) {
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-// bf16 operands, lhs [m][k] and rhs [k][n] tiles, v_mfma_f32_16x16x32_bf16.
-// LDS: lhs chunk [BM][32] (64-byte rows, 16-byte chunk c of row r at
-// c ^ ((r >> 2) & 3)), rhs chunk [32][BN] as tile_gemm_dma_kernel lays it
-// out (read with ds_read_b64_tr_b16).
-template <int BM_, int BN_>
+// bf16 operands, v_mfma_f32_16x16x32_bf16, in either layout per operand.
+// The MFMA takes, per lane l, 8 consecutive k of row m = l % 16 (lhs) or of
+// column n = l % 16 (rhs).  An operand whose contraction dimension is
+// contiguous in its tile ("k-rows": lhs [m][k], or rhs [n][k] when AT / BT
+// say so) is staged as [rows][32] (64-byte rows, 16-byte chunk c of row r at
+// c ^ ((r >> 2) & 3)) and read with one 16-byte LDS read per fragment.  An
+// operand whose free dimension is contiguous ("k-major": rhs [k][n], or lhs
+// [k][m]) is staged as [32][cols] as tile_gemm_dma_kernel lays it out and
+// read with two ds_read_b64_tr_b16 per fragment, which transpose 16-bit
+// elements across the lanes of a group.  The forward 'ij,jk->ik' uses
+// k-rows lhs and k-major rhs (AT = BT = false); the backward's 'ik,jk->ij'
+// reads its rhs as k-rows (BT) and 'ij,ik->jk' its lhs as k-major (AT).
+template <int BM_, int BN_, bool AT_ = false, bool BT_ = false>
 struct SegOpBf16 {
   using elem = uint16_t;
-  static constexpr bool kBf16 = true;
+  static constexpr bool kBf16 = true, AT = AT_, BT = BT_;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
-  static constexpr int A_ROWB = BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
-  static constexpr int B_ROWB = BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
-  static_assert(CHA == 4 && (CHB == 8 || CHB == 16), "row widths");
+  static constexpr int A_ROWB = AT ? BM * 2 : BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * BK * 2;
+  static constexpr int B_ROWB = BT ? BK * 2 : BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * BN * 2;
+  static_assert((AT ? (CHA == 8 || CHA == 16) : CHA == 4) &&
+                    (BT ? CHB == 4 : (CHB == 8 || CHB == 16)),
+                "row widths");
 
   // Element offset (inside a stage) of the 16 bytes that `lane` copies into
-  // LDS block `blk` (1 KB) of the lhs / rhs chunk.
+  // LDS block `blk` (1 KB) of a k-rows chunk (rows of 64 bytes; `stride` =
+  // the tile's row stride) or of a k-major chunk with CH 16-byte chunks per
+  // k-row (`stride` = the tile's k stride).
+  __device__ static uint32_t krows_src(int blk, int lane, int64_t stride) {
+    const int row = blk * 16 + lane / 4;
+    const int c = (lane % 4) ^ swz_a<4>(row);
+    return static_cast<uint32_t>(row * stride + c * 8);
+  }
+  template <int CH>
+  __device__ static uint32_t kmajor_src(int blk, int lane, int64_t stride) {
+    const int krow = blk * (64 / CH) + lane / CH;
+    const int j = (lane % CH) ^ swz_b<CH>(krow);
+    return static_cast<uint32_t>(krow * stride + j * 8);
+  }
   __device__ static uint32_t a_src(int blk, int lane, const GemmGeom &g) {
-    const int row = blk * (1024 / A_ROWB) + lane / CHA;
-    const int c = (lane % CHA) ^ swz_a<CHA>(row);
-    return static_cast<uint32_t>(row * g.a_sm + c * 8);
+    if constexpr (AT) return kmajor_src<CHA>(blk, lane, g.a_sk);
+    else return krows_src(blk, lane, g.a_sm);
   }
   __device__ static uint32_t b_src(int blk, int lane, const GemmGeom &g) {
-    const int krow = blk * (64 / CHB) + lane / CHB;
-    const int j = (lane % CHB) ^ swz_b<CHB>(krow);
-    return static_cast<uint32_t>(krow * g.b_sk + j * 8);
+    if constexpr (BT) return krows_src(blk, lane, g.b_sn);
+    else return kmajor_src<CHB>(blk, lane, g.b_sk);
   }
 
-  // Per-lane LDS read offsets of one wave (bytes inside a slot; rd[0] for
-  // the lhs, rd[1 + j] for rhs fragment j).  The lhs swizzle depends on the
-  // lane only, so fragment i sits a constant away from fragment 0.  Of the
-  // two rhs transpose reads of a fragment (k rows t and 4 + t of the lane
-  // group's 8) the second has the same swizzle, 4 rows further: an
-  // immediate offset.  The MFMA loop is seg_gemm_kernel's.
+  // Per-lane LDS read offsets (bytes inside a slot).  A k-rows operand needs
+  // one: its swizzle depends on the row inside 16 only, so fragment f sits
+  // f * 16 rows further.  A k-major operand needs one per fragment (the
+  // swizzle moves 16-byte chunks); of its two transpose reads (k rows t and
+  // 4 + t of the lane group's 8) the second has the same swizzle, 4 rows
+  // further: an immediate offset.  Order: lhs offsets, then rhs offsets.
+  template <int FM>
+  static constexpr int n_ra = AT ? FM : 1;
   template <int FN>
-  static constexpr int n_rd = 1 + FN;
+  static constexpr int n_rb = BT ? 1 : FN;
+  template <int FM, int FN>
+  static constexpr int n_rd = n_ra<FM> + n_rb<FN>;
+
+  __device__ static uint32_t krows_rd(int row0, int rowb, int lane) {
+    return static_cast<uint32_t>((row0 + (lane & 15)) * rowb +
+                                 (((lane >> 4) ^ swz_a<4>(lane & 15)) * 16));
+  }
+  template <int CH>
+  __device__ static uint32_t kmajor_rd(int col0, int rowb, int lane) {
+    const int t = (lane & 15) >> 2, qq = lane & 3;
+    const int jc = (col0 >> 3) + (qq >> 1);
+    const int krow = (lane >> 4) * 8 + t;
+    const int phys = jc ^ swz_b<CH>(krow);
+    return static_cast<uint32_t>(krow * rowb + phys * 16 + (qq & 1) * 8);
+  }
 
   template <int FM, int FN>
-  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FN>], int row0, int wcol,
+  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FM, FN>], int row0, int wcol,
                                       uint32_t b_region, int lane) {
-    rd[0] = static_cast<uint32_t>((row0 + (lane & 15)) * A_ROWB +
-                                  (((lane >> 4) ^ swz_a<CHA>(lane & 15)) * 16));
+    if constexpr (AT) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n0 = wcol + j * 16;
-      const int t = (lane & 15) >> 2, qq = lane & 3;
-      const int jc = (n0 >> 3) + (qq >> 1);
-      const int krow = (lane >> 4) * 8 + t;
-      const int phys = jc ^ swz_b<CHB>(krow);
-      rd[1 + j] = b_region + static_cast<uint32_t>(krow * B_ROWB + phys * 16 + (qq & 1) * 8);
+      for (int i = 0; i < FM; ++i) rd[i] = kmajor_rd<CHA>(row0 + i * 16, A_ROWB, lane);
+    } else {
+      rd[0] = krows_rd(row0, A_ROWB, lane);
+    }
+    constexpr int o = n_ra<FM>;
+    if constexpr (BT) {
+      rd[o] = b_region + krows_rd(wcol, B_ROWB, lane);
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) rd[o + j] = b_region + kmajor_rd<CHB>(wcol + j * 16, B_ROWB, lane);
     }
   }
 };
@@ -971,7 +1029,7 @@ struct SegOpBf16 {
 template <int BM_, int BN_>
 struct SegOpF32 {
   using elem = float;
-  static constexpr bool kBf16 = false;
+  static constexpr bool kBf16 = false, AT = false, BT = false;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int A_ROWB = BK * 4, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
   static constexpr int B_ROWB = BN * 4, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
@@ -994,11 +1052,11 @@ struct SegOpF32 {
   // Per-lane LDS read offsets (rd[h], h = 0, 1: lhs chunk 4h + g of row
   // row0 + (lane & 15); rd[2 + j]: column wcol + 16j + (lane & 15) of k-row
   // 4g).  The MFMA loop is seg_gemm_kernel's.
-  template <int FN>
+  template <int FM, int FN>
   static constexpr int n_rd = 2 + FN;
 
   template <int FM, int FN>
-  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FN>], int row0, int wcol,
+  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FM, FN>], int row0, int wcol,
                                       uint32_t b_region, int lane) {
     const int row = row0 + (lane & 15), g = lane >> 4;
 #pragma unroll
@@ -1014,8 +1072,18 @@ struct SegOpF32 {
   }
 };
 
+// Workgroups per CU the register allocation of a segment GEMM leaves room
+// for: two in general; four for the one-segment bf16 kernel with a k-rows rhs
+// (the lhs gradient of the backward, one long workgroup per lhs tile, all
+// of which should be resident at once), which fits 128 VGPRs without spills
+// when it runs one segment per workgroup.
+template <class Op, int G, bool MULTI>
+constexpr int seg_min_blocks() {
+  return Op::kBf16 && G == 1 && Op::BT && !Op::AT && !MULTI ? 4 : 2;
+}
+
 template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
-__global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
+__global__ __launch_bounds__(NW * 64, (seg_min_blocks<Op, G, MULTI>())) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
                                                            const typename Op::elem *__restrict__ B,
                                                            void *__restrict__ C, PairSrc src,
                                                            GemmGeom g, int64_t n_seg, int spw,
@@ -1032,7 +1100,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
   constexpr int LPA = A_BYTES / (1024 * NW), LPB = B_BYTES / (1024 * NW);  // 1 KB loads per wave
   static_assert(LPA * 1024 * NW == A_BYTES && LPB * 1024 * NW == B_BYTES, "chunks split over waves");
   constexpr int LPS = LPA + G * LPB;
-  static_assert(NS >= 2 && NS <= 6 && (NS - 2) * LPS < 64, "ring depth / vmcnt range");
+  static_assert(NS >= 2 && NS <= 5 && (NS - 1) * LPS < 64, "ring depth / vmcnt range");
   static_assert(G == 1 || G == 2 || G == 4, "group size");
   // Segments one workgroup covers: a group of G, or (G == 1) up to SMAX
   // consecutive segments computed one after another.
@@ -1073,13 +1141,13 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
   const int64_t bi = lb % g.batch;
   int64_t grp = lb / g.batch;
   if (grp * segs >= nseg) return;
-  // A run order (heaviest groups first on each XCD) replaces the block's
-  // group.  Its header, run_order[0], is the number of live groups it
+  // A run order (for instance heaviest groups first on each XCD) replaces
+  // the block's group (its n-, m- and batch blocks stay together).  Its header, run_order[0], is the number of live groups it
   // permutes (the launcher passes only an order made for groups of G): only
   // an order made for exactly ceil(nseg / G) live groups is followed, by
   // every block alike, so each live group runs once; any other order is
   // ignored as a whole.
-  if (G > 1 && !MULTI && src.run_order && g.nblocks == 1 && g.mblocks == 1 && g.batch == 1) {
+  if (!MULTI && src.run_order) {
     const int64_t ngroups = (nseg + segs - 1) / segs;
     if (ld_uniform(src.run_order, 0) == ngroups) {
       const int64_t o = ld_uniform(src.run_order, grp + 1);
@@ -1186,7 +1254,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
   for (int v = 0; v < LPA; ++v) a_src[v] = Op::a_src(v * NW + wave, lane, g);
 #pragma unroll
   for (int v = 0; v < LPB; ++v) b_src[v] = Op::b_src(v * NW + wave, lane, g);
-  const int64_t b_off0 = bi * g.b_sb + nb * BN;
+  const int64_t b_off0 = bi * g.b_sb + nb * BN * g.b_sn;
 
   // Issue cursor: m-block imb, pair ipos, K-chunk ikc.
   int64_t imb = mb0, ipos = 0;
@@ -1213,7 +1281,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
     }
     const int64_t a_tile = at < 0 ? 0 : at;
     unsigned char *slot = ring + (st % NS) * SLOT;
-    const T *ab = A + a_tile * g.a_elems + bi * g.a_sb + imb * BM * g.a_sm + ikc * BK;
+    const T *ab = A + a_tile * g.a_elems + bi * g.a_sb + imb * BM * g.a_sm + ikc * BK * g.a_sk;
 #pragma unroll
     for (int v = 0; v < LPA; ++v)
       __builtin_amdgcn_global_load_lds(ab + a_src[v], EJ_LDS(slot + (v * NW + wave) * 1024), 16,
@@ -1271,19 +1339,26 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
   for (int s0 = 0; s0 < NS - 1; ++s0)
     if (s0 < stages) issue(s0);
 
-  uint32_t rd[Op::template n_rd<FN>];
+  uint32_t rd[Op::template n_rd<FM, FN>];
   Op::template read_offsets<FM, FN>(rd, wm * WM, wcol,
                                     static_cast<uint32_t>(A_BYTES + wseg * B_BYTES), lane);
   int64_t cmb = mb0;      // compute cursor's m-block
   int64_t cleft = per_mb;  // stages left in it
   for (int64_t st = 0; st < stages; ++st) {
-    const int64_t later = stages - 1 - st < NS - 2 ? stages - 1 - st : NS - 2;
     const int slot = static_cast<int>(st % NS);
-    wait_stage<NS, LPS>(static_cast<int>(later));
+    // The next stage goes into the slot of stage st - 1 as soon as every
+    // wave is done with it, before this stage's data is waited for, so NS - 1
+    // stages are in flight while the waves wait and NS - 2 while they compute.
+    if (st > 0) {
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+    if (st + NS - 1 < stages) issue(st + NS - 1);
+    const int64_t later = stages - 1 - st < NS - 1 ? stages - 1 - st : NS - 1;
+    wait_stage_in<NS, LPS>(static_cast<int>(later));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const uint32_t code = static_cast<uint32_t>(codes >> (slot * 8)) & 0xFFu;
-    if (st + NS - 1 < stages) issue(st + NS - 1);
     // Whether this wave takes part: every wave for a shared stage or (one
     // segment per wave column group) any valid stage of a lone segment;
     // with G > 1, only the waves of the stage's segment.  Wave-uniform.
@@ -1297,25 +1372,43 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
       typedef const __attribute__((address_space(3))) unsigned char *lds_ptr;
       if constexpr (Op::kBf16) {
         constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
-        bf16x8_t af[FM];
-        i32x4_t bq[FN];
+        constexpr int RA = Op::template n_ra<FM>;
+        i32x4_t aq[FM], bq[FN];
+        if constexpr (Op::AT) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[i] = *reinterpret_cast<const bf16x8_t *>((lds_ptr)(size_t)(base + rd[0]) +
-                                                     i * 16 * A_ROWB);
+          for (int i = 0; i < FM; ++i) {
+            const i32x2_t h0 = ds_read_tr16_b64(base + rd[i]);
+            const i32x2_t h1 = ds_read_tr16_b64_at<4 * A_ROWB>(base + rd[i]);
+            aq[i] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
+          }
+        } else {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const i32x2_t h0 = ds_read_tr16_b64(base + rd[1 + j]);
-          const i32x2_t h1 = ds_read_tr16_b64_at<4 * B_ROWB>(base + rd[1 + j]);
-          bq[j] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
+          for (int i = 0; i < FM; ++i)
+            aq[i] = *reinterpret_cast<const i32x4_t *>((lds_ptr)(size_t)(base + rd[0]) +
+                                                      i * 16 * A_ROWB);
         }
-        lgkm_wait_all<FN>(bq);
+        if constexpr (Op::BT) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            bq[j] = *reinterpret_cast<const i32x4_t *>((lds_ptr)(size_t)(base + rd[RA]) +
+                                                      j * 16 * B_ROWB);
+        } else {
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const i32x2_t h0 = ds_read_tr16_b64(base + rd[RA + j]);
+            const i32x2_t h1 = ds_read_tr16_b64_at<4 * B_ROWB>(base + rd[RA + j]);
+            bq[j] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
+          }
+        }
+        if constexpr (Op::AT) lgkm_wait_all<FM>(aq);
+        if constexpr (!Op::BT) lgkm_wait_all<FN>(bq);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                af[i], __builtin_bit_cast(bf16x8_t, bq[j]), acc[i][j], 0, 0, 0);
+                __builtin_bit_cast(bf16x8_t, aq[i]), __builtin_bit_cast(bf16x8_t, bq[j]),
+                acc[i][j], 0, 0, 0);
       } else {
         constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
 #pragma unroll
@@ -1531,6 +1624,28 @@ constexpr int seg_ring_depth(int slot_bytes, int want) {
 constexpr int64_t kSegMinBlocks = 1024;
 constexpr int kSegMaxRun = 8;  // segments per workgroup when G == 1 (SMAX)
 
+// Work split of a segment GEMM launch: whether each workgroup loops over the
+// m-blocks (mb_loop), how many consecutive segments it runs when G == 1
+// (spw), and the workgroups per group.
+struct SegSplit {
+  int mb_loop, spw;
+  int64_t per_group;
+  bool multi() const { return mb_loop || spw > 1; }
+};
+SegSplit seg_split(int G, int64_t n_seg, int64_t batch, int64_t nblocks, int64_t mblocks,
+                   bool has_offsets) {
+  SegSplit r;
+  const int64_t groups = ceil_div(n_seg, G);
+  r.per_group = batch * nblocks;  // workgroups per group, m-blocks looped inside
+  r.mb_loop = mblocks > 1 && groups * r.per_group >= kSegMinBlocks ? 1 : 0;
+  if (!r.mb_loop) r.per_group *= mblocks;
+  r.spw = 1;
+  if (G == 1 && has_offsets)
+    while (r.spw < kSegMaxRun && ceil_div(n_seg, 2 * r.spw) * r.per_group >= kSegMinBlocks)
+      r.spw *= 2;
+  return r;
+}
+
 template <class Op, int G, int WGM, int NW, int NSW = EJ_SEG_NS>
 int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src_in,
                       const GemmGeom &g, int64_t n_seg, hipStream_t stream) {
@@ -1538,12 +1653,9 @@ int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src_
   PairSrc src = src_in;
   if (src.order_group != G) src.run_order = nullptr;  // an order for other groups
   const int64_t groups = ceil_div(n_seg, G);
-  int64_t per_group = g.batch * g.nblocks;  // workgroups per group, m-blocks looped inside
-  const int mb_loop = g.mblocks > 1 && groups * per_group >= kSegMinBlocks ? 1 : 0;
-  if (!mb_loop) per_group *= g.mblocks;
-  int spw = 1;
-  if (G == 1 && src.seg_off)
-    while (spw < kSegMaxRun && ceil_div(n_seg, 2 * spw) * per_group >= kSegMinBlocks) spw *= 2;
+  const SegSplit sp = seg_split(G, n_seg, g.batch, g.nblocks, g.mblocks, src.seg_off != nullptr);
+  const int mb_loop = sp.mb_loop, spw = sp.spw;
+  const int64_t per_group = sp.per_group;
   const int64_t nblk = ceil_div(groups, spw) * per_group;
   if (nblk >= (int64_t(1) << 32)) {
     set_error("einsum launch too large");
@@ -1568,15 +1680,30 @@ int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src_
 // column) with a 3-stage ring (72 KB of LDS, so two workgroups share a CU and
 // one's prologue and epilogue overlap the other's stream), or one segment on
 // 4 waves (2 x 2); 64 x 64 tiles on 4 waves.
-int launch_seg_gemm_bf16(int bm, int grp, const void *A, const void *B, void *C,
-                         const PairSrc &src, const GemmGeom &g, int64_t n_seg,
-                         hipStream_t stream) {
+template <bool AT, bool BT>
+int launch_seg_gemm_bf16_l(int bm, int grp, const void *A, const void *B, void *C,
+                           const PairSrc &src, const GemmGeom &g, int64_t n_seg,
+                           hipStream_t stream) {
   if (bm == 128) {
-    if (grp == 4) return launch_seg_gemm_t<SegOpBf16<128, 128>, 2, 2, 4, 3>(A, B, C, src, g, n_seg, stream);
-    return launch_seg_gemm_t<SegOpBf16<128, 128>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
+    if (grp == 4)
+      return launch_seg_gemm_t<SegOpBf16<128, 128, AT, BT>, 2, 2, 4, 3>(A, B, C, src, g, n_seg, stream);
+    return launch_seg_gemm_t<SegOpBf16<128, 128, AT, BT>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
   }
-  if (grp == 4) return launch_seg_gemm_t<SegOpBf16<64, 64>, 4, 1, 4>(A, B, C, src, g, n_seg, stream);
-  return launch_seg_gemm_t<SegOpBf16<64, 64>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
+  if (grp == 4) return launch_seg_gemm_t<SegOpBf16<64, 64, AT, BT>, 4, 1, 4>(A, B, C, src, g, n_seg, stream);
+  return launch_seg_gemm_t<SegOpBf16<64, 64, AT, BT>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
+}
+
+// Operand layouts: a_rows = lhs k-contiguous ([m][k]), b_rows = rhs
+// k-contiguous ([n][k]).  Both operands free-dimension-contiguous is not
+// instantiated (no einsum of this path produces it).
+int launch_seg_gemm_bf16(int bm, int grp, bool a_rows, bool b_rows, const void *A, const void *B,
+                         void *C, const PairSrc &src, const GemmGeom &g, int64_t n_seg,
+                         hipStream_t stream) {
+  if (a_rows && !b_rows) return launch_seg_gemm_bf16_l<false, false>(bm, grp, A, B, C, src, g, n_seg, stream);
+  if (a_rows && b_rows) return launch_seg_gemm_bf16_l<false, true>(bm, grp, A, B, C, src, g, n_seg, stream);
+  if (!a_rows && !b_rows) return launch_seg_gemm_bf16_l<true, false>(bm, grp, A, B, C, src, g, n_seg, stream);
+  set_error("no bf16 segment GEMM for a [k][m] lhs with an [n][k] rhs");
+  return EJ_E_UNSUPPORTED;
 }
 
 // fp32 on 4 waves: a group of 4 puts one segment on each wave (WGM = 1);
@@ -1607,14 +1734,22 @@ int fused_group(const ej_einsum_desc *d, int32_t dtype) {
   if (!d->is_gemm || d->seg_group <= 0 || d->seg_group % 4 != 0) return 1;
   const int vec = dtype == EJ_BF16 ? 8 : 4;
   const int bm = pick_block(d->m), bn = pick_block(d->n);
-  if (!bm || !bn || d->a_sk != 1 || d->a_sm % vec != 0 || d->b_sn != 1 || d->b_sk % vec != 0 ||
-      d->k % 32 != 0)
-    return 1;
-  if (dtype == EJ_BF16) return bm == bn && bm == 128 ? 2 : bm == bn && bm == 64 ? 4 : 1;
+  if (!bm || !bn || d->k % 32 != 0) return 1;
+  if (dtype == EJ_BF16) {
+    const bool a_rows = d->a_sk == 1 && d->a_sm % vec == 0;
+    const bool a_cols = d->a_sm == 1 && d->a_sk % vec == 0;
+    const bool b_rows = d->b_sk == 1 && d->b_sn % vec == 0;
+    const bool b_cols = d->b_sn == 1 && d->b_sk % vec == 0;
+    if (!((a_rows && (b_rows || b_cols)) || (a_cols && b_cols))) return 1;
+    return bm == bn && bm == 128 ? 2 : bm == bn && bm == 64 ? 4 : 1;
+  }
+  if (d->a_sk != 1 || d->a_sm % vec != 0 || d->b_sn != 1 || d->b_sk % vec != 0) return 1;
   return (bm == 32 || bm == 64 || bm == 128) && d->n % 32 == 0 ? 4 : 1;
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+
 
 // Chooses the MFMA path when the einsum is GEMM-shaped with tile-friendly
 // extents and 16-byte aligned operand rows; returns false to fall back.
@@ -1650,18 +1785,20 @@ bool try_gemm(const ej_einsum_desc *d, int32_t dtype, const void *A, const void 
   g.out_bf16 = d->out_dtype == EJ_BF16;
   const int64_t nblk = n_seg * g.batch * g.mblocks * g.nblocks;
   if (nblk >= (int64_t(1) << 32)) return false;
-  // bf16, k-contiguous lhs, n-contiguous rhs: the LDS-ring kernels (direct
-  // HBM -> LDS loads, transpose reads for the rhs operand).  Segments the
-  // caller marks as sharing their lhs tiles in runs of 4 go four to a
-  // workgroup; otherwise one segment per workgroup with 64-deep K stages.
-  if (dtype == EJ_BF16 && ad && !bd && d->k % 32 == 0 && d->b_sn == 1 && d->b_sk % 8 == 0 &&
-      bm == bn && (bm == 128 || bm == 64) && src.n_a_tiles < (int64_t(1) << 31) &&
-      src.n_b_tiles < (int64_t(1) << 31)) {
+  // bf16 with at least one operand k-contiguous: the LDS-ring kernels
+  // (direct HBM -> LDS loads, transpose reads for a free-dimension-contiguous
+  // operand).  Segments the caller marks as sharing their lhs tiles in runs
+  // of 4 go several to a workgroup.  Otherwise a k-contiguous lhs with an
+  // n-contiguous rhs runs one segment per workgroup with 64-deep K stages
+  // (tile_gemm_dma_kernel), and the transposed layouts of the backward run
+  // one segment per workgroup on the ring.
+  if (dtype == EJ_BF16 && (ad || !bd) && d->k % 32 == 0 && bm == bn && (bm == 128 || bm == 64) &&
+      src.n_a_tiles < (int64_t(1) << 31) && src.n_b_tiles < (int64_t(1) << 31)) {
     const uint16_t *a = static_cast<const uint16_t *>(A);
     const uint16_t *b = static_cast<const uint16_t *>(B);
     const bool grouped = src.seg_off && d->seg_group > 0 && d->seg_group % 4 == 0;
-    if (grouped || d->k % 64 != 0) {
-      *status = launch_seg_gemm_bf16(bm, grouped ? 4 : 1, a, b, C, src, g, n_seg, stream);
+    if (grouped || d->k % 64 != 0 || !ad || bd) {
+      *status = launch_seg_gemm_bf16(bm, grouped ? 4 : 1, ad, bd, a, b, C, src, g, n_seg, stream);
       return true;
     }
     if (bm == 128)
@@ -1775,6 +1912,25 @@ int check_desc(const ej_einsum_desc *d) {
                  "GEMM descriptor addresses elements outside its tiles");
   }
   return EJ_OK;
+}
+
+// The group size of the LDS-ring launch try_gemm makes for this descriptor
+// when it follows a run order (one workgroup per group: no m-block loop, no
+// run of segments, one n-block, batch 1), else 0.
+int ring_order_group(const ej_einsum_desc *d, int32_t dtype, int64_t n_seg, const void *A,
+                     const void *B) {
+  if (!d->is_gemm || dtype != EJ_BF16 || d->k % 32 != 0 || d->batch != 1) return 0;
+  const int bm = pick_block(d->m), bn = pick_block(d->n);
+  if (!bm || bm != bn || (bm != 128 && bm != 64) || d->m != bm || d->n != bn) return 0;
+  const bool ad = d->a_sk == 1 && d->a_sm % 8 == 0, acol = d->a_sm == 1 && d->a_sk % 8 == 0;
+  const bool bd = d->b_sk == 1 && d->b_sn % 8 == 0, bcol = d->b_sn == 1 && d->b_sk % 8 == 0;
+  if (!(ad || acol) || !(bd || bcol) || (!ad && bd)) return 0;
+  if (d->a_elems % 8 || d->b_elems % 8 || !aligned16(A) || !aligned16(B)) return 0;
+  const bool grouped = d->seg_group > 0 && d->seg_group % 4 == 0;
+  // the one-segment-per-workgroup DMA kernel takes no order
+  if (!grouped && d->k % 64 == 0 && ad && !bd) return 0;
+  const int G = grouped ? (bm == 128 ? 2 : 4) : 1;
+  return seg_split(G, n_seg, 1, 1, 1, true).multi() ? 0 : G;
 }
 
 int einsum_common(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B,
@@ -1932,6 +2088,20 @@ extern "C" int ej_segment_einsum_async(const ej_einsum_desc *desc, int32_t dtype
               run_order_group};
   return einsum_common(desc, dtype, lhs_values, rhs_values, src, max_segments, out,
                        as_stream(stream));
+}
+
+int ej::segment_einsum_order_group(const ej_einsum_desc *d, int32_t dtype, int64_t n_seg,
+                                   const void *A, const void *B) {
+  return ring_order_group(d, dtype, n_seg, A, B);
+}
+
+int ej::segment_einsum_ordered(const ej_einsum_desc *d, int32_t dtype, const void *A,
+                               const void *B, int64_t n_a_tiles, int64_t n_b_tiles,
+                               const int64_t *lidx, const int64_t *ridx, const int32_t *perm,
+                               const int32_t *seg_off, int64_t n_seg, const int32_t *run_order,
+                               int32_t order_group, void *out, hipStream_t stream) {
+  PairSrc src{lidx, ridx, perm, seg_off, n_a_tiles, n_b_tiles, nullptr, run_order, order_group};
+  return einsum_common(d, dtype, A, B, src, n_seg, out, stream);
 }
 
 extern "C" int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype,

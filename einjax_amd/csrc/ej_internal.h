@@ -103,6 +103,18 @@ struct SortTiling {
 };
 SortTiling sort_tiling(int64_t n);
 
+// The fused segment einsum (ej_einsum.hip) with a run order: segments per
+// group of the launch that follows an order for this descriptor and segment
+// count (0: the launch follows none), and the einsum itself given the order
+// (run_order[0] = live groups, run_order[1 + b] = the group block b runs).
+int segment_einsum_order_group(const ej_einsum_desc *d, int32_t dtype, int64_t n_seg,
+                               const void *A, const void *B);
+int segment_einsum_ordered(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B,
+                           int64_t n_a_tiles, int64_t n_b_tiles, const int64_t *lidx,
+                           const int64_t *ridx, const int32_t *perm, const int32_t *seg_off,
+                           int64_t n_seg, const int32_t *run_order, int32_t order_group,
+                           void *out, hipStream_t stream);
+
 // Zeroes n bytes (a multiple of 4, 4-byte aligned) with a kernel rather than
 // hipMemsetAsync, which misbehaves when a caller records the call into a
 // HIP graph.

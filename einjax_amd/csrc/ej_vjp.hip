@@ -62,6 +62,35 @@ __global__ void zero_kernel(T *p, int64_t n) {
     p[i] = T(0);
 }
 
+// Run order of the lhs gradient's segments: keys[s] = the rhs tile of
+// segment s's first pair (n_rhs for a segment without pairs), vals[s] = s.
+// Sorted stably, segments that contract the same rhs tiles become
+// neighbours, which the fused einsum places on one XCD at the same time, so
+// each rhs tile is fetched into that XCD's L2 once for all of them.
+__global__ __launch_bounds__(256) void seg_first_rhs_kernel(const int64_t *__restrict__ ridx,
+                                                            const int32_t *__restrict__ perm,
+                                                            const int32_t *__restrict__ off,
+                                                            int64_t n_seg, int64_t n_rhs,
+                                                            uint64_t *__restrict__ keys,
+                                                            int32_t *__restrict__ vals) {
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (s >= n_seg) return;
+  uint64_t k = static_cast<uint64_t>(n_rhs);
+  if (off[s] < off[s + 1]) {
+    const int64_t r = ridx[perm[off[s]]];
+    if (r >= 0 && r < n_rhs) k = static_cast<uint64_t>(r);
+  }
+  keys[s] = k;
+  vals[s] = static_cast<int32_t>(s);
+}
+
+__global__ __launch_bounds__(256) void write_order_kernel(const int32_t *__restrict__ vals,
+                                                          int64_t n, int32_t *__restrict__ order) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b == 0) order[0] = static_cast<int32_t>(n);
+  if (b < n) order[1 + b] = vals[b];
+}
+
 unsigned grid_capped(int64_t n) {
   const int64_t g = ceil_div(n > 0 ? n : 1, kBlock);
   return static_cast<unsigned>(g < 4096 ? g : 4096);
@@ -131,6 +160,10 @@ struct VjpWs {
   int32_t *perm_l, *off_l, *perm_r, *off_r;
   float *lhs32, *rhs32;
   PlanWs plan;
+  // run order of the lhs gradient's segments and its sort
+  int32_t *order, *ovals, *ovals_alt;
+  uint64_t *okeys, *okeys_alt;
+  void *osort_ws;
   size_t bytes;
 };
 
@@ -148,8 +181,33 @@ VjpWs carve_vjp(void *base, int64_t n_pairs, int64_t n_lhs, int64_t n_rhs, int64
     w.rhs32 = c.take<float>(n_rhs * rhs_elems);
   }
   w.plan = carve_plan(c, n_pairs);
+  w.order = c.take<int32_t>(n_lhs + 1);
+  w.ovals = c.take<int32_t>(n_lhs);
+  w.ovals_alt = c.take<int32_t>(n_lhs);
+  w.okeys = c.take<uint64_t>(n_lhs);
+  w.okeys_alt = c.take<uint64_t>(n_lhs);
+  w.osort_ws = c.take<char>(static_cast<int64_t>(sort_workspace_bytes(n_lhs)));
   w.bytes = c.off;
   return w;
+}
+
+// Sorts the lhs gradient's segments by the rhs tile of their first pair into
+// w.order (the fused einsum's run order for groups of one segment).
+int lhs_grad_order(const int64_t *ridx, const int32_t *perm, const int32_t *off, int64_t n_seg,
+                   int64_t n_rhs, const VjpWs &w, hipStream_t stream) {
+  int bits = 1;
+  while (bits < 63 && (int64_t(1) << bits) < n_rhs + 1) ++bits;
+  const bool alt = radix_passes(bits) % 2 == 1;
+  hipLaunchKernelGGL(seg_first_rhs_kernel, dim3(grid_for(n_seg)), dim3(kBlock), 0, stream, ridx,
+                     perm, off, n_seg, n_rhs, alt ? w.okeys_alt : w.okeys,
+                     alt ? w.ovals_alt : w.ovals);
+  EJ_LAUNCH_CHECK();
+  EJ_TRY(sort_pairs_u64(w.okeys, w.ovals, w.okeys_alt, w.ovals_alt, n_seg, bits, w.osort_ws,
+                        stream, alt));
+  hipLaunchKernelGGL(write_order_kernel, dim3(grid_for(n_seg)), dim3(kBlock), 0, stream, w.ovals,
+                     n_seg, w.order);
+  EJ_LAUNCH_CHECK();
+  return EJ_OK;
 }
 
 }  // namespace
@@ -243,6 +301,14 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
   }
   if (!grad_lhs && !grad_rhs) return EJ_OK;
   dl.out_dtype = dr.out_dtype = grad_dtype;
+  // The rhs gradient's segments are rhs tiles in index order.  Rhs tiles
+  // with equal join key pair with the same lhs tiles in the same order, and
+  // tiles sorted by coordinates keep equal keys adjacent when the key
+  // dimensions lead (every join of a matmul-shaped einsum): mark the segments
+  // as sharing their lhs tiles, so the fused kernel runs them grouped.  The
+  // kernel checks the property on each group's pairs and runs a group
+  // without it pair by pair, with the same results.
+  dr.seg_group = 4;
   VjpWs w = carve_vjp(workspace, n_pairs, n_lhs_tiles, n_rhs_tiles, lhs_elems, rhs_elems, dtype,
                       grad_dtype);
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
@@ -288,8 +354,17 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
       EJ_TRY(zero(grad_lhs, n_lhs_tiles * lhs_elems));
     } else {
       EJ_TRY(index_plan(lhs_idx, n_pairs, n_lhs_tiles, w.perm_l, w.off_l, w.plan, stream));
-      EJ_TRY(ej_segment_einsum(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
-                               rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, grad_lhs, stream_));
+      // One lhs tile per workgroup on the LDS ring: run the tiles that
+      // contract the same rhs tiles side by side (see seg_first_rhs_kernel).
+      const int og = segment_einsum_order_group(&dl, edt, n_lhs_tiles, grad_out, rhs_v);
+      const int32_t *order = nullptr;
+      if (og == 1) {
+        EJ_TRY(lhs_grad_order(rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, n_rhs_tiles, w, stream));
+        order = w.order;
+      }
+      EJ_TRY(segment_einsum_ordered(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
+                                    rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, order, 1,
+                                    grad_lhs, stream));
     }
   }
   if (grad_rhs && n_rhs_tiles > 0) {

@@ -249,6 +249,9 @@ EINSUM_CASES = [
     ("ij,kj->ik", (64, 32), (64, 32)),
     ("ji,jk->ik", (64, 64), (64, 128)),
     ("ji,kj->ik", (32, 64), (32, 32)),
+    ("ji,jk->ik", (64, 64), (64, 64)),      # [k][m] lhs on the LDS ring
+    ("ji,jk->ik", (128, 128), (128, 128)),
+    ("ij,kj->ik", (128, 128), (128, 128)),  # [n][k] rhs on the LDS ring
     ("bij,bjk->bik", (1, 64, 64), (1, 64, 64)),
     ("bij,bjk->bik", (4, 32, 32), (4, 32, 64)),
     ("ijk,kl->ijl", (8, 16, 32), (32, 32)),
@@ -289,7 +292,7 @@ def test_pair_einsum(gpu, spec, lt, rt, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["fp32", "bf16"])
-@pytest.mark.parametrize("spec,lt,rt", EINSUM_CASES[:11])
+@pytest.mark.parametrize("spec,lt,rt", EINSUM_CASES[:14])
 def test_segment_einsum_matches_pairs_plus_segsum(gpu, spec, lt, rt, dtype):
     """Fused mode == per-pair results summed in plan order (within fp32
     rounding), on random segment structure with skewed segment lengths."""
@@ -419,9 +422,11 @@ def _matmul_rels(rng, tile, rows, inner, cols, lhs_density, rhs_density=1.0):
             R.Rel(bc, bv, (inner * tile, cols * tile), (tile, tile)))
 
 
-def _segment_einsum_groups(lhs, rhs, groups, li_override=None):
+def _segment_einsum_groups(lhs, rhs, groups, li_override=None, spec="ij,jk->ik"):
     """Runs the device join, plan and fused einsum with each seg_group hint;
-    returns the plan's output coordinates and {hint: values}."""
+    returns the plan's output coordinates and {hint: values}.  spec
+    "ji,jk->ik" hands in every lhs tile transposed, "ij,kj->ik" every rhs
+    tile (the same product, other operand layouts)."""
     from einjax_amd import _device
 
     L, Rr = dev_rel(lhs, "bf16"), dev_rel(rhs, "bf16")
@@ -430,11 +435,16 @@ def _segment_einsum_groups(lhs, rhs, groups, li_override=None):
                                                   [sd._grid(L, 0), sd._grid(Rr, 1)])
     if li_override is not None:
         li = li_override(li)
-    desc = _device.describe("ij,jk->ik", lhs.tile_shape, rhs.tile_shape)
+    lvals, rvals = L.values, Rr.values
+    if spec == "ji,jk->ik":
+        lvals = lvals.transpose(1, 2).contiguous()
+    elif spec == "ij,kj->ik":
+        rvals = rvals.transpose(1, 2).contiguous()
+    desc = _device.describe(spec, lhs.tile_shape, rhs.tile_shape)
     out = {}
     for gsz in groups:
         desc.seg_group = gsz
-        out[gsz] = hv(_device.segment_einsum(desc, L.values, Rr.values, li, ri, perm, offs))
+        out[gsz] = hv(_device.segment_einsum(desc, lvals, rvals, li, ri, perm, offs))
     return coords.cpu().numpy(), out
 
 
@@ -454,6 +464,29 @@ def test_grouped_segment_einsum(gpu, tile, rows, inner, cols, dens):
     # same accumulation order per output tile: bitwise equal to one segment per workgroup
     npt.assert_array_equal(out[cols], out[0])
     assert R.rel_l2(out[cols], want.values) <= TOL["bf16"]
+
+
+@pytest.mark.parametrize("spec", ["ji,jk->ik", "ij,kj->ik"])
+@pytest.mark.parametrize("tile,rows,inner,cols,dens", [
+    (128, 6, 5, 8, 0.5),
+    (64, 5, 7, 12, 0.4),
+    (64, 2, 70, 4, 1.0),
+])
+def test_grouped_segment_einsum_layouts(gpu, spec, tile, rows, inner, cols, dens):
+    """The LDS-ring einsum with a transposed operand (a [k][m] lhs or an
+    [n][k] rhs tile, the layouts of the backward's gradient einsums), one
+    segment per workgroup and grouped: the standard-layout product."""
+    note("grouped segment einsum, layout", spec, tile, rows, inner, cols, dens)
+    rng = np.random.default_rng(tile + rows + inner + 1)
+    lhs, rhs = _matmul_rels(rng, tile, rows, inner, cols, dens)
+    coords, out = _segment_einsum_groups(lhs, rhs, (0, cols), spec=spec)
+    want = R.execute_sparse(lhs, rhs, [(1, 0)], "ij,jk->ik", [(0, 0), (1, 1)], precision="fp64")
+    npt.assert_array_equal(coords, want.coords)
+    npt.assert_array_equal(out[cols], out[0])
+    assert R.rel_l2(out[0], want.values) <= TOL["bf16"]
+    # the standard layout gives the same sums (same fp32 order), bit for bit
+    _, std = _segment_einsum_groups(lhs, rhs, (0,))
+    npt.assert_array_equal(out[0], std[0])
 
 
 @pytest.mark.parametrize("cols,rhs_dens", [(6, 1.0), (8, 0.6), (5, 1.0)])
