@@ -358,7 +358,7 @@ def test_dense_plan_applies_mirrors_the_library():
 def test_segment_einsum_group():
     """The group size a run order is made for: two 128 x 128 bf16 output
     tiles per workgroup, four 64 x 64 bf16 or fp32 ones, 1 without the
-    seg_group hint or for shapes the grouped kernels do not take."""
+    seg_group hint or for shapes and layouts the grouped kernels do not take."""
     lib = _lib.load()
 
     def group(spec, lt, rt, dtype, hint=4):
@@ -373,7 +373,12 @@ def test_segment_einsum_group():
     assert group("ij,jk->ik", (64, 64), (64, 64), _lib.EJ_BF16) == 4
     assert group("ij,jk->ik", (64, 64), (64, 64), _lib.EJ_F32) == 4
     assert group("ij,jk->ik", (128, 128), (128, 128), _lib.EJ_BF16, hint=0) == 1
-    assert group("ij,kj->ik", (128, 128), (128, 128), _lib.EJ_BF16) == 1  # rhs k-contiguous
+    # bf16 operands in either layout run grouped on the LDS ring, except a
+    # [k][m] lhs with an [n][k] rhs; fp32 takes [m][k] x [k][n] only
+    assert group("ij,kj->ik", (128, 128), (128, 128), _lib.EJ_BF16) == 2  # rhs k-contiguous
+    assert group("ji,jk->ik", (64, 64), (64, 64), _lib.EJ_BF16) == 4     # lhs m-contiguous
+    assert group("ji,kj->ik", (128, 128), (128, 128), _lib.EJ_BF16) == 1
+    assert group("ij,kj->ik", (64, 64), (64, 64), _lib.EJ_F32) == 1
     st, d = describe("ij,jk->ik", (32, 32), (32, 32))
     g = ctypes.c_int32(-1)
     assert lib.ej_segment_einsum_group(ctypes.byref(d), 7, ctypes.byref(g)) == _lib.EJ_E_INVAL
