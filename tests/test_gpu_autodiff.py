@@ -40,7 +40,9 @@ def rel_from_dense(dense, tile):
 # ---------------------------------------------------------------------------
 # pair grouping
 
-@pytest.mark.parametrize("n,targets", [(1, 1), (1000, 7), (70000, 5000), (5, 0)])
+@pytest.mark.parametrize("n,targets", [(1, 1), (1000, 7), (70000, 5000), (5, 0),
+                                       (65536, 4094), (30000, 1), (0, 9), (65537, 10),
+                                       (200, 4095)])
 def test_index_plan_parity(gpu, n, targets):
     note("index_plan", n, targets)
     rng = np.random.default_rng(n)
