@@ -150,18 +150,25 @@ __global__ __launch_bounds__(kProbeThreads) void probe_scan_small_kernel(
 // are written outright, so nothing needs clearing first; the n_clear int64s
 // at `clear` and the n_clear2 at `clear2` (a later phase's counters) are
 // zeroed on the way.  One launch replaces the clear, pack, sort and probe
-// launches of the general path.
+// launches of the general path.  With join keys of at most 32 bits (PACK)
+// each LDS entry is (key << 32 | row) and the build side may have up to
+// kJoinSmallBuildPacked rows.
 constexpr int kJoinSmallThreads = 1024;
 constexpr int kJoinSmallBuild = 4096;
+constexpr int kJoinSmallBuildPacked = 8192;
 
+template <bool PACK>
 __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
     const int32_t *__restrict__ lc, int n_build, KeySpec lks, const int32_t *__restrict__ rc,
     int64_t n_probe, KeySpec rks, int bits, int32_t *__restrict__ lperm,
     int64_t *__restrict__ lo_out, int64_t *__restrict__ offs, int64_t *__restrict__ scalars,
     int64_t *__restrict__ clear, int n_clear, int64_t *__restrict__ clear2, int n_clear2) {
   constexpr int NW = kJoinSmallThreads / 64;
-  __shared__ uint64_t skey[2][kJoinSmallBuild];
-  __shared__ int32_t sidx[2][kJoinSmallBuild];
+  constexpr int NB = PACK ? kJoinSmallBuildPacked : kJoinSmallBuild;
+  constexpr int KS = PACK ? 32 : 0;  // key position inside an entry
+  // entries: PACK: (key << 32 | row); otherwise the key, its row in sidx
+  __shared__ uint64_t skey[2][NB];
+  __shared__ int32_t sidx[PACK ? 1 : 2][PACK ? 1 : NB];
   __shared__ int32_t wcnt[NW][256];
   __shared__ int32_t dbase[256];
   __shared__ int bad_any;
@@ -183,8 +190,13 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   for (int i = tid; i < n_clear2; i += kJoinSmallThreads) clear2[i] = 0;
   __syncthreads();
   for (int i = tid; i < n_build; i += kJoinSmallThreads) {
-    skey[0][i] = pack_key(lc + static_cast<int64_t>(i) * lks.ncols, lks, &bad);
-    sidx[0][i] = i;
+    const uint64_t k = pack_key(lc + static_cast<int64_t>(i) * lks.ncols, lks, &bad);
+    if constexpr (PACK) {
+      skey[0][i] = (k << 32) | static_cast<uint32_t>(i);
+    } else {
+      skey[0][i] = k;
+      sidx[0][i] = i;
+    }
   }
   if (bad) bad_any = 1;
   int cur = 0;
@@ -192,7 +204,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
     if (tid < 256) dbase[tid] = 0;
     __syncthreads();
     for (int i = tid; i < n_build; i += kJoinSmallThreads)
-      atomicAdd(&dbase[(skey[cur][i] >> shift) & 255], 1);
+      atomicAdd(&dbase[(skey[cur][i] >> (KS + shift)) & 255], 1);
     __syncthreads();
     if (wave == 0) {  // exclusive scan of the 256 digit counts, 4 per lane
       int v[4], sum = 0;
@@ -221,7 +233,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
       const int i = r0 + tid;
       const bool valid = i < n_build;
       const uint64_t k = valid ? skey[cur][i] : 0;
-      const int d = static_cast<int>((k >> shift) & 255);
+      const int d = static_cast<int>((k >> (KS + shift)) & 255);
       uint64_t peers = __ballot(valid);
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
@@ -245,7 +257,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
       if (valid) {
         const int pos = dbase[d] + wcnt[wave][d] + rank;
         skey[cur ^ 1][pos] = k;
-        sidx[cur ^ 1][pos] = sidx[cur][i];
+        if constexpr (!PACK) sidx[cur ^ 1][pos] = sidx[cur][i];
       }
       __syncthreads();
       if (tid < 256) dbase[tid] += total;
@@ -253,8 +265,10 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
     cur ^= 1;
   }
   __syncthreads();
-  for (int i = tid; i < n_build; i += kJoinSmallThreads) lperm[i] = sidx[cur][i];
+  for (int i = tid; i < n_build; i += kJoinSmallThreads)
+    lperm[i] = PACK ? static_cast<int32_t>(skey[cur][i] & 0xFFFFFFFFu) : sidx[cur][i];
   const uint64_t *bk = skey[cur];
+  auto bkey = [&](int i) -> uint64_t { return bk[i] >> KS; };
   // Equal ranges of the PPT probe keys, searched side by side (branch-free,
   // fixed trip count); the counts stay in registers for the scan.
   int lb[PPT], ub[PPT];
@@ -266,8 +280,8 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
 #pragma unroll
     for (int u = 0; u < PPT; ++u) {
       if (u < pc) {  // pc is the same for every thread
-        lb[u] += bk[lb[u] + half] < pk[u] ? half : 0;
-        ub[u] += bk[ub[u] + half] <= pk[u] ? half : 0;
+        lb[u] += bkey(lb[u] + half) < pk[u] ? half : 0;
+        ub[u] += bkey(ub[u] + half) <= pk[u] ? half : 0;
       }
     }
     len -= half;
@@ -275,8 +289,8 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   int64_t s = 0;
 #pragma unroll
   for (int u = 0; u < PPT; ++u) {
-    lb[u] += bk[lb[u]] < pk[u] ? 1 : 0;
-    ub[u] += bk[ub[u]] <= pk[u] ? 1 : 0;
+    lb[u] += bkey(lb[u]) < pk[u] ? 1 : 0;
+    ub[u] += bkey(ub[u]) <= pk[u] ? 1 : 0;
     if (plo + u < phi) {
       lo_out[plo + u] = lb[u];
       s += ub[u] - lb[u];
@@ -409,8 +423,11 @@ namespace {
 // only): n_clear2 more.
 constexpr int kClearScalars = 8;
 
-bool join_small_ok(int32_t order, int64_t n_lhs, int64_t n_rhs) {
-  return order == EJ_ORDER_PROBE && n_lhs <= kJoinSmallBuild && n_rhs <= kProbeSmallMax;
+// Whether the one-workgroup join count takes these sides (bits: the join
+// key's width; wider than 32 bits allows kJoinSmallBuild build rows).
+bool join_small_ok(int32_t order, int64_t n_lhs, int64_t n_rhs, int bits) {
+  const int64_t nb = bits <= 32 ? kJoinSmallBuildPacked : kJoinSmallBuild;
+  return order == EJ_ORDER_PROBE && n_lhs <= nb && n_rhs <= kProbeSmallMax;
 }
 
 int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
@@ -446,11 +463,17 @@ int join_count_enqueue(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nco
   EJ_CHECK_ARG(workspace && workspace_bytes >= w.bytes, "workspace too small: %zu < %zu bytes",
                workspace_bytes, w.bytes);
   *dev_scalars = w.scalars;
-  if (join_small_ok(order, n_lhs, n_rhs)) {
-    hipLaunchKernelGGL(join_probe_small_kernel, dim3(1), dim3(kJoinSmallThreads), 0, stream,
-                       lhs_coords, static_cast<int>(n_lhs), lks, rhs_coords, n_rhs, rks, bits,
-                       w.lperm, w.lo, w.offs, w.scalars, clear, clear ? kClearScalars : 0,
-                       clear2, clear2 ? n_clear2 : 0);
+  if (join_small_ok(order, n_lhs, n_rhs, bits)) {
+    if (bits <= 32)
+      hipLaunchKernelGGL(join_probe_small_kernel<true>, dim3(1), dim3(kJoinSmallThreads), 0,
+                         stream, lhs_coords, static_cast<int>(n_lhs), lks, rhs_coords, n_rhs, rks,
+                         bits, w.lperm, w.lo, w.offs, w.scalars, clear,
+                         clear ? kClearScalars : 0, clear2, clear2 ? n_clear2 : 0);
+    else
+      hipLaunchKernelGGL(join_probe_small_kernel<false>, dim3(1), dim3(kJoinSmallThreads), 0,
+                         stream, lhs_coords, static_cast<int>(n_lhs), lks, rhs_coords, n_rhs, rks,
+                         bits, w.lperm, w.lo, w.offs, w.scalars, clear,
+                         clear ? kClearScalars : 0, clear2, clear2 ? n_clear2 : 0);
     EJ_LAUNCH_CHECK();
     return EJ_OK;
   }
@@ -976,11 +999,18 @@ __global__ __launch_bounds__(kOnePassThreads) void plan_one_pass_kernel(
   }
 }
 
-// Stores a caller's ticket into coherent host memory, fenced at system scope.
-__global__ void store_ticket_kernel(int64_t *host_slot, int64_t ticket) {
+// Copies the plan's six counts into coherent host memory and then stores the
+// caller's ticket after them, fenced at system scope (one launch in place of
+// a copy and the ticket kernel).
+__global__ void publish_counts_kernel(const int64_t *__restrict__ scalars,
+                                      int64_t *__restrict__ host_counts, int64_t ticket) {
+  if (threadIdx.x < 6) host_counts[threadIdx.x] = scalars[threadIdx.x];
   __threadfence_system();
-  *host_slot = ticket;
-  __threadfence_system();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    host_counts[6] = ticket;
+    __threadfence_system();
+  }
 }
 
 __global__ void seg_flags_kernel(const uint64_t *skeys, int64_t n, const int64_t *n_dev,
@@ -1320,7 +1350,9 @@ int pair_plan_impl(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
   SegWs sw = carve_seg(seg_workspace, pair_capacity);
   EJ_CHECK_ARG(seg_workspace && seg_workspace_bytes >= sw.bytes,
                "segment workspace too small: %zu < %zu bytes", seg_workspace_bytes, sw.bytes);
-  const bool small_join = join_small_ok(EJ_ORDER_PROBE, n_lhs, n_rhs);
+  int jbits = 0;
+  EJ_TRY(key_bits(join_radices, n_keys, &jbits));
+  const bool small_join = join_small_ok(EJ_ORDER_PROBE, n_lhs, n_rhs, jbits);
   JoinWs jw = carve_join(join_workspace, n_lhs, n_rhs, EJ_ORDER_PROBE);
   EJ_CHECK_ARG(counts_direct >= 0, "negative counts_direct");
   int64_t *direct = nullptr;  // device address of counts when the kernels store them
@@ -1392,11 +1424,13 @@ int pair_plan_impl(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
                        sw.scalars, a, out_coords, seg_offsets, perm, nullptr);
     EJ_LAUNCH_CHECK();
   }
-  EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
-  if (direct) {  // the ticket after the copy, in stream order
-    hipLaunchKernelGGL(store_ticket_kernel, dim3(1), dim3(1), 0, stream, direct + 6,
+  if (direct) {  // counts and then the ticket, stored by the device
+    hipLaunchKernelGGL(publish_counts_kernel, dim3(1), dim3(64), 0, stream, sw.scalars, direct,
                        int64_t(counts_direct));
     EJ_LAUNCH_CHECK();
+  } else {
+    EJ_HIP(hipMemcpyAsync(counts, sw.scalars, 6 * sizeof(int64_t), hipMemcpyDeviceToHost,
+                          stream));
   }
   return EJ_OK;
 }
