@@ -16,6 +16,8 @@
 #include <mutex>
 #include "ej_internal.h"
 
+#include <type_traits>
+
 namespace ej {
 
 namespace {
@@ -169,8 +171,11 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   // entries: PACK: (key << 32 | row); otherwise the key, its row in sidx
   __shared__ uint64_t skey[2][NB];
   __shared__ int32_t sidx[PACK ? 1 : 2][PACK ? 1 : NB];
-  __shared__ int32_t wcnt[NW][256];
-  __shared__ int32_t dbase[256];
+  // digits: 9 bits with packed entries (fewer passes for 9-bit keys), else 8
+  constexpr int DB = PACK ? 9 : 8, NBIN = 1 << DB;
+  using cnt_t = typename std::conditional<PACK, uint16_t, int32_t>::type;
+  __shared__ cnt_t wcnt[NW][NBIN];  // per wave and digit: count, then prefix over waves
+  __shared__ int32_t dbase[NBIN];
   __shared__ int bad_any;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -200,17 +205,18 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
   }
   if (bad) bad_any = 1;
   int cur = 0;
-  for (int shift = 0; shift < bits; shift += 8) {
-    if (tid < 256) dbase[tid] = 0;
+  for (int shift = 0; shift < bits; shift += DB) {
+    for (int x = tid; x < NBIN; x += kJoinSmallThreads) dbase[x] = 0;
     __syncthreads();
     for (int i = tid; i < n_build; i += kJoinSmallThreads)
-      atomicAdd(&dbase[(skey[cur][i] >> (KS + shift)) & 255], 1);
+      atomicAdd(&dbase[(skey[cur][i] >> (KS + shift)) & (NBIN - 1)], 1);
     __syncthreads();
-    if (wave == 0) {  // exclusive scan of the 256 digit counts, 4 per lane
-      int v[4], sum = 0;
+    if (wave == 0) {  // exclusive scan of the digit counts, NBIN / 64 per lane
+      constexpr int PL = NBIN / 64;
+      int v[PL], sum = 0;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        v[u] = dbase[lane * 4 + u];
+      for (int u = 0; u < PL; ++u) {
+        v[u] = dbase[lane * PL + u];
         sum += v[u];
       }
       int inc = sum;
@@ -221,35 +227,35 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
       }
       int run = inc - sum;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        dbase[lane * 4 + u] = run;
+      for (int u = 0; u < PL; ++u) {
+        dbase[lane * PL + u] = run;
         run += v[u];
       }
     }
     // Stable scatter, kJoinSmallThreads keys per round in index order.
     for (int r0 = 0; r0 < n_build; r0 += kJoinSmallThreads) {
-      for (int x = tid; x < NW * 256; x += kJoinSmallThreads) (&wcnt[0][0])[x] = 0;
+      for (int x = tid; x < NW * NBIN; x += kJoinSmallThreads) (&wcnt[0][0])[x] = 0;
       __syncthreads();
       const int i = r0 + tid;
       const bool valid = i < n_build;
       const uint64_t k = valid ? skey[cur][i] : 0;
-      const int d = static_cast<int>((k >> (KS + shift)) & 255);
+      const int d = static_cast<int>((k >> (KS + shift)) & (NBIN - 1));
       uint64_t peers = __ballot(valid);
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
+      for (int b = 0; b < DB; ++b) {
         const int bit = (d >> b) & 1;
         const uint64_t m = __ballot(bit);
         peers &= bit ? m : ~m;
       }
       const int rank = __popcll(peers & lt_mask);
-      if (valid && rank == 0) wcnt[wave][d] = __popcll(peers);
+      if (valid && rank == 0) wcnt[wave][d] = static_cast<cnt_t>(__popcll(peers));
       __syncthreads();
       int total = 0;
-      if (tid < 256) {  // per digit: exclusive prefix over the waves, in place
+      if (tid < NBIN) {  // per digit: exclusive prefix over the waves, in place
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
           const int c = wcnt[w][tid];
-          wcnt[w][tid] = total;
+          wcnt[w][tid] = static_cast<cnt_t>(total);
           total += c;
         }
       }
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(kJoinSmallThreads) void join_probe_small_kernel(
         if constexpr (!PACK) sidx[cur ^ 1][pos] = sidx[cur][i];
       }
       __syncthreads();
-      if (tid < 256) dbase[tid] += total;
+      if (tid < NBIN) dbase[tid] += total;
     }
     cur ^= 1;
   }
