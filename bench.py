@@ -77,10 +77,11 @@ def event_time_ms(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
-def wall_time_ms(fn, reps: int) -> float:
+def wall_time_ms(fn, reps: int, warm: int = 1) -> float:
     import torch
 
-    fn()
+    for _ in range(warm):
+        fn()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):
@@ -363,7 +364,7 @@ def measure_ingest(cpu: bool = True) -> dict:
     return out
 
 
-def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 5) -> dict:
+def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 20) -> dict:
     """Backward of the headline's per-pair einsum (sparse_einsum_raw's
     gradient): both operand gradients for a cotangent of every pair in the
     forward output's dtype (bf16: bf16 gradient einsums, fp32 sums), each
@@ -385,7 +386,7 @@ def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 5) -
     }
     out = {}
     for k, fn in run.items():
-        t = wall_time_ms(fn, reps)
+        t = wall_time_ms(fn, reps, warm=5)
         flops = 2 * F if k.startswith("both") else F
         out[f"{k}_ms"] = t
         out[f"{k}_tflops"] = flops / (t * 1e-3) / 1e12

@@ -1072,18 +1072,8 @@ struct SegOpF32 {
   }
 };
 
-// Workgroups per CU the register allocation of a segment GEMM leaves room
-// for: two in general; four for the one-segment bf16 kernel with a k-rows rhs
-// (the lhs gradient of the backward, one long workgroup per lhs tile, all
-// of which should be resident at once), which fits 128 VGPRs without spills
-// when it runs one segment per workgroup.
-template <class Op, int G, bool MULTI>
-constexpr int seg_min_blocks() {
-  return Op::kBf16 && G == 1 && Op::BT && !Op::AT && !MULTI ? 4 : 2;
-}
-
 template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
-__global__ __launch_bounds__(NW * 64, (seg_min_blocks<Op, G, MULTI>())) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
+__global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
                                                            const typename Op::elem *__restrict__ B,
                                                            void *__restrict__ C, PairSrc src,
                                                            GemmGeom g, int64_t n_seg, int spw,
@@ -1679,7 +1669,10 @@ int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src_
 // bf16: 128 x 128 tiles, a group of 2 on 4 waves (2 x 2, one segment per wave
 // column) with a 3-stage ring (72 KB of LDS, so two workgroups share a CU and
 // one's prologue and epilogue overlap the other's stream), or one segment on
-// 4 waves (2 x 2); 64 x 64 tiles on 4 waves.
+// 4 waves (2 x 2); 64 x 64 tiles on 4 waves.  One segment with a k-rows rhs
+// (the lhs gradient of the backward: long segments whose lhs tiles are each
+// read once) gets a 4-stage ring: 48 KB in flight per workgroup, two
+// workgroups per CU.
 template <bool AT, bool BT>
 int launch_seg_gemm_bf16_l(int bm, int grp, const void *A, const void *B, void *C,
                            const PairSrc &src, const GemmGeom &g, int64_t n_seg,
@@ -1687,7 +1680,8 @@ int launch_seg_gemm_bf16_l(int bm, int grp, const void *A, const void *B, void *
   if (bm == 128) {
     if (grp == 4)
       return launch_seg_gemm_t<SegOpBf16<128, 128, AT, BT>, 2, 2, 4, 3>(A, B, C, src, g, n_seg, stream);
-    return launch_seg_gemm_t<SegOpBf16<128, 128, AT, BT>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);
+    return launch_seg_gemm_t<SegOpBf16<128, 128, AT, BT>, 1, 2, 4, BT && !AT ? 4 : EJ_SEG_NS>(
+        A, B, C, src, g, n_seg, stream);
   }
   if (grp == 4) return launch_seg_gemm_t<SegOpBf16<64, 64, AT, BT>, 4, 1, 4>(A, B, C, src, g, n_seg, stream);
   return launch_seg_gemm_t<SegOpBf16<64, 64, AT, BT>, 1, 2, 4>(A, B, C, src, g, n_seg, stream);

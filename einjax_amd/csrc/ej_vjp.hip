@@ -18,6 +18,7 @@
 #include <string.h>
 
 #include <string>
+#include <vector>
 
 namespace ej {
 namespace {
@@ -46,6 +47,131 @@ __global__ __launch_bounds__(256) void plan_offsets_kernel(const uint64_t *__res
     else hi = mid;
   }
   offsets[t] = static_cast<int32_t>(lo);
+}
+
+// ---- counting plan ---------------------------------------------------------
+// For target counts whose histogram fits LDS, the plan is a stable counting
+// sort in three launches (the radix sort takes two passes of a histogram and
+// a scatter for 13 bits, plus keys and offsets: six launches).  Bins are the
+// targets [0, n_targets) plus one bin for invalid indices, which sorts last.
+// Blocks take kPlanChunk consecutive pairs each.
+//   plan_count:   hist[b][t] = pairs of block b with bin t;
+//   plan_colscan: hist[b][t] <- pairs of blocks before b with bin t, and per
+//                 group of 256 bins the exclusive prefix of the bin totals
+//                 (tpref) and the group's total (tsum);
+//   plan_scatter: a pair's position is the bins before its own (the groups'
+//                 totals before its group plus tpref), the pairs of its bin
+//                 in earlier blocks, and its rank among the pairs of its bin
+//                 earlier in the block (wave ballots on the bin's bits, then
+//                 the waves of a round in order through an LDS count per bin).
+constexpr int kPlanChunk = 1024;
+constexpr int64_t kPlanMaxBins = 63 * 256;  // LDS counts within 64 KB with the carries
+constexpr int kPlanMaxGroups = 64;
+
+__device__ inline uint32_t plan_bin(const int64_t *idx, int64_t i, int64_t n_targets) {
+  const int64_t t = idx[i];
+  return t >= 0 && t < n_targets ? static_cast<uint32_t>(t) : static_cast<uint32_t>(n_targets);
+}
+
+__global__ __launch_bounds__(256) void plan_count_kernel(const int64_t *__restrict__ idx,
+                                                         int64_t n, int64_t n_targets,
+                                                         uint32_t *__restrict__ hist) {
+  extern __shared__ uint32_t cnt[];
+  const int64_t bins = n_targets + 1;
+  for (int64_t t = threadIdx.x; t < bins; t += 256) cnt[t] = 0;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kPlanChunk;
+  uint32_t bin[kPlanChunk / 256];
+#pragma unroll
+  for (int r = 0; r < kPlanChunk / 256; ++r) {
+    const int64_t i = base + r * 256 + threadIdx.x;
+    bin[r] = i < n ? plan_bin(idx, i, n_targets) : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kPlanChunk / 256; ++r)
+    if (bin[r] != 0xFFFFFFFFu) atomicAdd(&cnt[bin[r]], 1u);
+  __syncthreads();
+  uint32_t *h = hist + static_cast<int64_t>(blockIdx.x) * bins;
+  for (int64_t t = threadIdx.x; t < bins; t += 256) h[t] = cnt[t];
+}
+
+__global__ __launch_bounds__(256) void plan_colscan_kernel(uint32_t *__restrict__ hist,
+                                                           int64_t nb, int64_t bins,
+                                                           uint32_t *__restrict__ tpref,
+                                                           uint32_t *__restrict__ tsum) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  uint32_t s = 0;
+  if (t < bins) {
+#pragma unroll 8
+    for (int64_t b = 0; b < nb; ++b) {
+      const uint32_t v = hist[b * bins + t];
+      hist[b * bins + t] = s;
+      s += v;
+    }
+  }
+  int64_t total;
+  const int64_t ex = block_exclusive_sum<256>(static_cast<int64_t>(s), &total);
+  if (t < bins) tpref[t] = static_cast<uint32_t>(ex);
+  if (threadIdx.x == 0) tsum[blockIdx.x] = static_cast<uint32_t>(total);
+}
+
+__global__ __launch_bounds__(256) void plan_scatter_kernel(
+    const int64_t *__restrict__ idx, int64_t n, int64_t n_targets, int key_bits,
+    const uint32_t *__restrict__ hist, const uint32_t *__restrict__ tpref,
+    const uint32_t *__restrict__ tsum, int32_t *__restrict__ perm, int32_t *__restrict__ offsets) {
+  extern __shared__ uint32_t run[];
+  __shared__ uint32_t carry[kPlanMaxGroups];
+  constexpr int R = kPlanChunk / 256;
+  const int64_t bins = n_targets + 1;
+  const int ngroups = static_cast<int>((bins + 255) / 256);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kPlanChunk;
+  const uint32_t *h = hist + static_cast<int64_t>(blockIdx.x) * bins;
+  // Every load that does not depend on the counts first: the pairs' bins,
+  // then the bins' prefixes (tpref, h) and the group totals.
+  uint32_t bin[R], pre[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t i = base + r * 256 + tid;
+    bin[r] = i < n ? plan_bin(idx, i, n_targets) : 0xFFFFFFFFu;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) pre[r] = bin[r] != 0xFFFFFFFFu ? tpref[bin[r]] + h[bin[r]] : 0u;
+  const uint32_t gsum = tid < ngroups ? tsum[tid] : 0u;
+  for (int64_t t = tid; t < bins; t += 256) run[t] = 0;
+  if (wave == 0) {  // exclusive prefix of the group totals
+    const uint32_t inc = static_cast<uint32_t>(wave_inclusive_sum(static_cast<int64_t>(gsum)));
+    if (lane < ngroups) carry[lane] = inc - gsum;
+  }
+  __syncthreads();
+  // Offsets, spread over the blocks: offsets[t] = pairs with a bin below t.
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + tid; t < bins;
+       t += static_cast<int64_t>(gridDim.x) * 256)
+    offsets[t] = static_cast<int32_t>(carry[t >> 8] + tpref[t]);
+  const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const bool valid = bin[r] != 0xFFFFFFFFu;
+    const uint32_t k = valid ? bin[r] : 0u;
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < key_bits; ++b) {
+      const bool bit = (k >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt_mask));
+    uint32_t before = 0;
+    // The waves of this round in order: each reads the count of its bins so
+    // far, then the first lane of each bin adds the wave's pairs of it.
+    for (int w = 0; w < 4; ++w) {
+      if (wave == w && valid) {
+        before = run[k];
+        if (rank == 0) run[k] = before + static_cast<uint32_t>(__popcll(peers));
+      }
+      __syncthreads();
+    }
+    if (valid) perm[carry[k >> 8] + pre[r] + before + rank] = static_cast<int32_t>(base + r * 256 + tid);
+  }
 }
 
 __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t *__restrict__ in,
@@ -100,18 +226,27 @@ struct PlanWs {
   uint64_t *keys, *keys_alt;
   int32_t *pos_alt;
   void *sort_ws;
-  size_t bytes;
+  size_t bytes;  // carved, alignment included
+  size_t span;   // from keys to the end
 };
 
 PlanWs carve_plan(Carver &c, int64_t n) {
   PlanWs w;
   const size_t start = c.off;
   w.keys = c.take<uint64_t>(n);
+  const size_t at_keys = c.off - sizeof(uint64_t) * static_cast<size_t>(n > 0 ? n : 1);
   w.keys_alt = c.take<uint64_t>(n);
   w.pos_alt = c.take<int32_t>(n);
   w.sort_ws = c.take<char>(static_cast<int64_t>(sort_workspace_bytes(n)));
   w.bytes = c.off - start;
+  w.span = c.off - at_keys;
   return w;
+}
+
+// Workspace of the counting plan (hist, tpref, tsum).
+size_t counting_plan_bytes(int64_t n, int64_t bins) {
+  return align_up(sizeof(uint32_t) * ceil_div(n, kPlanChunk) * bins, 256) +
+         align_up(sizeof(uint32_t) * bins, 256) + sizeof(uint32_t) * kPlanMaxGroups;
 }
 
 int index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *perm, int32_t *offsets,
@@ -121,6 +256,28 @@ int index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *perm, 
     while (b < 63 && (int64_t(1) << b) < n_targets + 1) ++b;
     return b;
   }();
+  const int64_t bins = n_targets + 1;
+  // The counting plan runs in the plan workspace carved for the radix sort
+  // (which depends on n only) when its histograms fit there.
+  if (n > 0 && bins <= kPlanMaxBins && counting_plan_bytes(n, bins) <= w.span) {
+    const int64_t nb = ceil_div(n, kPlanChunk);
+    char *c = static_cast<char *>(static_cast<void *>(w.keys));
+    uint32_t *hist = reinterpret_cast<uint32_t *>(c);
+    c += align_up(sizeof(uint32_t) * nb * bins, 256);
+    uint32_t *tpref = reinterpret_cast<uint32_t *>(c);
+    uint32_t *tsum = reinterpret_cast<uint32_t *>(c + align_up(sizeof(uint32_t) * bins, 256));
+    const size_t lds = sizeof(uint32_t) * static_cast<size_t>(bins);
+    hipLaunchKernelGGL(plan_count_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), lds, stream,
+                       idx, n, n_targets, hist);
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(plan_colscan_kernel, dim3(static_cast<unsigned>(ceil_div(bins, 256))),
+                       dim3(256), 0, stream, hist, nb, bins, tpref, tsum);
+    EJ_LAUNCH_CHECK();
+    hipLaunchKernelGGL(plan_scatter_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), lds,
+                       stream, idx, n, n_targets, bits, hist, tpref, tsum, perm, offsets);
+    EJ_LAUNCH_CHECK();
+    return EJ_OK;
+  }
   if (n > 0) {
     const bool alt = radix_passes(bits) % 2 == 1;
     hipLaunchKernelGGL(plan_keys_kernel, dim3(grid_for(n)), dim3(kBlock), 0, stream, idx, n,
@@ -159,7 +316,7 @@ int check_dtypes(int32_t dtype, int32_t grad_dtype) {
 struct VjpWs {
   int32_t *perm_l, *off_l, *perm_r, *off_r;
   float *lhs32, *rhs32;
-  PlanWs plan;
+  PlanWs plan, plan_r;  // the lhs and rhs gradients' sorts (they may run concurrently)
   // run order of the lhs gradient's segments and its sort
   int32_t *order, *ovals, *ovals_alt;
   uint64_t *okeys, *okeys_alt;
@@ -181,6 +338,7 @@ VjpWs carve_vjp(void *base, int64_t n_pairs, int64_t n_lhs, int64_t n_rhs, int64
     w.rhs32 = c.take<float>(n_rhs * rhs_elems);
   }
   w.plan = carve_plan(c, n_pairs);
+  w.plan_r = carve_plan(c, n_pairs);
   w.order = c.take<int32_t>(n_lhs + 1);
   w.ovals = c.take<int32_t>(n_lhs);
   w.ovals_alt = c.take<int32_t>(n_lhs);
@@ -208,6 +366,35 @@ int lhs_grad_order(const int64_t *ridx, const int32_t *perm, const int32_t *off,
                      n_seg, w.order);
   EJ_LAUNCH_CHECK();
   return EJ_OK;
+}
+
+// A second stream of the calling thread on the current device, with the two
+// events that fork work onto it from a caller's stream and join it back
+// (created once per thread and device, default priority, never destroyed).
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+bool side_stream(SideStream *out) {
+  thread_local std::vector<SideStream> per_device;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return false;
+  if (static_cast<int>(per_device.size()) <= dev) per_device.resize(dev + 1);
+  SideStream &ss = per_device[dev];
+  if (!ss.stream) {
+    SideStream n;
+    if (hipStreamCreateWithFlags(&n.stream, hipStreamNonBlocking) != hipSuccess) return false;
+    if (hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&n.join, hipEventDisableTiming) != hipSuccess) {
+      if (n.fork) (void)hipEventDestroy(n.fork);
+      (void)hipStreamDestroy(n.stream);
+      return false;
+    }
+    ss = n;
+  }
+  *out = ss;
+  return true;
 }
 
 }  // namespace
@@ -339,41 +526,61 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
   }
   // Operand dtype of the gradient einsums: the cotangent's.
   const int32_t edt = grad_dtype;
-  auto zero = [&](void *p, int64_t n) -> int {
+  auto zero = [&](void *p, int64_t n, hipStream_t st) -> int {
     if (grad_dtype == EJ_BF16)
-      hipLaunchKernelGGL(zero_kernel<uint16_t>, dim3(grid_capped(n)), dim3(kBlock), 0, stream,
+      hipLaunchKernelGGL(zero_kernel<uint16_t>, dim3(grid_capped(n)), dim3(kBlock), 0, st,
                          static_cast<uint16_t *>(p), n);
     else
-      hipLaunchKernelGGL(zero_kernel<float>, dim3(grid_capped(n)), dim3(kBlock), 0, stream,
+      hipLaunchKernelGGL(zero_kernel<float>, dim3(grid_capped(n)), dim3(kBlock), 0, st,
                          static_cast<float *>(p), n);
     EJ_LAUNCH_CHECK();
     return EJ_OK;
   };
-  if (grad_lhs && n_lhs_tiles > 0) {
-    if (n_pairs == 0 || n_rhs_tiles == 0) {
-      EJ_TRY(zero(grad_lhs, n_lhs_tiles * lhs_elems));
-    } else {
-      EJ_TRY(index_plan(lhs_idx, n_pairs, n_lhs_tiles, w.perm_l, w.off_l, w.plan, stream));
-      // One lhs tile per workgroup on the LDS ring: run the tiles that
-      // contract the same rhs tiles side by side (see seg_first_rhs_kernel).
-      const int og = segment_einsum_order_group(&dl, edt, n_lhs_tiles, grad_out, rhs_v);
-      const int32_t *order = nullptr;
-      if (og == 1) {
-        EJ_TRY(lhs_grad_order(rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, n_rhs_tiles, w, stream));
-        order = w.order;
-      }
-      EJ_TRY(segment_einsum_ordered(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
-                                    rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, order, 1,
-                                    grad_lhs, stream));
-    }
+  // The two gradients' einsums run one after the other on the caller's
+  // stream (run side by side they slow each other down more than they fill
+  // each other's idle CUs).  With both gradients, the lhs gradient's plan and
+  // run order are computed on a second stream while the rhs gradient's plan
+  // and einsum run; the lhs einsum waits for both.  Each plan has its own
+  // sort workspace.
+  const bool lhs_live = grad_lhs && n_lhs_tiles > 0 && n_pairs > 0 && n_rhs_tiles > 0;
+  const int og = lhs_live ? segment_einsum_order_group(&dl, edt, n_lhs_tiles, grad_out, rhs_v) : 0;
+  auto lhs_prep = [&](hipStream_t st) -> int {
+    EJ_TRY(index_plan(lhs_idx, n_pairs, n_lhs_tiles, w.perm_l, w.off_l, w.plan, st));
+    // One lhs tile per workgroup on the LDS ring: run the tiles that
+    // contract the same rhs tiles side by side (see seg_first_rhs_kernel).
+    if (og == 1) EJ_TRY(lhs_grad_order(rhs_idx, w.perm_l, w.off_l, n_lhs_tiles, n_rhs_tiles, w, st));
+    return EJ_OK;
+  };
+  auto rhs_grad = [&](hipStream_t st) -> int {
+    if (!grad_rhs || n_rhs_tiles == 0) return EJ_OK;
+    if (n_pairs == 0 || n_lhs_tiles == 0) return zero(grad_rhs, n_rhs_tiles * rhs_elems, st);
+    EJ_TRY(index_plan(rhs_idx, n_pairs, n_rhs_tiles, w.perm_r, w.off_r, w.plan_r, st));
+    return ej_segment_einsum(&dr, edt, lhs_v, grad_out, n_lhs_tiles, n_pairs, lhs_idx, nullptr,
+                             w.perm_r, w.off_r, n_rhs_tiles, grad_rhs,
+                             reinterpret_cast<ej_stream_t>(st));
+  };
+  SideStream side;
+  const bool fork = lhs_live && grad_rhs && n_rhs_tiles > 0 && side_stream(&side);
+  if (fork) {
+    EJ_HIP(hipEventRecord(side.fork, stream));
+    EJ_HIP(hipStreamWaitEvent(side.stream, side.fork, 0));
+    const int sl = lhs_prep(side.stream);
+    EJ_HIP(hipEventRecord(side.join, side.stream));
+    const int sr = rhs_grad(stream);
+    EJ_HIP(hipStreamWaitEvent(stream, side.join, 0));
+    EJ_TRY(sl);
+    EJ_TRY(sr);
+  } else {
+    if (lhs_live) EJ_TRY(lhs_prep(stream));
+    EJ_TRY(rhs_grad(stream));
   }
-  if (grad_rhs && n_rhs_tiles > 0) {
-    if (n_pairs == 0 || n_lhs_tiles == 0) {
-      EJ_TRY(zero(grad_rhs, n_rhs_tiles * rhs_elems));
+  if (grad_lhs && n_lhs_tiles > 0) {
+    if (!lhs_live) {
+      EJ_TRY(zero(grad_lhs, n_lhs_tiles * lhs_elems, stream));
     } else {
-      EJ_TRY(index_plan(rhs_idx, n_pairs, n_rhs_tiles, w.perm_r, w.off_r, w.plan, stream));
-      EJ_TRY(ej_segment_einsum(&dr, edt, lhs_v, grad_out, n_lhs_tiles, n_pairs, lhs_idx,
-                               nullptr, w.perm_r, w.off_r, n_rhs_tiles, grad_rhs, stream_));
+      EJ_TRY(segment_einsum_ordered(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
+                                    rhs_idx, w.perm_l, w.off_l, n_lhs_tiles,
+                                    og == 1 ? w.order : nullptr, 1, grad_lhs, stream));
     }
   }
   return EJ_OK;
