@@ -551,7 +551,13 @@ int ej_index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *per
  * the operand values; grad_dtype that of grad_out, grad_lhs and grad_rhs:
  * EJ_F32 (bf16 operands are then widened to fp32 in the workspace), or
  * EJ_BF16 with bf16 operands (the reference's dtype for bf16 values: the
- * einsums run on bf16 operands and each gradient is rounded once). */
+ * einsums run on bf16 operands and each gradient is rounded once).
+ * Asynchronous on `stream`.  With both gradients requested, part of the work
+ * (the lhs gradient's grouping) runs on a second stream that the library
+ * keeps per host thread and device: it starts after the work already queued
+ * on `stream`, and `stream` waits for it before the lhs gradient's einsum,
+ * so the call is ordered on `stream` as a whole (the fork and join are
+ * event records and waits). */
 int ej_pair_einsum_vjp_workspace_size(int64_t n_pairs, int64_t n_lhs_tiles, int64_t n_rhs_tiles,
                                       int64_t lhs_elems, int64_t rhs_elems, int32_t dtype,
                                       int32_t grad_dtype, size_t *bytes);
