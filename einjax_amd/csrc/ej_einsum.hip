@@ -282,18 +282,34 @@ __device__ inline T ld_uniform(const T *p, int64_t i) {
   return ((const __attribute__((address_space(4))) T *)(p))[i];
 }
 
-// Spreads the first `live` block ids over the 8 XCDs (block id b runs on XCD
-// b % 8) in contiguous chunks of logical blocks, so that neighbouring logical
-// blocks (sharing operand tiles) share an L2.  Block ids from `live` on keep
-// their id: they lie beyond the work of a grid sized for a bound.
-__device__ inline int64_t xcd_logical_block(int64_t live) {
+// Maps the first `live` block ids onto logical blocks (block id b runs on XCD
+// b % 8).  run == 0: the logical range is split into 8 contiguous parts, one
+// per XCD, so that neighbouring logical blocks (sharing operand tiles) share
+// an L2 over the widest window.  run > 0: runs of `run` consecutive logical
+// blocks go to one XCD, the runs dealt to the XCDs in turn, so that every XCD
+// gets a share of each region of the logical range (work that is heavier in
+// one region, as for skewed sparsity, stays balanced); the last, partial
+// round of runs is split into 8 contiguous parts.  Block ids from `live` on
+// keep their id: they lie beyond the work of a grid sized for a bound.
+__device__ inline int64_t xcd_logical_block(int64_t live, int64_t run = 0) {
   const int64_t bid = blockIdx.x;
   if (bid >= live) return bid;
-  const int64_t per = live / 8, rem = live % 8;
-  const int64_t xcd = bid % 8, local = bid / 8;
+  const int64_t full = run > 0 ? live / (8 * run) * (8 * run) : 0;
+  const int64_t xcd = bid % 8;
+  if (bid < full) {
+    const int64_t local = bid / 8;
+    return ((local / run) * 8 + xcd) * run + local % run;
+  }
+  const int64_t rest = live - full, local = (bid - full) / 8;
+  const int64_t per = rest / 8, rem = rest % 8;
   const int64_t start = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
-  return start + local;
+  return full + start + local;
 }
+
+// Run length of the dealt mapping for one-segment workgroups taken in plan
+// order (no run order): their neighbours share few tiles, and skewed
+// sparsity makes whole regions of the plan heavier.
+constexpr int64_t kXcdRun = 16;
 
 // Blocks that carry work when each segment takes blocks_per_seg of them: the
 // whole grid, or, given a device-side segment count, that many segments' blocks
@@ -1119,7 +1135,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
     const int64_t lg = (nseg + segs - 1) / segs * per_grp;
     live = lg < live ? lg : live;
   }
-  int64_t lb = xcd_logical_block(live);
+  int64_t lb = xcd_logical_block(live, G == 1 && !src.run_order ? kXcdRun : 0);
   const int64_t nb = lb % g.nblocks;
   lb /= g.nblocks;
   int64_t mb0 = 0, nmb = g.mblocks;
