@@ -211,7 +211,7 @@ CONFIG_NAMES = ["blocksparse_1k", "blocksparse_16k_bf16", "sparse_sparse_zipf",
                 "batched_banded_bf16", "order3"]
 
 
-def measure_config(name: str, reps: int = 5) -> dict:
+def measure_config(name: str, reps: int = 20, warm: int = 10) -> dict:
     """One workload at full size: the execute_sparse step (wall clock) and
     the fused segment einsum alone (HIP events), with the effective TFLOP/s,
     the MFMA fraction and the compulsory-byte rate of the fused kernel.
@@ -245,7 +245,7 @@ def measure_config(name: str, reps: int = 5) -> dict:
     def step():
         return execute_sparse(lhs, rhs, jk, ks, ak)
 
-    for _ in range(2):
+    for _ in range(warm):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
