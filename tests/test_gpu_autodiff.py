@@ -284,3 +284,40 @@ def test_vjp_blocksparse_16k_adjoint_and_rows(gpu):
     gl32b, gr32b = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g16.float())
     assert rel_l2(gl16.float().cpu().numpy(), gl32b.cpu().numpy()) <= 4e-3
     assert rel_l2(gr16.float().cpu().numpy(), gr32b.cpu().numpy()) <= 4e-3
+
+
+@pytest.mark.parametrize("n_lhs,n_pairs,seed", [(700, 3000, 1), (1100, 5000, 2), (600, 900, 3)])
+def test_vjp_lhs_gradient_ragged(gpu, n_lhs, n_pairs, seed):
+    """The lhs gradient of 128x128 bf16 tiles (the LDS-ring one-tile-per-
+    workgroup kernel with its run order) on ragged segments: many tiles with
+    no pair, a few with hundreds, invalid indices on either side.  Against a
+    float32 torch reference and the fp32-cotangent path; repeated calls
+    bitwise equal."""
+    note("vjp ragged lhs gradient", n_lhs, n_pairs, seed)
+    rng = np.random.default_rng(seed)
+    n_rhs = 300
+    # skewed lhs targets: a few heavy tiles, many light, some with none
+    heavy = rng.integers(0, n_lhs, size=8)
+    li_h = np.where(rng.random(n_pairs) < 0.3, rng.choice(heavy, size=n_pairs),
+                    rng.integers(0, n_lhs, size=n_pairs)).astype(np.int64)
+    li_h[rng.random(n_pairs) < 0.01] = -1
+    li_h[rng.random(n_pairs) < 0.01] = n_lhs + 5
+    ri_h = rng.integers(0, n_rhs, size=n_pairs).astype(np.int64)
+    ri_h[rng.random(n_pairs) < 0.01] = -3
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    lv = torch.randn((n_lhs, 128, 128), generator=gen, device="cuda").to(torch.bfloat16)
+    rv = (torch.randn((n_rhs, 128, 128), generator=gen, device="cuda") / 16).to(torch.bfloat16)
+    g = torch.randn((n_pairs, 128, 128), generator=gen, device="cuda").to(torch.bfloat16)
+    li, ri = torch.from_numpy(li_h).cuda(), torch.from_numpy(ri_h).cuda()
+    gl16, _ = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g, need_rhs=False)
+    again, _ = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g, need_rhs=False)
+    assert torch.equal(gl16, again)
+    gl32, _ = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g.float(), need_rhs=False)
+    assert rel_l2(gl16.float().cpu().numpy(), gl32.cpu().numpy()) <= 4e-3
+    ok = (li_h >= 0) & (li_h < n_lhs) & (ri_h >= 0) & (ri_h < n_rhs)
+    sel = torch.from_numpy(np.nonzero(ok)[0]).cuda()
+    prod = torch.bmm(g[sel].float(), rv[ri[sel]].float().transpose(1, 2).contiguous())
+    want = torch.zeros((n_lhs, 128, 128), device="cuda").index_add_(0, li[sel], prod)
+    assert rel_l2(gl16.float().cpu().numpy(), want.cpu().numpy()) <= 1e-2
+    untouched = np.setdiff1d(np.arange(n_lhs), li_h[ok])
+    assert untouched.size > 0 and not gl16[torch.from_numpy(untouched).cuda()].any()
