@@ -496,24 +496,31 @@ def main():
         lambda *a, **k: execute_sparse(*a, out_dtype=torch.float32, **k), lhs, rhs, jk, ks, ak,
         20)
     torch.cuda.synchronize()
+    # The collector runs now and is then off until the timed steps end: a
+    # collection between the warm-up and the timed steps idles the GPU long
+    # enough (tens of ms) for its clocks to drop, and the timed steps then
+    # start cold.
+    gc.collect()
+    gc.disable()
     # The fused einsum as the step launches it (after the device-side join
     # and plan, in the plan's run order): HIP events on the launch stream,
-    # 200 queued steps.  Measured last among the stages, right before the
-    # warm-up steps: its ~40 ms of sustained load also brings the GPU to its
-    # working clocks, which a handful of warm-up steps alone (~1 ms) do not.
-    t_fused = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, 200) or t_fused_exact
+    # 200 queued steps, right before the warm-up steps: its ~40 ms of
+    # sustained load also brings the GPU toward its working clocks, which a
+    # handful of warm-up steps alone (~1 ms) do not.  It is measured again
+    # after the timed steps, at the clocks they ran at; that figure is the
+    # roofline's (both are on the line).
+    t_fused_ramp = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, 200) or t_fused_exact
 
     # ---- the timed steps -------------------------------------------------
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    gc.collect()
-    gc.disable()  # no collector pause inside the timed steps
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = step()
     torch.cuda.synchronize()
     ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    t_fused = fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, 200) or t_fused_exact
     gc.enable()
 
     e = 2
@@ -569,6 +576,7 @@ def main():
         },
         "stages_ms": {
             "join": t_join, "segment_plan": t_plan, "fused_gemm_segsum": t_fused,
+            "fused_gemm_segsum_before_warmup": t_fused_ramp,
             "fused_gemm_segsum_exact_path": t_fused_exact,
             "gather": t_gather, "pair_gemm": t_pair, "segment_sum": t_segsum,
             "segment_sum_bf16_values": t_segsum16, "bucket_dense_A": t_bucket,
