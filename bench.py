@@ -77,6 +77,21 @@ def event_time_ms(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+def warm_up(fn, ms: float = 30.0, min_calls: int = 2) -> None:
+    """Calls fn until ~ms of GPU work has run (at least min_calls times):
+    the GPU's clocks rise over tens of ms of sustained load."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = 0
+    while n < min_calls or (time.perf_counter() - t0) * 1e3 < ms:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def wall_time_ms(fn, reps: int, warm: int = 1) -> float:
     import torch
 
@@ -245,9 +260,7 @@ def measure_config(name: str, reps: int = 20, warm: int = 10) -> dict:
     def step():
         return execute_sparse(lhs, rhs, jk, ks, ak)
 
-    for _ in range(warm):
-        step()
-    torch.cuda.synchronize()
+    warm_up(step, min_calls=warm)
     t0 = time.perf_counter()
     for _ in range(reps):
         step()
@@ -386,7 +399,8 @@ def measure_backward(lhs, rhs, li, ri, kernel_string, F: float, reps: int = 20) 
     }
     out = {}
     for k, fn in run.items():
-        t = wall_time_ms(fn, reps, warm=5)
+        warm_up(fn)
+        t = wall_time_ms(fn, reps, warm=0)
         flops = 2 * F if k.startswith("both") else F
         out[f"{k}_ms"] = t
         out[f"{k}_tflops"] = flops / (t * 1e-3) / 1e12
