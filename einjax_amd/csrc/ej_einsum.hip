@@ -954,7 +954,9 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 template <int BM_, int BN_, bool AT_ = false, bool BT_ = false>
 struct SegOpBf16 {
   using elem = uint16_t;
-  static constexpr bool kBf16 = true, AT = AT_, BT = BT_;
+  using a_elem = uint16_t;
+  using b_elem = uint16_t;
+  static constexpr bool kBf16 = true, kSplit = false, AT = AT_, BT = BT_;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int A_ROWB = AT ? BM * 2 : BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * BK * 2;
   static constexpr int B_ROWB = BT ? BK * 2 : BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * BN * 2;
@@ -1045,7 +1047,9 @@ struct SegOpBf16 {
 template <int BM_, int BN_>
 struct SegOpF32 {
   using elem = float;
-  static constexpr bool kBf16 = false, AT = false, BT = false;
+  using a_elem = float;
+  using b_elem = float;
+  static constexpr bool kBf16 = false, kSplit = false, AT = false, BT = false;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int A_ROWB = BK * 4, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
   static constexpr int B_ROWB = BN * 4, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
@@ -1088,14 +1092,94 @@ struct SegOpF32 {
   }
 };
 
+// An fp32 lhs [m][k] against an exactly-bf16 rhs [n][k] (the backward's lhs
+// gradient 'ik,jk->ij' under an fp32 cotangent with bf16 operands).  The
+// lhs stage is fp32 in LDS, laid out as SegOpF32's ([BM][32], 128-byte rows,
+// chunk c of row r at c ^ (r & 7) ^ ((r >> 3) & 1)); the rhs stage is bf16
+// k-rows as SegOpBf16's.  At read time each lane's 8 fp32 lhs values (k
+// 8g .. 8g + 7 of its row, chunks 2g and 2g + 1) are split into three bf16
+// terms whose sum is the value exactly (split3), and each product runs as
+// three v_mfma_f32_16x16x32_bf16 into one fp32 accumulator: with the rhs
+// exact in bf16, every partial product is exact and the sums are fp32, as
+// in an fp32 product.
+template <int BM_, int BN_>
+struct SegOpSplit {
+  using elem = void;
+  using a_elem = float;
+  using b_elem = uint16_t;
+  static constexpr bool kBf16 = false, kSplit = true, AT = false, BT = true;
+  static constexpr int BM = BM_, BN = BN_, BK = 32;
+  static constexpr int A_ROWB = BK * 4, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
+  static constexpr int B_ROWB = BK * 2, CHB = B_ROWB / 16, B_BYTES = BN * B_ROWB;
+  static_assert(CHA == 8 && CHB == 4, "row widths");
+
+  __device__ static int swa(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+  __device__ static uint32_t a_src(int blk, int lane, const GemmGeom &g) {
+    const int row = blk * (1024 / A_ROWB) + lane / CHA;
+    const int c = (lane % CHA) ^ swa(row);
+    return static_cast<uint32_t>(row * g.a_sm + c * 4);
+  }
+  __device__ static uint32_t b_src(int blk, int lane, const GemmGeom &g) {
+    return SegOpBf16<BM_, BN_, false, true>::krows_src(blk, lane, g.b_sn);
+  }
+
+  // rd[0], rd[1]: lhs chunks 2g and 2g + 1 of row row0 + (lane & 15) (the
+  // swizzle depends on the row inside 16 only, so fragment i is 16 rows
+  // further); rd[2]: the rhs k-row read of SegOpBf16 (fragment j 16 columns
+  // further).
+  template <int FM, int FN>
+  static constexpr int n_rd = 3;
+
+  template <int FM, int FN>
+  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FM, FN>], int row0, int wcol,
+                                      uint32_t b_region, int lane) {
+    const int row = row0 + (lane & 15), g = lane >> 4;
+    rd[0] = static_cast<uint32_t>(row * A_ROWB + (((2 * g) ^ swa(row)) * 16));
+    rd[1] = static_cast<uint32_t>(row * A_ROWB + (((2 * g + 1) ^ swa(row)) * 16));
+    rd[2] = b_region + SegOpBf16<BM_, BN_, false, true>::krows_rd(wcol, B_ROWB, lane);
+  }
+};
+
+// x = hi + mid + lo exactly, each a bf16: hi keeps the top 8 significand bits
+// of x (truncation), mid the next 8 of the remainder, lo the rest (x - hi and
+// its remainder are exact in fp32).  A non-finite x goes to hi alone (a NaN
+// keeps a quiet bit).  Packed two values per 32-bit word, element 0 low.
+__device__ inline void split3_pair(float x0, float x1, uint32_t &hi, uint32_t &mid,
+                                   uint32_t &lo) {
+  auto one = [](float x, uint32_t &h, uint32_t &m, uint32_t &l) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, x);
+    if ((b & 0x7F800000u) == 0x7F800000u) {
+      h = (b >> 16) | ((b & 0x007FFFFFu) ? 0x0040u : 0u);
+      m = 0;
+      l = 0;
+      return;
+    }
+    const float fh = __builtin_bit_cast(float, b & 0xFFFF0000u);
+    const float r = x - fh;
+    const uint32_t rb = __builtin_bit_cast(uint32_t, r);
+    const float fm = __builtin_bit_cast(float, rb & 0xFFFF0000u);
+    const float q = r - fm;
+    h = b >> 16;
+    m = rb >> 16;
+    l = __builtin_bit_cast(uint32_t, q) >> 16;
+  };
+  uint32_t h0, m0, l0, h1, m1, l1;
+  one(x0, h0, m0, l0);
+  one(x1, h1, m1, l1);
+  hi = h0 | (h1 << 16);
+  mid = m0 | (m1 << 16);
+  lo = l0 | (l1 << 16);
+}
+
 template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
-__global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op::elem *__restrict__ A,
-                                                           const typename Op::elem *__restrict__ B,
+__global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op::a_elem *__restrict__ A,
+                                                           const typename Op::b_elem *__restrict__ B,
                                                            void *__restrict__ C, PairSrc src,
                                                            GemmGeom g, int64_t n_seg, int spw,
                                                            int mb_loop) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using T = typename Op::elem;
+  using TA = typename Op::a_elem;
+  using TB = typename Op::b_elem;
   constexpr int BM = Op::BM, BN = Op::BN, BK = Op::BK;
   constexpr int WGN = NW / WGM;
   constexpr int WM = BM / WGM, WN = G * BN / WGN;
@@ -1287,7 +1371,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
     }
     const int64_t a_tile = at < 0 ? 0 : at;
     unsigned char *slot = ring + (st % NS) * SLOT;
-    const T *ab = A + a_tile * g.a_elems + bi * g.a_sb + imb * BM * g.a_sm + ikc * BK * g.a_sk;
+    const TA *ab = A + a_tile * g.a_elems + bi * g.a_sb + imb * BM * g.a_sm + ikc * BK * g.a_sk;
 #pragma unroll
     for (int v = 0; v < LPA; ++v)
       __builtin_amdgcn_global_load_lds(ab + a_src[v], EJ_LDS(slot + (v * NW + wave) * 1024), 16,
@@ -1295,7 +1379,7 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
 #pragma unroll
     for (int s = 0; s < G; ++s) {
       const int64_t b_tile = bt[s] < 0 ? 0 : bt[s];
-      const T *bb = B + b_tile * g.b_elems + b_off0 + ikc * BK * g.b_sk;
+      const TB *bb = B + b_tile * g.b_elems + b_off0 + ikc * BK * g.b_sk;
 #pragma unroll
       for (int v = 0; v < LPB; ++v)
         __builtin_amdgcn_global_load_lds(
@@ -1376,7 +1460,43 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
       // The stage's MFMAs (written out here: as a separate function taking the
       // accumulators by reference the compiler kept extra copies of them).
       typedef const __attribute__((address_space(3))) unsigned char *lds_ptr;
-      if constexpr (Op::kBf16) {
+      if constexpr (Op::kSplit) {
+        constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
+        i32x4_t bq[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          bq[j] = *reinterpret_cast<const i32x4_t *>((lds_ptr)(size_t)(base + rd[2]) +
+                                                    j * 16 * B_ROWB);
+        // terms[0] = lo, [1] = mid, [2] = hi of each lhs fragment
+        i32x4_t terms[3][FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const f32x4_t x0 = *reinterpret_cast<const f32x4_t *>((lds_ptr)(size_t)(base + rd[0]) +
+                                                                i * 16 * A_ROWB);
+          const f32x4_t x1 = *reinterpret_cast<const f32x4_t *>((lds_ptr)(size_t)(base + rd[1]) +
+                                                                i * 16 * A_ROWB);
+          uint32_t h, m, l;
+          split3_pair(x0[0], x0[1], h, m, l);
+          terms[2][i][0] = h; terms[1][i][0] = m; terms[0][i][0] = l;
+          split3_pair(x0[2], x0[3], h, m, l);
+          terms[2][i][1] = h; terms[1][i][1] = m; terms[0][i][1] = l;
+          split3_pair(x1[0], x1[1], h, m, l);
+          terms[2][i][2] = h; terms[1][i][2] = m; terms[0][i][2] = l;
+          split3_pair(x1[2], x1[3], h, m, l);
+          terms[2][i][3] = h; terms[1][i][3] = m; terms[0][i][3] = l;
+        }
+        // lo, then mid, then hi into each accumulator; consecutive MFMAs
+        // go to different accumulators
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_t, terms[t][i]), __builtin_bit_cast(bf16x8_t, bq[j]),
+                  acc[i][j], 0, 0, 0);
+      } else if constexpr (Op::kBf16) {
         constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
         constexpr int RA = Op::template n_ra<FM>;
         i32x4_t aq[FM], bq[FN];
@@ -1667,16 +1787,17 @@ int launch_seg_gemm_t(const void *A, const void *B, void *C, const PairSrc &src_
     set_error("einsum launch too large");
     return EJ_E_UNSUPPORTED;
   }
-  using T = typename Op::elem;
+  using TA = typename Op::a_elem;
+  using TB = typename Op::b_elem;
   if (mb_loop || spw > 1)
     hipLaunchKernelGGL((seg_gemm_kernel<Op, NS, G, WGM, NW, true>),
                        dim3(static_cast<unsigned>(nblk)), dim3(NW * 64), 0, stream,
-                       static_cast<const T *>(A), static_cast<const T *>(B), C, src, g, n_seg, spw,
-                       mb_loop);
+                       static_cast<const TA *>(A), static_cast<const TB *>(B), C, src, g, n_seg,
+                       spw, mb_loop);
   else
     hipLaunchKernelGGL((seg_gemm_kernel<Op, NS, G, WGM, NW, false>),
                        dim3(static_cast<unsigned>(nblk)), dim3(NW * 64), 0, stream,
-                       static_cast<const T *>(A), static_cast<const T *>(B), C, src, g, n_seg, 1,
+                       static_cast<const TA *>(A), static_cast<const TB *>(B), C, src, g, n_seg, 1,
                        0);
   EJ_LAUNCH_CHECK();
   return EJ_OK;
@@ -2112,6 +2233,36 @@ int ej::segment_einsum_ordered(const ej_einsum_desc *d, int32_t dtype, const voi
                                int32_t order_group, void *out, hipStream_t stream) {
   PairSrc src{lidx, ridx, perm, seg_off, n_a_tiles, n_b_tiles, nullptr, run_order, order_group};
   return einsum_common(d, dtype, A, B, src, n_seg, out, stream);
+}
+
+bool ej::segment_einsum_split_ok(const ej_einsum_desc *d, const void *A, const void *B) {
+  // fp32 k-rows lhs, bf16 k-rows rhs, 128 x 128 output blocks
+  return d && d->is_gemm && d->m % 128 == 0 && d->n % 128 == 0 && d->k % 32 == 0 &&
+         d->a_sk == 1 && d->a_sm % 4 == 0 && d->b_sk == 1 && d->b_sn % 8 == 0 &&
+         d->a_elems % 4 == 0 && d->b_elems % 8 == 0 && d->a_sb % 4 == 0 && d->b_sb % 8 == 0 &&
+         aligned16(A) && aligned16(B);
+}
+
+int ej::segment_einsum_split(const ej_einsum_desc *d, const float *A, const uint16_t *B,
+                             int64_t n_a_tiles, int64_t n_b_tiles, const int64_t *lidx,
+                             const int64_t *ridx, const int32_t *perm, const int32_t *seg_off,
+                             int64_t n_seg, const int32_t *run_order, int32_t order_group,
+                             void *out, hipStream_t stream) {
+  if (!segment_einsum_split_ok(d, A, B) || !seg_off || n_a_tiles >= (int64_t(1) << 31) ||
+      n_b_tiles >= (int64_t(1) << 31))
+    return EJ_E_UNSUPPORTED;
+  if (n_seg == 0) return EJ_OK;
+  GemmGeom g;
+  g.m = d->m; g.n = d->n; g.k = d->k; g.batch = d->batch;
+  g.a_sb = d->a_sb; g.a_sm = d->a_sm; g.a_sk = d->a_sk;
+  g.b_sb = d->b_sb; g.b_sk = d->b_sk; g.b_sn = d->b_sn;
+  g.c_sb = d->c_sb; g.c_sm = d->c_sm; g.c_sn = d->c_sn;
+  g.a_elems = d->a_elems; g.b_elems = d->b_elems; g.c_elems = d->c_elems;
+  g.mblocks = d->m / 128;
+  g.nblocks = d->n / 128;
+  g.out_bf16 = d->out_dtype == EJ_BF16;
+  PairSrc src{lidx, ridx, perm, seg_off, n_a_tiles, n_b_tiles, nullptr, run_order, order_group};
+  return launch_seg_gemm_t<SegOpSplit<128, 128>, 1, 2, 4, 3>(A, B, out, src, g, n_seg, stream);
 }
 
 extern "C" int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype,

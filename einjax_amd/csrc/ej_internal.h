@@ -115,6 +115,18 @@ int segment_einsum_ordered(const ej_einsum_desc *d, int32_t dtype, const void *A
                            int64_t n_seg, const int32_t *run_order, int32_t order_group,
                            void *out, hipStream_t stream);
 
+// The fused segment einsum for an fp32 lhs (k-contiguous [m][k] tiles) with
+// an exactly-bf16 rhs (k-contiguous [n][k] tiles), 128 x 128 output blocks:
+// the lhs is split into three bf16 terms per value and every product runs
+// as three bf16 MFMAs with fp32 sums (ej_einsum.hip).  EJ_E_UNSUPPORTED
+// (nothing launched) for other layouts; the caller then widens the rhs.
+bool segment_einsum_split_ok(const ej_einsum_desc *d, const void *A, const void *B);
+int segment_einsum_split(const ej_einsum_desc *d, const float *A, const uint16_t *B,
+                         int64_t n_a_tiles, int64_t n_b_tiles, const int64_t *lidx,
+                         const int64_t *ridx, const int32_t *perm, const int32_t *seg_off,
+                         int64_t n_seg, const int32_t *run_order, int32_t order_group, void *out,
+                         hipStream_t stream);
+
 // Zeroes n bytes (a multiple of 4, 4-byte aligned) with a kernel rather than
 // hipMemsetAsync, which misbehaves when a caller records the call into a
 // HIP graph.

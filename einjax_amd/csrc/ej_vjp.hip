@@ -505,10 +505,17 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
                    (!grad_rhs || n_lhs_tiles == 0 || lhs_values),
                "null operand values");
   const void *lhs_v = lhs_values, *rhs_v = rhs_values;
+  // An fp32 cotangent with bf16 operands, the lhs gradient on k-contiguous
+  // 128 x 128 blocks: the cotangent is split into three bf16 terms in the
+  // kernel and the rhs stays bf16 (segment_einsum_split), so the rhs is not
+  // widened.
+  const bool split = dtype == EJ_BF16 && grad_dtype == EJ_F32 && grad_lhs && n_lhs_tiles > 0 &&
+                     n_rhs_tiles > 0 && n_pairs > 0 &&
+                     segment_einsum_split_ok(&dl, grad_out, rhs_values);
   if (dtype == EJ_BF16 && grad_dtype == EJ_F32) {
-    // An fp32 cotangent with bf16 operands: the operands are widened to fp32
-    // once so the gradient einsums run in fp32 throughout.  (A bf16
-    // cotangent runs them on bf16 operands with fp32 sums.)
+    // Otherwise, with an fp32 cotangent and bf16 operands, the operands are
+    // widened to fp32 once so the gradient einsums run in fp32 throughout.
+    // (A bf16 cotangent runs them on bf16 operands with fp32 sums.)
     if (grad_rhs && n_lhs_tiles > 0) {
       hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_capped(n_lhs_tiles * lhs_elems)),
                          dim3(kBlock), 0, stream, static_cast<const uint16_t *>(lhs_values),
@@ -516,7 +523,7 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
       EJ_LAUNCH_CHECK();
       lhs_v = w.lhs32;
     }
-    if (grad_lhs && n_rhs_tiles > 0) {
+    if (grad_lhs && n_rhs_tiles > 0 && !split) {
       hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_capped(n_rhs_tiles * rhs_elems)),
                          dim3(kBlock), 0, stream, static_cast<const uint16_t *>(rhs_values),
                          w.rhs32, n_rhs_tiles * rhs_elems);
@@ -543,7 +550,9 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
   // and einsum run; the lhs einsum waits for both.  Each plan has its own
   // sort workspace.
   const bool lhs_live = grad_lhs && n_lhs_tiles > 0 && n_pairs > 0 && n_rhs_tiles > 0;
-  const int og = lhs_live ? segment_einsum_order_group(&dl, edt, n_lhs_tiles, grad_out, rhs_v) : 0;
+  const int og = split ? 1
+                 : lhs_live ? segment_einsum_order_group(&dl, edt, n_lhs_tiles, grad_out, rhs_v)
+                            : 0;
   auto lhs_prep = [&](hipStream_t st) -> int {
     EJ_TRY(index_plan(lhs_idx, n_pairs, n_lhs_tiles, w.perm_l, w.off_l, w.plan, st));
     // One lhs tile per workgroup on the LDS ring: run the tiles that
@@ -578,9 +587,15 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
     if (!lhs_live) {
       EJ_TRY(zero(grad_lhs, n_lhs_tiles * lhs_elems, stream));
     } else {
-      EJ_TRY(segment_einsum_ordered(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
-                                    rhs_idx, w.perm_l, w.off_l, n_lhs_tiles,
-                                    og == 1 ? w.order : nullptr, 1, grad_lhs, stream));
+      if (split)
+        EJ_TRY(segment_einsum_split(&dl, static_cast<const float *>(grad_out),
+                                    static_cast<const uint16_t *>(rhs_values), n_pairs,
+                                    n_rhs_tiles, nullptr, rhs_idx, w.perm_l, w.off_l,
+                                    n_lhs_tiles, w.order, 1, grad_lhs, stream));
+      else
+        EJ_TRY(segment_einsum_ordered(&dl, edt, grad_out, rhs_v, n_pairs, n_rhs_tiles, nullptr,
+                                      rhs_idx, w.perm_l, w.off_l, n_lhs_tiles,
+                                      og == 1 ? w.order : nullptr, 1, grad_lhs, stream));
     }
   }
   return EJ_OK;

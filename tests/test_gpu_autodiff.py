@@ -321,3 +321,13 @@ def test_vjp_lhs_gradient_ragged(gpu, n_lhs, n_pairs, seed):
     assert rel_l2(gl16.float().cpu().numpy(), want.cpu().numpy()) <= 1e-2
     untouched = np.setdiff1d(np.arange(n_lhs), li_h[ok])
     assert untouched.size > 0 and not gl16[torch.from_numpy(untouched).cuda()].any()
+    # an fp32 cotangent with full 24-bit significands: the lhs gradient splits
+    # it into three bf16 terms in the kernel; against float64
+    g32 = torch.randn((n_pairs, 128, 128), generator=gen, device="cuda")
+    gl, _ = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g32, need_rhs=False)
+    assert gl.dtype == torch.float32
+    prod64 = torch.bmm(g32[sel].double(), rv[ri[sel]].double().transpose(1, 2).contiguous())
+    want64 = torch.zeros((n_lhs, 128, 128), dtype=torch.float64, device="cuda").index_add_(
+        0, li[sel], prod64)
+    assert rel_l2(gl.cpu().numpy(), want64.cpu().numpy()) <= 1e-5
+    assert not gl[torch.from_numpy(untouched).cuda()].any()
