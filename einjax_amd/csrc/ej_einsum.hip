@@ -956,7 +956,7 @@ struct SegOpBf16 {
   using elem = uint16_t;
   using a_elem = uint16_t;
   using b_elem = uint16_t;
-  static constexpr bool kBf16 = true, kSplit = false, AT = AT_, BT = BT_;
+  static constexpr bool kBf16 = true, kSplit = false, kSplitB = false, AT = AT_, BT = BT_;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int A_ROWB = AT ? BM * 2 : BK * 2, CHA = A_ROWB / 16, A_BYTES = BM * BK * 2;
   static constexpr int B_ROWB = BT ? BK * 2 : BN * 2, CHB = B_ROWB / 16, B_BYTES = BK * BN * 2;
@@ -1049,7 +1049,7 @@ struct SegOpF32 {
   using elem = float;
   using a_elem = float;
   using b_elem = float;
-  static constexpr bool kBf16 = false, kSplit = false, AT = false, BT = false;
+  static constexpr bool kBf16 = false, kSplit = false, kSplitB = false, AT = false, BT = false;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int A_ROWB = BK * 4, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
   static constexpr int B_ROWB = BN * 4, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
@@ -1107,7 +1107,7 @@ struct SegOpSplit {
   using elem = void;
   using a_elem = float;
   using b_elem = uint16_t;
-  static constexpr bool kBf16 = false, kSplit = true, AT = false, BT = true;
+  static constexpr bool kBf16 = false, kSplit = true, kSplitB = false, AT = false, BT = true;
   static constexpr int BM = BM_, BN = BN_, BK = 32;
   static constexpr int A_ROWB = BK * 4, CHA = A_ROWB / 16, A_BYTES = BM * A_ROWB;
   static constexpr int B_ROWB = BK * 2, CHB = B_ROWB / 16, B_BYTES = BN * B_ROWB;
@@ -1170,6 +1170,59 @@ __device__ inline void split3_pair(float x0, float x1, uint32_t &hi, uint32_t &m
   mid = m0 | (m1 << 16);
   lo = l0 | (l1 << 16);
 }
+
+// An exactly-bf16 lhs [k][m] against an fp32 rhs [k][n] (the backward's rhs
+// gradient 'ij,ik->jk' under an fp32 cotangent with bf16 operands).  The lhs
+// stage is SegOpBf16's k-major one (transpose reads); the rhs stage is fp32
+// [32][BN] (512-byte k-rows for BN = 128) with 16-byte chunk c of k-row r at
+// c ^ 4 ((r >> 3) & 3), so that the four lane groups of a read (k-rows 8g + t)
+// hit four different bank quarters.  Each lane reads its 8 fp32 rhs values
+// (k 8g .. 8g + 7 of its column) with eight 4-byte reads, splits them into
+// three bf16 terms (split3_pair) and each product runs as three
+// v_mfma_f32_16x16x32_bf16.
+template <int BM_, int BN_>
+struct SegOpSplitB {
+  using elem = void;
+  using a_elem = uint16_t;
+  using b_elem = float;
+  static constexpr bool kBf16 = false, kSplit = false, kSplitB = true, AT = true, BT = false;
+  static constexpr int BM = BM_, BN = BN_, BK = 32;
+  static constexpr int A_ROWB = BM * 2, CHA = A_ROWB / 16, A_BYTES = BM * BK * 2;
+  static constexpr int B_ROWB = BN * 4, CHB = B_ROWB / 16, B_BYTES = BK * B_ROWB;
+  static_assert(BN == 128 && (CHA == 8 || CHA == 16), "row widths");
+  using BfOp = SegOpBf16<BM_, BN_, true, false>;
+
+  __device__ static int swb(int krow) { return 4 * ((krow >> 3) & 3); }
+  __device__ static uint32_t a_src(int blk, int lane, const GemmGeom &g) {
+    return BfOp::a_src(blk, lane, g);
+  }
+  __device__ static uint32_t b_src(int blk, int lane, const GemmGeom &g) {
+    const int krow = blk * (1024 / B_ROWB) + lane / CHB;
+    const int c = (lane % CHB) ^ swb(krow);
+    return static_cast<uint32_t>(krow * g.b_sk + c * 4);
+  }
+
+  // rd[i] (i < FM): the lhs transpose reads of SegOpBf16 (fragment i);
+  // rd[FM + j]: k-row 8g of column wcol + 16 j + (lane & 15) (the swizzle is
+  // the same for its 8 k-rows, which follow at 512-byte steps).
+  template <int FM, int FN>
+  static constexpr int n_rd = FM + FN;
+
+  template <int FM, int FN>
+  __device__ static void read_offsets(uint32_t (&rd)[n_rd<FM, FN>], int row0, int wcol,
+                                      uint32_t b_region, int lane) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      rd[i] = BfOp::template kmajor_rd<CHA>(row0 + i * 16, A_ROWB, lane);
+    const int g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = wcol + 16 * j + (lane & 15);
+      const int c = (n >> 2) ^ swb(8 * g);
+      rd[FM + j] = b_region + static_cast<uint32_t>(8 * g * B_ROWB + c * 16 + (n & 3) * 4);
+    }
+  }
+};
 
 template <class Op, int NS, int G, int WGM, int NW, bool MULTI>
 __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op::a_elem *__restrict__ A,
@@ -1495,6 +1548,41 @@ __global__ __launch_bounds__(NW * 64, 2) void seg_gemm_kernel(const typename Op:
             for (int j = 0; j < FN; ++j)
               acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                   __builtin_bit_cast(bf16x8_t, terms[t][i]), __builtin_bit_cast(bf16x8_t, bq[j]),
+                  acc[i][j], 0, 0, 0);
+      } else if constexpr (Op::kSplitB) {
+        constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
+        i32x4_t aq[FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const i32x2_t h0 = ds_read_tr16_b64(base + rd[i]);
+          const i32x2_t h1 = ds_read_tr16_b64_at<4 * A_ROWB>(base + rd[i]);
+          aq[i] = i32x4_t{h0[0], h0[1], h1[0], h1[1]};
+        }
+        lgkm_wait_all<FM>(aq);
+        // terms[0] = lo, [1] = mid, [2] = hi of each rhs fragment
+        i32x4_t terms[3][FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          float x[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            x[t] = *reinterpret_cast<const float *>((lds_ptr)(size_t)(base + rd[FM + j]) +
+                                                    t * B_ROWB);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint32_t h, m, l;
+            split3_pair(x[2 * q], x[2 * q + 1], h, m, l);
+            terms[2][j][q] = h; terms[1][j][q] = m; terms[0][j][q] = l;
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_t, aq[i]), __builtin_bit_cast(bf16x8_t, terms[t][j]),
                   acc[i][j], 0, 0, 0);
       } else if constexpr (Op::kBf16) {
         constexpr int A_ROWB = Op::A_ROWB, B_ROWB = Op::B_ROWB;
@@ -2263,6 +2351,35 @@ int ej::segment_einsum_split(const ej_einsum_desc *d, const float *A, const uint
   g.out_bf16 = d->out_dtype == EJ_BF16;
   PairSrc src{lidx, ridx, perm, seg_off, n_a_tiles, n_b_tiles, nullptr, run_order, order_group};
   return launch_seg_gemm_t<SegOpSplit<128, 128>, 1, 2, 4, 3>(A, B, out, src, g, n_seg, stream);
+}
+
+bool ej::segment_einsum_split_b_ok(const ej_einsum_desc *d, const void *A, const void *B) {
+  // bf16 k-major lhs ([k][m]), fp32 k-major rhs ([k][n]), 128 x 128 blocks
+  return d && d->is_gemm && d->m % 128 == 0 && d->n % 128 == 0 && d->k % 32 == 0 &&
+         d->a_sm == 1 && d->a_sk % 8 == 0 && d->b_sn == 1 && d->b_sk % 4 == 0 &&
+         d->a_elems % 8 == 0 && d->b_elems % 4 == 0 && d->a_sb % 8 == 0 && d->b_sb % 4 == 0 &&
+         aligned16(A) && aligned16(B);
+}
+
+int ej::segment_einsum_split_b(const ej_einsum_desc *d, const uint16_t *A, const float *B,
+                               int64_t n_a_tiles, int64_t n_b_tiles, const int64_t *lidx,
+                               const int64_t *ridx, const int32_t *perm, const int32_t *seg_off,
+                               int64_t n_seg, void *out, hipStream_t stream) {
+  if (!segment_einsum_split_b_ok(d, A, B) || !seg_off || n_a_tiles >= (int64_t(1) << 31) ||
+      n_b_tiles >= (int64_t(1) << 31))
+    return EJ_E_UNSUPPORTED;
+  if (n_seg == 0) return EJ_OK;
+  GemmGeom g;
+  g.m = d->m; g.n = d->n; g.k = d->k; g.batch = d->batch;
+  g.a_sb = d->a_sb; g.a_sm = d->a_sm; g.a_sk = d->a_sk;
+  g.b_sb = d->b_sb; g.b_sk = d->b_sk; g.b_sn = d->b_sn;
+  g.c_sb = d->c_sb; g.c_sm = d->c_sm; g.c_sn = d->c_sn;
+  g.a_elems = d->a_elems; g.b_elems = d->b_elems; g.c_elems = d->c_elems;
+  g.mblocks = d->m / 128;
+  g.nblocks = d->n / 128;
+  g.out_bf16 = d->out_dtype == EJ_BF16;
+  PairSrc src{lidx, ridx, perm, seg_off, n_a_tiles, n_b_tiles, nullptr, nullptr, 0};
+  return launch_seg_gemm_t<SegOpSplitB<128, 128>, 1, 2, 4, 3>(A, B, out, src, g, n_seg, stream);
 }
 
 extern "C" int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype,

@@ -127,6 +127,15 @@ int segment_einsum_split(const ej_einsum_desc *d, const float *A, const uint16_t
                          int64_t n_seg, const int32_t *run_order, int32_t order_group, void *out,
                          hipStream_t stream);
 
+// The same for an exactly-bf16 lhs with free-dimension-contiguous [k][m]
+// tiles against an fp32 rhs [k][n] (the rhs is split), one segment per
+// workgroup.
+bool segment_einsum_split_b_ok(const ej_einsum_desc *d, const void *A, const void *B);
+int segment_einsum_split_b(const ej_einsum_desc *d, const uint16_t *A, const float *B,
+                           int64_t n_a_tiles, int64_t n_b_tiles, const int64_t *lidx,
+                           const int64_t *ridx, const int32_t *perm, const int32_t *seg_off,
+                           int64_t n_seg, void *out, hipStream_t stream);
+
 // Zeroes n bytes (a multiple of 4, 4-byte aligned) with a kernel rather than
 // hipMemsetAsync, which misbehaves when a caller records the call into a
 // HIP graph.

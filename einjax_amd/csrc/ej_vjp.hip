@@ -512,11 +512,16 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
   const bool split = dtype == EJ_BF16 && grad_dtype == EJ_F32 && grad_lhs && n_lhs_tiles > 0 &&
                      n_rhs_tiles > 0 && n_pairs > 0 &&
                      segment_einsum_split_ok(&dl, grad_out, rhs_values);
+  // The same for the rhs gradient on [k][m] lhs blocks against the fp32
+  // cotangent (segment_einsum_split_b): the lhs is not widened.
+  const bool split_b = dtype == EJ_BF16 && grad_dtype == EJ_F32 && grad_rhs && n_rhs_tiles > 0 &&
+                       n_lhs_tiles > 0 && n_pairs > 0 &&
+                       segment_einsum_split_b_ok(&dr, lhs_values, grad_out);
   if (dtype == EJ_BF16 && grad_dtype == EJ_F32) {
     // Otherwise, with an fp32 cotangent and bf16 operands, the operands are
     // widened to fp32 once so the gradient einsums run in fp32 throughout.
     // (A bf16 cotangent runs them on bf16 operands with fp32 sums.)
-    if (grad_rhs && n_lhs_tiles > 0) {
+    if (grad_rhs && n_lhs_tiles > 0 && !split_b) {
       hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_capped(n_lhs_tiles * lhs_elems)),
                          dim3(kBlock), 0, stream, static_cast<const uint16_t *>(lhs_values),
                          w.lhs32, n_lhs_tiles * lhs_elems);
@@ -564,6 +569,11 @@ extern "C" int ej_pair_einsum_vjp(const char *kernel_string, const int64_t *lhs_
     if (!grad_rhs || n_rhs_tiles == 0) return EJ_OK;
     if (n_pairs == 0 || n_lhs_tiles == 0) return zero(grad_rhs, n_rhs_tiles * rhs_elems, st);
     EJ_TRY(index_plan(rhs_idx, n_pairs, n_rhs_tiles, w.perm_r, w.off_r, w.plan_r, st));
+    if (split_b)
+      return segment_einsum_split_b(&dr, static_cast<const uint16_t *>(lhs_values),
+                                    static_cast<const float *>(grad_out), n_lhs_tiles, n_pairs,
+                                    lhs_idx, nullptr, w.perm_r, w.off_r, n_rhs_tiles, grad_rhs,
+                                    st);
     return ej_segment_einsum(&dr, edt, lhs_v, grad_out, n_lhs_tiles, n_pairs, lhs_idx, nullptr,
                              w.perm_r, w.off_r, n_rhs_tiles, grad_rhs,
                              reinterpret_cast<ej_stream_t>(st));

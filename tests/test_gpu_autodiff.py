@@ -331,3 +331,14 @@ def test_vjp_lhs_gradient_ragged(gpu, n_lhs, n_pairs, seed):
         0, li[sel], prod64)
     assert rel_l2(gl.cpu().numpy(), want64.cpu().numpy()) <= 1e-5
     assert not gl[torch.from_numpy(untouched).cuda()].any()
+    # and the rhs gradient under it (the cotangent split as the rhs of
+    # 'ij,ik->jk', whose lhs tiles are read transposed)
+    _, gr = D.pair_einsum_vjp("ij,jk->ik", lv, rv, li, ri, g32, need_lhs=False)
+    assert gr.dtype == torch.float32
+    prodr = torch.bmm(lv[li[sel]].double().transpose(1, 2).contiguous(), g32[sel].double())
+    wantr = torch.zeros((n_rhs, 128, 128), dtype=torch.float64, device="cuda").index_add_(
+        0, ri[sel], prodr)
+    assert rel_l2(gr.cpu().numpy(), wantr.cpu().numpy()) <= 1e-5
+    untouched_r = np.setdiff1d(np.arange(n_rhs), ri_h[ok])
+    if untouched_r.size:
+        assert not gr[torch.from_numpy(untouched_r).cuda()].any()
