@@ -549,7 +549,10 @@ int ej_index_plan(const int64_t *idx, int64_t n, int64_t n_targets, int32_t *per
  * operands (a label of A found in neither C nor B) gives EJ_E_INVAL, as the
  * reference's jnp.einsum raises.  dtype (EJ_F32 / EJ_BF16) is the dtype of
  * the operand values; grad_dtype that of grad_out, grad_lhs and grad_rhs:
- * EJ_F32 (bf16 operands are then widened to fp32 in the workspace), or
+ * EJ_F32 (with bf16 operands each fp32 value is then split into three
+ * bf16 terms that sum to it exactly and the einsums run bf16 MFMAs with fp32
+ * sums, the precision of fp32 products; layouts the split kernels do not
+ * cover widen the operands to fp32 in the workspace), or
  * EJ_BF16 with bf16 operands (the reference's dtype for bf16 values: the
  * einsums run on bf16 operands and each gradient is rounded once).
  * Asynchronous on `stream`.  With both gradients requested, part of the work
