@@ -43,7 +43,8 @@ def rel_from_dense(dense, tile):
 @pytest.mark.parametrize("n,targets", [(1, 1), (1000, 7), (70000, 5000), (5, 0),
                                        (65536, 4094), (30000, 1), (0, 9), (65537, 10),
                                        (200, 4095), (1025, 3), (40000, 16127), (40000, 16128),
-                                       (3000, 200000)])
+                                       (3000, 200000), (32768, 4863), (32769, 100),
+                                       (20000, 4864), (2, 4863), (32768, 0), (26208, 4096)])
 def test_index_plan_parity(gpu, n, targets):
     note("index_plan", n, targets)
     rng = np.random.default_rng(n)
