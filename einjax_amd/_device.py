@@ -15,6 +15,7 @@ import ctypes
 import threading
 from math import prod
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -606,36 +607,40 @@ def scheme_stats(tile_shapes, shape, dense: torch.Tensor | None = None,
     shape, over the nonzero elements of a dense tensor or of COO entries."""
     lib = _lib.load()
     nd = len(shape)
-    tile_shapes = [tuple(int(t) for t in ts) for ts in tile_shapes]
     S = len(tile_shapes)
     if S == 0:
         return [], []
+    # numpy buffers: with 1,728 tile shapes, Python lists and ctypes arrays
+    # cost milliseconds per call on the host
+    ts = np.asarray(tile_shapes, dtype=np.int64)
+    if ts.shape != (S, nd):
+        raise ValueError(f"tile shapes must all have {nd} dims, got an array of shape {ts.shape}")
+    flat = np.ascontiguousarray(ts).reshape(-1)
     sh = i64_array(shape)
-    flat = i64_array([t for ts in tile_shapes for t in ts])
-    nt = (ctypes.c_int64 * S)()
-    vc = (ctypes.c_int64 * (S * nd))()
+    nt = np.zeros(S, dtype=np.int64)
+    vc = np.zeros(S * nd, dtype=np.int64)
+    p_flat, p_nt, p_vc = (a.ctypes.data_as(_lib._P_i64) for a in (flat, nt, vc))
     nbytes = ctypes.c_size_t()
     if dense is not None:
         dense = dense.contiguous()
-        check(lib.ej_scheme_stats_workspace_size(nd, sh, S, flat, -1, 0, ctypes.byref(nbytes)),
+        check(lib.ej_scheme_stats_workspace_size(nd, sh, S, p_flat, -1, 0, ctypes.byref(nbytes)),
               "ej_scheme_stats_workspace_size")
         ws = workspace(nbytes.value, dense.device)
-        check(lib.ej_scheme_stats_dense(ptr(dense), _elem_code(dense), nd, sh, S, flat, ptr(ws),
-                                        ws.numel(), nt, vc, stream_ptr()),
+        check(lib.ej_scheme_stats_dense(ptr(dense), _elem_code(dense), nd, sh, S, p_flat, ptr(ws),
+                                        ws.numel(), p_nt, p_vc, stream_ptr()),
               "ej_scheme_stats_dense")
     else:
         indices = indices.to(dtype=torch.int32).reshape(-1, nd).contiguous()
         values = values.contiguous().reshape(-1)
         n = values.numel()
-        check(lib.ej_scheme_stats_workspace_size(nd, sh, S, flat, n, bitmap_cap,
+        check(lib.ej_scheme_stats_workspace_size(nd, sh, S, p_flat, n, bitmap_cap,
                                                  ctypes.byref(nbytes)),
               "ej_scheme_stats_workspace_size")
         ws = workspace(nbytes.value, values.device)
         check(lib.ej_scheme_stats_coo(ptr(indices), ptr(values), _elem_code(values), n, nd, sh,
-                                      S, flat, bitmap_cap, ptr(ws), ws.numel(), nt, vc,
+                                      S, p_flat, bitmap_cap, ptr(ws), ws.numel(), p_nt, p_vc,
                                       stream_ptr()), "ej_scheme_stats_coo")
-    return ([int(nt[s]) for s in range(S)],
-            [tuple(int(vc[s * nd + l]) for l in range(nd)) for s in range(S)])
+    return nt.tolist(), list(map(tuple, vc.reshape(S, nd).tolist()))
 
 
 def index_plan(idx: torch.Tensor, n_targets: int) -> tuple[torch.Tensor, torch.Tensor]:
