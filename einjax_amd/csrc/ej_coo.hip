@@ -854,6 +854,126 @@ __global__ __launch_bounds__(256) void pool_chain_kernel(const uint32_t *__restr
   }
 }
 
+// A run of poolings by 2 along the next-to-last dimension, each pooled map
+// counted along its last-dimension chain, in one pass: each wave takes one
+// 16384-bit chunk (256 bits per lane) of 2^H consecutive rows of the input
+// map (a row = the last dimension's map bits, a multiple of 16384), ors them
+// pairwise level by level in registers, counts the nonempty groups of 2^k
+// bits of every pooled row for k = 1 .. levels[h] as pool_chain_kernel does
+// (and, for h >= 1, the pooled map's own bits), and writes only the level-H
+// row.  Level 0's chain is counted when `first` is set (its map's own bits
+// were counted by its producer).  Counts: per lane, then one atomic per
+// counter and block.
+constexpr int kBandMax = 3;  // row levels per launch: bands of 8 rows
+
+struct BandArgs {
+  int32_t H, first;
+  int32_t levels[kBandMax + 1];
+  int64_t rows_out, row_bits;
+  unsigned long long *chain[kBandMax + 1][kChainMax];
+  unsigned long long *pop[kBandMax + 1];
+};
+
+__global__ __launch_bounds__(256) void band_chain_kernel(const uint32_t *__restrict__ in,
+                                                         BandArgs a, uint32_t *__restrict__ out) {
+  constexpr int NR = 1 << kBandMax;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int H = a.H, nb = 1 << H;
+  const int64_t cpr = a.row_bits / kChainChunk;  // chunks per row
+  const int64_t items = a.rows_out * cpr;
+  uint32_t cnt[kBandMax + 1][kChainMax + 1];  // [h][0]: the map's bits, [h][k]: chain level k
+#pragma unroll
+  for (int h = 0; h <= kBandMax; ++h)
+#pragma unroll
+    for (int k = 0; k <= kChainMax; ++k) cnt[h][k] = 0;
+  auto count = [&](const uint64_t (&m)[4], int h) {
+    cnt[h][0] += __popcll(m[0]) + __popcll(m[1]) + __popcll(m[2]) + __popcll(m[3]);
+    uint64_t g[4] = {m[0], m[1], m[2], m[3]};
+#pragma unroll
+    for (int k = 1; k <= 6; ++k) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        g[r] = (g[r] | (g[r] >> (1 << (k - 1)))) & level_mask(k);
+        c += __popcll(g[r]);
+      }
+      cnt[h][k] += c;
+    }
+    cnt[h][7] += static_cast<uint32_t>((g[0] | g[1]) + (g[2] | g[3]));
+    const bool any = (g[0] | g[1] | g[2] | g[3]) != 0;
+    cnt[h][8] += any ? 1u : 0u;
+    uint64_t gb = __ballot(any);
+#pragma unroll
+    for (int k = 9; k <= 14; ++k) {
+      gb = (gb | (gb >> (1 << (k - 9)))) & level_mask(k - 8);
+      if (lane == 0) cnt[h][k] += __popcll(gb);
+    }
+  };
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * 4;
+  for (int64_t it = static_cast<int64_t>(blockIdx.x) * 4 + wave; it < items; it += n_waves) {
+    const int64_t band = it / cpr, c = it - band * cpr;
+    uint64_t m[NR][4];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (r < nb) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(in) +
+                           ((band * nb + r) * a.row_bits + c * kChainChunk + lane * 256) / 128;
+        const uint4 v0 = src[0], v1 = src[1];
+        m[r][0] = static_cast<uint64_t>(v0.x) | static_cast<uint64_t>(v0.y) << 32;
+        m[r][1] = static_cast<uint64_t>(v0.z) | static_cast<uint64_t>(v0.w) << 32;
+        m[r][2] = static_cast<uint64_t>(v1.x) | static_cast<uint64_t>(v1.y) << 32;
+        m[r][3] = static_cast<uint64_t>(v1.z) | static_cast<uint64_t>(v1.w) << 32;
+      }
+    }
+    if (a.first) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+        if (r < nb) count(m[r], 0);
+    }
+#pragma unroll
+    for (int h = 1; h <= kBandMax; ++h) {
+      if (h <= H) {
+#pragma unroll
+        for (int i = 0; i < (NR >> h); ++i) {
+          if (i < (nb >> h)) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) m[i][q] = m[2 * i][q] | m[2 * i + 1][q];
+            count(m[i], h);
+          }
+        }
+      }
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(out) + (band * a.row_bits + c * kChainChunk + lane * 256) / 128;
+    dst[0] = make_uint4(static_cast<uint32_t>(m[0][0]), static_cast<uint32_t>(m[0][0] >> 32),
+                        static_cast<uint32_t>(m[0][1]), static_cast<uint32_t>(m[0][1] >> 32));
+    dst[1] = make_uint4(static_cast<uint32_t>(m[0][2]), static_cast<uint32_t>(m[0][2] >> 32),
+                        static_cast<uint32_t>(m[0][3]), static_cast<uint32_t>(m[0][3] >> 32));
+  }
+  // Block totals: bits and levels 1-8 summed over the lanes, 9-14 held by lane 0.
+  __shared__ unsigned long long part[4][kBandMax + 1][kChainMax + 1];
+#pragma unroll
+  for (int h = 0; h <= kBandMax; ++h)
+#pragma unroll
+    for (int k = 0; k <= kChainMax; ++k) {
+      unsigned long long v = cnt[h][k];
+      if (k <= 8) {
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+      }
+      if (lane == 0) part[wave][h][k] = v;
+    }
+  __syncthreads();
+  for (int e = threadIdx.x; e < (kBandMax + 1) * (kChainMax + 1); e += 256) {
+    const int h = e / (kChainMax + 1), k = e % (kChainMax + 1);
+    if (h > H) continue;
+    unsigned long long *dst = nullptr;
+    if (k == 0) dst = h >= 1 ? a.pop[h] : nullptr;
+    else if (k <= a.levels[h] && (h >= 1 || a.first)) dst = a.chain[h][k - 1];
+    const unsigned long long t = part[0][h][k] + part[1][h][k] + part[2][h][k] + part[3][h][k];
+    if (dst && t) atomicAdd(dst, t);
+  }
+}
+
 // Tile index of entry i for the tile shape in ti; false when the entry is
 // dropped (value 0) or lies outside the tensor (then *bad is set).
 template <typename T>
@@ -1244,9 +1364,72 @@ int run_chain(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream) 
   return EJ_OK;
 }
 
-int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream) {
+// The kid of v pooled from it by 2 along dimension nd - 2, or -1.
+int row_pool_kid(const StatsPlan &pl, int v) {
+  if (pl.nd < 2) return -1;
+  for (int k : pl.nodes[v].kids) {
+    const StatNode &c = pl.nodes[k];
+    if (c.kind == kPool && c.pdim == pl.nd - 2 && c.pfac == 2) return k;
+  }
+  return -1;
+}
+
+// From materialised node v, a run of up to kBandMax row poolings (v's row
+// pool kid, its row pool kid, ...) whose inner nodes have no kids but their
+// chain and their row pool, every chain of at most kChainMax levels and map
+// rows a multiple of kChainChunk bits: one band_chain_kernel launch counts
+// the chains of the run (v's unless chain_done) and the inner and last
+// nodes' bits, and writes the last node's map.  *end = that node, or -1
+// when no run applies.
+int run_band(const StatsPlan &pl, int v, bool chain_done, const StatsWs &w, hipStream_t stream,
+             int *end) {
+  *end = -1;
+  if (pl.nd < 2) return EJ_OK;
+  const int64_t row_bits = pl.shape[pl.nd - 1] / pl.nodes[v].ts[pl.nd - 1];
+  if (row_bits % kChainChunk != 0 || chain_of(pl, v).size() > static_cast<size_t>(kChainMax))
+    return EJ_OK;
+  std::vector<int> run{v};
+  while (static_cast<int>(run.size()) <= kBandMax) {
+    const int u = run.back();
+    const int k = row_pool_kid(pl, u);
+    if (k < 0 || chain_of(pl, k).size() > static_cast<size_t>(kChainMax)) break;
+    if (u != v) {  // u becomes an inner node: nothing else may need its map
+      bool pure = true;
+      for (int c : pl.nodes[u].kids) pure = pure && (c == k || pl.nodes[c].kind == kChain);
+      if (!pure) break;
+    }
+    run.push_back(k);
+  }
+  const int H = static_cast<int>(run.size()) - 1;
+  if (H < 1) return EJ_OK;
+  BandArgs a{};
+  a.H = H;
+  a.first = chain_done ? 0 : 1;
+  a.row_bits = row_bits;
+  a.rows_out = pl.nodes[run[H]].cells / row_bits;
+  for (int h = 0; h <= H; ++h) {
+    const std::vector<int> ch = chain_of(pl, run[h]);
+    a.levels[h] = static_cast<int32_t>(ch.size());
+    for (size_t k = 0; k < ch.size(); ++k) a.chain[h][k] = w.counts + ch[k] * kCountStride;
+    a.pop[h] = h >= 1 ? w.counts + run[h] * kCountStride : nullptr;
+  }
+  const int64_t items = a.rows_out * (row_bits / kChainChunk);
+  hipLaunchKernelGGL(band_chain_kernel,
+                     dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(items, 4), 4096))),
+                     dim3(256), 0, stream, w.stack + pl.nodes[v].off / 4, a,
+                     w.stack + pl.nodes[run[H]].off / 4);
+  EJ_LAUNCH_CHECK();
+  *end = run[H];
+  return EJ_OK;
+}
+
+int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream,
+                bool chain_done = false) {
   const StatNode &n = pl.nodes[v];
-  bool chained = false;
+  int end = -1;
+  EJ_TRY(run_band(pl, v, chain_done, w, stream, &end));
+  const int banded = end >= 0 ? row_pool_kid(pl, v) : -1;  // handled by the band run
+  bool chained = chain_done || end >= 0;
   for (int k : n.kids) {
     const StatNode &kid = pl.nodes[k];
     if (kid.kind == kChain) {
@@ -1254,10 +1437,12 @@ int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream
       chained = true;
       continue;
     }
+    if (k == banded) continue;
     EJ_TRY(launch_pool(pl, kid, w.stack + n.off / 4, w.stack + kid.off / 4,
                        w.counts + k * kCountStride, stream));
     EJ_TRY(run_subtree(pl, k, w, stream));
   }
+  if (end >= 0) EJ_TRY(run_subtree(pl, end, w, stream, true));
   return EJ_OK;
 }
 
