@@ -974,6 +974,107 @@ __global__ __launch_bounds__(256) void band_chain_kernel(const uint32_t *__restr
   }
 }
 
+// The same for map rows shorter than a chunk (256 .. 8192 bits, whole
+// chunks in the map): a chunk holds 16384 / row_bits consecutive rows, row r
+// in lanes [r lpr, (r + 1) lpr) with lpr = row_bits / 256, and 2^H <= that
+// many rows form a band inside it.  Level h ors each lane with the lane
+// lpr 2^(h-1) away (every lane of a group of 2^h rows then holds the group's
+// or); the first row's lanes of each group count it, the others are masked.
+__global__ __launch_bounds__(256) void band_chain_small_kernel(const uint32_t *__restrict__ in,
+                                                               BandArgs a,
+                                                               uint32_t *__restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int H = a.H;
+  const int lpr = static_cast<int>(a.row_bits / 256);
+  const int row = lane / lpr;
+  const int64_t chunks = (a.rows_out << H) * a.row_bits / kChainChunk;
+  uint32_t cnt[kBandMax + 1][kChainMax + 1];
+#pragma unroll
+  for (int h = 0; h <= kBandMax; ++h)
+#pragma unroll
+    for (int k = 0; k <= kChainMax; ++k) cnt[h][k] = 0;
+  auto count = [&](const uint64_t (&m)[4], bool live, int h) {
+    uint64_t g[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) g[r] = live ? m[r] : 0;
+    cnt[h][0] += __popcll(g[0]) + __popcll(g[1]) + __popcll(g[2]) + __popcll(g[3]);
+#pragma unroll
+    for (int k = 1; k <= 6; ++k) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        g[r] = (g[r] | (g[r] >> (1 << (k - 1)))) & level_mask(k);
+        c += __popcll(g[r]);
+      }
+      cnt[h][k] += c;
+    }
+    cnt[h][7] += static_cast<uint32_t>((g[0] | g[1]) + (g[2] | g[3]));
+    const bool any = (g[0] | g[1] | g[2] | g[3]) != 0;
+    cnt[h][8] += any ? 1u : 0u;
+    uint64_t gb = __ballot(any);
+#pragma unroll
+    for (int k = 9; k <= 14; ++k) {
+      gb = (gb | (gb >> (1 << (k - 9)))) & level_mask(k - 8);
+      if (lane == 0) cnt[h][k] += __popcll(gb);
+    }
+  };
+  auto xor_lanes = [](uint64_t v, int d) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), d, 64);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), d, 64);
+    return static_cast<uint64_t>(lo) | static_cast<uint64_t>(hi) << 32;
+  };
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * 4;
+  for (int64_t ch = static_cast<int64_t>(blockIdx.x) * 4 + wave; ch < chunks; ch += n_waves) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(in) + (ch * kChainChunk + lane * 256) / 128;
+    const uint4 v0 = src[0], v1 = src[1];
+    uint64_t m[4];
+    m[0] = static_cast<uint64_t>(v0.x) | static_cast<uint64_t>(v0.y) << 32;
+    m[1] = static_cast<uint64_t>(v0.z) | static_cast<uint64_t>(v0.w) << 32;
+    m[2] = static_cast<uint64_t>(v1.x) | static_cast<uint64_t>(v1.y) << 32;
+    m[3] = static_cast<uint64_t>(v1.z) | static_cast<uint64_t>(v1.w) << 32;
+    if (a.first) count(m, true, 0);
+#pragma unroll
+    for (int h = 1; h <= kBandMax; ++h) {
+      if (h <= H) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) m[q] |= xor_lanes(m[q], lpr << (h - 1));
+        count(m, (row & ((1 << h) - 1)) == 0, h);
+      }
+    }
+    if ((row & ((1 << H) - 1)) == 0) {
+      const int64_t bit = ch * (kChainChunk >> H) + static_cast<int64_t>(row >> H) * a.row_bits +
+                          static_cast<int64_t>(lane % lpr) * 256;
+      uint4 *dst = reinterpret_cast<uint4 *>(out) + bit / 128;
+      dst[0] = make_uint4(static_cast<uint32_t>(m[0]), static_cast<uint32_t>(m[0] >> 32),
+                          static_cast<uint32_t>(m[1]), static_cast<uint32_t>(m[1] >> 32));
+      dst[1] = make_uint4(static_cast<uint32_t>(m[2]), static_cast<uint32_t>(m[2] >> 32),
+                          static_cast<uint32_t>(m[3]), static_cast<uint32_t>(m[3] >> 32));
+    }
+  }
+  __shared__ unsigned long long part[4][kBandMax + 1][kChainMax + 1];
+#pragma unroll
+  for (int h = 0; h <= kBandMax; ++h)
+#pragma unroll
+    for (int k = 0; k <= kChainMax; ++k) {
+      unsigned long long v = cnt[h][k];
+      if (k <= 8) {
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+      }
+      if (lane == 0) part[wave][h][k] = v;
+    }
+  __syncthreads();
+  for (int e = threadIdx.x; e < (kBandMax + 1) * (kChainMax + 1); e += 256) {
+    const int h = e / (kChainMax + 1), k = e % (kChainMax + 1);
+    if (h > H) continue;
+    unsigned long long *dst = nullptr;
+    if (k == 0) dst = h >= 1 ? a.pop[h] : nullptr;
+    else if (k <= a.levels[h] && (h >= 1 || a.first)) dst = a.chain[h][k - 1];
+    const unsigned long long t = part[0][h][k] + part[1][h][k] + part[2][h][k] + part[3][h][k];
+    if (dst && t) atomicAdd(dst, t);
+  }
+}
+
 // Tile index of entry i for the tile shape in ti; false when the entry is
 // dropped (value 0) or lies outside the tensor (then *bad is set).
 template <typename T>
@@ -1376,20 +1477,27 @@ int row_pool_kid(const StatsPlan &pl, int v) {
 
 // From materialised node v, a run of up to kBandMax row poolings (v's row
 // pool kid, its row pool kid, ...) whose inner nodes have no kids but their
-// chain and their row pool, every chain of at most kChainMax levels and map
-// rows a multiple of kChainChunk bits: one band_chain_kernel launch counts
-// the chains of the run (v's unless chain_done) and the inner and last
-// nodes' bits, and writes the last node's map.  *end = that node, or -1
-// when no run applies.
+// chain and their row pool, every chain of at most kChainMax levels: one
+// launch counts the chains of the run (v's unless chain_done) and the inner
+// and last nodes' bits, and writes the last node's map.  Map rows of whole
+// chunks take band_chain_kernel; rows of 256 .. 8192 bits in a map of whole
+// chunks take band_chain_small_kernel, with at most a chunk's rows per
+// band.  *end = the last node, or -1 when no run applies.
 int run_band(const StatsPlan &pl, int v, bool chain_done, const StatsWs &w, hipStream_t stream,
              int *end) {
   *end = -1;
   if (pl.nd < 2) return EJ_OK;
   const int64_t row_bits = pl.shape[pl.nd - 1] / pl.nodes[v].ts[pl.nd - 1];
-  if (row_bits % kChainChunk != 0 || chain_of(pl, v).size() > static_cast<size_t>(kChainMax))
+  const bool whole = row_bits % kChainChunk == 0;
+  const bool small = !whole && row_bits >= 256 && kChainChunk % row_bits == 0 &&
+                     pl.nodes[v].cells % kChainChunk == 0;
+  if ((!whole && !small) || chain_of(pl, v).size() > static_cast<size_t>(kChainMax))
     return EJ_OK;
+  int hmax = kBandMax;
+  if (small)
+    while (hmax > 0 && (int64_t(1) << hmax) > kChainChunk / row_bits) --hmax;
   std::vector<int> run{v};
-  while (static_cast<int>(run.size()) <= kBandMax) {
+  while (static_cast<int>(run.size()) <= hmax) {
     const int u = run.back();
     const int k = row_pool_kid(pl, u);
     if (k < 0 || chain_of(pl, k).size() > static_cast<size_t>(kChainMax)) break;
@@ -1413,11 +1521,15 @@ int run_band(const StatsPlan &pl, int v, bool chain_done, const StatsWs &w, hipS
     for (size_t k = 0; k < ch.size(); ++k) a.chain[h][k] = w.counts + ch[k] * kCountStride;
     a.pop[h] = h >= 1 ? w.counts + run[h] * kCountStride : nullptr;
   }
-  const int64_t items = a.rows_out * (row_bits / kChainChunk);
-  hipLaunchKernelGGL(band_chain_kernel,
-                     dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(items, 4), 4096))),
-                     dim3(256), 0, stream, w.stack + pl.nodes[v].off / 4, a,
-                     w.stack + pl.nodes[run[H]].off / 4);
+  const int64_t items = small ? pl.nodes[v].cells / kChainChunk
+                              : a.rows_out * (row_bits / kChainChunk);
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(items, 4), 4096)));
+  if (small)
+    hipLaunchKernelGGL(band_chain_small_kernel, grid, dim3(256), 0, stream,
+                       w.stack + pl.nodes[v].off / 4, a, w.stack + pl.nodes[run[H]].off / 4);
+  else
+    hipLaunchKernelGGL(band_chain_kernel, grid, dim3(256), 0, stream,
+                       w.stack + pl.nodes[v].off / 4, a, w.stack + pl.nodes[run[H]].off / 4);
   EJ_LAUNCH_CHECK();
   *end = run[H];
   return EJ_OK;
@@ -1428,6 +1540,9 @@ int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream
   const StatNode &n = pl.nodes[v];
   int end = -1;
   EJ_TRY(run_band(pl, v, chain_done, w, stream, &end));
+  // The band run's last map sits where v's row pool kid's subtree would, and
+  // v's other kids reuse that stack space: its subtree runs first.
+  if (end >= 0) EJ_TRY(run_subtree(pl, end, w, stream, true));
   const int banded = end >= 0 ? row_pool_kid(pl, v) : -1;  // handled by the band run
   bool chained = chain_done || end >= 0;
   for (int k : n.kids) {
@@ -1442,7 +1557,6 @@ int run_subtree(const StatsPlan &pl, int v, const StatsWs &w, hipStream_t stream
                        w.counts + k * kCountStride, stream));
     EJ_TRY(run_subtree(pl, k, w, stream));
   }
-  if (end >= 0) EJ_TRY(run_subtree(pl, end, w, stream, true));
   return EJ_OK;
 }
 

@@ -183,11 +183,14 @@ def test_scipy_to_relation_without_densifying(gpu):
 # counting pass; (4, 96, 32): chains from every (a, b, 1) map and odd factors;
 # (64, 16384), (4, 16, 16384), (8, 32768), (6, 16384): map rows of whole
 # 16384-bit chunks, so runs of row poolings are banded (one and two chunks per
-# row, a leading dimension with its own pools, a row count with a factor 3).
+# row, a leading dimension with its own pools, a row count with a factor 3);
+# (8, 64, 2048), (2, 32, 512), (64, 256): rows of 2048, 512 and 256 bits,
+# banded inside a chunk.
 STAT_SHAPES = [((12, 18), 0.05), ((8, 6, 10), 0.02), ((30,), 0.2), ((7, 4), 0.3),
                ((64, 48), 0.002), ((2, 3, 4, 5), 0.1), ((16, 16), 0.0), ((1, 1), 1.0),
                ((3, 65536), 0.0005), ((4, 96, 32), 0.01), ((64, 16384), 0.0005),
-               ((4, 16, 16384), 0.0003), ((8, 32768), 0.0002), ((6, 16384), 0.001)]
+               ((4, 16, 16384), 0.0003), ((8, 32768), 0.0002), ((6, 16384), 0.001),
+               ((8, 64, 2048), 0.0003), ((2, 32, 512), 0.002), ((64, 256), 0.01)]
 
 
 @pytest.mark.parametrize("dtype", ["f64", "f32", "bf16"])
