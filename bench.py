@@ -27,6 +27,7 @@ Usage: python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--no-cpu-baseline
 from __future__ import annotations
 
 import argparse
+import contextlib
 import gc
 import json
 import os
@@ -44,6 +45,24 @@ METRIC = "effective TFLOP/s (nnz tiles) + HBM GB/s per einsum, 1 MI355X vs host 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+@contextlib.contextmanager
+def gc_paused():
+    """Python's cyclic collector paused, after one collection, for a timed
+    region.  A full collection in a process holding torch takes ~50-65 ms on
+    the host (170k tracked objects); the host wrapper's allocations trigger
+    one every few hundred to few thousand calls, and it then lands in
+    whichever timed call triggered it (a ~3 ms average over 20 calls)."""
+    if not gc.isenabled():  # already paused by an enclosing region
+        yield
+        return
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
 
 
 def fused_in_step_ms(execute_sparse, lhs, rhs, jk, ks, ak, reps: int):
@@ -95,14 +114,15 @@ def warm_up(fn, ms: float = 30.0, min_calls: int = 2) -> None:
 def wall_time_ms(fn, reps: int, warm: int = 1) -> float:
     import torch
 
-    for _ in range(warm):
-        fn()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        fn()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / reps
+    with gc_paused():
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps
 
 
 def load_traffic(kernel: str):
@@ -260,12 +280,13 @@ def measure_config(name: str, reps: int = 20, warm: int = 10) -> dict:
     def step():
         return execute_sparse(lhs, rhs, jk, ks, ak)
 
-    warm_up(step, min_calls=warm)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        step()
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / reps
+    with gc_paused():
+        warm_up(step, min_calls=warm)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            step()
+        torch.cuda.synchronize()
+        ms_step = (time.perf_counter() - t0) * 1e3 / reps
     lc, rc = lhs.coords, rhs.coords
     li, ri = sd._join_dev(lhs, rhs, jk, lc, rc)
     P = li.numel()
@@ -474,6 +495,12 @@ def main():
         cpu = cpu_baseline(w, band_tiles=16)
 
     # ---- stages ----------------------------------------------------------
+    # The collector runs now and is then off until the timed steps end: a
+    # collection inside a timed region adds its ~60 ms to that region, and
+    # one between the warm-up and the timed steps idles the GPU long enough
+    # (tens of ms) for its clocks to drop, so that the timed steps start cold.
+    gc.collect()
+    gc.disable()
     lc, rc = lhs.coords, rhs.coords
     li, ri = sd._join_dev(lhs, rhs, jk, lc, rc)
     P = li.numel()
@@ -510,12 +537,6 @@ def main():
         lambda *a, **k: execute_sparse(*a, out_dtype=torch.float32, **k), lhs, rhs, jk, ks, ak,
         20)
     torch.cuda.synchronize()
-    # The collector runs now and is then off until the timed steps end: a
-    # collection between the warm-up and the timed steps idles the GPU long
-    # enough (tens of ms) for its clocks to drop, and the timed steps then
-    # start cold.
-    gc.collect()
-    gc.disable()
     # The fused einsum as the step launches it (after the device-side join
     # and plan, in the plan's run order): HIP events on the launch stream,
     # 200 queued steps, right before the warm-up steps: its ~40 ms of

@@ -22,6 +22,11 @@ from . import _lib
 from ._lib import check, i32_array, i64_array
 
 _VALUE_DTYPES = {torch.float32: _lib.EJ_F32, torch.bfloat16: _lib.EJ_BF16}
+# Tile einsums also take int32 tiles (integer arithmetic, int32 results).
+_EINSUM_DTYPES = {**_VALUE_DTYPES, torch.int32: _lib.EJ_I32}
+# Segment sums keep the values' dtype.
+_SEGSUM_DTYPES = {**_VALUE_DTYPES, torch.float64: _lib.EJ_F64, torch.float16: _lib.EJ_F16,
+                  torch.int32: _lib.EJ_I32, torch.int64: _lib.EJ_I64}
 
 
 _gpu_checked = False
@@ -56,6 +61,14 @@ def value_code(t: torch.Tensor) -> int:
         return _VALUE_DTYPES[t.dtype]
     except KeyError:
         raise TypeError(f"tile values must be float32 or bfloat16 on the device, got {t.dtype}")
+
+
+def einsum_code(t: torch.Tensor) -> int:
+    try:
+        return _EINSUM_DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError("tile einsum values must be float32, bfloat16 or int32 on the device, "
+                        f"got {t.dtype}")
 
 
 def as_coords(t: torch.Tensor, device) -> torch.Tensor:
@@ -179,6 +192,11 @@ def _set_out_dtype(desc, values: torch.Tensor, out_dtype) -> torch.dtype:
     operands' own dtype (float32, or bfloat16 for bfloat16 tiles), as the
     reference's jnp.einsum returns.  Written into the descriptor."""
     dt = values.dtype if out_dtype is None else out_dtype
+    if values.dtype == torch.int32 or dt == torch.int32:
+        if dt != values.dtype:
+            raise TypeError(f"int32 tiles give int32 results, not {dt}")
+        desc.out_dtype = _lib.EJ_I32
+        return dt
     if dt not in _VALUE_DTYPES:
         raise TypeError(f"einsum outputs are float32 or bfloat16, got {dt}")
     desc.out_dtype = _VALUE_DTYPES[dt]
@@ -188,8 +206,9 @@ def _set_out_dtype(desc, values: torch.Tensor, out_dtype) -> torch.dtype:
 def pair_einsum(desc, lhs_values, rhs_values, lhs_idx=None, rhs_idx=None, n_pairs=None,
                 out_dtype=None):
     """[P, *out_tile]: the tile einsum of every matched pair, summed in fp32,
-    in out_dtype (default: the operands' dtype)."""
-    code = value_code(lhs_values)
+    in out_dtype (default: the operands' dtype); int32 tiles give int32
+    results, formed with wrapping integer arithmetic."""
+    code = einsum_code(lhs_values)
     if rhs_values.dtype != lhs_values.dtype:
         raise TypeError("both operands must have the same value dtype")
     P = lhs_idx.numel() if lhs_idx is not None else int(n_pairs)
@@ -204,8 +223,9 @@ def pair_einsum(desc, lhs_values, rhs_values, lhs_idx=None, rhs_idx=None, n_pair
 def segment_einsum(desc, lhs_values, rhs_values, lhs_idx, rhs_idx, perm, seg_offsets,
                    out_dtype=None):
     """[U, *out_tile]: fused gather + tile einsum + segment sum, summed in
-    fp32, in out_dtype (default: the operands' dtype)."""
-    code = value_code(lhs_values)
+    fp32 (int32 tiles: in wrapping integer arithmetic), in out_dtype
+    (default: the operands' dtype)."""
+    code = einsum_code(lhs_values)
     if rhs_values.dtype != lhs_values.dtype:
         raise TypeError("both operands must have the same value dtype")
     U = seg_offsets.numel() - 1
@@ -232,6 +252,12 @@ class _Counts(threading.local):
 _counts = _Counts()
 
 
+def _next_ticket(ticket: int) -> int:
+    """The ticket after `ticket`: 1 .. 2^30 - 1, cycling (the plans take
+    tickets below 2^30)."""
+    return ticket % ((1 << 30) - 1) + 1
+
+
 def _count_buffer():
     """(host address, int64[8] view, new ticket) of this thread's count buffer."""
     if not _counts.addr:
@@ -239,7 +265,7 @@ def _count_buffer():
         check(_lib.load().ej_host_alloc(64, ctypes.byref(p)), "ej_host_alloc")
         _counts.addr = p.value
         _counts.view = (ctypes.c_int64 * 8).from_address(p.value)
-    _counts.ticket = _counts.ticket % (1 << 30) + 1
+    _counts.ticket = _next_ticket(_counts.ticket)
     return _counts.addr, _counts.view, _counts.ticket
 
 
@@ -349,9 +375,11 @@ def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_k
 
 
 class _DenseCounts(threading.local):
-    """Per-thread device counters of the dense plan, one buffer per device:
-    zeroed once, left zero by every plan (its first entry is the segment
-    count the einsum behind it reads)."""
+    """Per-thread device counters of the dense plan, one buffer per (device,
+    stream): zeroed once, left zero by every plan.  Its first entry is the
+    segment count that the einsum queued behind the plan reads while it runs,
+    so a buffer is only ever reused by work queued after that einsum on the
+    same stream; a step queued on another stream gets a buffer of its own."""
 
     bufs: dict = {}
 
@@ -362,10 +390,11 @@ class _DenseCounts(threading.local):
 _dense_state = _DenseCounts()
 
 
-def _dense_counts(dev) -> torch.Tensor:
-    buf = _dense_state.bufs.get(dev)
+def _dense_counts(dev, stream: int) -> torch.Tensor:
+    key = (dev, stream)
+    buf = _dense_state.bufs.get(key)
     if buf is None:
-        buf = _dense_state.bufs[dev] = torch.zeros(8, dtype=torch.int64, device=dev)
+        buf = _dense_state.bufs[key] = torch.zeros(8, dtype=torch.int64, device=dev)
     return buf
 
 
@@ -422,7 +451,7 @@ def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, 
     ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
     coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
     offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
-    dcounts = _dense_counts(dev)
+    dcounts = _dense_counts(dev, stream.value)
     odt = _set_out_dtype(desc, lhs_values, out_dtype)
     out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
     gq = ctypes.c_int32(1)
@@ -476,9 +505,15 @@ def _wait_packed_ticket(view, ticket: int) -> int:
 
 
 def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:
-    """[U, *tile] in the pair values' dtype (float32 or bfloat16): per-segment
-    sums in plan order, formed in fp32."""
-    code = value_code(pair_values)
+    """[U, *tile] in the pair values' dtype: per-segment sums in plan order,
+    formed in fp32 for float32 / bfloat16 values (a bf16 sum rounded once),
+    in the values' own arithmetic for float64, float16 (each addition rounded
+    to float16, as numpy adds float16) and int32 / int64 (wrapping)."""
+    try:
+        code = _SEGSUM_DTYPES[pair_values.dtype]
+    except KeyError:
+        raise TypeError(f"segment sums take float64, float32, float16, bfloat16, int32 or int64 "
+                        f"values on the device, got {pair_values.dtype}")
     U = seg_offsets.numel() - 1
     tile = tuple(pair_values.shape[1:])
     out = torch.empty((U, *tile), dtype=pair_values.dtype, device=pair_values.device)

@@ -23,6 +23,9 @@ EJ_E_RANGE = -5
 EJ_F32 = 0
 EJ_BF16 = 1
 EJ_F64 = 2
+EJ_I32 = 3
+EJ_I64 = 4
+EJ_F16 = 5
 
 EJ_ORDER_PROBE = 0
 EJ_ORDER_SORTED = 1

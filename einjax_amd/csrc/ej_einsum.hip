@@ -1740,11 +1740,35 @@ struct GenDesc {
   int32_t out_bf16;
 };
 
-template <typename T>
+// Arithmetic of the generic kernel.  Floating tiles (fp32, bf16): products
+// and sums in fp32, the result stored as fp32 or rounded once to bf16.
+// Integer tiles (int32): products and sums in two's-complement 32-bit
+// arithmetic, wrapping on overflow as an integer dot in XLA does (formed in
+// uint32_t, where wrapping is defined; the order of the terms then cannot
+// change the result).
+struct GenFloat {
+  using acc = float;
+  template <typename T>
+  __device__ static float load(const T *p) { return to_f32(*p); }
+  __device__ static void store(void *C, int64_t i, float v, bool bf16) {
+    if (bf16) put_out(static_cast<uint16_t *>(C) + i, v);
+    else put_out(static_cast<float *>(C) + i, v);
+  }
+};
+struct GenInt32 {
+  using acc = uint32_t;
+  __device__ static uint32_t load(const int32_t *p) { return static_cast<uint32_t>(*p); }
+  __device__ static void store(void *C, int64_t i, uint32_t v, bool) {
+    static_cast<int32_t *>(C)[i] = static_cast<int32_t>(v);
+  }
+};
+
+template <typename T, class Ar = GenFloat>
 __global__ __launch_bounds__(256) void generic_einsum_kernel(const T *__restrict__ A,
                                                              const T *__restrict__ B,
                                                              void *__restrict__ C, PairSrc src,
                                                              GenDesc d) {
+  using Acc = typename Ar::acc;
   const int64_t seg = blockIdx.x / d.eblocks;
   const int64_t e = (blockIdx.x % d.eblocks) * 256 + threadIdx.x;
   if (e >= d.c_elems || seg_dead(src, seg)) return;
@@ -1757,17 +1781,17 @@ __global__ __launch_bounds__(256) void generic_einsum_kernel(const T *__restrict
   }
   int64_t q0, q1;
   seg_range(src, seg, &q0, &q1);
-  float acc = 0.f;
+  Acc acc = 0;
   for (int64_t q = q0; q < q1; ++q) {
     int64_t at, bt;
     if (!pair_tiles(src, q, &at, &bt)) continue;
     const T *a = A + at * d.a_elems + aoff;
     const T *b = B + bt * d.b_elems + boff;
-    float pacc = 0.f;
+    Acc pacc = 0;
     int64_t idx[EJ_MAX_LABELS] = {0};
     int64_t ra = 0, rb = 0;
     for (int64_t r = 0; r < d.red_total; ++r) {
-      pacc += to_f32(a[ra]) * to_f32(b[rb]);
+      pacc += Ar::load(a + ra) * Ar::load(b + rb);
       // odometer increment over the contracted labels (last fastest)
       for (int i = d.n_red - 1; i >= 0; --i) {
         idx[i]++;
@@ -1781,8 +1805,7 @@ __global__ __launch_bounds__(256) void generic_einsum_kernel(const T *__restrict
     }
     acc += pacc;
   }
-  if (d.out_bf16) put_out(static_cast<uint16_t *>(C) + seg * d.c_elems + e, acc);
-  else put_out(static_cast<float *>(C) + seg * d.c_elems + e, acc);
+  Ar::store(C, seg * d.c_elems + e, acc, d.out_bf16 != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -2088,7 +2111,12 @@ int run_generic(const ej_einsum_desc *d, int32_t dtype, const void *A, const voi
     set_error("einsum launch too large");
     return EJ_E_UNSUPPORTED;
   }
-  if (dtype == EJ_BF16)
+  if (dtype == EJ_I32)
+    hipLaunchKernelGGL((generic_einsum_kernel<int32_t, GenInt32>),
+                       dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream,
+                       static_cast<const int32_t *>(A), static_cast<const int32_t *>(B), C, src,
+                       g);
+  else if (dtype == EJ_BF16)
     hipLaunchKernelGGL(generic_einsum_kernel<uint16_t>, dim3(static_cast<unsigned>(nblk)), dim3(256),
                        0, stream, static_cast<const uint16_t *>(A),
                        static_cast<const uint16_t *>(B), C, src, g);
@@ -2155,10 +2183,12 @@ int ring_order_group(const ej_einsum_desc *d, int32_t dtype, int64_t n_seg, cons
 int einsum_common(const ej_einsum_desc *d, int32_t dtype, const void *A, const void *B,
                   const PairSrc &src, int64_t n_seg, void *C, hipStream_t stream) {
   EJ_CHECK_ARG(d, "desc is null");
-  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
-  EJ_CHECK_ARG(d->out_dtype == EJ_F32 || (d->out_dtype == EJ_BF16 && dtype == EJ_BF16),
-               "output dtype %d with operand dtype %d: outputs are fp32, or bf16 for bf16 "
-               "operands", d->out_dtype, dtype);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_I32, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG((dtype == EJ_I32) == (d->out_dtype == EJ_I32) &&
+                   (d->out_dtype == EJ_F32 || d->out_dtype == EJ_I32 ||
+                    (d->out_dtype == EJ_BF16 && dtype == EJ_BF16)),
+               "output dtype %d with operand dtype %d: outputs are fp32, bf16 for bf16 "
+               "operands, int32 for int32 operands", d->out_dtype, dtype);
   EJ_CHECK_ARG(n_seg >= 0, "negative count");
   EJ_CHECK_ARG(d->n_out >= 0 && d->n_out <= EJ_MAX_LABELS && d->n_red >= 0 &&
                    d->n_red <= EJ_MAX_LABELS && d->c_elems >= 1 && d->a_elems >= 1 &&
@@ -2168,7 +2198,7 @@ int einsum_common(const ej_einsum_desc *d, int32_t dtype, const void *A, const v
   EJ_CHECK_ARG(A && B && C, "null pointer argument");
   EJ_TRY(check_desc(d));
   int status = EJ_OK;
-  if (try_gemm(d, dtype, A, B, C, src, n_seg, stream, &status)) return status;
+  if (dtype != EJ_I32 && try_gemm(d, dtype, A, B, C, src, n_seg, stream, &status)) return status;
   return run_generic(d, dtype, A, B, C, src, n_seg, stream);
 }
 
@@ -2242,6 +2272,44 @@ __global__ __launch_bounds__(256) void segment_sum_scalar_kernel(const T *__rest
   for (int32_t q = off[seg]; q < off[seg + 1]; ++q)
     acc += to_f32(vals[static_cast<int64_t>(perm[q]) * tile_elems + e]);
   put_out(out + seg * tile_elems + e, acc);
+}
+
+// Segment sums kept in the values' own type, one element per thread, the
+// pair tiles added one after another in plan order: float64 (double sums,
+// so each element's sum is formed exactly as a sequential float64 loop
+// forms it) and int32 / int64 (two's-complement wrapping, formed unsigned).
+template <typename T, typename Acc>
+__global__ __launch_bounds__(256) void segment_sum_exact_kernel(const T *__restrict__ vals,
+                                                                int64_t tile_elems,
+                                                                const int32_t *perm,
+                                                                const int32_t *off,
+                                                                int64_t eblocks,
+                                                                T *__restrict__ out) {
+  const int64_t seg = blockIdx.x / eblocks;
+  const int64_t e = (blockIdx.x % eblocks) * 256 + threadIdx.x;
+  if (e >= tile_elems) return;
+  Acc acc = 0;
+  for (int32_t q = off[seg]; q < off[seg + 1]; ++q)
+    acc += static_cast<Acc>(vals[static_cast<int64_t>(perm[q]) * tile_elems + e]);
+  out[seg * tile_elems + e] = static_cast<T>(acc);
+}
+
+// float16 values: each addition formed in fp32 and rounded to float16, as
+// numpy adds float16 arrays (so each element's sum matches the reference's
+// sequential float16 additions bit for bit).
+__global__ __launch_bounds__(256) void segment_sum_f16_kernel(const _Float16 *__restrict__ vals,
+                                                              int64_t tile_elems,
+                                                              const int32_t *perm,
+                                                              const int32_t *off, int64_t eblocks,
+                                                              _Float16 *__restrict__ out) {
+  const int64_t seg = blockIdx.x / eblocks;
+  const int64_t e = (blockIdx.x % eblocks) * 256 + threadIdx.x;
+  if (e >= tile_elems) return;
+  _Float16 acc = 0;
+  for (int32_t q = off[seg]; q < off[seg + 1]; ++q)
+    acc = static_cast<_Float16>(static_cast<float>(acc) +
+                                static_cast<float>(vals[static_cast<int64_t>(perm[q]) * tile_elems + e]));
+  out[seg * tile_elems + e] = acc;
 }
 
 template <typename V>
@@ -2386,8 +2454,8 @@ extern "C" int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype
                                        int32_t *group) {
   clear_error();
   EJ_CHECK_ARG(desc && group, "null pointer argument");
-  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
-  *group = fused_group(desc, dtype);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_I32, "unknown dtype %d", dtype);
+  *group = dtype == EJ_I32 ? 1 : fused_group(desc, dtype);
   return EJ_OK;
 }
 
@@ -2396,7 +2464,9 @@ extern "C" int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t ti
                               int64_t n_segments, void *out, ej_stream_t stream_) {
   clear_error();
   hipStream_t stream = as_stream(stream_);
-  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16, "unknown dtype %d", dtype);
+  EJ_CHECK_ARG(dtype == EJ_F32 || dtype == EJ_BF16 || dtype == EJ_F64 || dtype == EJ_F16 ||
+                   dtype == EJ_I32 || dtype == EJ_I64,
+               "unknown dtype %d", dtype);
   EJ_CHECK_ARG(tile_elems >= 1 && n_segments >= 0, "bad sizes");
   if (n_segments == 0) return EJ_OK;
   EJ_CHECK_ARG(pair_values && perm && seg_offsets && out, "null pointer argument");
@@ -2405,7 +2475,26 @@ extern "C" int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t ti
     return EJ_E_UNSUPPORTED;
   }
   const bool vec = aligned16(pair_values) && aligned16(out);
-  if (dtype == EJ_F32 && vec && tile_elems % 4 == 0) {
+  if (dtype == EJ_F64 || dtype == EJ_F16 || dtype == EJ_I32 || dtype == EJ_I64) {
+    const int64_t eb = ceil_div(tile_elems, 256);
+    const dim3 grid(static_cast<unsigned>(n_segments * eb));
+    if (dtype == EJ_F16)
+      hipLaunchKernelGGL(segment_sum_f16_kernel, grid, dim3(256), 0, stream,
+                         static_cast<const _Float16 *>(pair_values), tile_elems, perm, seg_offsets,
+                         eb, static_cast<_Float16 *>(out));
+    else if (dtype == EJ_F64)
+      hipLaunchKernelGGL((segment_sum_exact_kernel<double, double>), grid, dim3(256), 0, stream,
+                         static_cast<const double *>(pair_values), tile_elems, perm, seg_offsets,
+                         eb, static_cast<double *>(out));
+    else if (dtype == EJ_I32)
+      hipLaunchKernelGGL((segment_sum_exact_kernel<int32_t, uint32_t>), grid, dim3(256), 0,
+                         stream, static_cast<const int32_t *>(pair_values), tile_elems, perm,
+                         seg_offsets, eb, static_cast<int32_t *>(out));
+    else
+      hipLaunchKernelGGL((segment_sum_exact_kernel<int64_t, uint64_t>), grid, dim3(256), 0,
+                         stream, static_cast<const int64_t *>(pair_values), tile_elems, perm,
+                         seg_offsets, eb, static_cast<int64_t *>(out));
+  } else if (dtype == EJ_F32 && vec && tile_elems % 4 == 0) {
     const int64_t tv = tile_elems / 4, eb = ceil_div(tv, 256);
     hipLaunchKernelGGL(segment_sum_vec4_kernel, dim3(static_cast<unsigned>(n_segments * eb)),
                        dim3(256), 0, stream, static_cast<const float4 *>(pair_values), tv,

@@ -56,12 +56,11 @@ def _dev(x, dtype=None):
 
 
 def _dev_values(v):
-    """Tile values on the GPU as float32, or bfloat16 when already bfloat16.
-    float64 and float16 become float32, as the reference's jnp.array turns
-    float64 relation values into float32 before its einsum
-    (sparse_dispatch.py:125).  Integer and boolean values raise TypeError:
-    the tile einsums and segment sums compute in floating point only, where
-    the reference would keep an integer dtype (:164-169)."""
+    """Floating tile values on the GPU as float32, or bfloat16 when already
+    bfloat16: float64 and float16 become float32, as the reference's
+    jnp.array turns float64 relation values into float32 before its einsum
+    (sparse_dispatch.py:125).  Integer and boolean values take
+    _einsum_operands / _segsum_operand, which keep integer arithmetic."""
     import torch
 
     dt = v.dtype if _is_torch(v) else torch.from_numpy(np.zeros(0, dtype=v.dtype)).dtype
@@ -72,6 +71,137 @@ def _dev_values(v):
     if t.dtype not in (torch.float32, torch.bfloat16):
         t = t.to(torch.float32)
     return t
+
+
+# ---------------------------------------------------------------------------
+# Value dtypes.  The reference hands host tile values to jnp.array with
+# 64-bit types off (float64 -> float32, int64 -> int32, uint64 -> uint32,
+# sparse_dispatch.py:125) and jnp.einsum promotes the two operands: with a
+# floating operand the result is floating (bfloat16 when every floating
+# operand is bfloat16, else float32; float16 stays float16), two integer
+# (or boolean) operands give their promoted integer type, computed with
+# wrapping integer arithmetic.  segment_sum keeps the values' own numpy
+# dtype (:164-169).  Integer einsums run on the library's int32 kernel: a
+# result of a narrower integer type is the int32 result truncated, which
+# equals the narrower wrapping arithmetic; a boolean result is "nonzero",
+# which equals the OR of ANDs of a boolean contraction.
+
+_CANON = {np.dtype(np.float64): np.dtype(np.float32), np.dtype(np.int64): np.dtype(np.int32),
+          np.dtype(np.uint64): np.dtype(np.uint32)}
+
+
+def _value_np_dtype(v):
+    """numpy dtype of an array's elements, or None for bfloat16 tensors."""
+    if _is_torch(v):
+        import torch
+
+        if v.dtype == torch.bfloat16:
+            return None
+        return torch.empty(0, dtype=v.dtype).numpy().dtype
+    return np.asarray(v).dtype
+
+
+def _kind(dt) -> str:
+    if dt is None or dt.kind == "f":
+        return "f"
+    if dt.kind in "iub":
+        return "i"
+    raise TypeError(f"tile values of dtype {dt} are not supported (floating, integer or "
+                    "boolean values are)")
+
+
+def _einsum_types(lhs_values, rhs_values):
+    """(compute, result) of the tile einsum on these values: compute is the
+    torch dtype both operands take on the device (float32, bfloat16 or
+    int32); result is the reference's result dtype (a torch dtype for
+    floating results, a numpy dtype for integer / boolean ones)."""
+    import torch
+
+    ld, rd = _value_np_dtype(lhs_values), _value_np_dtype(rhs_values)
+    kl, kr = _kind(ld), _kind(rd)
+    if "f" in (kl, kr):
+        floats = [d for d, k in ((ld, kl), (rd, kr)) if k == "f"]
+        if all(d is None for d in floats):
+            return torch.bfloat16, torch.bfloat16
+        if all(d is not None and d == np.float16 for d in floats):
+            return torch.float32, torch.float16
+        return torch.float32, torch.float32
+    res = np.promote_types(_CANON.get(ld, ld), _CANON.get(rd, rd))
+    return torch.int32, _CANON.get(res, res)
+
+
+def _int32_bits(v):
+    """Integer / boolean values as int32 on the device: the jnp.array
+    canonical value (64-bit types truncated to 32 bits), uint32 by its bits."""
+    import torch
+
+    if _is_torch(v):
+        t = v
+        if t.dtype in (torch.int64,):
+            t = t.to(torch.int32)
+        elif t.dtype == getattr(torch, "uint64", None):
+            t = t.view(torch.int64).to(torch.int32)
+        elif t.dtype == getattr(torch, "uint32", None):
+            t = t.view(torch.int32)
+        return _dev(t.to(torch.int32))
+    a = np.asarray(v)
+    a = a.astype(_CANON.get(a.dtype, a.dtype), copy=False)
+    a = a.view(np.int32) if a.dtype == np.uint32 else a.astype(np.int32)
+    return _dev(a)
+
+
+def _einsum_operands(lhs_values, rhs_values):
+    """(a, b, result): both operands on the device in the compute dtype of
+    _einsum_types, and the result dtype."""
+    import torch
+
+    compute, result = _einsum_types(lhs_values, rhs_values)
+    if compute == torch.int32:
+        return _int32_bits(lhs_values), _int32_bits(rhs_values), result
+
+    def flt(v):
+        dt = _value_np_dtype(v)
+        if dt is not None and dt.kind in "iub":
+            # jnp.array's integer canonicalisation first, then the promotion
+            # converts the integer's value
+            if _is_torch(v):
+                t = v.to(torch.int32) if v.dtype == torch.int64 else v
+                return _dev(t).to(compute)
+            a = np.asarray(v)
+            return _dev(a.astype(_CANON.get(a.dtype, a.dtype)).astype(np.float32)).to(compute)
+        return _dev_values(v).to(compute)
+
+    return flt(lhs_values), flt(rhs_values), result
+
+
+def _to_result(t, result):
+    """An einsum result computed in float32 / bfloat16 / int32 in the
+    reference's result dtype (on the device; uint32 as a torch uint32 view
+    where torch has the type)."""
+    import torch
+
+    if isinstance(result, torch.dtype):
+        return t if t.dtype == result else t.to(result)
+    if result == np.int32:
+        return t
+    if result == np.bool_:
+        return t != 0
+    if result == np.uint32:
+        u = getattr(torch, "uint32", None)
+        return t.view(u) if u is not None else t
+    return t.to(torch.from_numpy(np.zeros(0, dtype=result)).dtype)
+
+
+def _host_result(t, result):
+    """_to_result for host callers: a numpy array of the result dtype."""
+    import torch
+
+    if isinstance(result, torch.dtype):
+        return _host(_to_result(t, result))
+    a = t.cpu().numpy()
+    if result == np.uint32:
+        return a.view(np.uint32)
+    return a.astype(result)
 
 
 def _dev_coords(c, ndim):
@@ -91,14 +221,6 @@ def _host(t):
     if t.dtype == torch.bfloat16:
         t = t.float()
     return t.cpu().numpy()
-
-
-def _same_dtype(a, b):
-    import torch
-
-    if a.dtype != b.dtype:
-        return a.to(torch.float32), b.to(torch.float32)
-    return a, b
 
 
 def _grid(rel: SparseTensorRelation, d: int) -> int:
@@ -125,9 +247,58 @@ def _retry_radices(fn, make_radices, cols):
     for coords, d in cols:
         lo, hi = _device.coords_range(coords)
         if coords.shape[0] and lo[d] < 0:
-            raise ValueError("tile coordinates must be non-negative")
+            raise _NegativeCoords()
         maxima.append(hi[d] + 1 if coords.shape[0] else 1)
     return fn(make_radices(maxima))
+
+
+class _NegativeCoords(Exception):
+    """A joined or output coordinate column holds negative values.  The
+    kernels pack coordinates >= 0; the public functions catch this and run
+    again on coordinates shifted column by column (_shift_columns)."""
+
+
+def _column_shifts(lc, rc, keys, out_cols):
+    """Per-column shifts (<= 0) that make the coordinates the kernels pack
+    non-negative: columns linked by a join key share one shift (the minimum
+    over them), so equal keys stay equal and every order stays as it was.
+    keys: [(lhs_dim, rhs_dim)]; out_cols: [(0 | 1, dim)] also packed.
+    Returns (lhs shifts, rhs shifts)."""
+    lo = [_device.coords_range(c)[0] if c.shape[0] else [0] * c.shape[1] for c in (lc, rc)]
+    parent = {}
+
+    def find(x):
+        while parent.setdefault(x, x) != x:
+            x = parent[x]
+        return x
+
+    for a, b in keys:
+        parent[find((0, a))] = find((1, b))
+    low = {}
+    for side, cols in ((0, range(lc.shape[1])), (1, range(rc.shape[1]))):
+        for c in cols:
+            r = find((side, c))
+            low[r] = min(low.get(r, 0), lo[side][c])
+    shifts = ([0] * lc.shape[1], [0] * rc.shape[1])
+    used = {find((0, a)) for a, _ in keys} | {find((s, d)) for s, d in out_cols}
+    for side, n in ((0, lc.shape[1]), (1, rc.shape[1])):
+        for c in range(n):
+            r = find((side, c))
+            if r in used:
+                shifts[side][c] = low[r]
+    return shifts
+
+
+def _shift_columns(coords, shifts):
+    """coords - shifts, column by column (int32 on the device)."""
+    import torch
+
+    if not any(shifts) or coords.shape[0] == 0:
+        return coords
+    _, hi = _device.coords_range(coords)
+    if any(h - s >= 2 ** 31 for h, s in zip(hi, shifts)):
+        raise ValueError("coordinate range exceeds 2^31")
+    return coords - torch.tensor(shifts, dtype=torch.int32, device=coords.device)
 
 
 # ---------------------------------------------------------------------------
@@ -259,7 +430,15 @@ def coordinate_join(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_k
     host = _on_host(lhs, rhs)
     lc = _dev_coords(lhs.coords, lhs.ndim)
     rc = _dev_coords(rhs.coords, rhs.ndim)
-    li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
+    try:
+        li, ri = _join_dev(lhs, rhs, join_keys, lc, rc)
+    except _NegativeCoords:
+        keys = [tuple(k) for k in join_keys]
+        sl, sr = _column_shifts(lc, rc, keys, [])
+        lc, rc = _shift_columns(lc, sl), _shift_columns(rc, sr)
+        li, ri = _join_dev(SparseTensorRelation(lc, lhs.values, lhs.shape, lhs.tile_shape),
+                           SparseTensorRelation(rc, rhs.values, rhs.shape, rhs.tile_shape),
+                           keys, lc, rc)
     return (_host(li), _host(ri)) if host else (li, ri)
 
 
@@ -296,9 +475,13 @@ def _infer_output_tile_shape(kernel_string: str, lhs_tile_shape, rhs_tile_shape)
 
 def kernel_einsum(lhs_values, rhs_values, lhs_indices, rhs_indices, kernel_string: str):
     """einsum(kernel_string) of every matched tile pair, [P, *out_tile] of the
-    operands' dtype, as the reference's jnp.einsum returns (sparse_dispatch.py:
-    85-126): float32, or bfloat16 for bfloat16 tiles (summed in fp32 and
-    rounded once).  No pairs gives zeros of the lhs values' dtype."""
+    dtype the reference's jnp.einsum returns (sparse_dispatch.py:85-126):
+    float32 (float64 and float32 values, or a float with an integer),
+    bfloat16 for bfloat16 tiles (summed in fp32 and rounded once), float16
+    for float16 tiles (summed in fp32), or for integer / boolean tiles their
+    promoted integer type (int64 counted as int32, as jnp.array makes it),
+    computed with wrapping integer arithmetic.  No pairs gives zeros of the
+    lhs values' dtype."""
     host = _on_host(lhs_values, rhs_values, lhs_indices, rhs_indices)
     n = int(lhs_indices.shape[0]) if hasattr(lhs_indices, "shape") else len(lhs_indices)
     lt, rt = tuple(lhs_values.shape[1:]), tuple(rhs_values.shape[1:])
@@ -311,13 +494,13 @@ def kernel_einsum(lhs_values, rhs_values, lhs_indices, rhs_indices, kernel_strin
         return torch.zeros((0, *out_tile), dtype=lhs_values.dtype, device=lhs_values.device)
     _add_batch_dim(kernel_string)  # same ValueError as the reference for a missing "->"
     desc = _device.describe(kernel_string, lt, rt)
-    a, b = _same_dtype(_dev_values(lhs_values), _dev_values(rhs_values))
+    a, b, result = _einsum_operands(lhs_values, rhs_values)
     li = _dev(np.asarray(lhs_indices) if not _is_torch(lhs_indices) else lhs_indices)
     ri = _dev(np.asarray(rhs_indices) if not _is_torch(rhs_indices) else rhs_indices)
     import torch
 
     out = _device.pair_einsum(desc, a, b, li.to(torch.int64), ri.to(torch.int64))
-    return _host(out) if host else out
+    return _host_result(out, result) if host else _to_result(out, result)
 
 
 # ---------------------------------------------------------------------------
@@ -355,19 +538,68 @@ def _plan_from_coords(oc):
     agg = [(0, d) for d in range(nd)]
     if nd == 0:
         return _device.segment_plan(oc, oc, idx, idx, agg, [])
-    # No grid metadata: size the radices from the data directly.
+    # No grid metadata: size the radices from the data directly.  Negative
+    # coordinates are planned shifted by their column's minimum (the order of
+    # the unique coordinates does not change) and shifted back.
     lo, hi = _device.coords_range(oc)
-    if min(lo) < 0:
-        raise ValueError("output coordinates must be non-negative")
-    return _device.segment_plan(oc, oc, idx, idx, agg, [h + 1 for h in hi])
+    shift = [min(0, x) for x in lo]
+    if any(h - s >= 2 ** 31 for h, s in zip(hi, shift)):
+        raise ValueError("coordinate range exceeds 2^31")
+    if any(shift):
+        oc = _shift_columns(oc, shift)
+    coords, offsets, perm, seg_ids = _device.segment_plan(
+        oc, oc, idx, idx, agg, [h - s + 1 for h, s in zip(hi, shift)])
+    if any(shift):
+        coords = coords + torch.tensor(shift, dtype=torch.int32, device=coords.device)
+    return coords, offsets, perm, seg_ids
+
+
+def _segsum_operand(values):
+    """(values on the device in a dtype the library sums, result converter):
+    the library sums float64, float32, float16, bfloat16, int32 and int64
+    values in their own arithmetic; other integer types are summed as int32 /
+    int64 (unsigned ones by their bits) and truncated back, which equals
+    their own wrapping arithmetic; booleans are summed as int32 and read as
+    "nonzero", which equals numpy's boolean +=, a logical OR."""
+    import torch
+
+    if _is_torch(values):
+        t = _dev(values)
+        dt = t.dtype
+        if dt in (torch.float64, torch.float32, torch.float16, torch.bfloat16, torch.int32,
+                  torch.int64):
+            return t, lambda r: r
+        if dt == torch.bool:
+            return t.to(torch.int32), lambda r: r != 0
+        for u, w in ((getattr(torch, "uint32", None), torch.int32),
+                     (getattr(torch, "uint64", None), torch.int64)):
+            if u is not None and dt == u:
+                return t.view(w), lambda r, u=u: r.view(u)
+        if not dt.is_floating_point and not dt.is_complex:
+            return t.to(torch.int32), lambda r, dt=dt: r.to(dt)
+        raise TypeError(f"segment_sum does not take values of dtype {dt}")
+    a = np.ascontiguousarray(values)
+    dt = a.dtype
+    if dt in (np.float64, np.float32, np.float16, np.int32, np.int64):
+        return _dev(a), lambda r: r
+    if dt in (np.uint32, np.uint64):
+        w = np.int32 if dt == np.uint32 else np.int64
+        return _dev(a.view(w)), lambda r, dt=dt: r.cpu().numpy().view(dt)
+    if dt == np.bool_:
+        return _dev(a.astype(np.int32)), lambda r: r != 0
+    if dt.kind in "iu":
+        return _dev(a.astype(np.int32)), lambda r, dt=dt: r.cpu().numpy().astype(dt)
+    raise TypeError(f"segment_sum does not take values of dtype {dt}")
 
 
 def segment_sum(values, output_coords):
     """Sums the pair tiles of equal output coordinate (reference:
     sparse_dispatch.py:129-171).  Returns (unique_coords int32 [U, nd] in
     ascending lexicographic order, aggregated [U, *tile] in the values' dtype,
-    float32 or bfloat16, as the reference keeps it, :165); tiles are added in
-    pair order, as the reference does, in fp32."""
+    as the reference keeps it, :165); tiles are added in pair order, as the
+    reference does: float32 and bfloat16 values in fp32 (a bfloat16 sum
+    rounded once), float64 and float16 in their own arithmetic, integers with
+    wrapping, booleans as a logical OR.  Output coordinates may be negative."""
     import torch
 
     host = _on_host(values, output_coords)
@@ -379,10 +611,12 @@ def segment_sum(values, output_coords):
         return (torch.zeros((0, nd), dtype=torch.int32, device=values.device),
                 torch.zeros((0, *tile), dtype=values.dtype, device=values.device))
     oc = _dev_coords(output_coords, output_coords.shape[1] if output_coords.ndim > 1 else 0)
-    vals = _dev_values(values)
+    vals, back = _segsum_operand(values)
     coords, offsets, perm, _ = _plan_from_coords(oc)
-    agg = _device.segment_sum(vals, perm, offsets)
-    return (_host(coords), _host(agg)) if host else (coords, agg)
+    agg = back(_device.segment_sum(vals, perm, offsets))
+    if host:
+        return _host(coords), agg if isinstance(agg, np.ndarray) else _host(agg)
+    return coords, agg
 
 
 # ---------------------------------------------------------------------------
@@ -406,6 +640,43 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
                    kernel_string: str, agg_keys, output_shape=None, output_tile_shape=None, *,
                    fused: bool = True, out_dtype=None,
                    _einsum_events=None) -> SparseTensorRelation:
+    try:
+        return _execute_sparse(lhs, rhs, join_keys, kernel_string, agg_keys, output_shape,
+                               output_tile_shape, fused=fused, out_dtype=out_dtype,
+                               _einsum_events=_einsum_events)
+    except _NegativeCoords:
+        pass
+    # Negative joined or output coordinates: run on columns shifted to be
+    # non-negative (joined columns by one shift, so the pairs and their order
+    # are the same) and shift the output coordinates back.
+    host = _on_host(lhs, rhs)
+    keys = [tuple(k) for k in join_keys]
+    agg = [tuple(k) for k in agg_keys]
+    lc = _dev_coords(lhs.coords, lhs.ndim)
+    rc = _dev_coords(rhs.coords, rhs.ndim)
+    sl, sr = _column_shifts(lc, rc, keys, agg)
+    out = _execute_sparse(
+        SparseTensorRelation(_shift_columns(lc, sl), lhs.values, lhs.shape, lhs.tile_shape),
+        SparseTensorRelation(_shift_columns(rc, sr), rhs.values, rhs.shape, rhs.tile_shape),
+        keys, kernel_string, agg, output_shape, output_tile_shape, fused=fused,
+        out_dtype=out_dtype)
+    back = [(sl if s == 0 else sr)[d] for s, d in agg][:out.coords.shape[1]]
+    back += [0] * (out.coords.shape[1] - len(back))
+    if any(back) and out.coords.shape[0]:
+        if _is_torch(out.coords):
+            import torch
+
+            coords = out.coords + torch.tensor(back, dtype=torch.int32, device=out.coords.device)
+        else:
+            coords = (out.coords + np.asarray(back, dtype=np.int32)).astype(np.int32)
+        out = SparseTensorRelation(coords, out.values, out.shape, out.tile_shape)
+    return out.to_host() if host and out.is_device else out
+
+
+def _execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_keys,
+                    kernel_string: str, agg_keys, output_shape=None, output_tile_shape=None, *,
+                    fused: bool = True, out_dtype=None,
+                    _einsum_events=None) -> SparseTensorRelation:
     """Sparse tensor-relational einsum (reference: sparse_dispatch.py:226-297).
 
     join_keys: [(lhs_dim, rhs_dim)] contracted tile dims; kernel_string: the
@@ -420,7 +691,10 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     for bfloat16 tiles, rounded once from the fp32 sum); ``torch.float32``
     keeps fp32 results for bfloat16 tiles.  ``_einsum_events`` (measurement
     only): a list that collects timing events recorded around the fused
-    einsum of a queued call."""
+    einsum of a queued call.  Integer or boolean tiles (and a float with an
+    integer) follow the reference's jnp promotion (kernel_einsum) and run on
+    the library's integer kernel; joined and output coordinates may be
+    negative."""
     if output_tile_shape is None:
         output_tile_shape = _infer_output_tile_shape(kernel_string, lhs.tile_shape,
                                                      rhs.tile_shape)
@@ -436,10 +710,23 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     rc = _dev_coords(rhs.coords, rhs.ndim)
     n_out = len(output_tile_shape)
 
+    import torch
+
+    compute, result = _einsum_types(lhs.values, rhs.values)
+    integer = compute == torch.int32
+    if integer and out_dtype is not None:
+        raise TypeError("out_dtype applies to floating tiles; integer tiles give the "
+                        "reference's integer result dtype")
+    if out_dtype is None and compute != result:
+        fin = result  # computed in float32 / int32, returned in the reference's dtype
+    else:
+        fin = None
+
     def operands():
         desc = _device.describe(kernel_string, lhs.tile_shape, rhs.tile_shape)
         desc.seg_group = _segment_run(rhs, [tuple(k) for k in join_keys], agg)
-        return (desc, *_same_dtype(_dev_values(lhs.values), _dev_values(rhs.values)))
+        a, b, _ = _einsum_operands(lhs.values, rhs.values)
+        return desc, a, b
 
     def radices(maxima):
         out = []
@@ -455,9 +742,9 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     hint_key = None
     bound = None
     queued = None
-    if fused and keys and lc.shape[0] and rc.shape[0]:
+    if fused and keys and lc.shape[0] and rc.shape[0] and not integer:
         queued = _dense_step(lhs, rhs, keys, agg, lc, rc, operands, out_dtype, _einsum_events)
-    if queued is None and fused and keys and lc.shape[0] and rc.shape[0]:
+    if queued is None and fused and keys and lc.shape[0] and rc.shape[0] and not integer:
         j_rad = _join_radices(lhs, rhs, keys, None)
         hint_key = _hint_key(lhs, rhs, (tuple(lc.shape), tuple(rc.shape), tuple(keys),
                                         tuple(j_rad), tuple(agg)))
@@ -500,6 +787,12 @@ def execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_ke
     if tuple(vals.shape[1:]) != output_tile_shape and vals[0].numel() == int(
             np.prod(output_tile_shape)):
         vals = vals.reshape((vals.shape[0], *output_tile_shape))
+    if fin is not None:
+        if host:
+            out = SparseTensorRelation(_host(coords), _host_result(vals, fin), output_shape,
+                                       output_tile_shape)
+            return out
+        vals = _to_result(vals, fin)
     out = SparseTensorRelation(coords, vals, output_shape, output_tile_shape)
     return out.to_host() if host else out
 

@@ -9,7 +9,8 @@ from __future__ import annotations
 import numpy as np
 
 from .. import _device, _lib
-from ..execution.sparse_dispatch import _dev_coords, _host, _on_host
+from ..execution.sparse_dispatch import (_column_shifts, _dev_coords, _host, _on_host,
+                                         _shift_columns)
 
 
 def _norm(join_dims) -> list:
@@ -37,9 +38,14 @@ def _join(lhs_coords, rhs_coords, join_dims, order):
     if keys:
         llo, lhi = _device.coords_range(lc)
         rlo, rhi = _device.coords_range(rc)
+        if any(llo[a] < 0 or rlo[b] < 0 for a, b in keys):
+            # negative key columns: joined columns shifted by one common
+            # minimum, which keeps the match set and both pair orders
+            sl, sr = _column_shifts(lc, rc, keys, [])
+            lc, rc = _shift_columns(lc, sl), _shift_columns(rc, sr)
+            llo, lhi = _device.coords_range(lc)
+            rlo, rhi = _device.coords_range(rc)
         for a, b in keys:
-            if llo[a] < 0 or rlo[b] < 0:
-                raise ValueError("join-key coordinates must be non-negative")
             radices.append(max(lhi[a], rhi[b]) + 1)
     li, ri = _device.join(lc, rc, keys, radices, order)
     return (_host(li), _host(ri)) if host else (li, ri)

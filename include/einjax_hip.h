@@ -76,7 +76,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 12
+#define EJ_ABI_VERSION 13
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -87,7 +87,10 @@ extern "C" {
 
 #define EJ_F32 0
 #define EJ_BF16 1
-#define EJ_F64 2 /* tiling, COO ingest and to_dense only (the einsums take EJ_F32 / EJ_BF16) */
+#define EJ_F64 2 /* tiling, COO ingest, to_dense and ej_segment_sum */
+#define EJ_I32 3 /* integer tile einsums (ej_pair_einsum, ej_segment_einsum) and ej_segment_sum */
+#define EJ_I64 4 /* ej_segment_sum */
+#define EJ_F16 5 /* ej_segment_sum */
 
 /* Pair orders of the join.  With n_keys == 0 both give the cross product in
  * lhs-major order (sparse_dispatch.py:53-59, pallas_gather.py:50-54). */
@@ -132,7 +135,8 @@ typedef struct ej_einsum_desc {
   int64_t b_sb, b_sk, b_sn;
   int64_t c_sb, c_sm, c_sn;
   /* Output dtype, set by the caller (ej_einsum_describe writes EJ_F32):
-   * EJ_F32, or EJ_BF16 with bf16 operands (fp32 sums rounded once). */
+   * EJ_F32, or EJ_BF16 with bf16 operands (fp32 sums rounded once), or
+   * EJ_I32 with (and only with) EJ_I32 operands. */
   int32_t out_dtype;
   int32_t reserved;
 } ej_einsum_desc;
@@ -386,6 +390,10 @@ int ej_gather_tiles(const void *values, int64_t n_tiles, int64_t tile_bytes, con
  * run on the MFMA kernel; every other descriptor, or one whose is_gemm the
  * caller cleared, runs on the generic strided kernel.  A pair whose tile
  * index lies outside [0, n_*_tiles) contributes nothing.
+ * dtype EJ_I32 (int32 tiles, the reference's jnp arrays of integer values
+ * with 64-bit types off) runs on the generic kernel with products and sums
+ * in two's-complement int32, wrapping as an integer dot in XLA does; the
+ * descriptor's out_dtype must then be EJ_I32.
  * Per-pair mode: out[p] = einsum(lhs_values[lhs_idx[p]], rhs_values[rhs_idx[p]])
  * for p < n_pairs, [n_pairs, c_elems] of desc->out_dtype.  lhs_idx / rhs_idx
  * may be NULL, meaning pair p reads tile p (a gathered panel). */
@@ -431,8 +439,12 @@ int ej_segment_einsum_group(const ej_einsum_desc *desc, int32_t dtype, int32_t *
 /* ---- segment sum (reference: segment_sum accumulation, :164-171) -------- */
 /* out[u] = sum_{q in [seg_offsets[u], seg_offsets[u+1])} pair_values[perm[q]],
  * added sequentially in q order (the reference's order).  pair_values and out
- * are both of dtype (EJ_F32 or EJ_BF16, the reference keeps the values' dtype,
- * :165); the sums are formed in fp32 and a bf16 output is rounded once. */
+ * are both of dtype, the reference keeping the values' dtype (:165): EJ_F32
+ * or EJ_BF16 (sums formed in fp32, a bf16 output rounded once), EJ_F64 (sums
+ * in float64, each element's exactly as the reference's sequential numpy
+ * additions form it), EJ_F16 (each addition formed in fp32 and rounded to
+ * float16, as numpy adds float16) or EJ_I32 / EJ_I64 (two's-complement,
+ * wrapping as numpy's integer additions do). */
 int ej_segment_sum(const void *pair_values, int32_t dtype, int64_t tile_elems,
                    const int32_t *perm, const int32_t *seg_offsets, int64_t n_segments,
                    void *out, ej_stream_t stream);

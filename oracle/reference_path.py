@@ -283,6 +283,55 @@ def kernel_einsum(lhs_values, rhs_values, lhs_idx, rhs_idx, kernel_string, preci
     return batched_einsum(add_batch_dim(kernel_string), L, R).astype(dt, copy=False)
 
 
+# dtype of jnp.array(x) for a host array with JAX's default 64-bit types off
+_JNP_CANON = {np.dtype(np.float64): np.dtype(np.float32), np.dtype(np.int64): np.dtype(np.int32),
+              np.dtype(np.uint64): np.dtype(np.uint32)}
+
+
+def jnp_einsum_dtype(lhs_dtype, rhs_dtype):
+    """Result dtype of jnp.einsum(jnp.array(l), jnp.array(r)) with 64-bit
+    types off (execution/sparse_dispatch.py:125): each operand canonicalised
+    (float64 -> float32, int64 -> int32, uint64 -> uint32); a floating
+    operand makes the result floating (float16 with float16 or integers,
+    float32 otherwise); two integer or boolean operands give their promoted
+    type, canonicalised again."""
+    ld = _JNP_CANON.get(np.dtype(lhs_dtype), np.dtype(lhs_dtype))
+    rd = _JNP_CANON.get(np.dtype(rhs_dtype), np.dtype(rhs_dtype))
+    floats = [d for d in (ld, rd) if d.kind == "f"]
+    if floats:
+        return np.dtype(np.float16) if all(d == np.float16 for d in floats) else np.dtype(np.float32)
+    res = np.promote_types(ld, rd)
+    return _JNP_CANON.get(res, res)
+
+
+def kernel_einsum_typed(lhs_values, rhs_values, lhs_idx, rhs_idx, kernel_string):
+    """kernel_einsum (execution/sparse_dispatch.py:85-126) with the dtypes of
+    its jnp.array / jnp.einsum calls (:125) kept: a floating result is formed
+    in float64 and returned in jnp_einsum_dtype; an integer or boolean result
+    is formed exactly in int64 from the canonicalised operands and reduced to
+    the result type (truncation mod 2^bits, "nonzero" for booleans), which is
+    what wrapping arithmetic in the result type gives."""
+    lhs_values, rhs_values = np.asarray(lhs_values), np.asarray(rhs_values)
+    res = jnp_einsum_dtype(lhs_values.dtype, rhs_values.dtype)
+    lhs_idx = np.asarray(lhs_idx)
+    if len(lhs_idx) == 0:
+        shape = infer_output_tile_shape(kernel_string, lhs_values.shape[1:], rhs_values.shape[1:])
+        return np.zeros((0, *shape), dtype=lhs_values.dtype)
+
+    def canon(v):
+        return v.astype(_JNP_CANON.get(v.dtype, v.dtype))
+
+    L = canon(lhs_values)[lhs_idx]
+    R = canon(rhs_values)[np.asarray(rhs_idx)]
+    spec = add_batch_dim(kernel_string)
+    if res.kind == "f":
+        return np.einsum(spec, L.astype(np.float64), R.astype(np.float64)).astype(res)
+    exact = np.einsum(spec, L.astype(np.int64), R.astype(np.int64))
+    if res == np.bool_:
+        return exact != 0
+    return exact.astype(res)
+
+
 def reverse_einsum_string(kernel_string: str) -> tuple:
     """autodiff/custom_vjp.py:31-62: "A,B->C" -> ("C,B->A", "A,C->B");
     ValueError without "->"."""

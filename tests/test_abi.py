@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 12
+    assert _lib.load().ej_version() == 13
 
 
 def describe(spec, lt, rt):
@@ -270,8 +270,21 @@ def test_output_dtype_validation():
     d.out_dtype = 7
     assert lib.ej_pair_einsum(ctypes.byref(d), _lib.EJ_BF16, fake, fake, 1, 1, None, None, 0,
                               fake, None) == _lib.EJ_E_INVAL
-    assert lib.ej_segment_sum(fake, 5, 4, fake, fake, 0, fake, None) == _lib.EJ_E_INVAL
-    assert lib.ej_segment_sum(fake, _lib.EJ_BF16, 4, fake, fake, 0, fake, None) == _lib.EJ_OK
+    assert lib.ej_segment_sum(fake, 9, 4, fake, fake, 0, fake, None) == _lib.EJ_E_INVAL
+    for code in (_lib.EJ_BF16, _lib.EJ_F32, _lib.EJ_F64, _lib.EJ_F16, _lib.EJ_I32, _lib.EJ_I64):
+        assert lib.ej_segment_sum(fake, code, 4, fake, fake, 0, fake, None) == _lib.EJ_OK
+    # int32 tiles give int32 results and only int32 tiles do
+    d.out_dtype = _lib.EJ_F32
+    assert lib.ej_pair_einsum(ctypes.byref(d), _lib.EJ_I32, fake, fake, 1, 1, None, None, 0,
+                              fake, None) == _lib.EJ_E_INVAL
+    d.out_dtype = _lib.EJ_I32
+    assert lib.ej_pair_einsum(ctypes.byref(d), _lib.EJ_I32, fake, fake, 1, 1, None, None, 0,
+                              fake, None) == _lib.EJ_OK
+    assert lib.ej_pair_einsum(ctypes.byref(d), _lib.EJ_F32, fake, fake, 1, 1, None, None, 0,
+                              fake, None) == _lib.EJ_E_INVAL
+    g = ctypes.c_int32(0)
+    assert lib.ej_segment_einsum_group(ctypes.byref(d), _lib.EJ_I32, ctypes.byref(g)) == 0
+    assert g.value == 1
 
 
 def test_pair_plan_host_validation():
@@ -383,3 +396,17 @@ def test_segment_einsum_group():
     g = ctypes.c_int32(-1)
     assert lib.ej_segment_einsum_group(ctypes.byref(d), 7, ctypes.byref(g)) == _lib.EJ_E_INVAL
     assert lib.ej_segment_einsum_group(ctypes.byref(d), _lib.EJ_F32, None) == _lib.EJ_E_INVAL
+
+
+def test_plan_ticket_cycle_stays_below_the_plans_limit():
+    """The queued plans take tickets 1 .. 2^30 - 1 (ej_dense_plan_async rejects
+    2^30 and above); the host's ticket counter cycles inside that range."""
+    from einjax_amd import _device
+
+    t, seen = 0, set()
+    for _ in range(3):
+        t = _device._next_ticket(t)
+        seen.add(t)
+    assert seen == {1, 2, 3}
+    assert _device._next_ticket((1 << 30) - 2) == (1 << 30) - 1
+    assert _device._next_ticket((1 << 30) - 1) == 1

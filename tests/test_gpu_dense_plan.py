@@ -374,3 +374,30 @@ def test_dense_run_order_balances_xcds(gpu):
     assert max(loads) / np.mean(loads) < 1.03
     naive = [2 * 16 * lens[16 * x:16 * x + 16].sum() for x in range(8)]
     assert max(naive) / np.mean(naive) > 1.10
+
+
+def test_dense_steps_on_two_streams(gpu):
+    """Two dense steps of different sizes queued from one thread on two
+    streams, back to back without a wait between them: each stream's plan
+    has its own device counters, so both results equal the same steps run
+    alone on one stream, bitwise."""
+    note("dense steps on two streams")
+    wa = G.workload_blocksparse_16k(seed=4, m=2048, n=1024, density=0.2)
+    wb = G.workload_blocksparse_1k(n=512, tile=32, density=0.1)
+    runs = []
+    for w in (wa, wb):
+        lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
+        runs.append((lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"]))
+    alone = [ej.execute_sparse(*r) for r in runs]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            a = ej.execute_sparse(*runs[0])
+        with torch.cuda.stream(s2):
+            b = ej.execute_sparse(*runs[1])
+        torch.cuda.synchronize()
+        for got, want in ((a, alone[0]), (b, alone[1])):
+            assert torch.equal(got.coords, want.coords)
+            bits = torch.int16 if got.values.dtype == torch.bfloat16 else torch.int32
+            assert torch.equal(got.values.view(bits), want.values.view(bits))

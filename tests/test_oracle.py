@@ -546,3 +546,78 @@ def test_pair_einsum_vjp_finite_differences(spec, lt, rt):
     # tiles in no pair get zero gradient
     unused = np.setdiff1d(np.arange(nl), li)
     assert np.all(gl[unused] == 0)
+
+
+# ---------------------------------------------------------------------------
+# kernel_einsum with the reference's dtypes (jnp.array / jnp.einsum with 64-bit
+# types off, sparse_dispatch.py:125) and segment_sum in the values' dtype
+
+def test_kernel_einsum_typed_reference_single_pair():
+    # tests/test_rigorous.py:938-945: float64 identity with an int64 tile
+    lhs = np.eye(2).reshape(1, 2, 2)
+    rhs = np.array([[[1, 2], [3, 4]]])
+    out = R.kernel_einsum_typed(lhs, rhs, np.array([0]), np.array([0]), "ij,jk->ik")
+    assert out.dtype == np.float32
+    npt.assert_array_equal(out[0], [[1, 2], [3, 4]])
+
+
+@pytest.mark.parametrize("a,b,want", [
+    (np.int64, np.int64, np.int32), (np.int8, np.int8, np.int8), (np.uint8, np.int8, np.int16),
+    (np.int32, np.float64, np.float32), (np.uint32, np.int32, np.int32),
+    (np.bool_, np.bool_, np.bool_), (np.bool_, np.int8, np.int8), (np.float16, np.int8, np.float16),
+    (np.float16, np.float32, np.float32), (np.uint64, np.uint8, np.uint32),
+    (np.float64, np.float64, np.float32)])
+def test_jnp_einsum_dtype_table(a, b, want):
+    # JAX's promotion lattice with 64-bit types canonicalised to 32 bits
+    assert R.jnp_einsum_dtype(a, b) == np.dtype(want)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.int8, np.uint32])
+def test_kernel_einsum_typed_wraps_like_fixed_width_ints(dt):
+    # brute force in Python integers, reduced mod 2^bits of the result type
+    rng = np.random.default_rng(3)
+    info = np.iinfo(dt)
+    lo, hi = max(info.min, -2 ** 31), min(info.max, 2 ** 31 - 1)
+    L = rng.integers(lo, hi, size=(3, 3, 4), endpoint=True).astype(dt)
+    Rt = rng.integers(lo, hi, size=(2, 4, 2), endpoint=True).astype(dt)
+    li, ri = np.array([0, 2, 1]), np.array([1, 0, 1])
+    out = R.kernel_einsum_typed(L, Rt, li, ri, "ij,jk->ik")
+    res = R.jnp_einsum_dtype(dt, dt)
+    assert out.dtype == res
+    bits = np.iinfo(res).bits
+    for p in range(3):
+        a = [[int(x) for x in row] for row in L[li[p]]]
+        b = [[int(x) for x in row] for row in Rt[ri[p]]]
+        if dt in (np.int64, np.uint64):  # jnp.array truncates 64-bit ints to 32 bits first
+            a = [[x % 2 ** 32 - (2 ** 32 if dt == np.int64 and x % 2 ** 32 >= 2 ** 31 else 0)
+                  for x in row] for row in a]
+            b = [[x % 2 ** 32 - (2 ** 32 if dt == np.int64 and x % 2 ** 32 >= 2 ** 31 else 0)
+                  for x in row] for row in b]
+        for i in range(3):
+            for k in range(2):
+                v = sum(a[i][j] * b[j][k] for j in range(4)) % 2 ** bits
+                got = int(out[p, i, k]) % 2 ** bits
+                assert got == v
+
+
+def test_kernel_einsum_typed_bool_is_or_of_and():
+    rng = np.random.default_rng(4)
+    L = rng.random((2, 3, 5)) < 0.3
+    Rt = rng.random((2, 5, 4)) < 0.3
+    out = R.kernel_einsum_typed(L, Rt, np.array([0, 1]), np.array([1, 0]), "ij,jk->ik")
+    assert out.dtype == np.bool_
+    for p, (a, b) in enumerate(((0, 1), (1, 0))):
+        want = [[any(L[a, i, j] and Rt[b, j, k] for j in range(5)) for k in range(4)]
+                for i in range(3)]
+        npt.assert_array_equal(out[p], want)
+
+
+def test_segment_sum_keeps_integer_dtype_and_wraps():
+    # tests/test_rigorous.py:958-963 (ints, single entry) and wrapping as numpy adds int8
+    coords, agg = R.segment_sum(np.array([[[1, 2], [3, 4]]]), np.array([[0, 0]]))
+    assert agg.dtype == np.array([1]).dtype
+    npt.assert_array_equal(agg[0], [[1, 2], [3, 4]])
+    v = np.array([[100], [100], [-7]], dtype=np.int8)
+    _, agg = R.segment_sum(v, np.array([[0], [0], [1]]))
+    assert agg.dtype == np.int8
+    npt.assert_array_equal(agg[:, 0], [np.int8(-56), -7])  # 200 mod 256 = -56
