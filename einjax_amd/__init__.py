@@ -3,12 +3,14 @@
 The public names mirror the reference package's sparse-path exports
 (reference: __init__.py:9-86 and kernels/__init__.py): einsum / analyze,
 relations, dense and sparse tensor metadata and tile-shape selection, the
-three-phase execute_sparse, the kernel registry, the block-sparse matmul
+three-phase execute_sparse, the execution engine over chains of sparse
+steps, the kernel registry, the block-sparse matmul
 and the coordinate joins.  All computation runs in
 libejhip.so (HIP kernels behind a C ABI, include/einjax_hip.h).
 """
 
 from .autodiff import sparse_einsum, sparse_einsum_raw, sparse_einsum_raw_vjp
+from .execution.engine import ExecutionEngine, build_dependency_graph, topological_sort
 from .execution.sparse_dispatch import (
     coordinate_join,
     execute_sharded_sparse,
@@ -65,4 +67,5 @@ __all__ = [
     "kernel_einsum", "segment_sum", "execute_sparse", "execute_sharded_sparse", "KernelRegistry",
     "KernelInfo", "block_sparse_matmul", "block_sparse_matmul_generic", "coordinate_join_hash",
     "coordinate_join_sorted", "sparse_einsum", "sparse_einsum_raw", "sparse_einsum_raw_vjp",
+    "ExecutionEngine", "build_dependency_graph", "topological_sort",
 ]

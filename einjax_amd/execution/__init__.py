@@ -1,5 +1,6 @@
 """The sparse execution path."""
 
+from .engine import ExecutionEngine, build_dependency_graph, topological_sort
 from .sparse_dispatch import (
     coordinate_join,
     execute_sharded_sparse,
@@ -9,4 +10,5 @@ from .sparse_dispatch import (
 )
 
 __all__ = ["coordinate_join", "kernel_einsum", "segment_sum", "execute_sparse",
-           "execute_sharded_sparse"]
+           "execute_sharded_sparse", "ExecutionEngine", "build_dependency_graph",
+           "topological_sort"]

@@ -37,6 +37,15 @@ class TilingScheme:
     cost: float = 0.0
     comm: float = 0.0
     flops: float = 0.0
+    accumulated_cost: float = 0.0
+    accumulated_comm: float = 0.0
+    accumulated_flops: float = 0.0
+    # dependency tracking: the schemes this one is computed from (the
+    # execution engine walks them)
+    source: tuple = field(default_factory=tuple)
+    dependencies: set = field(default_factory=set)
+    partition_spec: Any = None
+    mesh_axes: Any = None
 
     def __post_init__(self):
         self.shape = tuple(self.shape)
