@@ -8,10 +8,15 @@ for device memory and the current HIP stream only.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libejhip.so"
+# A host-side test run may load the sanitized host-only build instead
+# (einjax_amd/csrc/build.py --sanitize); nothing else sets this.
+if os.environ.get("EINJAX_AMD_SANITIZED_LIB"):
+    LIB_PATH = Path(os.environ["EINJAX_AMD_SANITIZED_LIB"])
 
 EJ_OK = 0
 EJ_E_INVAL = -1

@@ -33,7 +33,28 @@ void clear_error();
     }                                                                          \
   } while (0)
 
-#define EJ_LAUNCH_CHECK() EJ_HIP(hipGetLastError())
+// ---- fault injection -----------------------------------------------------
+// EJ_INJECT_FAULT (environment, read at every check): a comma-separated list
+// of sites that then fail as if the HIP runtime had returned an error there:
+//   host_alloc  hipHostMalloc in ej_host_alloc (hipErrorOutOfMemory)
+//   launch      every kernel launch check (hipErrorLaunchFailure; the
+//               kernel itself was enqueued)
+// It lets tests drive the EJ_E_HIP paths, status and message, without a
+// failing device.  Unset, every check is a plain hipGetLastError.
+bool fault_injected(const char *site);
+
+#define EJ_LAUNCH_CHECK()                                                      \
+  do {                                                                         \
+    const bool inj_ = ::ej::fault_injected("launch");                          \
+    hipError_t e_ = inj_ ? hipErrorLaunchFailure : hipGetLastError();          \
+    if (e_ != hipSuccess) {                                                    \
+      ::ej::set_error("kernel launch failed: %s%s (%s:%d)",                    \
+                      hipGetErrorString(e_),                                   \
+                      inj_ ? " (injected by EJ_INJECT_FAULT)" : "", __FILE__,  \
+                      __LINE__);                                               \
+      return EJ_E_HIP;                                                         \
+    }                                                                          \
+  } while (0)
 
 #define EJ_TRY(expr)                                                           \
   do {                                                                         \

@@ -2,6 +2,8 @@
 // prefix primitives, plus the library's error state and version entry points.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "ej_internal.h"
 
@@ -19,6 +21,20 @@ void set_error(const char *fmt, ...) {
 }
 
 void clear_error() { g_error.clear(); }
+
+bool fault_injected(const char *site) {
+  const char *env = getenv("EJ_INJECT_FAULT");
+  if (!env || !*env) return false;
+  const size_t n = strlen(site);
+  for (const char *p = env; *p;) {
+    const char *end = strchr(p, ',');
+    const size_t len = end ? static_cast<size_t>(end - p) : strlen(p);
+    if (len == n && strncmp(p, site, n) == 0) return true;
+    if (!end) break;
+    p = end + 1;
+  }
+  return false;
+}
 
 __global__ void zero_words_kernel(uint32_t *p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -374,9 +390,13 @@ extern "C" int ej_host_alloc(size_t bytes, void **host_ptr) {
     return EJ_E_INVAL;
   }
   *host_ptr = nullptr;
-  const hipError_t e = hipHostMalloc(host_ptr, bytes, hipHostMallocMapped | hipHostMallocCoherent);
+  const bool injected = ej::fault_injected("host_alloc");
+  const hipError_t e = injected ? hipErrorOutOfMemory
+                                : hipHostMalloc(host_ptr, bytes,
+                                                hipHostMallocMapped | hipHostMallocCoherent);
   if (e != hipSuccess) {
-    ej::set_error("hipHostMalloc failed: %s", hipGetErrorString(e));
+    ej::set_error("hipHostMalloc failed: %s%s", hipGetErrorString(e),
+                  injected ? " (injected by EJ_INJECT_FAULT)" : "");
     return EJ_E_HIP;
   }
   return EJ_OK;

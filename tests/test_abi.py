@@ -410,3 +410,38 @@ def test_plan_ticket_cycle_stays_below_the_plans_limit():
     assert seen == {1, 2, 3}
     assert _device._next_ticket((1 << 30) - 2) == (1 << 30) - 1
     assert _device._next_ticket((1 << 30) - 1) == 1
+
+
+def test_injected_host_alloc_failure(monkeypatch):
+    """EJ_INJECT_FAULT=host_alloc: ej_host_alloc fails as if hipHostMalloc had
+    run out of memory (EJ_E_HIP and a message), and the Python wrapper that
+    takes the queued plan's count buffer raises with that message."""
+    import threading
+
+    from einjax_amd import _device
+
+    lib = _lib.load()
+    monkeypatch.setenv("EJ_INJECT_FAULT", "launch,host_alloc")
+    p = ctypes.c_void_p()
+    assert lib.ej_host_alloc(64, ctypes.byref(p)) == _lib.EJ_E_HIP
+    msg = lib.ej_last_error()
+    assert b"hipHostMalloc failed" in msg and b"injected by EJ_INJECT_FAULT" in msg
+    assert p.value is None
+    err = []
+
+    def fresh_thread():  # the count buffer is per thread
+        try:
+            _device._count_buffer()
+        except RuntimeError as e:
+            err.append(str(e))
+
+    t = threading.Thread(target=fresh_thread)
+    t.start()
+    t.join()
+    assert err and "HIP error in ej_host_alloc" in err[0] and "injected" in err[0]
+    # other site names do not match
+    monkeypatch.setenv("EJ_INJECT_FAULT", "host_allocx,launch")
+    lib.ej_host_alloc(64, ctypes.byref(p))
+    assert b"injected" not in lib.ej_last_error()
+    if p.value:
+        lib.ej_host_free(p)

@@ -307,3 +307,27 @@ def test_scheme_stats_blocksparse_16k_all_tile_shapes(gpu):
     c2, t2 = D.bucket_coo(idx, vals, (16384, 16384), (128, 128))
     npt.assert_array_equal(c2.cpu().numpy(), coords)
     assert torch.equal(t2, tiles.to(torch.bfloat16).float())
+
+
+def test_scheme_stats_order3_all_tile_shapes(gpu):
+    """The 2048^3 fp32 order-3 operand with 0.5% of its 32^3 tiles nonzero
+    (34.4 GB dense), all 1,728 tile shapes (every extent a power of two, so
+    each divides or is a multiple of 32), against the closed form of a
+    block-sparse tensor: the map, pooling and banded counting kernels at
+    their full size."""
+    w = G.workload_order3(values=False)
+    coords = w["lhs"].coords
+    note("stats order-3 2048^3", len(coords), "tiles")
+    tiles = torch.rand((len(coords), 32, 32, 32), device="cuda", dtype=torch.float32) + 0.5
+    rel = SparseTensorRelation(torch.from_numpy(coords).cuda(), tiles, (2048, 2048, 2048),
+                               (32, 32, 32))
+    dense = rel.to_dense()
+    del tiles, rel
+    shapes = R.all_tile_shapes((2048, 2048, 2048))
+    assert len(shapes) == 1728
+    nt, vc = D.scheme_stats(shapes, (2048, 2048, 2048), dense=dense)
+    for ts, n, v in zip(shapes, nt, vc):
+        assert (n, v) == blocksparse_closed_form(coords, (32, 32, 32), ts), ts
+    assert D.count_nonzero(dense) == len(coords) * 32 ** 3
+    del dense
+    torch.cuda.empty_cache()

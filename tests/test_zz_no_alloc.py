@@ -24,10 +24,9 @@ def note(*a):
     print("[case]", *a, flush=True)
 
 
-def _plan(noalloc: bool, w: dict, cap_p: int, group: int):
-    """Runs one entry point on workload w's coordinates; returns the results
-    clipped to the counts, as host arrays."""
-    lib = _lib.load()
+def _args(w: dict, cap_p: int, group: int):
+    """Device buffers and the argument lists of both entry points for
+    workload w's coordinates: (head, tail, buffers)."""
     L, Rr = w["lhs"], w["rhs"]
     lc = torch.from_numpy(L.coords).cuda()
     rc = torch.from_numpy(Rr.coords).cuda()
@@ -54,6 +53,19 @@ def _plan(noalloc: bool, w: dict, cap_p: int, group: int):
     tail = (_device.ptr(li), _device.ptr(ri), _device.ptr(coords), _device.ptr(offsets),
             _device.ptr(perm), cap_u, group, _device.ptr(order), ctypes.byref(written),
             ctypes.c_void_p(counts.data_ptr()), 0, _device.stream_ptr())
+    bufs = dict(lc=lc, rc=rc, li=li, ri=ri, coords=coords, offsets=offsets, perm=perm,
+                order=order, written=written, counts=counts, cap_u=cap_u, dev=dev)
+    return head, tail, bufs
+
+
+def _plan(noalloc: bool, w: dict, cap_p: int, group: int):
+    """Runs one entry point on workload w's coordinates; returns the results
+    clipped to the counts, as host arrays."""
+    lib = _lib.load()
+    head, tail, b = _args(w, cap_p, group)
+    lc, rc, dev = b["lc"], b["rc"], b["dev"]
+    li, ri, coords, offsets, perm = b["li"], b["ri"], b["coords"], b["offsets"], b["perm"]
+    order, written, counts, cap_u = b["order"], b["written"], b["counts"], b["cap_u"]
     if noalloc:
         _lib.check(lib.ej_pair_plan_async_noalloc(*head, *tail), "ej_pair_plan_async_noalloc")
     else:
@@ -113,3 +125,23 @@ def test_noalloc_plan_rejects_oversize(gpu):
     w = G.workload_blocksparse_1k(values=False)
     with pytest.raises(_lib.CapacityError, match="static scratch"):
         _plan(True, w, 2_000_000, 0)  # ~80 MB of segment workspace
+
+
+def test_noalloc_plan_allocates_no_device_memory(gpu):
+    """The property the entry point exists for: after a warm call, a call
+    leaves the driver's free device memory unchanged (every buffer it gets is
+    the caller's or the static scratch)."""
+    note("noalloc plan: device memory before and after a call")
+    lib = _lib.load()
+    w = G.workload_sparse_sparse_zipf(seed=2, n=4096, values=False)
+    head, tail, bufs = _args(w, 1 << 16, 0)
+    for _ in range(2):  # warm: code objects, scratch and runtime pools are in place
+        _lib.check(lib.ej_pair_plan_async_noalloc(*head, *tail), "ej_pair_plan_async_noalloc")
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        _lib.check(lib.ej_pair_plan_async_noalloc(*head, *tail), "ej_pair_plan_async_noalloc")
+        torch.cuda.synchronize()
+        free1, _ = torch.cuda.mem_get_info()
+        assert free1 == free0
+    assert bufs["counts"][4].item() > 0
