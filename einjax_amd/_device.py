@@ -43,6 +43,10 @@ def require_gpu() -> torch.device:
     return torch.device("cuda", torch._C._cuda_getDevice())
 
 
+def current_device_index() -> int:
+    return torch._C._cuda_getDevice()
+
+
 def stream_ptr() -> ctypes.c_void_p:
     """hipStream_t of torch's current stream on the current device."""
     return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice()))
@@ -281,97 +285,146 @@ def _wait_ticket(view, ticket: int) -> None:
         raise RuntimeError("the queued plan did not report its counts")
 
 
-def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys,
-                          agg_radices, desc, lhs_values, rhs_values, pair_bound: int,
-                          out_dtype=None, einsum_events=None):
-    """Join, segment plan and fused segment einsum queued back to back on the
-    current stream, with the pair count bounded by pair_bound instead of
-    read first.  The plan stores its counts in coherent host memory followed
-    by this call's ticket; the host waits only for the ticket (the einsum is
-    already queued behind the plan), then checks the counts.
+def _carve(sizes_bytes):
+    """Offsets (bytes, 256-byte aligned) of consecutive regions of one
+    buffer, and its total size in int64 elements."""
+    offs, off = [], 0
+    for n in sizes_bytes:
+        offs.append(off)
+        off += (max(int(n), 1) + 255) // 256 * 256
+    return offs, off // 8
 
-    Returns (status, result).  status "ok": result = (P, coords [U, n_out],
-    seg_offsets, perm, values [U, *out_tile], li, ri), views clipped to the
-    counts.  "bound": P exceeded pair_bound (result[0] = P); "range": a
-    coordinate fell outside its radix.  Either way the caller runs the exact
-    path; every kernel clips its work to the device-side counts, so an
-    exceeded bound costs a rerun, never a stray access.  einsum_events: an
-    optional list; when given, a (start, end) pair of timing events recorded
-    around the einsum launch is appended to it (for measurement; the records
-    add a little to the step)."""
-    lib = _lib.load()
-    dev = lhs_coords.device
-    code = value_code(lhs_values)
-    if rhs_values.dtype != lhs_values.dtype:
-        raise TypeError("both operands must have the same value dtype")
-    n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
-    nk = len(join_keys)
-    cap_p = max(int(pair_bound), 1)
-    cap_u = max(1, min(cap_p, prod(agg_radices)))
-    n_out = len(agg_keys)
-    base, counts, ticket = _count_buffer()
+
+class QueuedStep:
+    """ej_pair_plan_async + ej_segment_einsum_async for one combination of
+    coordinate arrays, join and output keys, radices, descriptor, operand
+    values and pair bound.  Everything that depends only on those is
+    computed once here (workspace sizes, capacities, the argument lists);
+    run_queued_step queues one call: join, segment plan and fused einsum back
+    to back on the current stream, with one wait for the plan's counts.  The
+    step holds the tensors' addresses, not the tensors: whoever reuses it
+    checks that the same tensors are still in place."""
+
+    def __init__(self, lhs_coords, rhs_coords, join_keys, join_radices, agg_keys, agg_radices,
+                 desc, lhs_values, rhs_values, pair_bound: int, out_dtype=None):
+        lib = self.lib = _lib.load()
+        self.dev = lhs_coords.device
+        code = value_code(lhs_values)
+        if rhs_values.dtype != lhs_values.dtype:
+            raise TypeError("both operands must have the same value dtype")
+        n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
+        nk = len(join_keys)
+        self.cap_p = cap_p = max(int(pair_bound), 1)
+        self.cap_u = cap_u = max(1, min(cap_p, prod(agg_radices)))
+        self.n_out = n_out = len(agg_keys)
+        nbytes = ctypes.c_size_t()
+        check(lib.ej_join_workspace_size(n_l, n_r, _lib.EJ_ORDER_PROBE, ctypes.byref(nbytes)),
+              "ej_join_workspace_size")
+        jws = nbytes.value
+        check(lib.ej_segment_workspace_size(cap_p, ctypes.byref(nbytes)),
+              "ej_segment_workspace_size")
+        sws = nbytes.value
+        self.odt = _set_out_dtype(desc, lhs_values, out_dtype)
+        self.out_tile = _out_tile(desc)
+        self.desc = desc
+        # The einsum's segments per workgroup when it runs grouped (its
+        # seg_group hint): the plan may also write the run order of those groups.
+        gq = ctypes.c_int32(1)
+        check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
+              "ej_segment_einsum_group")
+        self.group = group = gq.value if gq.value > 1 else 0
+        n_order = 1 + (cap_u + group - 1) // group if group else 1
+        (self.o_jws, self.o_sws, self.o_li, self.o_ri, self.o_off, self.o_perm,
+         self.o_ord), self.ws_elems = _carve([jws, sws, 8 * cap_p, 8 * cap_p, 4 * (cap_u + 1),
+                                              4 * cap_p, 4 * n_order])
+        self.jws_size, self.sws_size = jws, sws
+        self.order_written = ctypes.c_int32(0)
+        self._arrays = arr = (i32_array([k[0] for k in join_keys]),
+                              i32_array([k[1] for k in join_keys]), i64_array(join_radices),
+                              i32_array([s for s, _ in agg_keys]), i32_array([d for _, d in agg_keys]),
+                              i64_array(agg_radices))
+        self.plan_head = (lhs_coords.data_ptr(), n_l, lhs_coords.shape[1], rhs_coords.data_ptr(),
+                          n_r, rhs_coords.shape[1], nk, arr[0], arr[1], arr[2], n_out, arr[3],
+                          arr[4], arr[5], cap_p)
+        self.einsum_head = (ctypes.byref(desc), code, lhs_values.data_ptr(),
+                            rhs_values.data_ptr(), lhs_values.shape[0], rhs_values.shape[0])
+
+
+def run_queued_step(step: QueuedStep, einsum_events=None):
+    """Queues one call of a prepared QueuedStep and waits for the plan's
+    counts.  Returns (status, result): "ok" with result = (P, U, coords
+    [cap_u, n_out], values [cap_u, *out_tile], workspace) (the first U rows
+    of coords and values are the output), "bound" with result = (P,) when P
+    exceeded the step's pair bound, "range" when a coordinate fell outside
+    its radix (result None).  Either failure leaves nothing but ignored
+    output: every kernel clips its work to the device-side counts.
+    einsum_events: an optional list; when given, a (start, end) pair of
+    timing events recorded around the einsum launch is appended to it."""
+    lib, dev = step.lib, step.dev
     stream = stream_ptr()
-    order = _lib.EJ_ORDER_PROBE
-    # Every buffer first, so that the launches below reach the GPU back to back.
-    nbytes = ctypes.c_size_t()
-    check(lib.ej_join_workspace_size(n_l, n_r, order, ctypes.byref(nbytes)),
-          "ej_join_workspace_size")
-    jws = workspace(nbytes.value, dev)
-    check(lib.ej_segment_workspace_size(cap_p, ctypes.byref(nbytes)),
-          "ej_segment_workspace_size")
-    sws = workspace(nbytes.value, dev)
-    li = torch.empty(cap_p, dtype=torch.int64, device=dev)
-    ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
-    coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
-    offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
-    perm = torch.empty(cap_p, dtype=torch.int32, device=dev)
-    odt = _set_out_dtype(desc, lhs_values, out_dtype)
-    out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
-    # The einsum's segments per workgroup when it runs grouped (its seg_group
-    # hint): the plan may also write the run order of those groups.
-    gq = ctypes.c_int32(1)
-    check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
-          "ej_segment_einsum_group")
-    group = gq.value if gq.value > 1 else 0
-    order = torch.empty(1 + (cap_u + group - 1) // group if group else 1, dtype=torch.int32,
-                        device=dev)
-    order_written = ctypes.c_int32(0)
-    ldims = i32_array([k[0] for k in join_keys])
-    rdims = i32_array([k[1] for k in join_keys])
-    jrad = i64_array(join_radices)
-    src = i32_array([s for s, _ in agg_keys])
-    dim = i32_array([d for _, d in agg_keys])
-    rad = i64_array(agg_radices)
-
-    check(lib.ej_pair_plan_async(
-        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1], nk,
-        ldims, rdims, jrad, n_out, src, dim, rad, cap_p, ptr(jws), jws.numel(), ptr(sws),
-        sws.numel(), ptr(li), ptr(ri), ptr(coords), ptr(offsets), ptr(perm), cap_u, group,
-        ptr(order) if group else None, ctypes.byref(order_written), ctypes.c_void_p(base), ticket,
-        stream), "ej_pair_plan_async")
+    ws = torch.empty(step.ws_elems, dtype=torch.int64, device=dev)
+    coords = torch.empty((step.cap_u, step.n_out), dtype=torch.int32, device=dev)
+    out = torch.empty((step.cap_u, *step.out_tile), dtype=step.odt, device=dev)
+    w = ws.data_ptr()
+    li, ri, off, perm = w + step.o_li, w + step.o_ri, w + step.o_off, w + step.o_perm
+    order = w + step.o_ord if step.group else None
+    base, counts, ticket = _count_buffer()
+    check(lib.ej_pair_plan_async(*step.plan_head, w + step.o_jws, step.jws_size,
+                                 w + step.o_sws, step.sws_size, li, ri, coords.data_ptr(), off,
+                                 perm, step.cap_u, step.group, order,
+                                 ctypes.byref(step.order_written), base, ticket, stream),
+          "ej_pair_plan_async")
     if einsum_events is not None:
         einsum_events.append((torch.cuda.Event(enable_timing=True),
                               torch.cuda.Event(enable_timing=True)))
         einsum_events[-1][0].record()
-    check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
-                                      lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
-                                      ptr(perm), ptr(offsets), cap_u, ptr(sws),
-                                      ptr(order) if order_written.value else None, group,
-                                      ptr(out), stream),
-          "ej_segment_einsum_async")
+    check(lib.ej_segment_einsum_async(*step.einsum_head, li, ri, perm, off, step.cap_u,
+                                      w + step.o_sws,
+                                      order if step.order_written.value else None, step.group,
+                                      out.data_ptr(), stream), "ej_segment_einsum_async")
     if einsum_events is not None:
         einsum_events[-1][1].record()
     _wait_ticket(counts, ticket)
     U, bad_plan, _, _, P, bad_join = (int(counts[i]) for i in range(6))
     if bad_join:
         return "range", None
-    if P > cap_p:
+    if P > step.cap_p:
         return "bound", (P,)
     if bad_plan:
         return "range", None
-    if U > cap_u:  # cannot happen: U <= min(P, prod(agg_radices))
-        raise RuntimeError(f"segment count {U} exceeds its bound {cap_u}")
-    return "ok", (P, coords[:U], offsets[:U + 1], perm[:P], out[:U], li[:P], ri[:P])
+    if U > step.cap_u:  # cannot happen: U <= min(P, prod(agg_radices))
+        raise RuntimeError(f"segment count {U} exceeds its bound {step.cap_u}")
+    return "ok", (P, U, coords, out, ws)
+
+
+def queued_segment_einsum(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys,
+                          agg_radices, desc, lhs_values, rhs_values, pair_bound: int,
+                          out_dtype=None, einsum_events=None):
+    """Join, segment plan and fused segment einsum queued back to back on the
+    current stream, with the pair count bounded by pair_bound instead of
+    read first (QueuedStep + run_queued_step).  The plan stores its counts in
+    coherent host memory followed by this call's ticket; the host waits only
+    for the ticket (the einsum is already queued behind the plan), then
+    checks the counts.
+
+    Returns (status, result).  status "ok": result = (P, coords [U, n_out],
+    seg_offsets, perm, values [U, *out_tile], li, ri), views clipped to the
+    counts.  "bound": P exceeded pair_bound (result[0] = P); "range": a
+    coordinate fell outside its radix.  Either way the caller runs the exact
+    path; every kernel clips its work to the device-side counts, so an
+    exceeded bound costs a rerun, never a stray access."""
+    step = QueuedStep(lhs_coords, rhs_coords, join_keys, join_radices, agg_keys, agg_radices,
+                      desc, lhs_values, rhs_values, pair_bound, out_dtype)
+    status, res = run_queued_step(step, einsum_events)
+    if status != "ok":
+        return status, res
+    P, U, coords, out, ws = res
+    b = ws.view(torch.uint8)
+    li = b[step.o_li:step.o_li + 8 * P].view(torch.int64)
+    ri = b[step.o_ri:step.o_ri + 8 * P].view(torch.int64)
+    offsets = b[step.o_off:step.o_off + 4 * (U + 1)].view(torch.int32)
+    perm = b[step.o_perm:step.o_perm + 4 * P].view(torch.int32)
+    return "ok", (P, coords[:U], offsets, perm, out[:U], li, ri)
 
 
 class _DenseCounts(threading.local):
@@ -421,53 +474,75 @@ def dense_plan_applies(n_lhs: int, lhs_ncols: int, rhs_ncols: int, join_keys, ag
     return all(d in ld for d in range(nlo, lhs_ncols))
 
 
-def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
-                         lhs_values, rhs_values, out_dtype=None, einsum_events=None):
-    """Join, segment plan (ej_dense_plan_async: one launch, for a dense rhs
-    and increasing lhs coordinates) and the fused segment einsum, queued back
-    to back on the current stream; the host waits only for the plan's ticket.
+class DenseStep:
+    """ej_dense_plan_async + ej_segment_einsum_async for one combination of
+    coordinate arrays, join and output keys, grids, descriptor and operand
+    values, with everything that depends only on those computed once
+    (run_dense_step queues one call).  supported is False when the join's
+    structure cannot take the dense plan (beyond its 32-bit indices).  The
+    step holds the tensors' addresses, not the tensors: whoever reuses it
+    checks that the same tensors are still in place."""
 
-    Returns (status, result): "ok" with result = (P, coords [U, n_out],
-    seg_offsets, None, values [U, *out_tile], li, ri); "miss" when the data
+    def __init__(self, lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
+                 lhs_values, rhs_values, out_dtype=None):
+        lib = self.lib = _lib.load()
+        self.dev = lhs_coords.device
+        code = value_code(lhs_values)
+        if rhs_values.dtype != lhs_values.dtype:
+            raise TypeError("both operands must have the same value dtype")
+        n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
+        nk = len(join_keys)
+        NK = prod(int(rhs_grid[d]) for d in range(nk, len(rhs_grid)))
+        nlo = len(agg_keys) - (len(rhs_grid) - nk)
+        self.cap_p = cap_p = n_l * NK
+        self.supported = not (cap_p >= 1 << 30 or prod(int(g) for g in rhs_grid) >= 1 << 31)
+        if not self.supported:
+            return  # beyond the plan's 32-bit indices
+        self.cap_u = cap_u = max(1, min(n_l, prod(int(lhs_grid[d]) for d in range(nlo))) * NK)
+        self.n_out = n_out = len(agg_keys)
+        self.odt = _set_out_dtype(desc, lhs_values, out_dtype)
+        self.out_tile = _out_tile(desc)
+        self.desc = desc
+        gq = ctypes.c_int32(1)
+        check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
+              "ej_segment_einsum_group")
+        self.group = group = gq.value if gq.value > 1 else 0
+        n_order = 1 + (cap_u + group - 1) // group if group else 1
+        (self.o_li, self.o_ri, self.o_off, self.o_ord), self.ws_elems = _carve(
+            [8 * cap_p, 8 * cap_p, 4 * (cap_u + 1), 4 * n_order])
+        self.order_written = ctypes.c_int32(0)
+        self._arrays = arr = (i32_array([k[0] for k in join_keys]),
+                              i32_array([k[1] for k in join_keys]), i64_array(lhs_grid),
+                              i64_array(rhs_grid), i32_array([a for a, _ in agg_keys]),
+                              i32_array([b for _, b in agg_keys]))
+        self.plan_head = (lhs_coords.data_ptr(), n_l, lhs_coords.shape[1], rhs_coords.data_ptr(),
+                          n_r, rhs_coords.shape[1], nk, arr[0], arr[1], arr[2], arr[3], n_out,
+                          arr[4], arr[5])
+        self.einsum_head = (ctypes.byref(desc), code, lhs_values.data_ptr(),
+                            rhs_values.data_ptr(), lhs_values.shape[0], rhs_values.shape[0])
+
+
+def run_dense_step(step: DenseStep, einsum_events=None):
+    """Queues one call of a prepared DenseStep: the one-launch dense plan and
+    the fused segment einsum back to back on the current stream, then waits
+    for the plan's ticket.  Returns (status, result): "ok" with result =
+    (P, U, coords [cap_u, n_out], values [cap_u, *out_tile], workspace) (the
+    first U rows of coords and values are the output); "miss" when the data
     does not have the dense structure (the queued einsum did no work);
-    "unsupported" when the join's structure does not suit the dense plan."""
-    lib = _lib.load()
-    dev = lhs_coords.device
-    code = value_code(lhs_values)
-    if rhs_values.dtype != lhs_values.dtype:
-        raise TypeError("both operands must have the same value dtype")
-    n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
-    nk = len(join_keys)
-    NK = prod(int(rhs_grid[d]) for d in range(nk, len(rhs_grid)))
-    nlo = len(agg_keys) - (len(rhs_grid) - nk)
-    cap_p = n_l * NK
-    if cap_p >= 1 << 30 or prod(int(g) for g in rhs_grid) >= 1 << 31:
-        return "unsupported", None  # beyond the plan's 32-bit indices
-    cap_u = max(1, min(n_l, prod(int(lhs_grid[d]) for d in range(nlo))) * NK)
-    n_out = len(agg_keys)
-    base, counts, ticket = _count_buffer()
+    "unsupported" when the library refuses the structure."""
+    lib, dev = step.lib, step.dev
     stream = stream_ptr()
-    li = torch.empty(cap_p, dtype=torch.int64, device=dev)
-    ri = torch.empty(cap_p, dtype=torch.int64, device=dev)
-    coords = torch.empty((cap_u, n_out), dtype=torch.int32, device=dev)
-    offsets = torch.empty(cap_u + 1, dtype=torch.int32, device=dev)
-    dcounts = _dense_counts(dev, stream.value)
-    odt = _set_out_dtype(desc, lhs_values, out_dtype)
-    out = torch.empty((cap_u, *_out_tile(desc)), dtype=odt, device=dev)
-    gq = ctypes.c_int32(1)
-    check(lib.ej_segment_einsum_group(ctypes.byref(desc), code, ctypes.byref(gq)),
-          "ej_segment_einsum_group")
-    group = gq.value if gq.value > 1 else 0
-    order = torch.empty(1 + (cap_u + group - 1) // group if group else 1, dtype=torch.int32,
-                        device=dev)
-    order_written = ctypes.c_int32(0)
-    st = lib.ej_dense_plan_async(
-        ptr(lhs_coords), n_l, lhs_coords.shape[1], ptr(rhs_coords), n_r, rhs_coords.shape[1],
-        nk, i32_array([k[0] for k in join_keys]), i32_array([k[1] for k in join_keys]),
-        i64_array(lhs_grid), i64_array(rhs_grid), n_out, i32_array([a for a, _ in agg_keys]),
-        i32_array([b for _, b in agg_keys]), ptr(li), ptr(ri), cap_p, ptr(coords), ptr(offsets),
-        cap_u, group, ptr(order) if group else None, ctypes.byref(order_written), ptr(dcounts),
-        ctypes.c_void_p(base), ticket, stream)
+    ws = torch.empty(step.ws_elems, dtype=torch.int64, device=dev)
+    coords = torch.empty((step.cap_u, step.n_out), dtype=torch.int32, device=dev)
+    out = torch.empty((step.cap_u, *step.out_tile), dtype=step.odt, device=dev)
+    w = ws.data_ptr()
+    li, ri, off = w + step.o_li, w + step.o_ri, w + step.o_off
+    order = w + step.o_ord if step.group else None
+    dcounts = _dense_counts(dev, stream.value).data_ptr()
+    base, counts, ticket = _count_buffer()
+    st = lib.ej_dense_plan_async(*step.plan_head, li, ri, step.cap_p, coords.data_ptr(), off,
+                                 step.cap_u, step.group, order, ctypes.byref(step.order_written),
+                                 dcounts, base, ticket, stream)
     if st == _lib.EJ_E_UNSUPPORTED:
         return "unsupported", None
     check(st, "ej_dense_plan_async")
@@ -475,19 +550,42 @@ def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, 
         einsum_events.append((torch.cuda.Event(enable_timing=True),
                               torch.cuda.Event(enable_timing=True)))
         einsum_events[-1][0].record()
-    check(lib.ej_segment_einsum_async(ctypes.byref(desc), code, ptr(lhs_values), ptr(rhs_values),
-                                      lhs_values.shape[0], rhs_values.shape[0], ptr(li), ptr(ri),
-                                      None, ptr(offsets), cap_u, ptr(dcounts),
-                                      ptr(order) if order_written.value else None, group,
-                                      ptr(out), stream),
-          "ej_segment_einsum_async")
+    check(lib.ej_segment_einsum_async(*step.einsum_head, li, ri, None, off, step.cap_u, dcounts,
+                                      order if step.order_written.value else None, step.group,
+                                      out.data_ptr(), stream), "ej_segment_einsum_async")
     if einsum_events is not None:
         einsum_events[-1][1].record()
     word = _wait_packed_ticket(counts, ticket)
-    U, miss, P = word & 0xFFFFFFFF, (word >> 32) & 1, cap_p
+    U, miss = word & 0xFFFFFFFF, (word >> 32) & 1
     if miss:
         return "miss", None
-    return "ok", (P, coords[:U], offsets[:U + 1], None, out[:U], li[:P], ri[:P])
+    return "ok", (step.cap_p, U, coords, out, ws)
+
+
+def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
+                         lhs_values, rhs_values, out_dtype=None, einsum_events=None):
+    """Join, segment plan (ej_dense_plan_async: one launch, for a dense rhs
+    and increasing lhs coordinates) and the fused segment einsum, queued back
+    to back on the current stream (DenseStep + run_dense_step); the host
+    waits only for the plan's ticket.
+
+    Returns (status, result): "ok" with result = (P, coords [U, n_out],
+    seg_offsets, None, values [U, *out_tile], li, ri); "miss" when the data
+    does not have the dense structure (the queued einsum did no work);
+    "unsupported" when the join's structure does not suit the dense plan."""
+    step = DenseStep(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
+                     lhs_values, rhs_values, out_dtype)
+    if not step.supported:
+        return "unsupported", None
+    status, res = run_dense_step(step, einsum_events)
+    if status != "ok":
+        return status, res
+    P, U, coords, out, ws = res
+    b = ws.view(torch.uint8)
+    li = b[step.o_li:step.o_li + 8 * P].view(torch.int64)
+    ri = b[step.o_ri:step.o_ri + 8 * P].view(torch.int64)
+    offsets = b[step.o_off:step.o_off + 4 * (U + 1)].view(torch.int32)
+    return "ok", (P, coords[:U], offsets, None, out[:U], li, ri)
 
 
 def _wait_packed_ticket(view, ticket: int) -> int:

@@ -44,6 +44,14 @@ class SparseTensorRelation:
         self.shape = tuple(int(s) for s in self.shape)
         self.tile_shape = tuple(int(t) for t in self.tile_shape)
 
+    @classmethod
+    def _from_parts(cls, coords, values, shape: tuple, tile_shape: tuple):
+        """A relation from parts already in normal form (shape and tile_shape
+        tuples of ints), without the constructor's conversions."""
+        rel = object.__new__(cls)
+        rel.coords, rel.values, rel.shape, rel.tile_shape = coords, values, shape, tile_shape
+        return rel
+
     @property
     def num_tuples(self) -> int:
         """Number of non-empty tiles (sparse.py:49-52)."""

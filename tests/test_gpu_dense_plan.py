@@ -198,25 +198,28 @@ def test_dense_step_bitwise_equals_general_plan(gpu, idx, monkeypatch):
     name, w = list(workloads())[idx]
     note("dense step vs general", name)
     statuses = []
-    real = _device.dense_segment_einsum
+    real = _device.run_dense_step
 
     def spy(*a, **k):
         st, res = real(*a, **k)
         statuses.append(st)
         return st, res
 
-    monkeypatch.setattr(_device, "dense_segment_einsum", spy)
+    monkeypatch.setattr(_device, "run_dense_step", spy)
     lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
     args = (lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
     want = R.execute_sparse(w["lhs"], w["rhs"], w["join_keys"], w["kernel_string"],
                             w["agg_keys"], precision="fp64")
     for out_dtype in (None, torch.float32):
         sd._pair_hints.clear()
+        sd._steps.clear()
         dense = [ej.execute_sparse(*args, out_dtype=out_dtype) for _ in range(2)]
         assert statuses[-2:] == ["ok", "ok"]
         with monkeypatch.context() as m:
             m.setattr(sd, "_dense_step", lambda *a, **k: None)
+            sd._steps.clear()
             general = ej.execute_sparse(*args, out_dtype=out_dtype)
+            sd._steps.clear()
         for d in dense:
             assert torch.equal(d.coords, general.coords)
             bits = torch.int16 if d.values.dtype == torch.bfloat16 else torch.int32
@@ -264,15 +267,16 @@ def test_dense_plan_misses_fall_back(gpu, case, monkeypatch):
     st, res = run_plan(L, Rr, w["join_keys"], w["agg_keys"], lshape=lshape)
     assert st == _lib.EJ_OK and res["counts"][1] == 1 and res["dev_u"] == 0, name
     statuses = []
-    real = _device.dense_segment_einsum
+    real = _device.run_dense_step
 
     def spy(*a, **k):
         st, r = real(*a, **k)
         statuses.append(st)
         return st, r
 
-    monkeypatch.setattr(_device, "dense_segment_einsum", spy)
+    monkeypatch.setattr(_device, "run_dense_step", spy)
     sd._pair_hints.clear()
+    sd._steps.clear()
     lhs = dev_rel(L, shape=lshape)
     rhs = dev_rel(Rr)
     want = R.execute_sparse(L, Rr, w["join_keys"], w["kernel_string"], w["agg_keys"],

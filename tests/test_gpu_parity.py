@@ -758,16 +758,17 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
     else:
         w = G.workload_sparse_sparse_zipf(n=4096)
     statuses = []
-    real = _device_mod().queued_segment_einsum
+    real = _device_mod().run_queued_step
 
     def spy(*a, **k):
         st, res = real(*a, **k)
         statuses.append(st)
         return st, res
 
-    monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    monkeypatch.setattr(_device_mod(), "run_queued_step", spy)
     monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
     sd._pair_hints.clear()
+    sd._steps.clear()
     lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
     run = lambda: ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
     exact = run()
@@ -781,6 +782,7 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
     assert R.rel_l2(ref_v, want.values) <= TOL[w["dtype"]]
     for bound, status in [(P, "ok"), (max(P - 1, 1), "bound"), (3 * P + 7, "ok")]:
         sd._hint_set(key, lhs, rhs, bound)
+        sd._steps.clear()  # the hint, not a prepared step, bounds this call
         got = run()
         assert statuses[-1] == status, (bound, statuses)
         npt.assert_array_equal(got.coords.cpu().numpy(), ref_c)
@@ -803,15 +805,16 @@ def test_queued_step_range_fallback(gpu, monkeypatch):
     note("queued step range fallback")
     w = G.workload_blocksparse_1k()
     statuses = []
-    real = _device_mod().queued_segment_einsum
+    real = _device_mod().run_queued_step
 
     def spy(*a, **k):
         st, res = real(*a, **k)
         statuses.append(st)
         return st, res
 
-    monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    monkeypatch.setattr(_device_mod(), "run_queued_step", spy)
     sd._pair_hints.clear()
+    sd._steps.clear()
     L, Rr = w["lhs"], w["rhs"]
     small = lambda r: R.Rel(r.coords, r.values, r.tile_shape, r.tile_shape)
     lhs, rhs = dev_rel(small(L), w["dtype"]), dev_rel(small(Rr), w["dtype"])
@@ -831,14 +834,14 @@ def test_queued_step_large_join(gpu, monkeypatch):
     range flag sends it to the exact path."""
     note("queued step, large join")
     statuses = []
-    real = _device_mod().queued_segment_einsum
+    real = _device_mod().run_queued_step
 
     def spy(*a, **k):
         st, res = real(*a, **k)
         statuses.append(st)
         return st, res
 
-    monkeypatch.setattr(_device_mod(), "queued_segment_einsum", spy)
+    monkeypatch.setattr(_device_mod(), "run_queued_step", spy)
     w = G.workload_sparse_sparse_zipf(values=False)
     gen = torch.Generator(device="cuda").manual_seed(4)
 
@@ -850,6 +853,7 @@ def test_queued_step_large_join(gpu, monkeypatch):
     assert lhs.num_tuples > 4096
     run = lambda a, b: ej.execute_sparse(a, b, w["join_keys"], w["kernel_string"], w["agg_keys"])
     sd._pair_hints.clear()
+    sd._steps.clear()
     exact = run(lhs, rhs)
     queued = run(lhs, rhs)
     assert statuses == ["ok"]
@@ -858,6 +862,7 @@ def test_queued_step_large_join(gpu, monkeypatch):
     oc_lhs = SparseTensorRelation(lhs.coords, lhs.values, lhs.tile_shape, lhs.tile_shape)
     oc_rhs = SparseTensorRelation(rhs.coords, rhs.values, rhs.tile_shape, rhs.tile_shape)
     sd._pair_hints.clear()
+    sd._steps.clear()
     for _ in range(2):
         got = run(oc_lhs, oc_rhs)
         assert torch.equal(got.coords, exact.coords)
@@ -925,6 +930,7 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
 
     monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
     sd._pair_hints.clear()
+    sd._steps.clear()
     exact = ej.execute_sparse(*args)
     monkeypatch.setattr(lib, "ej_pair_plan_async", spy)
     for _ in range(2):
@@ -1115,3 +1121,39 @@ def test_device_to_dense_roundtrip(gpu):
     npt.assert_array_equal(dense.cpu().numpy(), R.relation_to_dense(w["lhs"]).astype(np.float32))
     back = SparseTensor("a", dense).to_relation((32, 32))
     assert torch.equal(back.coords, rel.coords) and torch.equal(back.values, rel.values)
+
+
+@pytest.mark.parametrize("name", ["blocksparse_1k", "zipf_small"])
+def test_repeated_calls_track_the_data(gpu, name):
+    """A repeated execute_sparse on the same relations takes its prepared
+    step (argument lists built once) and still joins, plans and multiplies
+    the data as it is at each call: bitwise equal to the first call, twice
+    the result after the lhs values are doubled in place, and the oracle's
+    result after the lhs coordinates are replaced by another tensor."""
+    note("repeated calls", name)
+    w = (G.workload_blocksparse_1k() if name == "blocksparse_1k"
+         else G.workload_sparse_sparse_zipf(n=4096))
+    sd._steps.clear()
+    sd._pair_hints.clear()
+    lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
+    run = lambda: ej.execute_sparse(lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
+    first = [run() for _ in range(3)]
+    assert len(sd._steps) == 1
+    for r in first[1:]:
+        assert torch.equal(r.coords, first[0].coords)
+        assert torch.equal(r.values.view(torch.int32), first[0].values.view(torch.int32))
+    lhs.values.mul_(2)
+    doubled = run()
+    assert torch.equal(doubled.coords, first[0].coords)
+    assert torch.equal(doubled.values, first[0].values * 2)
+    lhs.values.div_(2)
+    keep = np.arange(0, len(w["lhs"].coords), 2)
+    L2 = R.Rel(w["lhs"].coords[keep], w["lhs"].values[keep], w["lhs"].shape, w["lhs"].tile_shape)
+    lhs.coords = torch.from_numpy(np.ascontiguousarray(L2.coords)).cuda()
+    lhs.values = lhs.values[torch.from_numpy(keep).cuda()].contiguous()
+    want = R.execute_sparse(L2, w["rhs"], w["join_keys"], w["kernel_string"], w["agg_keys"],
+                            precision="fp64")
+    for _ in range(2):
+        got = run()
+        npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+        assert R.rel_l2(hv(got.values), want.values) <= TOL[w["dtype"]]
