@@ -285,6 +285,21 @@ def _wait_ticket(view, ticket: int) -> None:
         raise RuntimeError("the queued plan did not report its counts")
 
 
+# Grouped fused einsums (several output segments per workgroup sharing each
+# lhs stage) pay only with enough workgroups to fill the GPU: below 2048
+# segments a group of 4 gives fewer than 512 workgroups (two per CU), and
+# one segment per workgroup is faster (1024^2 fp32 block-sparse, 992
+# segments: 10.1 against 15.3 us).
+GROUP_MIN_SEGMENTS = 2048
+
+
+def drop_small_grouping(desc, n_segments: int) -> None:
+    """Clears the descriptor's seg_group hint when at most n_segments
+    segments are too few for grouped workgroups."""
+    if n_segments < GROUP_MIN_SEGMENTS:
+        desc.seg_group = 0
+
+
 def _carve(sizes_bytes):
     """Offsets (bytes, 256-byte aligned) of consecutive regions of one
     buffer, and its total size in int64 elements."""
@@ -316,6 +331,7 @@ class QueuedStep:
         nk = len(join_keys)
         self.cap_p = cap_p = max(int(pair_bound), 1)
         self.cap_u = cap_u = max(1, min(cap_p, prod(agg_radices)))
+        drop_small_grouping(desc, cap_u)
         self.n_out = n_out = len(agg_keys)
         nbytes = ctypes.c_size_t()
         check(lib.ej_join_workspace_size(n_l, n_r, _lib.EJ_ORDER_PROBE, ctypes.byref(nbytes)),
@@ -499,6 +515,7 @@ class DenseStep:
         if not self.supported:
             return  # beyond the plan's 32-bit indices
         self.cap_u = cap_u = max(1, min(n_l, prod(int(lhs_grid[d]) for d in range(nlo))) * NK)
+        drop_small_grouping(desc, cap_u)
         self.n_out = n_out = len(agg_keys)
         self.odt = _set_out_dtype(desc, lhs_values, out_dtype)
         self.out_tile = _out_tile(desc)

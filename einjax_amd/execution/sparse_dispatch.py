@@ -896,6 +896,7 @@ def _execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_k
             lambda r: _device.segment_plan(lc, rc, li, ri, agg, r), radices, cols)
         desc, a, b = operands()
         if fused:
+            _device.drop_small_grouping(desc, offsets.numel() - 1)
             vals = _device.segment_einsum(desc, a, b, li, ri, perm, offsets, out_dtype)
         else:
             pair_vals = _device.pair_einsum(desc, a, b, li, ri, out_dtype=out_dtype)
