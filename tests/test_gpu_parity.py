@@ -914,13 +914,17 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
     grouped einsum (two output tiles per workgroup) in the plan's run order
     (groups of 2, heaviest first per XCD); its output must be bit-identical
     to the exact path's (own plan, no order), with 4 to 12 output tiles per
-    row and 30 to 112 groups (66 and 30: not a multiple of the 8 XCDs)."""
+    row and 30 to 112 groups (66 and 30: not a multiple of the 8 XCDs).
+    Grouping is forced here: below GROUP_MIN_SEGMENTS output segments the
+    steps run one segment per workgroup, which writes no run order and gives
+    the same bits."""
     note("queued run order bf16", m, n, density)
+    dm = _device_mod()
     w = G.workload_blocksparse_16k(seed=3, m=m, n=n, density=density)
     lhs, rhs = dev_rel(w["lhs"], "bf16"), dev_rel(w["rhs"], "bf16")
     args = (lhs, rhs, w["join_keys"], w["kernel_string"], w["agg_keys"])
     written = []
-    lib = _device_mod()._lib.load()
+    lib = dm._lib.load()
     real = lib.ej_pair_plan_async
 
     def spy(*a):
@@ -929,6 +933,7 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
         return rc
 
     monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
+    monkeypatch.setattr(dm, "GROUP_MIN_SEGMENTS", 0)
     sd._pair_hints.clear()
     sd._steps.clear()
     exact = ej.execute_sparse(*args)
@@ -938,6 +943,17 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
         assert torch.equal(got.coords, exact.coords)
         assert torch.equal(got.values.view(torch.int16), exact.values.view(torch.int16))
     assert written and all(g == 2 and wr == 1 for g, wr in written), written
+    # the default threshold: these few segments run ungrouped
+    monkeypatch.undo()
+    assert dm.GROUP_MIN_SEGMENTS > (m // 128) * (n // 128)
+    monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)
+    monkeypatch.setattr(lib, "ej_pair_plan_async", spy)
+    sd._steps.clear()
+    written.clear()
+    got = ej.execute_sparse(*args)
+    assert torch.equal(got.coords, exact.coords)
+    assert torch.equal(got.values.view(torch.int16), exact.values.view(torch.int16))
+    assert written and all(g == 0 for g, _ in written), written
 
 
 def test_run_order_header_must_match_live_groups(gpu):
