@@ -27,10 +27,12 @@ namespace {
 
 constexpr int kDenseThreads = 1024;
 constexpr int kDenseTilesPerThread = 16;  // lhs tiles each thread scans
-constexpr int kDenseMaxLhs = kDenseThreads * kDenseTilesPerThread;  // jrow in LDS
-constexpr int kDenseMaxRuns = 8192;       // run starts held in LDS (run_of is 16-bit)
+constexpr int kDenseMaxLhs = kDenseThreads * kDenseTilesPerThread;  // run-start bits in LDS
+constexpr int kDenseMaxRuns = 8192;       // run starts held in LDS (rank_of is 16-bit)
 constexpr int kDenseMinPairsPerBlock = 2 * kDenseThreads;
-constexpr int kDenseMaxBlocks = 1024;     // every block rescans the lhs coordinates
+// Every block rescans the lhs coordinates for run starts: at most one block
+// per CU.
+constexpr int kDenseMaxBlocks = 256;
 
 // Every count and grid extent is below 2^31 (checked on the host), so the
 // kernel's index arithmetic and divisions are 32-bit.
@@ -48,12 +50,13 @@ struct DenseSpec {
 };
 
 // Blocks of kDenseThreads threads; LN and RN are the lhs and rhs coordinate
-// ranks (0: read from the spec, up to EJ_MAX_DIMS).  Every block scans the
-// lhs coordinates (run starts, order and range checks) and keeps in LDS the
-// run starts and, per lhs tile, its run and its rhs join row.  Block b then
-// writes its share of the segments, the pairs of the lhs-major pair indices
-// [b * ppb, (b + 1) * ppb) (pair index i is lhs tile i / NK meeting free
-// index i % NK; its place in segment order follows from the tile's run), its
+// ranks (0: read from the spec, up to EJ_MAX_DIMS).  Every block finds the
+// run starts among all lhs tiles (one bit per tile in LDS, ranked by a scan
+// of the words' counts, and the table of run starts) and checks its own
+// slice of the lhs tiles (range, join bounds, order).  A pair's lhs tile gives
+// its run by the bits and its rhs join row by its coordinates.  Block b then
+// writes its share of the segments, the pairs at
+// positions [b * ppb, (b + 1) * ppb) of the segment-ordered pair list, its
 // share of the rhs check (the first row loaded before the lhs scan, so that
 // the two latencies overlap) and (run_order) the order of the XCD chunks
 // assigned to it.  The last block to finish publishes the counts: scal[0] =
@@ -75,8 +78,8 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   constexpr int LD = LN ? LN : EJ_MAX_DIMS, RD = RN ? RN : EJ_MAX_DIMS;
   constexpr int NW = kDenseThreads / 64;
   __shared__ int32_t run_start[kDenseMaxRuns + 1];
-  __shared__ int32_t jrow[kDenseMaxLhs];
-  __shared__ uint16_t run_of[kDenseMaxLhs];
+  __shared__ unsigned long long start_bits[kDenseMaxLhs / 64];  // bit: the tile starts a run
+  __shared__ int32_t word_base[kDenseMaxLhs / 64];              // runs started before the word
   __shared__ int32_t cls_base[NW][256];
   const int lncols = LN ? LN : s.lncols, rncols = RN ? RN : s.rncols;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -107,70 +110,94 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   };
   if (rfirst < r1) load_r(rfirst);
 
-  // ---- lhs scan: this thread's tiles [t0, t1), contiguous --------------------
-  const int per = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;
-  const int t0 = min(s.n_lhs, tid * per), t1 = min(s.n_lhs, t0 + per);
-  uint32_t newmask = 0;  // bit i: tile t0 + i starts a run
-  int nnew = 0;
-  int32_t pv[LD];
-  if (t0 > 0 && t0 < t1) {
+  // ---- run starts: one bit per lhs tile, every block over every tile -------
+  // Tile t starts a run when one of its output dims (0 .. nlo-1) differs from
+  // tile t - 1's.  Thread tid takes tiles tid, tid + kDenseThreads, ... (each
+  // wave's loads coalesced), eight tiles per pass with their loads (clamped,
+  // always valid indices) issued before any is used.
+  const int nm = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;  // <= kDenseTilesPerThread
+  constexpr int kScanBatch = 8;
+  for (int m0 = 0; m0 < nm; m0 += kScanBatch) {
+    int32_t cvb[kScanBatch][LD], pvb[kScanBatch][LD];
 #pragma unroll
-    for (int d = 0; d < LD; ++d) pv[d] = d < lncols ? lc[(t0 - 1) * lncols + d] : 0;
+    for (int k = 0; k < kScanBatch; ++k) {
+      const int tc = min((m0 + k) * kDenseThreads + tid, s.n_lhs - 1), tp = max(tc - 1, 0);
+#pragma unroll
+      for (int d = 0; d < LD; ++d) cvb[k][d] = d < lncols ? lc[tc * lncols + d] : 0;
+#pragma unroll
+      for (int d = 0; d < LD; ++d) pvb[k][d] = d < lncols ? lc[tp * lncols + d] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kScanBatch; ++k) {
+      const int m = m0 + k;
+      if (m >= nm) break;  // uniform
+      const int t = m * kDenseThreads + tid;
+      bool newrun = t == 0;
+#pragma unroll
+      for (int d = 0; d < LD; ++d) newrun = newrun || (d < s.nlo && cvb[k][d] != pvb[k][d]);
+      const unsigned long long bits = __ballot(t < s.n_lhs && newrun);
+      if (lane == 0) start_bits[m * NW + wave] = bits;
+    }
   }
-  for (int t = t0; t < t1; ++t) {
-    int32_t cv[LD];
+
+  // ---- lhs checks: this block's slice of the tiles -------------------------
+  // Coordinates inside the lhs grid, join coordinates inside the rhs grid,
+  // strictly increasing rows; the blocks' failures meet in the publish.
+  {
+    const int tpb = (s.n_lhs + nblk - 1) / nblk;
+    const int c0 = min(s.n_lhs, blk * tpb), c1 = min(s.n_lhs, c0 + tpb);
+    for (int t = c0 + tid; t < c1; t += kDenseThreads) {
+      int32_t cv[LD], pv[LD];
 #pragma unroll
-    for (int d = 0; d < LD; ++d) cv[d] = d < lncols ? lc[t * lncols + d] : 0;
+      for (int d = 0; d < LD; ++d) cv[d] = d < lncols ? lc[t * lncols + d] : 0;
 #pragma unroll
-    for (int d = 0; d < LD; ++d)
-      if (d < lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
-    uint32_t j = 0;  // the rhs join row: its join coordinates over the join grid
-#pragma unroll
-    for (int i = 0; i < RD; ++i)
-      if (i < s.nk) {
-        int32_t c = 0;
-#pragma unroll
-        for (int d = 0; d < LD; ++d) c = d == s.ldim[i] ? cv[d] : c;
-        if (c >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
-        j = j * static_cast<uint32_t>(s.rgrid[i]) + static_cast<uint32_t>(c);
-      }
-    bool newrun = t == 0;
-    if (t > 0) {
-      int cmp = 0, first = LD;
+      for (int d = 0; d < LD; ++d) pv[d] = d < lncols && t > 0 ? lc[(t - 1) * lncols + d] : 0;
 #pragma unroll
       for (int d = 0; d < LD; ++d)
-        if (d < lncols && cmp == 0 && cv[d] != pv[d]) {
-          cmp = cv[d] < pv[d] ? -1 : 1;
-          first = d;
-        }
-      if (cmp <= 0) bad = 1;  // coordinates must be strictly increasing
-      newrun = first < s.nlo;
-    }
-    if (newrun) {
-      newmask |= 1u << (t - t0);
-      ++nnew;
-    }
-    jrow[t] = static_cast<int32_t>(j);
+        if (d < lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
 #pragma unroll
-    for (int d = 0; d < LD; ++d) pv[d] = cv[d];
+      for (int i = 0; i < RD; ++i)
+        if (i < s.nk) {
+          int32_t c = 0;
+#pragma unroll
+          for (int d = 0; d < LD; ++d) c = d == s.ldim[i] ? cv[d] : c;
+          if (c >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
+        }
+      if (t > 0) {
+        int cmp = 0;
+#pragma unroll
+        for (int d = 0; d < LD; ++d)
+          if (d < lncols && cmp == 0 && cv[d] != pv[d]) cmp = cv[d] < pv[d] ? -1 : 1;
+        if (cmp <= 0) bad = 1;  // coordinates must be strictly increasing
+      }
+    }
   }
   if (rfirst < r1 && !rhs_ok(rfirst)) bad = 1;
+  __syncthreads();
 
+  // ---- run table: run r starts at tile run_start[r] ------------------------
+  const int nwords = nm * NW;
   int64_t nruns64 = 0;
-  const int rbase = static_cast<int>(block_exclusive_sum<kDenseThreads>(nnew, &nruns64));
+  const int64_t wb = block_exclusive_sum<kDenseThreads>(
+      tid < nwords ? __popcll(start_bits[tid]) : 0, &nruns64);
+  if (tid < nwords) word_base[tid] = static_cast<int32_t>(wb);
   const int nruns = static_cast<int>(nruns64);
   const bool fits = nruns <= kDenseMaxRuns;
-  if (fits) {
-    int r = rbase - 1;  // the run of tile t0 - 1 (tile 0 always starts one)
-    for (int t = t0; t < t1; ++t) {
-      if (newmask >> (t - t0) & 1u) run_start[++r] = t;
-      run_of[t] = static_cast<uint16_t>(r);
-    }
-    if (tid == 0) run_start[nruns] = s.n_lhs;
-  } else {
-    bad = 1;
+  if (fits && tid < nwords) {
+    unsigned long long bits = start_bits[tid];
+    for (int r = static_cast<int>(wb); bits; ++r, bits &= bits - 1ull)
+      run_start[r] = tid * 64 + __builtin_ctzll(bits);
   }
+  if (fits && tid == 0) run_start[nruns] = s.n_lhs;
+  if (!fits) bad = 1;
   __syncthreads();
+  // Run of tile t: the run starts at or before it, less one (tile 0 starts run 0).
+  auto run_of = [&](uint32_t t) {
+    const unsigned long long bits = start_bits[t >> 6];
+    const uint32_t b = t & 63u;
+    const unsigned long long upto = b == 63u ? bits : bits & ((2ull << b) - 1ull);
+    return word_base[t >> 6] + __popcll(upto) - 1;
+  };
   const int64_t U = fits ? static_cast<int64_t>(nruns) * s.NK : 0;
   const int live_u = static_cast<int>(U < seg_cap ? U : seg_cap);
   if (U > seg_cap) bad = 1;
@@ -200,17 +227,28 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
         }
     }
     if (blk == 0 && tid == 0 && U <= seg_cap) seg_offsets[U] = s.P;
-    // ---- pairs: lhs-major indices [i0, i1), placed in segment order -------
-    const int64_t i0 = static_cast<int64_t>(blk) * s.ppb;
-    const int64_t i1 = min(static_cast<int64_t>(s.P), i0 + s.ppb);
-    for (int64_t i = i0 + tid; i < i1; i += kDenseThreads) {
-      const uint32_t ui = static_cast<uint32_t>(i);
-      const uint32_t t = ui / nk32, kk = ui - t * nk32;
-      const int r = run_of[t];
+    // ---- pairs: positions [q0, q1) of the segment-ordered pair list ---------
+    // Run r owns positions [rs * NK, (rs + len) * NK), so position q lies in
+    // the run of lhs tile q / NK; there q - rs * NK = kk * len + p, the pair of
+    // lhs tile rs + p and free index kk.  Consecutive threads write
+    // consecutive positions.
+    const int64_t q0 = static_cast<int64_t>(blk) * s.ppb;
+    const int64_t q1 = min(static_cast<int64_t>(s.P), q0 + s.ppb);
+    for (int64_t q = q0 + tid; q < q1; q += kDenseThreads) {
+      const uint32_t uq = static_cast<uint32_t>(q);
+      const int r = run_of(uq / nk32);
       const int rs = run_start[r], len = run_start[r + 1] - rs;
-      const int q = rs * s.NK + static_cast<int>(kk) * len + (static_cast<int>(t) - rs);
+      const uint32_t off = uq - static_cast<uint32_t>(rs) * nk32;
+      const uint32_t kk = off / static_cast<uint32_t>(len), p = off - kk * static_cast<uint32_t>(len);
+      const int t = rs + static_cast<int>(p);
+      uint32_t j = 0;  // the rhs join row: the tile's join coordinates over the join grid
+#pragma unroll
+      for (int i = 0; i < RD; ++i)
+        if (i < s.nk)
+          j = j * static_cast<uint32_t>(s.rgrid[i]) +
+              static_cast<uint32_t>(lc[t * lncols + s.ldim[i]]);
       lidx[q] = t;
-      ridx[q] = static_cast<int64_t>(jrow[t]) * s.NK + kk;
+      ridx[q] = static_cast<int64_t>(j) * s.NK + kk;
     }
   }
 
@@ -284,8 +322,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   if (snake) {
     const int ngroups = live_u / group;
     if (blk == 0 && tid == 0) run_order[0] = ngroups;
-    __syncthreads();  // the pairs loop is done with run_of
-    uint16_t *const rank_of = run_of;  // rank of run r (reuses the LDS)
+    __shared__ uint16_t rank_of[kDenseMaxRuns];  // rank of run r
     const int rpw = ((nruns + NW - 1) / NW + 63) & ~63;  // runs per wave, whole 64-run steps
     const int w0 = min(nruns, wave * rpw), w1 = min(nruns, w0 + rpw);
     auto run_cls = [&](int r) {
