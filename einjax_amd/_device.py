@@ -580,6 +580,123 @@ def run_dense_step(step: DenseStep, einsum_events=None):
     return "ok", (step.cap_p, U, coords, out, ws)
 
 
+# Limits of ej_row_plan_async (the library refuses beyond them).
+ROW_MAX_LHS, ROW_MAX_JOIN, ROW_MAX_FREE, ROW_MAX_RUNS = 16384, 65536, 8192, 8192
+_ROW_COUNT_MASK = (1 << 21) - 1
+
+
+def row_plan_applies(n_lhs: int, lhs_grid, rhs_grid, join_keys, agg_keys) -> bool:
+    """Whether a join suits ej_row_plan_async (the device then checks the
+    data): the structure of the dense plan (dense_plan_applies) with a rhs
+    that need not be full, within the plan's limits on lhs tiles, join keys,
+    free indices and runs."""
+    nl, nr, nk = len(lhs_grid), len(rhs_grid), len(join_keys)
+    if not dense_plan_applies(min(n_lhs, ROW_MAX_LHS), nl, nr, join_keys, agg_keys):
+        return False
+    nlo = len(agg_keys) - (nr - nk)
+    runs = min(n_lhs, prod(int(g) for g in lhs_grid[:nlo]))
+    return (1 <= n_lhs <= ROW_MAX_LHS and prod(int(g) for g in rhs_grid[:nk]) <= ROW_MAX_JOIN
+            and prod(int(g) for g in rhs_grid[nk:]) <= ROW_MAX_FREE and runs <= ROW_MAX_RUNS)
+
+
+def _ticket20(ticket: int) -> int:
+    """A count-buffer ticket folded to 1 .. 2^20 - 1 (consecutive tickets stay
+    distinct), for the row plan's packed word."""
+    return (ticket - 1) % ((1 << 20) - 1) + 1
+
+
+class RowStep:
+    """ej_row_plan_async + ej_segment_einsum_async for one combination of
+    sorted coordinate arrays, join and output keys, grids, descriptor,
+    operand values and pair bound, with everything that depends only on those
+    computed once (run_row_step queues one call).  The step holds the
+    tensors' addresses, not the tensors: whoever reuses it checks that the
+    same tensors are still in place."""
+
+    def __init__(self, lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
+                 lhs_values, rhs_values, pair_bound: int, out_dtype=None):
+        lib = self.lib = _lib.load()
+        self.dev = lhs_coords.device
+        code = value_code(lhs_values)
+        if rhs_values.dtype != lhs_values.dtype:
+            raise TypeError("both operands must have the same value dtype")
+        n_l, n_r = lhs_coords.shape[0], rhs_coords.shape[0]
+        nk = len(join_keys)
+        NK = prod(int(rhs_grid[d]) for d in range(nk, len(rhs_grid)))
+        nlo = len(agg_keys) - (len(rhs_grid) - nk)
+        self.cap_p = cap_p = max(int(pair_bound), 1)
+        runs = min(n_l, prod(int(lhs_grid[d]) for d in range(nlo)))
+        self.cap_u = cap_u = max(1, min(cap_p, runs * NK))
+        drop_small_grouping(desc, cap_u)
+        desc.seg_group = 0  # a sparse rhs shows no runs of segments sharing lhs tiles
+        self.n_out = n_out = len(agg_keys)
+        self.odt = _set_out_dtype(desc, lhs_values, out_dtype)
+        self.out_tile = _out_tile(desc)
+        self.desc = desc
+        nbytes = ctypes.c_size_t()
+        check(lib.ej_row_plan_workspace_size(n_l, n_r, prod(int(rhs_grid[d]) for d in range(nk)),
+                                             ctypes.byref(nbytes)), "ej_row_plan_workspace_size")
+        self.rws_size = nbytes.value
+        (self.o_rws, self.o_li, self.o_ri, self.o_off), self.ws_elems = _carve(
+            [self.rws_size, 8 * cap_p, 8 * cap_p, 4 * (cap_u + 1)])
+        self._arrays = arr = (i32_array([k[0] for k in join_keys]),
+                              i32_array([k[1] for k in join_keys]), i64_array(lhs_grid),
+                              i64_array(rhs_grid), i32_array([a for a, _ in agg_keys]),
+                              i32_array([b for _, b in agg_keys]))
+        self.plan_head = (lhs_coords.data_ptr(), n_l, lhs_coords.shape[1], rhs_coords.data_ptr(),
+                          n_r, rhs_coords.shape[1], nk, arr[0], arr[1], arr[2], arr[3], n_out,
+                          arr[4], arr[5])
+        self.einsum_head = (ctypes.byref(desc), code, lhs_values.data_ptr(),
+                            rhs_values.data_ptr(), lhs_values.shape[0], rhs_values.shape[0])
+
+
+def run_row_step(step: RowStep, einsum_events=None):
+    """Queues one call of a prepared RowStep: the three-launch row plan and
+    the fused segment einsum back to back on the current stream, then waits
+    for the plan's packed count word.  Returns (status, result): "ok" with
+    result = (P, U, coords [cap_u, n_out], values [cap_u, *out_tile],
+    workspace) (the first U rows of coords and values are the output);
+    "bound" with result = (P,) when the pairs or segments exceeded the
+    step's capacities (P below 2^21 - 1: a larger bound will do); "miss"
+    when the data does not have the sorted structure or is beyond the plan's
+    2^21 counts; "unsupported" when the library refuses the structure.  The
+    einsum does no work after a failure."""
+    lib, dev = step.lib, step.dev
+    stream = stream_ptr()
+    ws = torch.empty(step.ws_elems, dtype=torch.int64, device=dev)
+    coords = torch.empty((step.cap_u, step.n_out), dtype=torch.int32, device=dev)
+    out = torch.empty((step.cap_u, *step.out_tile), dtype=step.odt, device=dev)
+    w = ws.data_ptr()
+    li, ri, off = w + step.o_li, w + step.o_ri, w + step.o_off
+    dcounts = _dense_counts(dev, stream.value).data_ptr()
+    base, counts, ticket = _count_buffer()
+    t20 = _ticket20(ticket)
+    st = lib.ej_row_plan_async(*step.plan_head, li, ri, step.cap_p, coords.data_ptr(), off,
+                               step.cap_u, w + step.o_rws, step.rws_size, dcounts, base, t20,
+                               stream)
+    if st == _lib.EJ_E_UNSUPPORTED:
+        return "unsupported", None
+    check(st, "ej_row_plan_async")
+    if einsum_events is not None:
+        einsum_events.append((torch.cuda.Event(enable_timing=True),
+                              torch.cuda.Event(enable_timing=True)))
+        einsum_events[-1][0].record()
+    check(lib.ej_segment_einsum_async(*step.einsum_head, li, ri, None, off, step.cap_u, dcounts,
+                                      None, 0, out.data_ptr(), stream), "ej_segment_einsum_async")
+    if einsum_events is not None:
+        einsum_events[-1][1].record()
+    word = _wait_word(counts, t20, 44, "the row plan")
+    flag = (word >> 42) & 3
+    P, U = (word >> 21) & _ROW_COUNT_MASK, word & _ROW_COUNT_MASK
+    if flag & 1:
+        return "miss", None
+    if flag & 2:
+        if P >= _ROW_COUNT_MASK or U >= _ROW_COUNT_MASK:
+            return "miss", None
+        return "bound", (P,)
+    return "ok", (P, U, coords, out, ws)
+
+
 def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, rhs_grid, desc,
                          lhs_values, rhs_values, out_dtype=None, einsum_events=None):
     """Join, segment plan (ej_dense_plan_async: one launch, for a dense rhs
@@ -606,18 +723,26 @@ def dense_segment_einsum(lhs_coords, rhs_coords, join_keys, agg_keys, lhs_grid, 
     return "ok", (P, coords[:U], offsets, None, out[:U], li, ri)
 
 
+def _wait_word(view, ticket: int, shift: int, who: str) -> int:
+    """Waits until the GPU has stored a word whose bits from `shift` up hold
+    `ticket` in view[6] and returns it (as _wait_ticket, bounded by a stream
+    sync)."""
+    mask = (1 << 64) - 1  # the int64 view's word, read unsigned
+    for _ in range(200000):
+        w = view[6] & mask
+        if w >> shift == ticket:
+            return w
+    torch.cuda.current_stream().synchronize()
+    w = view[6] & mask
+    if w >> shift != ticket:
+        raise RuntimeError(f"{who} did not report its counts")
+    return w
+
+
 def _wait_packed_ticket(view, ticket: int) -> int:
     """Waits until the GPU has stored the word ticket << 33 | flag << 32 | U
     in view[6] and returns it (as _wait_ticket, bounded by a stream sync)."""
-    for _ in range(200000):
-        w = view[6]
-        if w >> 33 == ticket:
-            return w
-    torch.cuda.current_stream().synchronize()
-    w = view[6]
-    if w >> 33 != ticket:
-        raise RuntimeError("the dense plan did not report its counts")
-    return w
+    return _wait_word(view, ticket, 33, "the dense plan")
 
 
 def segment_sum(pair_values: torch.Tensor, perm, seg_offsets) -> torch.Tensor:

@@ -125,6 +125,10 @@ SIGNATURES = {
     "ej_dense_plan_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32,
                                    _P_i64, _P_i64, _i32, _P_i32, _P_i32, _vp, _vp, _i64, _vp,
                                    _vp, _i64, _i32, _vp, _P_i32, _vp, _vp, _i32, _vp]),
+    "ej_row_plan_async": (_i32, [_vp, _i64, _i32, _vp, _i64, _i32, _i32, _P_i32, _P_i32, _P_i64,
+                                 _P_i64, _i32, _P_i32, _P_i32, _vp, _vp, _i64, _vp, _vp, _i64,
+                                 _vp, _sz, _vp, _vp, _i32, _vp]),
+    "ej_row_plan_workspace_size": (_i32, [_i64, _i64, _i64, _P_sz]),
     "ej_host_alloc": (_i32, [_sz, ctypes.POINTER(_vp)]),
     "ej_host_free": (_i32, [_vp]),
     "ej_index_plan_workspace_size": (_i32, [_i64, _P_sz]),

@@ -455,6 +455,47 @@ DenseKernel dense_kernel_for(int ln, int rn) {
 }
 
 }  // namespace
+
+int run_plan_structure(const char *who, int n_keys, const int32_t *lhs_dims,
+                       const int32_t *rhs_dims, int lhs_ncols, int rhs_ncols, int n_out,
+                       const int32_t *agg_src, const int32_t *agg_dim, int32_t *ldim, int *nlo_out) {
+  // Join dims: rhs dims 0 .. nk-1, each once, their lhs dims increasing in
+  // rhs-dim order (so that lhs order within a run is rhs order).
+  for (int i = 0; i < n_keys; ++i) ldim[i] = -1;
+  for (int k = 0; k < n_keys; ++k) {
+    const int r = rhs_dims[k], l = lhs_dims[k];
+    if (r < 0 || r >= n_keys || ldim[r] >= 0 || l < 0 || l >= lhs_ncols) {
+      set_error("%s needs the join to cover rhs dims 0 .. %d once each", who, n_keys - 1);
+      return EJ_E_UNSUPPORTED;
+    }
+    ldim[r] = l;
+  }
+  for (int i = 1; i < n_keys; ++i)
+    if (ldim[i] <= ldim[i - 1]) {
+      set_error("%s needs the join's lhs dims in the rhs dims' order", who);
+      return EJ_E_UNSUPPORTED;
+    }
+  // Output: lhs dims 0 .. nlo-1, then every rhs dim from nk on, in order.
+  int nlo = 0;
+  while (nlo < n_out && agg_src[nlo] == 0 && agg_dim[nlo] == nlo) ++nlo;
+  bool agg_ok = nlo >= 1 && n_out == nlo + (rhs_ncols - n_keys);
+  for (int d = nlo; agg_ok && d < n_out; ++d)
+    agg_ok = agg_src[d] == 1 && agg_dim[d] == n_keys + (d - nlo);
+  // Every lhs dim from nlo on is a join dim (it varies within a run).
+  for (int d = nlo; agg_ok && d < lhs_ncols; ++d) {
+    bool joined = false;
+    for (int i = 0; i < n_keys; ++i) joined = joined || ldim[i] == d;
+    agg_ok = joined;
+  }
+  if (!agg_ok) {
+    set_error("%s needs output dims = a prefix of the lhs dims, then the rhs dims after its "
+              "join dims", who);
+    return EJ_E_UNSUPPORTED;
+  }
+  *nlo_out = nlo;
+  return EJ_OK;
+}
+
 }  // namespace ej
 
 using namespace ej;
@@ -489,39 +530,9 @@ extern "C" int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int
   s.lncols = lhs_ncols;
   s.rncols = rhs_ncols;
   s.nk = n_keys;
-  // Join dims: rhs dims 0 .. nk-1, each once, their lhs dims increasing in
-  // rhs-dim order (so that lhs order within a run is rhs order).
-  for (int i = 0; i < n_keys; ++i) s.ldim[i] = -1;
-  for (int k = 0; k < n_keys; ++k) {
-    const int r = rhs_dims[k], l = lhs_dims[k];
-    if (r < 0 || r >= n_keys || s.ldim[r] >= 0 || l < 0 || l >= lhs_ncols) {
-      set_error("the dense plan needs the join to cover rhs dims 0 .. %d once each", n_keys - 1);
-      return EJ_E_UNSUPPORTED;
-    }
-    s.ldim[r] = l;
-  }
-  for (int i = 1; i < n_keys; ++i)
-    if (s.ldim[i] <= s.ldim[i - 1]) {
-      set_error("the dense plan needs the join's lhs dims in the rhs dims' order");
-      return EJ_E_UNSUPPORTED;
-    }
-  // Output: lhs dims 0 .. nlo-1, then every rhs dim from nk on, in order.
   int nlo = 0;
-  while (nlo < n_out && agg_src[nlo] == 0 && agg_dim[nlo] == nlo) ++nlo;
-  bool agg_ok = nlo >= 1 && n_out == nlo + (rhs_ncols - n_keys);
-  for (int d = nlo; agg_ok && d < n_out; ++d)
-    agg_ok = agg_src[d] == 1 && agg_dim[d] == n_keys + (d - nlo);
-  // Every lhs dim from nlo on is a join dim (it varies within a run).
-  for (int d = nlo; agg_ok && d < lhs_ncols; ++d) {
-    bool joined = false;
-    for (int i = 0; i < n_keys; ++i) joined = joined || s.ldim[i] == d;
-    agg_ok = joined;
-  }
-  if (!agg_ok) {
-    set_error("the dense plan needs output dims = a prefix of the lhs dims, then the rhs "
-              "dims after its join dims");
-    return EJ_E_UNSUPPORTED;
-  }
+  EJ_TRY(run_plan_structure("the dense plan", n_keys, lhs_dims, rhs_dims, lhs_ncols, rhs_ncols,
+                            n_out, agg_src, agg_dim, s.ldim, &nlo));
   s.nlo = nlo;
   s.n_out = n_out;
   // The grid product stops growing past 2^31 (no overflow); such a grid is

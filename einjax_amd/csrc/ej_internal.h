@@ -157,6 +157,15 @@ int segment_einsum_split_b(const ej_einsum_desc *d, const uint16_t *A, const flo
                            const int64_t *ridx, const int32_t *perm, const int32_t *seg_off,
                            int64_t n_seg, void *out, hipStream_t stream);
 
+// Structure shared by the closed-form plans (ej_dense_plan.hip): the join
+// covers rhs dims 0 .. n_keys-1 once each, their lhs dims (ldim[i] for rhs
+// dim i) increasing; the output is lhs dims 0 .. nlo-1 followed by the rhs
+// dims after the join dims; every lhs dim from nlo on is joined.  Otherwise
+// EJ_E_UNSUPPORTED with a message naming `who`.
+int run_plan_structure(const char *who, int n_keys, const int32_t *lhs_dims,
+                       const int32_t *rhs_dims, int lhs_ncols, int rhs_ncols, int n_out,
+                       const int32_t *agg_src, const int32_t *agg_dim, int32_t *ldim, int *nlo);
+
 // Zeroes n bytes (a multiple of 4, 4-byte aligned) with a kernel rather than
 // hipMemsetAsync, which misbehaves when a caller records the call into a
 // HIP graph.

@@ -427,6 +427,39 @@ def _dense_step(lhs, rhs, keys, agg, lc, rc, operands, out_dtype, events):
     return None
 
 
+def _row_step(lhs, rhs, keys, agg, lc, rc, operands, out_dtype, bound, pair_key, events):
+    """The whole step on the sorted row plan (three plan launches, then the
+    fused einsum) when the join's structure suits it: (result, step,
+    row hint key), or None.  A pair bound that proves too small is raised to
+    the count and the step queued once more; a device-side miss (data not
+    sorted, or beyond the plan's counts) is remembered for these coordinate
+    arrays, so later calls go straight to the general plan."""
+    nl, nr = lc.shape[1], rc.shape[1]
+    if nl != lhs.ndim or nr != rhs.ndim:
+        return None
+    lgrid = [_grid(lhs, d) for d in range(nl)]
+    rgrid = [_grid(rhs, d) for d in range(nr)]
+    if not _device.row_plan_applies(lc.shape[0], lgrid, rgrid, keys, agg):
+        return None
+    rkey = _hint_key(lhs, rhs, ("row", tuple(lc.shape), tuple(rc.shape), tuple(keys),
+                                tuple(agg)))
+    if _hint_get(rkey, lhs, rhs) == -1:
+        return None
+    for _ in range(2):
+        desc, a, b = operands()
+        step = _device.RowStep(lc, rc, keys, agg, lgrid, rgrid, desc, a, b, bound, out_dtype)
+        status, res = _device.run_row_step(step, events)
+        if status == "ok":
+            _hint_set(pair_key, lhs, rhs, res[0])
+            return res, step, rkey
+        if status != "bound":
+            break
+        bound = res[0]
+        _hint_set(pair_key, lhs, rhs, bound)
+    _hint_set(rkey, lhs, rhs, -1)
+    return None
+
+
 # ---------------------------------------------------------------------------
 # Repeated calls.  A queued step on device relations keeps its prepared plan
 # and einsum (a DenseStep or QueuedStep: argument lists, capacities, output
@@ -475,6 +508,8 @@ def _run_cached_step(key, lhs, rhs, output_shape, output_tile_shape, events):
         return None
     if ent.kind == "dense":
         status, res = _device.run_dense_step(ent.step, events)
+    elif ent.kind == "row":
+        status, res = _device.run_row_step(ent.step, events)
     else:
         status, res = _device.run_queued_step(ent.step, events)
     if status != "ok":
@@ -485,6 +520,12 @@ def _run_cached_step(key, lhs, rhs, output_shape, output_tile_shape, events):
         hk = ent.hint_key
         if ent.kind == "dense":
             _hint_set(hk, lhs, rhs, -1)
+        elif ent.kind == "row":
+            pair_key, row_key = hk
+            if status == "bound":
+                _hint_set(pair_key, lhs, rhs, res[0])
+            else:
+                _hint_set(row_key, lhs, rhs, -1)
         else:
             _hint_set(hk, lhs, rhs, res[0] if status == "bound" else -1)
         return None
@@ -866,6 +907,14 @@ def _execute_sparse(lhs: SparseTensorRelation, rhs: SparseTensorRelation, join_k
                                         tuple(j_rad), tuple(agg)))
         bound = _hint_get(hint_key, lhs, rhs)
         if bound is not None and bound > 0:
+            done = _row_step(lhs, rhs, keys, agg, lc, rc, operands, out_dtype, bound, hint_key,
+                             _einsum_events)
+            if done is not None:
+                queued, step, rkey = done
+                kind, dkey = "row", (hint_key, rkey)
+            else:
+                bound = _hint_get(hint_key, lhs, rhs)
+        if queued is None and bound is not None and bound > 0:
             desc, a, b = operands()
             step = _device.QueuedStep(lc, rc, keys, j_rad, agg, radices(None), desc, a, b,
                                       bound, out_dtype)

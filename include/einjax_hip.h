@@ -76,7 +76,7 @@
 extern "C" {
 #endif
 
-#define EJ_ABI_VERSION 13
+#define EJ_ABI_VERSION 14
 
 #define EJ_OK 0
 #define EJ_E_INVAL (-1)       /* bad argument (shape, null pointer, bad string) */
@@ -372,6 +372,57 @@ int ej_dense_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_nc
                         int32_t *seg_offsets, int64_t seg_capacity, int32_t group,
                         int32_t *run_order, int32_t *run_order_written, int64_t *dev_counts,
                         int64_t *counts, int32_t counts_direct, ej_stream_t stream);
+
+/* Join and segment plan, in three launches and without sorting, for a join
+ * of two sorted sparse relations with the structure of ej_dense_plan_async
+ * (no counterpart in the reference, whose join and grouping run on the host,
+ * sparse_dispatch.py:29-82, :129-171; the results are the same): the join
+ * covers rhs dims 0 .. n_keys-1 once each, their lhs dims increasing; the
+ * output is lhs dims 0 .. nlo-1 followed by rhs dims n_keys .. rhs_ncols-1;
+ * every other lhs dim is a join dim; both relations' coordinates strictly
+ * increasing in lexicographic order and inside their grids.  The rhs need
+ * not hold every tile.  Then the lhs tiles sharing their first nlo
+ * coordinates form a run, lhs tile t meets the rhs tiles with its join key
+ * (a contiguous "row" of the rhs, in rhs order), the run's segments are the
+ * distinct values F of the rhs dims after the join dims among the rows its
+ * tiles meet (ascending: the reference's sorted output coordinates), and
+ * segment (run, F) holds one pair per run tile whose row holds F, in lhs
+ * order (the reference's accumulation order).  The plan writes the pairs in
+ * segment order (perm = identity: pass perm = NULL to the einsum),
+ * seg_offsets[0 .. U] and out_coords [U, n_out].  Limits (else
+ * EJ_E_UNSUPPORTED, take the general plan): 1 <= n_lhs <= 16384, n_rhs >= 1,
+ * at most 65536 join keys (the product of rhs_grid over the join dims), 8192
+ * values of F (the product over the rhs dims after them) and 8192 runs
+ * (min(n_lhs, product of lhs_grid over dims 0 .. nlo-1)).  workspace: at
+ * least ej_row_plan_workspace_size(n_lhs, n_rhs, join keys) bytes.  Data that fails
+ * a check on the device (order, grids) gives flag bit 0; P > pair_capacity,
+ * U > seg_capacity, or P or U at or above 2^21 gives flag bit 1; either way
+ * nothing is written and the device-side segment count is 0, so that an
+ * einsum queued behind does no work (bit 0: take the general plan; bit 1:
+ * retry with capacities for P, when P < 2^21).  dev_counts: device int64[8]
+ * whose entries [6] and [7] are zero at the call (the plan returns them to
+ * zero; the buffer of ej_dense_plan_async on the same stream serves);
+ * afterwards dev_counts[0 .. 5] = (U, or 0 after a failure; flag; min(P,
+ * pair_capacity); 0; P; 0), dev_counts[0] being the n_segments_dev of
+ * ej_segment_einsum_async.  counts (pinned host memory): with counts_direct
+ * == 0 those six counts are copied there in stream order; counts_direct > 0
+ * (a ticket below 2^20) declares counts coherent host memory from
+ * ej_host_alloc, and the plan stores the single word counts[6] = ticket << 44
+ * | flag << 42 | min(P, 2^21 - 1) << 21 | min(U, 2^21 - 1) instead.
+ * Asynchronous. */
+int ej_row_plan_async(const int32_t *lhs_coords, int64_t n_lhs, int32_t lhs_ncols,
+                      const int32_t *rhs_coords, int64_t n_rhs, int32_t rhs_ncols,
+                      int32_t n_keys, const int32_t *lhs_dims, const int32_t *rhs_dims,
+                      const int64_t *lhs_grid, const int64_t *rhs_grid, int32_t n_out,
+                      const int32_t *agg_src, const int32_t *agg_dim, int64_t *lhs_idx,
+                      int64_t *rhs_idx, int64_t pair_capacity, int32_t *out_coords,
+                      int32_t *seg_offsets, int64_t seg_capacity, void *workspace,
+                      size_t workspace_bytes, int64_t *dev_counts, int64_t *counts,
+                      int32_t counts_direct, ej_stream_t stream);
+
+/* Workspace bytes of ej_row_plan_async for n_lhs lhs tiles (1 .. 16384),
+ * n_rhs rhs tiles and n_join rhs join keys (1 .. 65536). */
+int ej_row_plan_workspace_size(int64_t n_lhs, int64_t n_rhs, int64_t n_join, size_t *bytes);
 
 /* Coherent, device-mapped host memory (hipHostMalloc, mapped | coherent) for
  * counts that kernels store directly (ej_pair_plan_async, counts_direct). */

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().ej_version() == 13
+    assert _lib.load().ej_version() == 14
 
 
 def describe(spec, lt, rt):
@@ -445,3 +445,40 @@ def test_injected_host_alloc_failure(monkeypatch):
     assert b"injected" not in lib.ej_last_error()
     if p.value:
         lib.ej_host_free(p)
+
+
+def test_row_plan_structure_and_arguments():
+    """row_plan_applies follows the dense plan's structure with a sparse rhs
+    and the row plan's limits; ej_row_plan_async and its workspace size
+    refuse bad arguments and structures before any launch."""
+    from einjax_amd import _device as D
+
+    lib = _lib.load()
+    assert D.row_plan_applies(5243, [512, 512], [512, 512], [(1, 0)], [(0, 0), (1, 1)])
+    assert D.row_plan_applies(40, [3, 12, 10], [3, 10, 14], [(0, 0), (2, 1)],
+                              [(0, 0), (0, 1), (1, 2)])
+    assert not D.row_plan_applies(16385, [512, 512], [512, 512], [(1, 0)], [(0, 0), (1, 1)])
+    assert not D.row_plan_applies(100, [512, 512], [512, 8193], [(1, 0)], [(0, 0), (1, 1)])
+    assert not D.row_plan_applies(100, [512, 512], [65537, 4], [(1, 0)], [(0, 0), (1, 1)])
+    assert not D.row_plan_applies(100, [512, 512], [512, 512], [(0, 0)], [(0, 1), (1, 1)])
+    assert not D.row_plan_applies(9000, [9000, 4], [4, 4], [(1, 0)], [(0, 0), (1, 1)])
+    nb = ctypes.c_size_t()
+    assert lib.ej_row_plan_workspace_size(5243, 5243, 512, ctypes.byref(nb)) == _lib.EJ_OK
+    assert nb.value >= 513 * 4 + 82 * 8 + 5243 * 4 + 5243 * 20
+    assert lib.ej_row_plan_workspace_size(16385, 5, 512, ctypes.byref(nb)) == _lib.EJ_E_INVAL
+    assert lib.ej_row_plan_workspace_size(10, 0, 512, ctypes.byref(nb)) == _lib.EJ_E_INVAL
+    assert lib.ej_row_plan_workspace_size(10, 5, 65537, ctypes.byref(nb)) == _lib.EJ_E_INVAL
+
+    def call(keys, agg, lgrid, rgrid, ticket=1, ws_bytes=1 << 20, n_lhs=4, lncols=2):
+        z = ctypes.c_void_p(16)  # never dereferenced: refused before any launch
+        return lib.ej_row_plan_async(
+            z, n_lhs, lncols, z, 4, len(rgrid), len(keys), _lib.i32_array([k[0] for k in keys]),
+            _lib.i32_array([k[1] for k in keys]), _lib.i64_array(lgrid), _lib.i64_array(rgrid),
+            len(agg), _lib.i32_array([a for a, _ in agg]), _lib.i32_array([b for _, b in agg]),
+            z, z, 16, z, z, 16, z, ws_bytes, z, z, ticket, None)
+
+    assert call([(0, 0)], [(0, 1), (1, 1)], [4, 4], [4, 4]) == _lib.EJ_E_UNSUPPORTED
+    assert b"row plan" in lib.ej_last_error()
+    assert call([(1, 0)], [(0, 0), (1, 1)], [4, 4], [4, 9000]) == _lib.EJ_E_UNSUPPORTED
+    assert call([(1, 0)], [(0, 0), (1, 1)], [4, 4], [4, 4], ticket=1 << 20) == _lib.EJ_E_INVAL
+    assert call([(1, 0)], [(0, 0), (1, 1)], [4, 4], [4, 4], ws_bytes=8) == _lib.EJ_E_CAPACITY

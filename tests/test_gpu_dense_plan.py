@@ -217,6 +217,7 @@ def test_dense_step_bitwise_equals_general_plan(gpu, idx, monkeypatch):
         assert statuses[-2:] == ["ok", "ok"]
         with monkeypatch.context() as m:
             m.setattr(sd, "_dense_step", lambda *a, **k: None)
+            m.setattr(sd, "_row_step", lambda *a, **k: None)
             sd._steps.clear()
             general = ej.execute_sparse(*args, out_dtype=out_dtype)
             sd._steps.clear()

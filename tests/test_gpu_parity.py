@@ -767,6 +767,7 @@ def test_queued_step_matches_exact_path(gpu, name, monkeypatch):
 
     monkeypatch.setattr(_device_mod(), "run_queued_step", spy)
     monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
+    monkeypatch.setattr(sd, "_row_step", lambda *a, **k: None)
     sd._pair_hints.clear()
     sd._steps.clear()
     lhs, rhs = dev_rel(w["lhs"], w["dtype"]), dev_rel(w["rhs"], w["dtype"])
@@ -842,6 +843,7 @@ def test_queued_step_large_join(gpu, monkeypatch):
         return st, res
 
     monkeypatch.setattr(_device_mod(), "run_queued_step", spy)
+    monkeypatch.setattr(sd, "_row_step", lambda *a, **k: None)  # the general queued plan
     w = G.workload_sparse_sparse_zipf(values=False)
     gen = torch.Generator(device="cuda").manual_seed(4)
 
@@ -933,6 +935,7 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
         return rc
 
     monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)  # the general queued plan
+    monkeypatch.setattr(sd, "_row_step", lambda *a, **k: None)
     monkeypatch.setattr(dm, "GROUP_MIN_SEGMENTS", 0)
     sd._pair_hints.clear()
     sd._steps.clear()
@@ -947,6 +950,7 @@ def test_queued_run_order_bf16_groups(gpu, m, n, density, monkeypatch):
     monkeypatch.undo()
     assert dm.GROUP_MIN_SEGMENTS > (m // 128) * (n // 128)
     monkeypatch.setattr(sd, "_dense_step", lambda *a, **k: None)
+    monkeypatch.setattr(sd, "_row_step", lambda *a, **k: None)
     monkeypatch.setattr(lib, "ej_pair_plan_async", spy)
     sd._steps.clear()
     written.clear()
