@@ -36,11 +36,11 @@
 //                    its pairs, its segments (offsets and coordinates) and its
 //                    pairs placed stably by free index.  Block 0 publishes the
 //                    counts; the last block to finish clears scal[6 .. 7].
-// A run's tiles are read kRowChunk at a time into a pair table in LDS; its
-// pairs are looked up kRowWindow at a time (binary searches in the table
-// stepped together, then one round of free-index loads); a run of at most
-// kRowChunk tiles and kRowCache pairs keeps its pairs' lookups in LDS for
-// both of the fill's walks.
+// A run's tiles are read kRowChunk at a time into a pair table in LDS, and
+// its pairs mapped to their tiles kRowMapWindow at a time (each tile marks
+// its first pair, a running maximum fills in the rest); a run of at most
+// kRowChunk tiles and kRowCache pairs keeps its pairs' tiles and free
+// indices in LDS for both of the fill's walks.
 #include "ej_internal.h"
 
 namespace ej {
@@ -59,10 +59,10 @@ constexpr int kRowCountBits = 21;               // P and U in the published word
 constexpr int kRowChunk = 1024;                 // run tiles per pair table
 constexpr int kRowChunkBits = 10;
 constexpr int kRowTPT = kRowChunk / kRowThreads;  // table tiles per thread
-constexpr int kRowWindow = 4096;                // pairs looked up per round: 16 per thread
-constexpr int kRowPerThread = kRowWindow / kRowThreads;
 constexpr int kRowCache = 8192;                 // pairs of a run kept in LDS between walks
 constexpr int kRowQuarterFree = kRowMaxFree / kRowWaves;  // free indices of the per-wave scatter
+constexpr int kRowMapWindow = 4096;             // pairs mapped to their tiles at a time
+constexpr int kRowLoads = 8;                    // free-index loads per thread in flight
 constexpr int kRowPreRuns = 4;                  // run counts per thread loaded up front
 static_assert((1 << kRowChunkBits) == kRowChunk, "binary search depth");
 
@@ -92,6 +92,49 @@ __device__ inline void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// One DPP move of a 64-bit value (its two halves); lanes the move does not
+// reach take 0.
+template <int CTRL, int ROWS>
+__device__ inline int64_t dpp64(int64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROWS, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, ROWS, 0xf, false);
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+
+// Inclusive sum across the 64 lanes of a wave with DPP moves (row shifts
+// within 16 lanes, then the broadcasts of lanes 15 and 31), no LDS traffic.
+__device__ inline int64_t wave_sum_dpp(int64_t v) {
+  v += dpp64<0x111, 0xf>(v);  // row_shr:1
+  v += dpp64<0x112, 0xf>(v);  // row_shr:2
+  v += dpp64<0x114, 0xf>(v);  // row_shr:4
+  v += dpp64<0x118, 0xf>(v);  // row_shr:8
+  v += dpp64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Exclusive prefix sum over the block's threads in order, and the block's
+// total (the row plan's scans: DPP within waves, LDS across them).  Every
+// thread calls it.
+__device__ inline int64_t row_block_sum(int64_t v, int64_t *total) {
+  __shared__ int64_t wave_tot[kRowWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t inc = wave_sum_dpp(v);
+  if (lane == 63) wave_tot[wave] = inc;
+  lds_barrier();
+  int64_t off = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) {
+    const int64_t t = wave_tot[w];
+    off += w < wave ? t : 0;
+    all += t;
+  }
+  lds_barrier();  // wave_tot is reused by the next call
+  *total = all;
+  return off + inc - v;
 }
 
 // Join key of rhs coordinates (clamped into the grid).
@@ -210,7 +253,7 @@ __device__ inline int load_runs(const unsigned long long *__restrict__ bits, con
   const int nwords = (s.n_lhs + 63) / 64;
   const unsigned long long b = tid < nwords ? bits[tid] : 0ull;
   int64_t total = 0;
-  const int64_t before = block_exclusive_sum<kRowThreads>(__popcll(b), &total);
+  const int64_t before = row_block_sum(__popcll(b), &total);
   if (tid < nwords) {
     sbits[tid] = b;
     wbase[tid] = static_cast<int32_t>(before);
@@ -227,9 +270,18 @@ __device__ inline int run_first(int r, int nwords, const unsigned long long *sbi
     const int mid = (lo + hi + 1) >> 1;
     if (wbase[mid] <= r) lo = mid; else hi = mid - 1;
   }
-  unsigned long long b = sbits[lo];
-  for (int k = r - wbase[lo]; k > 0; --k) b &= b - 1ull;
-  return lo * 64 + __builtin_ctzll(b);
+  // the k-th set bit of the word: halve the window by popcounts
+  const unsigned long long b = sbits[lo];
+  int k = r - wbase[lo], pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const int c = __popcll((b >> pos) & ((1ull << w) - 1ull));
+    if (k >= c) {
+      k -= c;
+      pos += w;
+    }
+  }
+  return lo * 64 + pos;
 }
 
 // A run's tiles are taken kRowChunk at a time (thread tid holds chunk tiles
@@ -245,7 +297,7 @@ __device__ inline int chunk_table(const int *a, const int *len, int32_t *row_a, 
     loc += len[j];
   }
   int64_t tot = 0;
-  const int base = static_cast<int>(block_exclusive_sum<kRowThreads>(loc, &tot));
+  const int base = static_cast<int>(row_block_sum(loc, &tot));
 #pragma unroll
   for (int j = 0; j < kRowTPT; ++j) {
     row_a[kRowTPT * threadIdx.x + j] = a[j];
@@ -256,50 +308,128 @@ __device__ inline int chunk_table(const int *a, const int *len, int32_t *row_a, 
   return static_cast<int>(tot);
 }
 
-// Chunk tiles x[q] holding chunk pairs p[q] (the last x with pre[x] <= p):
-// kRowPerThread binary searches stepped together, so that their LDS reads
-// overlap.  Pairs at or past n get x = 0.
-__device__ inline void find_tiles(const int *p, int n, const int32_t *pre, int *x) {
-  int lo[kRowPerThread], hi[kRowPerThread];
-#pragma unroll
-  for (int q = 0; q < kRowPerThread; ++q) {
-    lo[q] = 0;
-    hi[q] = p[q] < n ? kRowChunk - 1 : 0;
+// Chunk tile and free index of one chunk pair p < n (the uncached walks of
+// long runs; kept small, as they run rarely).
+__device__ inline void one_pair(int p, const int32_t *row_a, const int32_t *pre,
+                                const int32_t *__restrict__ fidx, int *x, int *f) {
+  int lo = 0, hi = kRowChunk - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pre[mid] <= p) lo = mid; else hi = mid - 1;
   }
-  // Each step reads pre[mid] for every search unconditionally (mid stays in
-  // [0, kRowChunk - 1]) and updates without branches, so that a step's
-  // kRowPerThread LDS reads are in flight together.
-#pragma unroll
-  for (int step = 0; step < kRowChunkBits; ++step) {
-    int v[kRowPerThread], mid[kRowPerThread];
-#pragma unroll
-    for (int q = 0; q < kRowPerThread; ++q) {
-      mid[q] = (lo[q] + hi[q] + 1) >> 1;
-      v[q] = pre[mid[q]];
-    }
-#pragma unroll
-    for (int q = 0; q < kRowPerThread; ++q) {
-      const bool open = lo[q] < hi[q], up = v[q] <= p[q];
-      lo[q] = open && up ? mid[q] : lo[q];
-      hi[q] = open && !up ? mid[q] - 1 : hi[q];
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < kRowPerThread; ++q) x[q] = lo[q];
+  *x = lo;
+  *f = fidx[row_a[lo] + (p - pre[lo])];
 }
 
-// Free index and chunk tile of the chunk pairs [w0, w0 + kRowWindow) below n:
-// f[q] (-1 past n) and x[q] for pair w0 + q * kRowThreads + tid.  One round of
-// kRowPerThread loads.
-__device__ inline void window_pairs(int w0, int n, const int32_t *row_a, const int32_t *pre,
-                                    const int32_t *__restrict__ fidx, int *x, int *f) {
-  int p[kRowPerThread];
+// Inclusive maximum scan of v >= 0 across the 64 lanes of a wave, with DPP
+// moves (row shifts within 16 lanes, then the row broadcasts of lanes 15 and
+// 31) rather than LDS-routed shuffles.  Lanes a move does not reach take 0.
+__device__ inline int wave_inclusive_max(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return v;
+}
+
+// Block-wide exclusive maximum of v (-1 for thread 0); *total = the
+// maximum over the block.  Every thread calls it.
+__device__ inline int block_exclusive_max(int v, int *total) {
+  __shared__ int wave_max[kRowWaves];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
 #pragma unroll
-  for (int q = 0; q < kRowPerThread; ++q) p[q] = w0 + q * kRowThreads + threadIdx.x;
-  find_tiles(p, n, pre, x);
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc = max(inc, o);
+  }
+  if (lane == 63) wave_max[wave] = inc;
+  lds_barrier();
+  int before = -1, all = -1;
 #pragma unroll
-  for (int q = 0; q < kRowPerThread; ++q)
-    f[q] = p[q] < n ? fidx[row_a[x[q]] + (p[q] - pre[x[q]])] : -1;
+  for (int w = 0; w < kRowWaves; ++w) {
+    const int m = wave_max[w];
+    if (w < wave) before = max(before, m);
+    all = max(all, m);
+  }
+  int ex = __shfl_up(inc, 1, 64);
+  if (lane == 0) ex = -1;
+  lds_barrier();  // wave_max is reused by the next call
+  *total = all;
+  return max(before, ex);
+}
+
+// Chunk tiles of the chunk pairs [w0, w0 + n).  Each chunk tile with pairs
+// marks its first pair (as tile + 1), then a running maximum fills in the
+// rest: wave w scans the positions [w * span, (w + 1) * span), 64 at a time
+// (lane l on position base + l) and four steps together, so that their LDS
+// reads and DPP scans overlap, carrying each step's maximum to the next.
+// The waves' carries are joined into wbefore[w] (the maximum before wave
+// w's positions); the tile of pair w0 + i is then max(map[i], wbefore[i /
+// span]) - 1, which readers form (map_tile).  carry_in is the previous
+// window's carry (tile + 1 of pair w0 - 1; 0 for the first window); returns
+// this window's.  Work per wave grows with the pairs, not with a fixed number
+// of positions per thread.
+struct PairMap {
+  int span;
+  int carry;
+};
+
+__device__ inline PairMap map_pairs(int w0, int n, int carry_in, const int32_t *pre, uint16_t *map,
+                                    int32_t *wbefore) {
+  __shared__ int32_t wcarry[kRowWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int p = tid; p < n; p += kRowThreads) map[p] = 0;
+  lds_barrier();
+#pragma unroll
+  for (int j = 0; j < kRowTPT; ++j) {
+    const int c = kRowTPT * tid + j;
+    const int a = pre[c], b = pre[c + 1];
+    if (b > a && a >= w0 && a < w0 + n) map[a - w0] = static_cast<uint16_t>(c + 1);
+  }
+  lds_barrier();
+  const int span = (n + kRowThreads - 1) / kRowThreads * 64;
+  const int q0 = wave * span, q1 = min(n, q0 + span);
+  int carry = 0;
+  for (int b0 = q0; b0 < q1; b0 += 4 * 64) {  // uniform within the wave
+    int v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = b0 + 64 * u + lane;
+      v[u] = p < q1 ? static_cast<int>(map[p]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = wave_inclusive_max(v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[u] = max(v[u], carry);
+      carry = __builtin_amdgcn_readlane(v[u], 63);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int p = b0 + 64 * u + lane;
+      if (p < q1) map[p] = static_cast<uint16_t>(v[u]);
+    }
+  }
+  if (lane == 0) wcarry[wave] = carry;
+  lds_barrier();
+  int all = carry_in;
+  if (tid < kRowWaves) {
+    int before = carry_in;
+    for (int w = 0; w < tid; ++w) before = max(before, wcarry[w]);
+    wbefore[tid] = before;
+  }
+#pragma unroll
+  for (int w = 0; w < kRowWaves; ++w) all = max(all, wcarry[w]);
+  lds_barrier();
+  return PairMap{span, all};
+}
+
+// The tile of mapped pair i (see map_pairs).
+__device__ inline int map_tile(const uint16_t *map, const int32_t *wbefore, int span, int i) {
+  return max(static_cast<int>(map[i]), wbefore[i / span]) - 1;
 }
 
 template <int LN, int RN>
@@ -313,6 +443,8 @@ __global__ __launch_bounds__(kRowThreads) void row_count_kernel(
   __shared__ int32_t wbase[kRowMaxWords];
   __shared__ uint32_t fmap[kRowMaxFree / 32];
   __shared__ int32_t row_a[kRowChunk], pre[kRowChunk + 1];
+  __shared__ uint16_t map[kRowMapWindow];
+  __shared__ int32_t wbefore[kRowWaves];
   if (scal[6] != 0) return;  // the data failed a check: nothing to count
   const int tid = threadIdx.x;
   const int nruns = load_runs(bits, s, sbits, wbase);
@@ -348,12 +480,23 @@ __global__ __launch_bounds__(kRowThreads) void row_count_kernel(
           tile_len[t] = len[j];
         }
       }
-      for (int w0 = 0; w0 < cp; w0 += kRowWindow) {
-        int x[kRowPerThread], f[kRowPerThread];
-        window_pairs(w0, cp, row_a, pre, fidx, x, f);
+      for (int w0 = 0, carry = 0; w0 < cp; w0 += kRowMapWindow) {
+        const int n = min(kRowMapWindow, cp - w0);
+        const PairMap pm = map_pairs(w0, n, carry, pre, map, wbefore);
+        carry = pm.carry;
+        for (int i0 = 0; i0 < n; i0 += kRowLoads * kRowThreads) {
+          int f[kRowLoads];
 #pragma unroll
-        for (int q = 0; q < kRowPerThread; ++q)
-          if (f[q] >= 0) atomicOr(&fmap[f[q] >> 5], 1u << (f[q] & 31));
+          for (int u = 0; u < kRowLoads; ++u) {
+            const int i = i0 + u * kRowThreads + tid;
+            const int x = i < n ? map_tile(map, wbefore, pm.span, i) : 0;
+            f[u] = i < n ? fidx[row_a[x] + (w0 + i - pre[x])] : -1;
+          }
+#pragma unroll
+          for (int u = 0; u < kRowLoads; ++u)
+            if (f[u] >= 0) atomicOr(&fmap[f[u] >> 5], 1u << (f[u] & 31));
+        }
+        lds_barrier();  // map is rebuilt for the next window
       }
       lds_barrier();  // the table is rebuilt for the next chunk
       pc += cp;
@@ -361,7 +504,7 @@ __global__ __launch_bounds__(kRowThreads) void row_count_kernel(
     int mine = 0;
     for (int w = tid; w < fwords; w += kRowThreads) mine += __popc(fmap[w]);
     int64_t sc = 0;
-    block_exclusive_sum<kRowThreads>(mine, &sc);
+    row_block_sum(mine, &sc);
     if (tid == 0) {
       run_pc[r] = pc;
       run_sc[r] = static_cast<int32_t>(sc);
@@ -384,6 +527,7 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
   __shared__ int32_t hist[kRowMaxFree];  // per free index: count, then cursor
   __shared__ int32_t row_a[kRowChunk], pre[kRowChunk + 1];
   __shared__ uint16_t fcache[kRowCache], xcache[kRowCache];  // a cached run's pairs
+  __shared__ int32_t wbefore[kRowWaves];
   __shared__ int64_t my_pb[kRowRunsPerBlock], my_pc[kRowRunsPerBlock];
   __shared__ int32_t my_sb[kRowRunsPerBlock];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -436,8 +580,8 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
         sv = run_sc[r];
       }
       int64_t ptot = 0, stot = 0;
-      const int64_t pb = block_exclusive_sum<kRowThreads>(pv, &ptot);
-      const int64_t sb = block_exclusive_sum<kRowThreads>(sv, &stot);
+      const int64_t pb = row_block_sum(pv, &ptot);
+      const int64_t sb = row_block_sum(sv, &stot);
       if (r < nruns && r >= static_cast<int>(blockIdx.x) &&
           (r - static_cast<int>(blockIdx.x)) % static_cast<int>(gridDim.x) == 0) {
         const int k = (r - static_cast<int>(blockIdx.x)) / static_cast<int>(gridDim.x);
@@ -532,28 +676,34 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
       };
       // ---- pass 0: the free-index histogram of the run's pairs --------------
       if (cached) {
-        const int cp = table(rs);
-        for (int w0 = 0; w0 < cp; w0 += kRowWindow) {
-          int x[kRowPerThread], f[kRowPerThread];
-          window_pairs(w0, cp, row_a, pre, fidx, x, f);
+        // the run's pairs are positions [0, npairs) of its one chunk; xcache
+        // holds each pair's tile
+        table(rs);
+        const PairMap pm = map_pairs(0, npairs, 0, pre, xcache, wbefore);
+        for (int i0 = 0; i0 < npairs; i0 += kRowLoads * kRowThreads) {
+          int f[kRowLoads], x[kRowLoads];
 #pragma unroll
-          for (int q = 0; q < kRowPerThread; ++q)
-            if (f[q] >= 0) {
-              const int p = w0 + q * kRowThreads + tid;
-              fcache[p] = static_cast<uint16_t>(f[q]);
-              xcache[p] = static_cast<uint16_t>(x[q]);
-              atomicAdd(&hist[(quarters ? (p / qlen) * NK : 0) + f[q]], 1);
+          for (int u = 0; u < kRowLoads; ++u) {
+            const int p = i0 + u * kRowThreads + tid;
+            x[u] = p < npairs ? map_tile(xcache, wbefore, pm.span, p) : 0;
+            f[u] = p < npairs ? fidx[row_a[x[u]] + (p - pre[x[u]])] : -1;
+          }
+#pragma unroll
+          for (int u = 0; u < kRowLoads; ++u)
+            if (f[u] >= 0) {
+              const int p = i0 + u * kRowThreads + tid;
+              fcache[p] = static_cast<uint16_t>(f[u]);
+              xcache[p] = static_cast<uint16_t>(x[u]);  // the tile itself from here on
+              atomicAdd(&hist[(quarters ? (p / qlen) * NK : 0) + f[u]], 1);
             }
         }
       } else {
         for (int tb = rs; tb < re; tb += kRowChunk) {
           const int cp = table(tb);
-          for (int w0 = 0; w0 < cp; w0 += kRowWindow) {
-            int x[kRowPerThread], f[kRowPerThread];
-            window_pairs(w0, cp, row_a, pre, fidx, x, f);
-#pragma unroll
-            for (int q = 0; q < kRowPerThread; ++q)
-              if (f[q] >= 0) atomicAdd(&hist[f[q]], 1);
+          for (int p = tid; p < cp; p += kRowThreads) {
+            int x, f;
+            one_pair(p, row_a, pre, fidx, &x, &f);
+            atomicAdd(&hist[f], 1);
           }
           lds_barrier();  // the table is rebuilt for the next chunk
         }
@@ -577,8 +727,8 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
           segs += h > 0 ? 1 : 0;
         }
         int64_t tot = 0;
-        int off = static_cast<int>(block_exclusive_sum<kRowThreads>(cnt, &tot));
-        int u = SB + static_cast<int>(block_exclusive_sum<kRowThreads>(segs, &tot));
+        int off = static_cast<int>(row_block_sum(cnt, &tot));
+        int u = SB + static_cast<int>(row_block_sum(segs, &tot));
         for (int f = f0; f < f1; ++f) {
           const int h = count(f);
           if (h > 0) {
@@ -608,11 +758,18 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
       if (quarters) {
         const int q0 = wave * qlen, q1 = min(npairs, q0 + qlen);
         int32_t *cur = hist + wave * NK;
+        // each step reads the next step's pair ahead, so that only the cursor's
+        // read and write stay on the step's critical path
+        int p = q0 + lane;
+        bool valid = p < q1;
+        uint32_t F = valid ? fcache[p] : 0u;
+        int x = valid ? xcache[p] : 0;
         for (int b0 = q0; b0 < q1; b0 += 64) {  // uniform within the wave
-          const int p = b0 + lane;
-          const bool valid = p < q1;
-          const uint32_t F = valid ? fcache[p] : 0u;
-          const int x = valid ? xcache[p] : 0;
+          const int pn = b0 + 64 + lane;
+          const bool vn = pn < q1;
+          const uint32_t Fn = vn ? fcache[pn] : 0u;
+          const int xn = vn ? xcache[pn] : 0;
+          const int rt = row_a[x] + (p - pre[x]);
           uint64_t peers = __ballot(valid);
           for (int b = 0; b < fbits; ++b) {
             const bool bit = (F >> b) & 1u;
@@ -626,28 +783,29 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
             if (rank == 0) cur[F] = base + __popcll(peers);
             const int64_t qpos = PB + base + rank;
             lidx[qpos] = rs + x;
-            ridx[qpos] = row_a[x] + (p - pre[x]);
+            ridx[qpos] = rt;
           }
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // cur before the next step
+          p = pn;
+          valid = vn;
+          F = Fn;
+          x = xn;
         }
       } else if (cached) {
         for (int p0 = 0; p0 < npairs; p0 += kRowThreads) {
           const int p = p0 + tid;
           const bool valid = p < npairs;
-          place(rs, p, valid, valid ? fcache[p] : 0u, valid ? xcache[p] : 0);
+          place(rs, p, valid, valid ? fcache[p] : 0u,
+                valid ? xcache[p] : 0);
         }
       } else {
         for (int tb = rs; tb < re; tb += kRowChunk) {
           const int cp = table(tb);
-          for (int w0 = 0; w0 < cp; w0 += kRowWindow) {
-            int x[kRowPerThread], f[kRowPerThread];
-            window_pairs(w0, cp, row_a, pre, fidx, x, f);
-#pragma unroll
-            for (int q = 0; q < kRowPerThread; ++q) {
-              if (w0 + q * kRowThreads >= cp) break;  // uniform
-              place(tb, w0 + q * kRowThreads + tid, f[q] >= 0,
-                    f[q] >= 0 ? static_cast<uint32_t>(f[q]) : 0u, x[q]);
-            }
+          for (int p0 = 0; p0 < cp; p0 += kRowThreads) {
+            const int p = p0 + tid;
+            int x = 0, f = 0;
+            if (p < cp) one_pair(p, row_a, pre, fidx, &x, &f);
+            place(tb, p, p < cp, static_cast<uint32_t>(f), x);
           }
           lds_barrier();  // the table is rebuilt for the next chunk
         }
