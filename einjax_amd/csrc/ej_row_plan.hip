@@ -46,7 +46,7 @@
 namespace ej {
 namespace {
 
-constexpr int kRowThreads = 256;
+constexpr int kRowThreads = 512;
 constexpr int kRowWaves = kRowThreads / 64;
 constexpr int kRowMaxLhs = 16384;               // run-start bits held in LDS
 constexpr int kRowMaxWords = kRowMaxLhs / 64;
