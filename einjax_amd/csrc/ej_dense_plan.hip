@@ -281,7 +281,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       return x < srem ? (x + 1) * (sper + 1) : srem * (sper + 1) + (x + 1 - srem) * sper;
     };
     if (tid < 8) share_load[tid] = 0;
-    __syncthreads();
+    lds_barrier();
     // pair totals of the consecutive shares: thread tid walks runs [ra, rb)
     const int rpt = (nruns + kDenseThreads - 1) / kDenseThreads;
     const int ra = min(nruns, tid * rpt), rb = min(nruns, ra + rpt);
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       }
       atomicAdd(&share_load[x], acc);
     }
-    __syncthreads();
+    lds_barrier();
     unsigned long long mx = 0, tot = 0;
 #pragma unroll
     for (int y = 0; y < 8; ++y) {
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
     for (int c = lane; c < 256; c += 64) cls_base[wave][c] = 0;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     for (int r = w0 + lane; r < w1; r += 64) atomicAdd(&cls_base[wave][run_cls(r)], 1);
-    __syncthreads();
+    lds_barrier();
     // Exclusive scan of the class counts in (class, wave) order: thread tid
     // holds entries 4 tid .. 4 tid + 3 of the 256 x NW.
     int hv[4], hs = 0;
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       cls_base[e % NW][e / NW] = hrun;
       hrun += hv[k];
     }
-    __syncthreads();
+    lds_barrier();
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     for (int rb = w0; rb < w1; rb += 64) {
       const int r = rb + lane;
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       if (valid && (peers & lt) == 0) cls_base[wave][c] = base + __popcll(peers);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    __syncthreads();
+    lds_barrier();
     // Rank p goes to XCD snake(p) as its (p / 8)-th run; XCD x holds n(x)
     // runs: one per full round of eight and one more if the last round
     // reaches it.

@@ -197,14 +197,35 @@ __device__ inline int64_t live_count(int64_t cap, const int64_t *dev) {
 }
 
 // ---- block-level scans ------------------------------------------------------
-// Inclusive prefix sum across the 64 lanes of a wave.
+// A workgroup barrier that orders LDS only: each wave's LDS operations are
+// complete, its global stores stay in flight (__syncthreads would wait for
+// them as well, a round trip to memory after every phase that writes).
+__device__ inline void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One DPP move of a 64-bit value (its two halves, DPP control CTRL, rows
+// ROWS); lanes the move does not reach take 0.
+template <int CTRL, int ROWS>
+__device__ inline int64_t dpp_move64(int64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROWS, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, ROWS, 0xf, false);
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave, with DPP moves (row
+// shifts by 1, 2, 4 and 8 within 16 lanes, then the broadcasts of lanes 15
+// and 31 into the rows after them) rather than LDS-routed shuffles.
 __device__ inline int64_t wave_inclusive_sum(int64_t v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int64_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+  v += dpp_move64<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_move64<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_move64<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_move64<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_move64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_move64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
   return v;
 }
 

@@ -85,44 +85,13 @@ struct RowSpec {
 
 __device__ inline int32_t clamp_coord(int32_t c, int32_t g) { return c < 0 ? 0 : (c >= g ? g - 1 : c); }
 
-// A workgroup barrier that orders LDS only: each wave's LDS operations are
-// complete, its global stores stay in flight (__syncthreads would wait for
-// them as well, a round trip to memory after every phase that writes).
-__device__ inline void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// One DPP move of a 64-bit value (its two halves); lanes the move does not
-// reach take 0.
-template <int CTRL, int ROWS>
-__device__ inline int64_t dpp64(int64_t v) {
-  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROWS, 0xf, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, ROWS, 0xf, false);
-  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
-                              static_cast<uint32_t>(lo));
-}
-
-// Inclusive sum across the 64 lanes of a wave with DPP moves (row shifts
-// within 16 lanes, then the broadcasts of lanes 15 and 31), no LDS traffic.
-__device__ inline int64_t wave_sum_dpp(int64_t v) {
-  v += dpp64<0x111, 0xf>(v);  // row_shr:1
-  v += dpp64<0x112, 0xf>(v);  // row_shr:2
-  v += dpp64<0x114, 0xf>(v);  // row_shr:4
-  v += dpp64<0x118, 0xf>(v);  // row_shr:8
-  v += dpp64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-  v += dpp64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-  return v;
-}
-
 // Exclusive prefix sum over the block's threads in order, and the block's
 // total (the row plan's scans: DPP within waves, LDS across them).  Every
 // thread calls it.
 __device__ inline int64_t row_block_sum(int64_t v, int64_t *total) {
   __shared__ int64_t wave_tot[kRowWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t inc = wave_sum_dpp(v);
+  const int64_t inc = wave_inclusive_sum(v);
   if (lane == 63) wave_tot[wave] = inc;
   lds_barrier();
   int64_t off = 0, all = 0;
