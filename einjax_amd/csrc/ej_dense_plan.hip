@@ -27,7 +27,7 @@ namespace {
 
 constexpr int kDenseThreads = 1024;
 constexpr int kDenseTilesPerThread = 16;  // lhs tiles each thread scans
-constexpr int kDenseMaxLhs = kDenseThreads * kDenseTilesPerThread;  // run-start bits in LDS
+constexpr int kDenseMaxLhs = kDenseThreads * kDenseTilesPerThread;  // bits and join rows in LDS
 constexpr int kDenseMaxRuns = 8192;       // run starts held in LDS (rank_of is 16-bit)
 constexpr int kDenseMinPairsPerBlock = 2 * kDenseThreads;
 // Every block rescans the lhs coordinates for run starts: at most one block
@@ -52,13 +52,13 @@ struct DenseSpec {
 // Blocks of kDenseThreads threads; LN and RN are the lhs and rhs coordinate
 // ranks (0: read from the spec, up to EJ_MAX_DIMS).  Every block finds the
 // run starts among all lhs tiles (one bit per tile in LDS, ranked by a scan
-// of the words' counts, and the table of run starts) and checks its own
-// slice of the lhs tiles (range, join bounds, order).  A pair's lhs tile gives
-// its run by the bits and its rhs join row by its coordinates.  Block b then
-// writes its share of the segments, the pairs at
+// of the words' counts, and the table of run starts) and each lhs tile's rhs
+// join row (LDS), and in the same pass checks its own slice of the lhs tiles
+// (range, join bounds, order).  Block b then writes its share of the
+// segments, the pairs at
 // positions [b * ppb, (b + 1) * ppb) of the segment-ordered pair list, its
-// share of the rhs check (the first row loaded before the lhs scan, so that
-// the two latencies overlap) and (run_order) the order of the XCD chunks
+// share of the rhs check (the first row loaded with the lhs scan's first
+// pass, so that the latencies overlap) and (run_order) the order of the XCD chunks
 // assigned to it.  The last block to finish publishes the counts: scal[0] =
 // U (0 when a check failed), scal[1] = not-applicable flag, scal[2] = scal[4]
 // = P, scal[3] = scal[5] = 0, and, given host_counts, the single word
@@ -78,6 +78,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   constexpr int LD = LN ? LN : EJ_MAX_DIMS, RD = RN ? RN : EJ_MAX_DIMS;
   constexpr int NW = kDenseThreads / 64;
   __shared__ int32_t run_start[kDenseMaxRuns + 1];
+  __shared__ int32_t jrow[kDenseMaxLhs];  // the rhs join row of each lhs tile
   __shared__ unsigned long long start_bits[kDenseMaxLhs / 64];  // bit: the tile starts a run
   __shared__ int32_t word_base[kDenseMaxLhs / 64];              // runs started before the word
   __shared__ int32_t cls_base[NW][256];
@@ -108,7 +109,6 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       }
     return ok;
   };
-  if (rfirst < r1) load_r(rfirst);
 
   // ---- run starts: one bit per lhs tile, every block over every tile -------
   // Tile t starts a run when one of its output dims (0 .. nlo-1) differs from
@@ -117,16 +117,25 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
   // always valid indices) issued before any is used.
   const int nm = (s.n_lhs + kDenseThreads - 1) / kDenseThreads;  // <= kDenseTilesPerThread
   constexpr int kScanBatch = 8;
+  // This block's slice of the tiles, checked in the same pass: coordinates
+  // inside the lhs grid, join coordinates inside the rhs grid, strictly
+  // increasing rows; the blocks' failures meet in the publish.
+  const int tpb = (s.n_lhs + nblk - 1) / nblk;
+  const int c0 = min(s.n_lhs, blk * tpb), c1 = min(s.n_lhs, c0 + tpb);
   for (int m0 = 0; m0 < nm; m0 += kScanBatch) {
     int32_t cvb[kScanBatch][LD], pvb[kScanBatch][LD];
 #pragma unroll
     for (int k = 0; k < kScanBatch; ++k) {
+      if (m0 + k >= nm) break;  // uniform: no loads for passes past the tiles
       const int tc = min((m0 + k) * kDenseThreads + tid, s.n_lhs - 1), tp = max(tc - 1, 0);
 #pragma unroll
       for (int d = 0; d < LD; ++d) cvb[k][d] = d < lncols ? lc[tc * lncols + d] : 0;
 #pragma unroll
       for (int d = 0; d < LD; ++d) pvb[k][d] = d < lncols ? lc[tp * lncols + d] : 0;
     }
+    // the rhs check's first row, loaded behind the first pass's lhs loads so
+    // that the latencies overlap
+    if (m0 == 0 && rfirst < r1) load_r(rfirst);
 #pragma unroll
     for (int k = 0; k < kScanBatch; ++k) {
       const int m = m0 + k;
@@ -137,38 +146,38 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       for (int d = 0; d < LD; ++d) newrun = newrun || (d < s.nlo && cvb[k][d] != pvb[k][d]);
       const unsigned long long bits = __ballot(t < s.n_lhs && newrun);
       if (lane == 0) start_bits[m * NW + wave] = bits;
-    }
-  }
-
-  // ---- lhs checks: this block's slice of the tiles -------------------------
-  // Coordinates inside the lhs grid, join coordinates inside the rhs grid,
-  // strictly increasing rows; the blocks' failures meet in the publish.
-  {
-    const int tpb = (s.n_lhs + nblk - 1) / nblk;
-    const int c0 = min(s.n_lhs, blk * tpb), c1 = min(s.n_lhs, c0 + tpb);
-    for (int t = c0 + tid; t < c1; t += kDenseThreads) {
-      int32_t cv[LD], pv[LD];
+      if (t < s.n_lhs) {
+        uint32_t j = 0;  // the rhs join row: the tile's join coordinates over the join grid
 #pragma unroll
-      for (int d = 0; d < LD; ++d) cv[d] = d < lncols ? lc[t * lncols + d] : 0;
+        for (int i = 0; i < RD; ++i)
+          if (i < s.nk) {
+            int32_t c = 0;
 #pragma unroll
-      for (int d = 0; d < LD; ++d) pv[d] = d < lncols && t > 0 ? lc[(t - 1) * lncols + d] : 0;
-#pragma unroll
-      for (int d = 0; d < LD; ++d)
-        if (d < lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
-#pragma unroll
-      for (int i = 0; i < RD; ++i)
-        if (i < s.nk) {
-          int32_t c = 0;
-#pragma unroll
-          for (int d = 0; d < LD; ++d) c = d == s.ldim[i] ? cv[d] : c;
-          if (c >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
-        }
-      if (t > 0) {
-        int cmp = 0;
+            for (int d = 0; d < LD; ++d) c = d == s.ldim[i] ? cvb[k][d] : c;
+            j = j * static_cast<uint32_t>(s.rgrid[i]) + static_cast<uint32_t>(c);
+          }
+        jrow[t] = static_cast<int32_t>(j);
+      }
+      if (t >= c0 && t < c1) {
+        const int32_t *cv = cvb[k], *pv = pvb[k];
 #pragma unroll
         for (int d = 0; d < LD; ++d)
-          if (d < lncols && cmp == 0 && cv[d] != pv[d]) cmp = cv[d] < pv[d] ? -1 : 1;
-        if (cmp <= 0) bad = 1;  // coordinates must be strictly increasing
+          if (d < lncols && (cv[d] < 0 || cv[d] >= s.lgrid[d])) bad = 1;
+#pragma unroll
+        for (int i = 0; i < RD; ++i)
+          if (i < s.nk) {
+            int32_t c = 0;
+#pragma unroll
+            for (int d = 0; d < LD; ++d) c = d == s.ldim[i] ? cv[d] : c;
+            if (c >= s.rgrid[i]) bad = 1;  // no rhs tile to meet
+          }
+        if (t > 0) {
+          int cmp = 0;
+#pragma unroll
+          for (int d = 0; d < LD; ++d)
+            if (d < lncols && cmp == 0 && cv[d] != pv[d]) cmp = cv[d] < pv[d] ? -1 : 1;
+          if (cmp <= 0) bad = 1;  // coordinates must be strictly increasing
+        }
       }
     }
   }
@@ -241,14 +250,8 @@ __global__ __launch_bounds__(kDenseThreads) void dense_plan_kernel(
       const uint32_t off = uq - static_cast<uint32_t>(rs) * nk32;
       const uint32_t kk = off / static_cast<uint32_t>(len), p = off - kk * static_cast<uint32_t>(len);
       const int t = rs + static_cast<int>(p);
-      uint32_t j = 0;  // the rhs join row: the tile's join coordinates over the join grid
-#pragma unroll
-      for (int i = 0; i < RD; ++i)
-        if (i < s.nk)
-          j = j * static_cast<uint32_t>(s.rgrid[i]) +
-              static_cast<uint32_t>(lc[t * lncols + s.ldim[i]]);
       lidx[q] = t;
-      ridx[q] = static_cast<int64_t>(j) * s.NK + kk;
+      ridx[q] = static_cast<int64_t>(jrow[t]) * s.NK + kk;
     }
   }
 
