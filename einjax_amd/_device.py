@@ -270,6 +270,12 @@ def _count_buffer():
         _counts.addr = p.value
         _counts.view = (ctypes.c_int64 * 8).from_address(p.value)
     _counts.ticket = _next_ticket(_counts.ticket)
+    # The plans publish differently packed words in slot 6 (the general plan
+    # its ticket, the dense and row plans ticket, flags and counts in one
+    # word), and a previous call's word could read as this call's ticket in
+    # another packing; every previous publication has been waited for, so
+    # clearing the slot leaves only this call's word to wait for.
+    _counts.view[6] = 0
     return _counts.addr, _counts.view, _counts.ticket
 
 

@@ -412,6 +412,27 @@ def test_plan_ticket_cycle_stays_below_the_plans_limit():
     assert _device._next_ticket((1 << 30) - 1) == 1
 
 
+def test_count_slot_cleared_before_each_plan(monkeypatch):
+    """A dense plan's packed word (ticket << 33 | flag << 32 | U) for ticket
+    2^20 + 510 reads as the row plan's next ticket (folded to 512) when
+    shifted by 44; the host clears slot 6 before each plan, so a previous
+    call's word is never taken for the next call's."""
+    from einjax_amd import _device
+
+    t_dense = (1 << 20) + 510
+    t_row = _device._ticket20(_device._next_ticket(t_dense))
+    stale = t_dense << 33 | 5
+    assert stale >> 44 == t_row  # the collision the clearing prevents
+    buf = (ctypes.c_int64 * 8)()
+    buf[6] = stale
+    state = _device._Counts()
+    state.addr, state.view, state.ticket = ctypes.addressof(buf), buf, t_dense
+    monkeypatch.setattr(_device, "_counts", state)
+    addr, view, ticket = _device._count_buffer()
+    assert (addr, ticket) == (ctypes.addressof(buf), t_dense + 1)
+    assert view[6] == 0 and (view[6] & ((1 << 64) - 1)) >> 44 != t_row
+
+
 def test_injected_host_alloc_failure(monkeypatch):
     """EJ_INJECT_FAULT=host_alloc: ej_host_alloc fails as if hipHostMalloc had
     run out of memory (EJ_E_HIP and a message), and the Python wrapper that
