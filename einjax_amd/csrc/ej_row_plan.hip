@@ -601,8 +601,8 @@ __global__ __launch_bounds__(kRowThreads) void row_fill_kernel(
       // its pairs' free indices and chunk tiles stay in LDS for both walks.
       const bool cached = re - rs <= kRowChunk && npairs <= kRowCache;
       // Cached with at most kRowQuarterFree free indices: wave w places the
-      // pairs of quarter w of the run on its own cursors (hist as
-      // [kRowWaves][NK]), without barriers between its steps.
+      // pairs of part w of the run's kRowWaves equal parts on its own
+      // cursors (hist as [kRowWaves][NK]), without barriers between its steps.
       const bool quarters = cached && NK <= kRowQuarterFree;
       const int qlen = (npairs + kRowWaves - 1) / kRowWaves;
       const int hn = quarters ? kRowWaves * NK : NK;

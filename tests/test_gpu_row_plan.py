@@ -54,6 +54,15 @@ def sparse_rel(rng, grid_shape, tile, density, drop_rows=()):
     return R.Rel(coords, vals, tuple(g * t for g, t in zip(grid_shape, tile)), tuple(tile))
 
 
+def rel_from_mask(rng, keep):
+    """1x1 tiles at the mask's true entries (at least one), lexicographic."""
+    if not keep.any():
+        keep.flat[0] = True
+    coords = np.ascontiguousarray(np.argwhere(keep), dtype=np.int32)
+    vals = rng.standard_normal((len(coords), *(1,) * keep.ndim)).astype(np.float32)
+    return R.Rel(coords, vals, keep.shape, (1,) * keep.ndim)
+
+
 def workloads():
     rng = np.random.default_rng(11)
     yield "zipf_small", G.workload_sparse_sparse_zipf(n=4096, tile=64, density=0.05)
@@ -78,6 +87,24 @@ def workloads():
     Rr = sparse_rel(rng, (16,), (4,), 0.6)
     yield "no_free_dim", dict(lhs=L, rhs=Rr, join_keys=[(1, 0)], agg_keys=[(0, 0)],
                               kernel_string="ij,j->i", dtype="fp32")
+    # long runs (1x1 tiles, 3,000 free indices: one set of cursors per run):
+    # run 0 holds all 2,500 lhs tiles (three 1,024-tile chunks, ~24k pairs:
+    # the per-pair walks), run 1 exactly 1,024 tiles over sparse rhs rows (one
+    # chunk, ~6k pairs kept in LDS), run 2 ~250 tiles
+    keep = np.zeros((3, 2500), dtype=bool)
+    keep[0] = True
+    keep[1, :1024] = True
+    keep[2] = rng.random(2500) < 0.1
+    L = rel_from_mask(rng, keep)
+    rk = rng.random((2500, 3000)) < np.where(np.arange(2500) < 1024, 0.002, 0.004)[:, None]
+    Rr = rel_from_mask(rng, rk)
+    yield "long_runs", dict(lhs=L, rhs=Rr, join_keys=[(1, 0)], agg_keys=[(0, 0), (1, 1)],
+                            kernel_string="ij,jk->ik", dtype="fp32")
+    # more runs (3,000 lhs rows) than count and fill blocks
+    L = rel_from_mask(rng, rng.random((3000, 6)) < 0.3)
+    Rr = rel_from_mask(rng, rng.random((6, 40)) < 0.3)
+    yield "many_runs", dict(lhs=L, rhs=Rr, join_keys=[(1, 0)], agg_keys=[(0, 0), (1, 1)],
+                            kernel_string="ij,jk->ik", dtype="fp32")
 
 
 WL = list(workloads())
