@@ -412,6 +412,22 @@ def test_plan_ticket_cycle_stays_below_the_plans_limit():
     assert _device._next_ticket((1 << 30) - 1) == 1
 
 
+def test_row_ticket_fold():
+    """The row plan's packed word holds 20 ticket bits: tickets fold to
+    1 .. 2^20 - 1, never 0 (a cleared slot), consecutive ones stay distinct,
+    also across the 2^30 cycle of the host counter."""
+    from einjax_amd import _device
+
+    m = (1 << 20) - 1
+    assert [_device._ticket20(t) for t in (1, 2, m, m + 1, m + 2)] == [1, 2, m, 1, 2]
+    t = (1 << 30) - 1
+    nxt = _device._next_ticket(t)
+    assert nxt == 1 and _device._ticket20(t) != _device._ticket20(nxt)
+    for t in range(1, 3 * m, 997):
+        f = _device._ticket20(t)
+        assert 1 <= f <= m and f != _device._ticket20(_device._next_ticket(t))
+
+
 def test_count_slot_cleared_before_each_plan(monkeypatch):
     """A dense plan's packed word (ticket << 33 | flag << 32 | U) for ticket
     2^20 + 510 reads as the row plan's next ticket (folded to 512) when
