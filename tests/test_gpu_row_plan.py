@@ -303,6 +303,44 @@ def test_row_step_bitwise_equals_general_plan(gpu, idx, dtype, monkeypatch):
     assert R.rel_l2(got.values.float().cpu().numpy(), want.values) <= tol
 
 
+@pytest.mark.parametrize("idx", [0, 1])
+@pytest.mark.parametrize("dt", [torch.float64, torch.float16], ids=["f64", "f16"])
+def test_row_step_other_float_dtypes(gpu, idx, dt, monkeypatch):
+    """float64 and float16 relations through the row step (operands in fp32,
+    results in the reference's dtype: float32 for float64 tiles, float16 for
+    float16 tiles): bitwise the exact path's result, the oracle's
+    coordinates, values within tolerance of float64 math."""
+    name, w = WL[idx]
+    note("row step dtype", name, dt)
+    L, Rr, keys, agg, ks = w["lhs"], w["rhs"], w["join_keys"], w["agg_keys"], w["kernel_string"]
+    vals = lambda r: torch.from_numpy(np.ascontiguousarray(r.values, dtype=np.float64)).cuda().to(dt)
+    lhs = SparseTensorRelation(torch.from_numpy(np.ascontiguousarray(L.coords)).cuda(), vals(L),
+                               L.shape, L.tile_shape)
+    rhs = SparseTensorRelation(torch.from_numpy(np.ascontiguousarray(Rr.coords)).cuda(),
+                               vals(Rr), Rr.shape, Rr.tile_shape)
+    used = []
+    real = _device.run_row_step
+    monkeypatch.setattr(_device, "run_row_step",
+                        lambda step, ev=None: used.append(1) or real(step, ev))
+    sd._pair_hints.clear()
+    sd._steps.clear()
+    first = ej.execute_sparse(lhs, rhs, keys, ks, agg)  # exact path
+    got = ej.execute_sparse(lhs, rhs, keys, ks, agg)
+    again = ej.execute_sparse(lhs, rhs, keys, ks, agg)
+    assert len(used) == 2
+    want_dt = torch.float32 if dt == torch.float64 else torch.float16
+    for res in (first, got, again):
+        assert res.values.dtype == want_dt
+    assert torch.equal(got.coords, first.coords) and torch.equal(got.values, first.values)
+    assert torch.equal(again.values, first.values)
+    Lh = R.Rel(L.coords, vals(L).double().cpu().numpy(), L.shape, L.tile_shape)
+    Rh = R.Rel(Rr.coords, vals(Rr).double().cpu().numpy(), Rr.shape, Rr.tile_shape)
+    want = R.execute_sparse(Lh, Rh, keys, ks, agg, precision="fp64")
+    npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+    tol = 1e-5 if dt == torch.float64 else 2e-3
+    assert R.rel_l2(got.values.double().cpu().numpy(), want.values) <= tol
+
+
 def test_row_step_full_size_zipf(gpu, monkeypatch):
     """The 32768^2 Zipf sparse x sparse workload (P = 54,516, U = 31,573)
     through the row plan: bitwise equal to the exact path's result and within
