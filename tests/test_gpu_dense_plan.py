@@ -230,6 +230,47 @@ def test_dense_step_bitwise_equals_general_plan(gpu, idx, monkeypatch):
         assert R.rel_l2(dense[0].values.float().cpu().numpy(), want.values) <= tol
 
 
+@pytest.mark.parametrize("dt", [torch.float64, torch.float16], ids=["f64", "f16"])
+def test_dense_step_other_float_dtypes(gpu, dt, monkeypatch):
+    """float64 and float16 relations through the dense step (operands in
+    fp32, results in the reference's dtype: float32 for float64 tiles,
+    float16 for float16 tiles): bitwise the exact path's result, the
+    oracle's coordinates, values within tolerance of float64 math."""
+    name, w = list(workloads())[0]
+    note("dense step dtype", name, dt)
+    L, Rr = w["lhs"], w["rhs"]
+    keys, agg, ks = w["join_keys"], w["agg_keys"], w["kernel_string"]
+    vals = lambda r: torch.from_numpy(np.ascontiguousarray(r.values, dtype=np.float64)).cuda().to(dt)
+    lhs = SparseTensorRelation(torch.from_numpy(L.coords).cuda(), vals(L), L.shape, L.tile_shape)
+    rhs = SparseTensorRelation(torch.from_numpy(Rr.coords).cuda(), vals(Rr), Rr.shape,
+                               Rr.tile_shape)
+    statuses = []
+    real = _device.run_dense_step
+    monkeypatch.setattr(_device, "run_dense_step",
+                        lambda *a, **k: statuses.append(1) or real(*a, **k))
+    sd._pair_hints.clear()
+    sd._steps.clear()
+    res = [ej.execute_sparse(lhs, rhs, keys, ks, agg) for _ in range(3)]
+    assert statuses
+    want_dt = torch.float32 if dt == torch.float64 else torch.float16
+    for r in res:
+        assert r.values.dtype == want_dt
+        assert torch.equal(r.coords, res[0].coords) and torch.equal(r.values, res[0].values)
+    with monkeypatch.context() as m:
+        m.setattr(sd, "_dense_step", lambda *a, **k: None)
+        m.setattr(sd, "_row_step", lambda *a, **k: None)
+        sd._steps.clear()
+        general = ej.execute_sparse(lhs, rhs, keys, ks, agg, fused=True)
+        sd._steps.clear()
+    assert torch.equal(general.values, res[0].values)
+    Lh = R.Rel(L.coords, vals(L).double().cpu().numpy(), L.shape, L.tile_shape)
+    Rh = R.Rel(Rr.coords, vals(Rr).double().cpu().numpy(), Rr.shape, Rr.tile_shape)
+    want = R.execute_sparse(Lh, Rh, keys, ks, agg, precision="fp64")
+    npt.assert_array_equal(res[1].coords.cpu().numpy(), want.coords)
+    tol = 1e-5 if dt == torch.float64 else 2e-3
+    assert R.rel_l2(res[1].values.double().cpu().numpy(), want.values) <= tol
+
+
 def _shuffled(r: R.Rel, seed: int) -> R.Rel:
     p = np.random.default_rng(seed).permutation(len(r.coords))
     return R.Rel(r.coords[p], r.values[p], r.shape, r.tile_shape)
