@@ -303,6 +303,36 @@ def test_row_step_bitwise_equals_general_plan(gpu, idx, dtype, monkeypatch):
     assert R.rel_l2(got.values.float().cpu().numpy(), want.values) <= tol
 
 
+@pytest.mark.parametrize("idx", [0, 2])
+def test_row_step_bf16_with_fp32_output(gpu, idx, monkeypatch):
+    """bf16 relations with out_dtype=float32 through the row step: fp32
+    output tiles, bitwise the general plan's, within 1e-5 of float64 math on
+    the bf16-rounded inputs."""
+    name, w = WL[idx]
+    note("row step bf16 -> fp32", name)
+    L, Rr, keys, agg, ks = w["lhs"], w["rhs"], w["join_keys"], w["agg_keys"], w["kernel_string"]
+    L = R.Rel(L.coords, R.bf16_round(L.values), L.shape, L.tile_shape)
+    Rr = R.Rel(Rr.coords, R.bf16_round(Rr.values), Rr.shape, Rr.tile_shape)
+    lhs, rhs = dev_rel(L, "bf16"), dev_rel(Rr, "bf16")
+    used = []
+    real = _device.run_row_step
+    monkeypatch.setattr(_device, "run_row_step",
+                        lambda step, ev=None: used.append(1) or real(step, ev))
+    sd._pair_hints.clear()
+    sd._steps.clear()
+    f32 = torch.float32
+    ej.execute_sparse(lhs, rhs, keys, ks, agg, out_dtype=f32)
+    got = ej.execute_sparse(lhs, rhs, keys, ks, agg, out_dtype=f32)
+    assert used and got.values.dtype == f32
+    monkeypatch.setattr(sd, "_row_step", lambda *a, **k: None)
+    sd._steps.clear()
+    general = ej.execute_sparse(lhs, rhs, keys, ks, agg, out_dtype=f32)
+    assert torch.equal(got.coords, general.coords) and torch.equal(got.values, general.values)
+    want = R.execute_sparse(L, Rr, keys, ks, agg, precision="fp64")
+    npt.assert_array_equal(got.coords.cpu().numpy(), want.coords)
+    assert R.rel_l2(got.values.cpu().numpy(), want.values) <= 1e-5
+
+
 @pytest.mark.parametrize("idx", [0, 1])
 @pytest.mark.parametrize("dt", [torch.float64, torch.float16], ids=["f64", "f16"])
 def test_row_step_other_float_dtypes(gpu, idx, dt, monkeypatch):
