@@ -333,6 +333,33 @@ def test_row_step_bf16_with_fp32_output(gpu, idx, monkeypatch):
     assert R.rel_l2(got.values.cpu().numpy(), want.values) <= 1e-5
 
 
+def test_row_step_host_relations(gpu, monkeypatch):
+    """Host (NumPy) relations called repeatedly: the later calls take the row
+    step on device copies and return host arrays with the reference's dtypes
+    (int32 coordinates, float32 values), equal to the first call's."""
+    name, w = WL[1]
+    note("row step, host relations", name)
+    L, Rr, keys, agg, ks = w["lhs"], w["rhs"], w["join_keys"], w["agg_keys"], w["kernel_string"]
+    lhs = SparseTensorRelation(L.coords, L.values, L.shape, L.tile_shape)
+    rhs = SparseTensorRelation(Rr.coords, Rr.values, Rr.shape, Rr.tile_shape)
+    used = []
+    real = _device.run_row_step
+    monkeypatch.setattr(_device, "run_row_step",
+                        lambda step, ev=None: used.append(1) or real(step, ev))
+    sd._pair_hints.clear()
+    sd._steps.clear()
+    res = [ej.execute_sparse(lhs, rhs, keys, ks, agg) for _ in range(3)]
+    assert used
+    for r in res:
+        assert isinstance(r.coords, np.ndarray) and isinstance(r.values, np.ndarray)
+        assert r.coords.dtype == np.int32 and r.values.dtype == np.float32
+        npt.assert_array_equal(r.coords, res[0].coords)
+        npt.assert_array_equal(r.values, res[0].values)
+    want = R.execute_sparse(L, Rr, keys, ks, agg, precision="fp64")
+    npt.assert_array_equal(res[-1].coords, want.coords)
+    assert R.rel_l2(res[-1].values, want.values) <= 1e-5
+
+
 @pytest.mark.parametrize("idx", [0, 1])
 @pytest.mark.parametrize("dt", [torch.float64, torch.float16], ids=["f64", "f16"])
 def test_row_step_other_float_dtypes(gpu, idx, dt, monkeypatch):
