@@ -333,6 +333,40 @@ def test_row_step_bf16_with_fp32_output(gpu, idx, monkeypatch):
     assert R.rel_l2(got.values.cpu().numpy(), want.values) <= 1e-5
 
 
+def test_row_steps_on_two_streams(gpu, monkeypatch):
+    """Two row steps of different sizes queued from one thread on two
+    streams, back to back without a wait between them: each stream's plan
+    has its own device counters, so both results equal the same steps run
+    alone on one stream, bitwise."""
+    note("row steps on two streams")
+    used = []
+    real = _device.run_row_step
+    monkeypatch.setattr(_device, "run_row_step",
+                        lambda step, ev=None: used.append(1) or real(step, ev))
+    runs = []
+    for idx in (0, 5):
+        name, w = WL[idx]
+        runs.append((dev_rel(w["lhs"]), dev_rel(w["rhs"]), w["join_keys"], w["kernel_string"],
+                     w["agg_keys"]))
+    sd._pair_hints.clear()
+    sd._steps.clear()
+    alone = [ej.execute_sparse(*r) for r in runs]  # exact path: sets the pair hints
+    alone = [ej.execute_sparse(*r) for r in runs]
+    torch.cuda.synchronize()
+    assert len(used) == 2
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            a = ej.execute_sparse(*runs[0])
+        with torch.cuda.stream(s2):
+            b = ej.execute_sparse(*runs[1])
+        torch.cuda.synchronize()
+        for got, want in ((a, alone[0]), (b, alone[1])):
+            assert torch.equal(got.coords, want.coords)
+            assert torch.equal(got.values, want.values)
+    assert len(used) == 8
+
+
 def test_row_step_host_relations(gpu, monkeypatch):
     """Host (NumPy) relations called repeatedly: the later calls take the row
     step on device copies and return host arrays with the reference's dtypes
